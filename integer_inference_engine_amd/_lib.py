@@ -1,0 +1,61 @@
+"""ctypes binding of ``libimie_gfx950.so`` (the gfx950 producer library).
+
+The library is REQUIRED: ``lib()`` raises ``ImportError`` when the in-tree ``.so`` is missing, so no caller can
+silently run without the HIP kernels. Whether a usable gfx950 device is present is a separate question answered
+by ``device_available()`` (the reference's ``bonsai_gpu_available`` probe).
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int, c_int64, c_uint64, c_void_p
+from functools import lru_cache
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libimie_gfx950.so"
+
+# name -> (restype, argtypes). Every symbol declared in include/imie_bonsai.h and include/imie_nmc.h.
+SIGNATURES = {
+    # runtime (include/imie_bonsai.h)
+    "bonsai_gpu_available": (c_int, []),
+    "bonsai_gpu_mem_info": (c_int, [c_void_p, c_void_p]),
+    "imie_abi_version": (c_int, []),
+    "imie_last_error": (ctypes.c_char_p, []),
+    "imie_default_stream": (c_void_p, []),
+    "imie_synchronize": (c_int, []),
+    "imie_probe_mfma": (c_int, [c_void_p, c_void_p, c_void_p]),
+    # Q1_0 linear
+    "bonsai_q1_linear_gpu": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "bonsai_q1_register_weight": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
+    "bonsai_q1_register_weight_i32": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
+    "bonsai_q1_apply_resident": (c_int, [c_int64, c_void_p, c_int64, c_int64, c_void_p]),
+    "bonsai_q1_free_weights": (None, []),
+    "bonsai_q1_resident_weight_bytes": (c_uint64, []),
+    "imie_q1_repack_host": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "imie_q1_apply_dev": (c_int, [c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_q1_weight_info": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
+    "imie_q1_linear_simple_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                          c_void_p, c_void_p]),
+}
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python -m integer_inference_engine_amd.build`")
+    so = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(so, name)
+        fn.restype = res
+        fn.argtypes = args
+    return so
+
+
+@lru_cache(maxsize=1)
+def device_available() -> bool:
+    """True iff the library loaded and a gfx950 device is usable (rc 0 from ``bonsai_gpu_available``)."""
+    return lib().bonsai_gpu_available() == 0
+
+
+def last_error() -> str:
+    v = lib().imie_last_error()
+    return v.decode() if v else ""

@@ -1,0 +1,111 @@
+// Process-global runtime: device probe, default stream, error notes, workspace buffers, memory info.
+#include "imie_common.h"
+#include <stdio.h>
+#include <string.h>
+
+static hipStream_t g_stream = nullptr;
+static int g_ready = -1;
+static char g_last_error[256];
+
+std::recursive_mutex& imie_lock() {
+  static std::recursive_mutex m;
+  return m;
+}
+
+void imie_note_error(hipError_t e, const char* what) {
+  snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(e));
+}
+
+int imie_device_ready() {
+  if (g_ready >= 0) return g_ready == 1 ? 0 : 1;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) { g_ready = 0; return 1; }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) != hipSuccess) { g_ready = 0; return 1; }
+  // The kernels are built for gfx950 only; refuse any other architecture loudly (rc != 0).
+  g_ready = (strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : 0;
+  if (!g_ready) snprintf(g_last_error, sizeof(g_last_error), "device %s is not gfx950", prop.gcnArchName);
+  return g_ready == 1 ? 0 : 1;
+}
+
+hipStream_t imie_stream() {
+  if (!g_stream) {
+    if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) g_stream = nullptr;
+  }
+  return g_stream;
+}
+
+int DevBuf::ensure(size_t bytes) {
+  if (bytes <= cap && p) return 0;
+  if (p) { (void)hipFree(p); p = nullptr; cap = 0; }
+  size_t want = bytes < 256 ? 256 : bytes;
+  if (hipMalloc(&p, want) != hipSuccess) { p = nullptr; return 1; }
+  cap = want;
+  return 0;
+}
+
+void DevBuf::release() {
+  if (p) (void)hipFree(p);
+  p = nullptr;
+  cap = 0;
+}
+
+extern "C" {
+
+// 0 iff a usable gfx950 device is present (bonsai_q1_gpu.cu `bonsai_gpu_available` contract).
+int bonsai_gpu_available(void) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  return imie_device_ready();
+}
+
+int imie_abi_version(void) { return 1; }
+
+const char* imie_last_error(void) { return g_last_error; }
+
+int bonsai_gpu_mem_info(uint64_t* free_b, uint64_t* total_b) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  if (!free_b || !total_b || imie_device_ready() != 0) return IMIE_EARG;
+  size_t f = 0, t = 0;
+  IMIE_HIP(hipMemGetInfo(&f, &t));
+  *free_b = f;
+  *total_b = t;
+  return IMIE_OK;
+}
+
+// Library stream as an opaque handle so a host runtime can order its own work around the library.
+void* imie_default_stream(void) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  return (void*)imie_stream();
+}
+
+int imie_synchronize(void) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  IMIE_HIP(hipStreamSynchronize(imie_stream()));
+  return IMIE_OK;
+}
+
+}  // extern "C"
+
+// One v_mfma_i32_16x16x64_i8 over caller-provided per-lane operands (A, B: 64 lanes x 16 int8; D: 64 lanes x 4
+// int32). Lets the tests pin the operand / accumulator lane mapping the Q1 kernels rely on.
+__global__ void imie_probe_mfma_kernel(const v4i* a, const v4i* b, v4i* d) {
+  const int l = threadIdx.x;
+  v4i acc = {0, 0, 0, 0};
+  d[l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[l], b[l], acc, 0, 0, 0);
+}
+
+extern "C" int imie_probe_mfma(const int8_t* a_host, const int8_t* b_host, int32_t* d_host) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  if (!a_host || !b_host || !d_host || imie_device_ready() != 0) return IMIE_EARG;
+  void *a = nullptr, *b = nullptr, *d = nullptr;
+  IMIE_HIP(hipMalloc(&a, 1024));
+  IMIE_HIP(hipMalloc(&b, 1024));
+  IMIE_HIP(hipMalloc(&d, 1024));
+  IMIE_HIP(hipMemcpy(a, a_host, 1024, hipMemcpyHostToDevice));
+  IMIE_HIP(hipMemcpy(b, b_host, 1024, hipMemcpyHostToDevice));
+  hipLaunchKernelGGL(imie_probe_mfma_kernel, dim3(1), dim3(64), 0, 0, (const v4i*)a, (const v4i*)b, (v4i*)d);
+  IMIE_HIP(hipGetLastError());
+  IMIE_HIP(hipMemcpy(d_host, d, 1024, hipMemcpyDeviceToHost));
+  (void)hipFree(a); (void)hipFree(b); (void)hipFree(d);
+  return IMIE_OK;
+}
