@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X: packed Q1_0 matvec HBM GB/s (BASELINE.json metric, config 1).
+
+One step = one launch of the Q1_0 matvec over a rotation of R distinct 4096x4096 weight replicas (R=384,
+~1.2 GB of resident weights, so the working set cannot live in the 256 MB Infinity Cache) against one int8-range
+activation vector, all inputs already resident in HBM. Scales are codec-range (round(fp16 * 2^16) of random
+finite fp16 values), which do not fit int32, so the resident layout keeps 8-byte scales.
+
+Prints ONE JSON line (driver contract) with ``roofline`` (dominant kernel timed with HIP events on its own
+stream) and ``cpu_baseline`` (the reference's C kernel ``bonsai_q1_linear_i64`` compiled from its sources into
+oracle/_ref, timed on this host's cores on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+HBM_PEAK_GBS = 8000.0
+K = 4096
+NB = K // 128
+
+
+def codec_scales(rng, shape):
+    """round_half_even(v * 2^16) for v uniform over finite fp16 bit patterns with a random sign."""
+    h = rng.integers(0, 0x7C00, size=shape, dtype=np.uint16)
+    v = h.view(np.float16).astype(np.float64)
+    v = np.where(rng.integers(0, 2, size=shape) == 1, -v, v)
+    return np.rint(v * 65536.0).astype(np.int64)
+
+
+def matvec_bytes(scale_bytes: int) -> int:
+    """Algorithmic HBM bytes of one 4096x4096 Q1_0 matvec: bits + scales + x + y."""
+    return K * NB * 16 + K * NB * scale_bytes + K * 8 + K * 8
+
+
+def cpu_worker(npz: str, seconds: float) -> None:
+    """Time the reference CPU kernel (or the C restatement) on the config-1 matvec; print one JSON line."""
+    import ctypes
+    d = np.load(npz)
+    x, bits, scale, gpu_out = d["x"], d["bits"], d["scale"], d["out"]
+    ref = ROOT / "oracle" / "_ref" / "libbonsai_q1_kernel.so"
+    if ref.exists():
+        so = ctypes.CDLL(str(ref))
+        fn, kind = so.bonsai_q1_linear_i64, "reference"
+    else:
+        from oracle import c_oracle
+        so = c_oracle.lib()
+        fn, kind = so.imo_q1_linear, "port"
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_void_p]
+    out = np.empty((1, K), dtype=np.int64)
+    call = lambda: fn(x.ctypes.data, bits.ctypes.data, scale.ctypes.data, 1, K, NB, 16, out.ctypes.data)
+    assert call() == 0
+    match = bool(np.array_equal(out, gpu_out))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = matvec_bytes(8) * n / el / 1e9
+    print(json.dumps({"value": gbs, "unit": "GB/s", "kind": kind, "calls": n, "seconds": el, "match": match}))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--replicas", type=int, default=384)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if args.cpu_worker:
+        cpu_worker(args.cpu_worker, args.cpu_seconds)
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py: this build measures ONE MI355X; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import ctypes
+    import torch
+    from integer_inference_engine_amd import _lib
+    so = _lib.lib()
+    assert _lib.device_available(), "no usable gfx950 device"
+    R = args.replicas
+    N = K * R
+    rng = np.random.default_rng(2026)
+    print(f"[bench] generating {R} replicas of a {K}x{K} Q1_0 weight", file=sys.stderr, flush=True)
+    bits = rng.integers(0, 256, size=(N, NB, 16), dtype=np.uint8)
+    scale = codec_scales(rng, (N, NB))
+    h = so.bonsai_q1_register_weight(bits.ctypes.data, scale.ctypes.data, N, NB)
+    assert h >= 0, _lib.last_error()
+    nn, nbb, sb = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    so.imie_q1_weight_info(h, ctypes.byref(nn), ctypes.byref(nbb), ctypes.byref(sb))
+    scale_bytes = int(sb.value)
+    x_host = rng.integers(-127, 128, size=(1, K), dtype=np.int64)
+    x = torch.from_numpy(x_host).cuda()
+    out = torch.empty((1, N), dtype=torch.int64, device="cuda")
+    stream = torch.cuda.Stream()          # a real (non-null) stream shared by the kernels and the timing events
+    torch.cuda.set_stream(stream)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        rc = so.imie_q1_apply_dev(h, ctypes.c_void_p(x.data_ptr()), 1, 16, ctypes.c_void_p(out.data_ptr()), sp)
+        assert rc == 0, _lib.last_error()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # exactness spot check of replica 0 against the library's independent thread-per-output kernel
+    b0 = torch.from_numpy(np.ascontiguousarray(bits[:K])).cuda()
+    s0 = torch.from_numpy(np.ascontiguousarray(scale[:K])).cuda()
+    chk = torch.empty((1, K), dtype=torch.int64, device="cuda")
+    assert so.imie_q1_linear_simple_dev(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(b0.data_ptr()),
+                                        ctypes.c_void_p(s0.data_ptr()), 1, K, NB, 16, ctypes.c_void_p(chk.data_ptr()),
+                                        sp) == 0
+    torch.cuda.synchronize()
+    exact = bool(torch.equal(chk[0], out[0, :K]))
+
+    so.imie_profile_begin()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    kms, kcnt = ctypes.c_double(), ctypes.c_int64()
+    so.imie_profile_read(1, ctypes.byref(kms), ctypes.byref(kcnt))
+    pms, pcnt = ctypes.c_double(), ctypes.c_int64()
+    so.imie_profile_read(0, ctypes.byref(pms), ctypes.byref(pcnt))
+    so.imie_profile_end()
+
+    step_bytes = R * matvec_bytes(scale_bytes)
+    value = step_bytes * args.steps / (ms / 1e3) / 1e9
+    k_avg_s = kms.value / max(1, kcnt.value) / 1e3
+    achieved = step_bytes / k_avg_s / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "q1_matvec_c1_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        with tempfile.TemporaryDirectory() as td:
+            npz = os.path.join(td, "c1.npz")
+            np.savez(npz, x=x_host, bits=bits[:K], scale=scale[:K], out=out[:, :K].cpu().numpy())
+            cores = min(os.cpu_count() or 1, 16)
+            env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close")
+            r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-worker", npz, "--cpu-seconds",
+                                str(args.cpu_seconds)], env=env, capture_output=True, text=True, timeout=300)
+            if r.returncode == 0:
+                c = json.loads(r.stdout.strip().splitlines()[-1])
+                cpu = {"value": round(c["value"], 3), "unit": "GB/s", "cores": cores, "kind": c["kind"],
+                       "sample": f"config-1 4096x4096 Q1_0 matvec (int64 codec-range scales), {c['calls']} calls "
+                                 f"in {c['seconds']:.1f} s; output byte-equal to GPU: {c['match']}"}
+            else:
+                print(r.stderr[-2000:], file=sys.stderr)
+
+    line = {
+        "metric": "Q1 matvec HBM GB/s (% of peak); 8B-shape decode tok/s b=1; byte-exact",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int64 (int8 MFMA limbs, i32 accumulate)", "data": "synthetic",
+        "config": {"workload": f"config-1 Q1_0 matvec 4096x4096, b=1, rotated over {R} resident replicas "
+                               f"(one launch = {R} matvecs, {step_bytes / 1e9:.2f} GB)",
+                   "replicas": R, "scale_bytes": scale_bytes, "frac": 16, "byte_exact_replica0": exact,
+                   "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+                   "us_per_matvec": round(ms / args.steps / R * 1e3, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
+                     "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

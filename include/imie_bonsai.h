@@ -6,7 +6,7 @@
  *   process-global registries that live until the matching *_free call. Not reentrant (one caller at a time;
  *   entry points serialize on a process lock).
  * Entry points prefixed imie_ have no counterpart in the reference: they take DEVICE pointers and an optional
- * hipStream_t (as void*, NULL = library stream) and are asynchronous.
+ * hipStream_t (as void*; NULL is HIP's null stream) and are asynchronous.
  */
 #ifndef IMIE_BONSAI_H
 #define IMIE_BONSAI_H
@@ -24,6 +24,11 @@ int imie_abi_version(void);
 const char *imie_last_error(void);
 void *imie_default_stream(void);
 int imie_synchronize(void);
+/* per-kernel HIP-event timing on the stream each kernel runs on (kernel ids: 0 q1 prep, 1 q1 matvec,
+ * 2 q1 GEMM, 3 attention, 4 Q4_K/Q6_K linear); read synchronizes. */
+void imie_profile_begin(void);
+int imie_profile_read(int kernel, double *total_ms, int64_t *count);
+void imie_profile_end(void);
 /* one int8 MFMA over per-lane operands (A, B: 64x16 int8, D: 64x4 int32); pins the lane mapping in tests. */
 int imie_probe_mfma(const int8_t *a, const int8_t *b, int32_t *d);
 

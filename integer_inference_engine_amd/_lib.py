@@ -23,6 +23,9 @@ SIGNATURES = {
     "imie_default_stream": (c_void_p, []),
     "imie_synchronize": (c_int, []),
     "imie_probe_mfma": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "imie_profile_begin": (None, []),
+    "imie_profile_read": (c_int, [c_int, c_void_p, c_void_p]),
+    "imie_profile_end": (None, []),
     # Q1_0 linear
     "bonsai_q1_linear_gpu": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "bonsai_q1_register_weight": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),

@@ -72,3 +72,12 @@ __device__ __forceinline__ int64_t imie_wave_sum_i64(int64_t v) {
   for (int o = 32; o >= 1; o >>= 1) v = (int64_t)((uint64_t)v + (uint64_t)__shfl_xor(v, o, 64));
   return v;
 }
+
+// ---------------------------------------------------------------------------------------------------------
+// Per-kernel HIP-event timing (enabled by imie_profile_begin; used by the benchmark to time the dominant
+// kernel on the stream it runs on). Kernel ids below.
+// ---------------------------------------------------------------------------------------------------------
+enum { IMIE_K_Q1_PREP = 0, IMIE_K_Q1_GEMV = 1, IMIE_K_Q1_GEMM = 2, IMIE_K_ATTN = 3, IMIE_K_QK = 4,
+       IMIE_K_COUNT = 16 };
+bool imie_prof_on();
+void imie_prof_mark(int kernel, hipStream_t st, bool begin);

@@ -129,103 +129,152 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------------
-// MFMA matvec / small-T linear. Grid: (ceil(ntiles / R), token chunks of Tc). Block: W waves; wave w handles
-// slabs w, w + W, ... of each of the workgroup's R tiles. The per-row partial sums of the waves meet in an
-// LDS int64 accumulator (ds_add_u64; integer addition is order-free, so the result is deterministic).
-// The A operands (digit table) are read from the L2-resident xq table by the 16 active lanes only.
+// MFMA matvec / small-T linear.
+//   * MFMA rows m = 4*blk + (s & 3): lane (g, n) of the accumulator holds, for block g of the slab and output
+//     row n, the four partials of shifts 0..3 (d0) and 4..7 (d1). 128*pos = sum d0[r] << (7-r) +
+//     sum_{r<3} d1[r] << (3-r) - d1[3]  (8 v_lshl_add, no cross-lane traffic); the A operand is non-zero in
+//     lane (m, g) iff m >> 2 == g and the MFMA's shift matches m & 3.
+//   * Each wave streams its own R tiles over a slab range with double-buffered 16 B/lane loads; the digit
+//     table of the slab range (up to Lcap limbs) is staged once per workgroup in LDS.
+//   * grid.y splits K: with ksplit > 1 the waves add their int64 partials into a zeroed output with 64-bit
+//     atomics (integer addition: order-free and exact).
 // ------------------------------------------------------------------------------------------------------
-template <bool S64>
-__global__ __launch_bounds__(1024) void q1_gemv_mfma_kernel(
+template <bool S64, int R, int TT>
+__global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     const uint4* __restrict__ bitsT, const void* __restrict__ scaleT, const uint4* __restrict__ xq,
-    const int64_t* __restrict__ totals, const int* __restrict__ lslab, int64_t N, int64_t ntiles,
-    int64_t nslabs, int64_t nbp, int T, int Tc, int R, int frac, int64_t* __restrict__ out) {
+    const int64_t* __restrict__ totals, const int* __restrict__ lslab, int64_t N, int64_t ntiles, int64_t nslabs,
+    int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, int64_t* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
+  uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int W = blockDim.x >> 6;
-  const int64_t tile0 = (int64_t)blockIdx.x * R;
-  const int t0 = blockIdx.y * Tc;
-  const int tn = min(Tc, T - t0);
+  const int64_t s0 = (int64_t)blockIdx.y * spk;
+  const int64_t s1 = min(nslabs, s0 + spk);
+  const int64_t nsl = s1 - s0;
 
-  uint64_t* acc = (uint64_t*)smem;                           // [tn][R*16]
-  for (int i = threadIdx.x; i < tn * R * 16; i += blockDim.x) acc[i] = 0;
+  // stage the digit operands of this slab range (the same x for every wave of the workgroup)
+  for (int t = 0; t < T; ++t)
+    for (int64_t j = 0; j < nsl; ++j) {
+      const int L = min(lslab[t * nslabs + s0 + j], Lcap);
+      uint4* dst = stage + ((t * spk + j) * Lcap) * 32;
+      for (int i = threadIdx.x; i < L * 32; i += blockDim.x) {
+        const int l = i >> 5, e = i & 31;
+        dst[i] = xq[(((int64_t)t * kMaxLimbs + l) * nbp + (s0 + j) * kSlabBlocks) * 8 + e];
+      }
+    }
   __syncthreads();
 
-  const int g = lane >> 4;       // block within slab (B / epilogue view); shift group in the D view
+  const int64_t tile0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+  if (tile0 >= ntiles) return;
+  const int g = lane >> 4;       // block within the slab
   const int n = lane & 15;       // output row within the tile
-  // A-operand activity: lane (m = n, grp = g) carries digits for MFMA shift s iff m == grp + 4 * (s & 3).
-  const int arow = n - g;
-  const bool aact = arow >= 0 && (arow & 3) == 0;
-  const int as = arow >> 2;      // the s & 3 this lane is active for
-  const int hi = (g >> 1) & 1, lo = g & 1;
-
+  const bool aact = (n >> 2) == g;
+  const int as = n & 3;          // this lane feeds A for shifts as and as + 4
   v4i areg[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s) areg[s] = v4i{0, 0, 0, 0};
 
-  for (int r = 0; r < R; ++r) {
-    const int64_t tile = tile0 + r;
-    if (tile >= ntiles) break;
-    for (int64_t sl = wave; sl < nslabs; sl += W) {
-      const int64_t idx = (tile * nslabs + sl) * 64 + lane;
-      const uint4 wb = bitsT[idx];
-      int64_t sc;
-      if (S64) sc = ((const int64_t*)scaleT)[idx];
-      else sc = ((const int32_t*)scaleT)[idx];
-      v4i bq[8];
+  uint64_t acc[TT][R];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t m = 0x01010101u << s;
-        bq[s] = v4i{(int)(wb.x & m), (int)(wb.y & m), (int)(wb.z & m), (int)(wb.w & m)};
-      }
-      for (int t = 0; t < tn; ++t) {
-        const int L = lslab[(t0 + t) * nslabs + sl];
-        const uint4* xt = xq + ((int64_t)(t0 + t) * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8;
-        const int64_t total = totals[(int64_t)(t0 + t) * nbp + sl * kSlabBlocks + g];
-        uint64_t pos = 0;
-        for (int l = 0; l < L; ++l) {
-          // masked loads: only the lanes active for shift s write areg[s]; the others keep zeros
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            if (aact && as == (s & 3)) {
-              const uint4 a = xt[(int64_t)l * nbp * 8 + s];
-              areg[s] = v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+    for (int r = 0; r < R; ++r) acc[t][r] = 0;
+
+  uint4 wb[2][R];
+  int64_t sc[2][R];
+  auto load = [&](int buf, int64_t sl) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t tl = tile0 + r < ntiles ? tile0 + r : tile0;
+      const int64_t idx = (tl * nslabs + sl) * 64 + lane;
+      const v4i wv = __builtin_nontemporal_load(&((const v4i*)bitsT)[idx]);
+      wb[buf][r] = uint4{(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
+      if (S64) sc[buf][r] = __builtin_nontemporal_load(&((const int64_t*)scaleT)[idx]);
+      else sc[buf][r] = __builtin_nontemporal_load(&((const int32_t*)scaleT)[idx]);
+    }
+  };
+  auto compute = [&](int buf, int64_t sl) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t >= T) break;
+      const int L = lslab[t * nslabs + sl];
+      const int64_t total = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
+      const uint4* st = stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8;
+      const uint4* gx = xq + ((int64_t)t * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8;
+      uint64_t pos[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) pos[r] = 0;
+      for (int l = 0; l < L; ++l) {
+        // masked loads: only the lanes active for shift s write areg[s]; the others keep zeros
+        if (aact) {
+          const uint4 a0 = l < Lcap ? st[l * 32 + as] : gx[(int64_t)l * nbp * 8 + as];
+          const uint4 a1 = l < Lcap ? st[l * 32 + as + 4] : gx[(int64_t)l * nbp * 8 + as + 4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if (as == s) {
+              areg[s] = v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
+              areg[s + 4] = v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
             }
-          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
           v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
 #pragma unroll
-          for (int s = 0; s < 4; ++s) d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], bq[s], d0, 0, 0, 0);
-#pragma unroll
-          for (int s = 4; s < 8; ++s) d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], bq[s], d1, 0, 0, 0);
-          // lane (g = shift group, n): v_r = partial of block r over shifts g and g+4 (shift 7 reads -128)
-          int v[4];
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int hiv = d1[rr] >> (g + 4);
-            v[rr] = (d0[rr] >> g) + (g == 3 ? -hiv : hiv);
+          for (int s = 0; s < 8; ++s) {
+            uint32_t m = 0x01010101u << s;
+            asm volatile("" : "+s"(m));   // keep each B expansion next to its MFMA (no hoisting across tiles)
+            const uint4 w = wb[buf][r];
+            const v4i b = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
+            if (s < 4) d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], b, d0, 0, 0, 0);
+            else d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], b, d1, 0, 0, 0);
           }
-          // reduce-scatter over the 4 lane groups: group g ends with block g
-          const int send0 = hi ? v[0] : v[2], send1 = hi ? v[1] : v[3];
-          const int keep0 = hi ? v[2] : v[0], keep1 = hi ? v[3] : v[1];
-          const int u0 = keep0 + __shfl_xor(send0, 32, 64);
-          const int u1 = keep1 + __shfl_xor(send1, 32, 64);
-          const int sendq = lo ? u0 : u1, keepq = lo ? u1 : u0;
-          const int p = keepq + __shfl_xor(sendq, 16, 64);
-          pos += (uint64_t)(int64_t)p << (8 * l);
+          // 128 * pos for (block g, row n); shift 7 bytes read as -128
+          const int p128 = (d0[0] << 7) + (d0[1] << 6) + (d0[2] << 5) + (d0[3] << 4) + (d1[0] << 3) +
+                           (d1[1] << 2) + (d1[2] << 1) - d1[3];
+          pos[r] += (uint64_t)(int64_t)(p128 >> 7) << (8 * l);
         }
-        const uint64_t S = 2u * pos - (uint64_t)total;
-        const int64_t prod = (int64_t)(S * (uint64_t)sc);
-        const int64_t term = imie_floor_shift(prod, frac);
-        atomicAdd((unsigned long long*)&acc[(t * R + r) * 16 + n], (unsigned long long)term);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint64_t S = 2u * pos[r] - (uint64_t)total;
+        const int64_t prod = (int64_t)(S * (uint64_t)sc[buf][r]);
+        acc[t][r] += (uint64_t)imie_floor_shift(prod, frac);
+      }
+    }
+  };
+
+  // software pipeline over the slab range: prefetch slab j+1 while computing slab j
+  load(0, s0);
+  int64_t sl = s0;
+  for (; sl + 1 < s1; sl += 2) {
+    load(1, sl + 1);
+    compute(0, sl);
+    if (sl + 2 < s1) load(0, sl + 2);
+    compute(1, sl + 1);
+  }
+  if (sl < s1) compute(0, sl);
+
+  // sum the 4 blocks of each row (lane groups g) and write / accumulate row totals
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    if (t >= T) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint64_t v = acc[t][r];
+      v += (uint64_t)__shfl_xor((int64_t)v, 16, 64);
+      v += (uint64_t)__shfl_xor((int64_t)v, 32, 64);
+      const int64_t row = (tile0 + r) * kTileRows + n;
+      if (g == 0 && tile0 + r < ntiles && row < N) {
+        if (atomic_out) atomicAdd((unsigned long long*)&out[(int64_t)t * N + row], (unsigned long long)v);
+        else out[(int64_t)t * N + row] = (int64_t)v;
       }
     }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < tn * R * 16; i += blockDim.x) {
-    const int t = i / (R * 16), rem = i % (R * 16);
-    const int64_t row = (tile0 + rem / 16) * kTileRows + (rem % 16);
-    if (row < N) out[(int64_t)(t0 + t) * N + row] = (int64_t)acc[i];
-  }
+}
+
+__global__ void q1_zero_kernel(int64_t* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = 0;
 }
 
 // Straightforward exact kernel (thread per output): used for shapes the MFMA path declines and as an
@@ -265,24 +314,50 @@ static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int6
       g_ws.lslab.ensure((size_t)T * w.nslabs * 4))
     return IMIE_EARG;
   const int64_t K = w.nb * 128;
+  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
   hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)w.nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w.nb, nbp,
                      w.nslabs, (uint32_t*)g_ws.xq.p, (int64_t*)g_ws.totals.p, (int*)g_ws.lslab.p);
+  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
   IMIE_HIP(hipGetLastError());
-  int W = (int)(w.nslabs < 16 ? w.nslabs : 16);
-  int R = (int)(w.ntiles / 1024);
-  R = R < 1 ? 1 : (R > 8 ? 8 : R);
-  int Tc = (int)(T < 4 ? T : 4);
+  // Work split: waves = tile groups of R tiles; grid.y splits the slabs when there are too few tile groups
+  // to keep ~8 waves per CU busy (decode-sized matvecs).
+  const int R = w.ntiles >= 4 * 16384 ? 4 : (w.ntiles >= 2 * 8192 ? 2 : 1);
+  const int64_t groups = (w.ntiles + R - 1) / R;
+  int64_t ksplit = 1;
+  while (groups * ksplit < 8 * 1024 && ksplit * 2 <= w.nslabs && ksplit < 8) ksplit *= 2;
+  const int64_t spk = (w.nslabs + ksplit - 1) / ksplit;
+  ksplit = (w.nslabs + spk - 1) / spk;
+  const int TT = T <= 1 ? 1 : (T <= 2 ? 2 : 4);
+  const int Tc = TT;
+  const size_t budget = 48 * 1024;
+  int Lcap = (int)(budget / ((size_t)Tc * spk * 512));
+  Lcap = Lcap < 1 ? 1 : (Lcap > kMaxLimbs ? kMaxLimbs : Lcap);
+  const size_t lds = (size_t)Tc * spk * Lcap * 512;
   const int fr = (int)(frac > 63 ? 63 : frac);
-  const dim3 grid((unsigned)((w.ntiles + R - 1) / R), (unsigned)((T + Tc - 1) / Tc));
-  const size_t lds = (size_t)Tc * R * 16 * 8;
-  if (w.scale64)
-    hipLaunchKernelGGL(q1_gemv_mfma_kernel<true>, grid, dim3(64 * W), lds, st, w.bits, w.scale,
-                       (const uint4*)g_ws.xq.p, (const int64_t*)g_ws.totals.p, (const int*)g_ws.lslab.p, w.N,
-                       w.ntiles, w.nslabs, nbp, (int)T, Tc, R, fr, out_dev);
-  else
-    hipLaunchKernelGGL(q1_gemv_mfma_kernel<false>, grid, dim3(64 * W), lds, st, w.bits, w.scale,
-                       (const uint4*)g_ws.xq.p, (const int64_t*)g_ws.totals.p, (const int*)g_ws.lslab.p, w.N,
-                       w.ntiles, w.nslabs, nbp, (int)T, Tc, R, fr, out_dev);
+  const dim3 grid((unsigned)((groups + 3) / 4), (unsigned)ksplit);
+  imie_prof_mark(IMIE_K_Q1_GEMV, st, true);
+  for (int64_t t0 = 0; t0 < T; t0 += Tc) {
+    const int tn = (int)(T - t0 < Tc ? T - t0 : Tc);
+    int64_t* o = out_dev + t0 * w.N;
+    const uint4* xq = (const uint4*)g_ws.xq.p + t0 * kMaxLimbs * nbp * 8;
+    const int64_t* tot = (const int64_t*)g_ws.totals.p + t0 * nbp;
+    const int* ls = (const int*)g_ws.lslab.p + t0 * w.nslabs;
+    if (ksplit > 1)
+      hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((tn * w.N + 255) / 256)), dim3(256), 0, st, o,
+                         (int64_t)tn * w.N);
+#define IMIE_Q1_LAUNCH(S64_, R_, TT_)                                                                        \
+  hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, R_, TT_>), grid, dim3(256), lds, st, w.bits, w.scale, xq, tot, ls, \
+                     w.N, w.ntiles, w.nslabs, nbp, tn, fr, spk, Lcap, ksplit > 1 ? 1 : 0, o)
+#define IMIE_Q1_LAUNCH_R(S64_, TT_)                                                                          \
+  if (R == 4) IMIE_Q1_LAUNCH(S64_, 4, TT_); else if (R == 2) IMIE_Q1_LAUNCH(S64_, 2, TT_); else IMIE_Q1_LAUNCH(S64_, 1, TT_)
+#define IMIE_Q1_LAUNCH_T(S64_)                                                                               \
+  if (TT == 1) { IMIE_Q1_LAUNCH_R(S64_, 1); } else if (TT == 2) { IMIE_Q1_LAUNCH_R(S64_, 2); } else { IMIE_Q1_LAUNCH_R(S64_, 4); }
+    if (w.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
+#undef IMIE_Q1_LAUNCH_T
+#undef IMIE_Q1_LAUNCH_R
+#undef IMIE_Q1_LAUNCH
+  }
+  imie_prof_mark(IMIE_K_Q1_GEMV, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
@@ -400,7 +475,7 @@ int imie_q1_apply_dev(int64_t handle, const int64_t* x_dev, int64_t tokens, int6
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   const Q1Weight* w = q1_get(handle);
   if (!w || !x_dev || !out_dev || tokens < 0 || frac < 0) return IMIE_EARG;
-  return q1_apply_dev(*w, x_dev, tokens, frac, out_dev, stream ? (hipStream_t)stream : imie_stream());
+  return q1_apply_dev(*w, x_dev, tokens, frac, out_dev, (hipStream_t)stream);
 }
 
 // Weight geometry of a handle: out_features, n_blocks, scale width in bytes (4 or 8).
@@ -422,7 +497,7 @@ int imie_q1_linear_simple_dev(const int64_t* x_dev, const uint8_t* bits_dev, con
   if (!x_dev || !bits_dev || !scale_dev || !out_dev || tokens < 0 || frac < 0) return IMIE_EARG;
   const int64_t n = tokens * out_features;
   if (n == 0) return IMIE_OK;
-  hipStream_t st = stream ? (hipStream_t)stream : imie_stream();
+  hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(q1_linear_simple_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x_dev,
                      bits_dev, scale_dev, tokens, out_features, n_blocks, (int)(frac > 63 ? 63 : frac), out_dev);
   IMIE_HIP(hipGetLastError());

@@ -109,3 +109,64 @@ extern "C" int imie_probe_mfma(const int8_t* a_host, const int8_t* b_host, int32
   (void)hipFree(a); (void)hipFree(b); (void)hipFree(d);
   return IMIE_OK;
 }
+
+// ---- per-kernel event profiler ---------------------------------------------------------------------------
+namespace {
+struct ProfSlot {
+  std::vector<hipEvent_t> ev;   // begin/end pairs
+  size_t used = 0;
+};
+bool g_prof = false;
+ProfSlot g_slots[IMIE_K_COUNT];
+}  // namespace
+
+bool imie_prof_on() { return g_prof; }
+
+void imie_prof_mark(int kernel, hipStream_t st, bool begin) {
+  if (!g_prof || kernel < 0 || kernel >= IMIE_K_COUNT) return;
+  ProfSlot& s = g_slots[kernel];
+  if (begin && s.used + 2 > s.ev.size()) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return;
+    s.ev.push_back(a);
+    s.ev.push_back(b);
+  }
+  if (begin) {
+    (void)hipEventRecord(s.ev[s.used], st);
+  } else {
+    (void)hipEventRecord(s.ev[s.used + 1], st);
+    s.used += 2;
+  }
+}
+
+extern "C" {
+
+void imie_profile_begin(void) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  g_prof = true;
+  for (auto& s : g_slots) s.used = 0;
+}
+
+// Total milliseconds and launch count recorded for `kernel` since imie_profile_begin (synchronizes).
+int imie_profile_read(int kernel, double* total_ms, int64_t* count) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  if (kernel < 0 || kernel >= IMIE_K_COUNT || !total_ms || !count) return IMIE_EARG;
+  ProfSlot& s = g_slots[kernel];
+  double tot = 0;
+  for (size_t i = 0; i < s.used; i += 2) {
+    IMIE_HIP(hipEventSynchronize(s.ev[i + 1]));
+    float ms = 0;
+    IMIE_HIP(hipEventElapsedTime(&ms, s.ev[i], s.ev[i + 1]));
+    tot += ms;
+  }
+  *total_ms = tot;
+  *count = (int64_t)(s.used / 2);
+  return IMIE_OK;
+}
+
+void imie_profile_end(void) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  g_prof = false;
+}
+
+}  // extern "C"
