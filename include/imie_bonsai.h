@@ -59,6 +59,78 @@ int imie_q1_linear_simple_dev(const int64_t *x_dev, const uint8_t *bits_dev, con
                               int64_t tokens, int64_t out_features, int64_t n_blocks, int64_t frac,
                               int64_t *out_dev, void *stream);
 
+/* ---- integer RMSNorm / element-wise ---------------------------------------------------------------- */
+/* bonsai_q1_gpu.cu:625-670 `bonsai_rmsnorm_gpu` (gpu_native.py:129-138, 390-415): rc 4 on the 128-bit / gain envelope. */
+int bonsai_rmsnorm_gpu(const int64_t *x, int64_t rows, int64_t cols, int64_t frac, int64_t eps, const int64_t *gain,
+                       int64_t *out);
+int imie_rmsnorm_dev(const int64_t *x, int64_t rows, int64_t cols, int64_t frac, int64_t eps, const int64_t *gain,
+                     int64_t *out, int *status, void *stream);
+/* bonsai_q1_kernel.c:1729-1767 `bonsai_silu_i64` (q1_native.py:1895 `silu_native`) on the GPU: (x*sigmoid(x))>>frac. */
+int bonsai_silu_gpu(const int64_t *x, int64_t n, int64_t frac, int64_t *out);
+/* rope_v2.py:92-117 NeoX apply (bonsai_q1_gpu.cu:812-827 / :1746-1761 `rope_kernel` / `rope_decode_kernel`);
+ * row r uses table row pos[r]; rc 2 where the oracle raises (rope.py:26-39). */
+int imie_rope_neox_gpu(const int64_t *x, int64_t rows, int64_t nh, int64_t hd, const int64_t *pos, const int64_t *cos,
+                       const int64_t *sin, int64_t n_pos, int64_t frac, int64_t *out);
+/* lowest-index argmax (reference_bonsai.py:812-827; bonsai_q1_kernel.c:468-543 merge rule). */
+int imie_argmax_gpu(const int64_t *logits, int64_t rows, int64_t cols, int64_t *ids);
+
+/* ---- fixed-point attention -------------------------------------------------------------------------- */
+/* bonsai_q1_gpu.cu:731-797 `bonsai_attention_prefill_gpu` (gpu_native.py:139-151, 418-446). */
+int bonsai_attention_prefill_gpu(const int64_t *q, const int64_t *k, const int64_t *v, int64_t H, int64_t Hkv,
+                                 int64_t hd, int64_t M, int64_t L, int64_t start, int64_t frac, int64_t inv_sqrt,
+                                 int64_t *out);
+/* bonsai_q1_gpu.cu:1409-1470 `bonsai_attention_decode_batched_gpu` (gpu_native.py:449-468). */
+int bonsai_attention_decode_batched_gpu(const int64_t *q, const int64_t *K, const int64_t *V, const int64_t *lengths,
+                                        int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t cap, int64_t frac,
+                                        int64_t inv_sqrt, int64_t *out);
+
+/* stage probe (tests): runs the causal pipeline with V = K up to `stage` (1 scores, 2 softmax, 3 PV) and returns
+ * the score/probability rows (H*M, L), the row maxima (H*M) and, at stage 3, the int64 PV accumulator (H*M, hd). */
+int imie_attention_scores_probe(const int64_t *q, const int64_t *k, int64_t H, int64_t Hkv, int64_t hd, int64_t M,
+                                int64_t L, int64_t start, int64_t frac, int64_t inv_sqrt, int64_t *scores,
+                                int64_t *rowmax, int stage, int64_t *acc_out);
+
+/* ---- resident model: monolith prefill and decode context -------------------------------------------- */
+/* bonsai_q1_gpu.cu `bonsai_buf_upload_i64` (gpu_native.py:154-160, 549-556): handle >= 0 or -1. */
+int64_t bonsai_buf_upload_i64(const int64_t *host, int64_t n);
+const int64_t *imie_buf_device_ptr(int64_t handle);
+void imie_buf_free_all(void);
+/* bonsai_q1_gpu.cu:3694-3819 `bonsai_prefill_forward_gpu` (gpu_native.py:161-172, 559-595). */
+int bonsai_prefill_forward_gpu(const int64_t *x_embed, int64_t T, int64_t d, int64_t n_layers, int64_t H, int64_t Hkv,
+                               int64_t hd, int64_t dff, int64_t frac, int64_t eps, int64_t inv_sqrt,
+                               const int64_t *wq, const int64_t *wk, const int64_t *wv, const int64_t *wo,
+                               const int64_t *w1, const int64_t *wu, const int64_t *w2, const int64_t *n1g,
+                               const int64_t *n2g, const int64_t *qng, const int64_t *kng, int64_t finalg,
+                               int64_t out_head, int64_t cos_h, int64_t sin_h, int64_t *out_logits, int64_t *out_k,
+                               int64_t *out_v);
+/* bonsai_q1_gpu.cu:3517-3562 `bonsai_decode_ctx_create` (gpu_native.py:483-506). */
+int64_t bonsai_decode_ctx_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d,
+                                 int64_t dff, int64_t cap, int64_t vocab, int64_t frac, int64_t eps, int64_t inv_sqrt,
+                                 const int64_t *wq, const int64_t *wk, const int64_t *wv, const int64_t *wo,
+                                 const int64_t *w1, const int64_t *wu, const int64_t *w2, const int64_t *n1g,
+                                 const int64_t *n2g, const int64_t *qng, const int64_t *kng, int64_t finalg,
+                                 int64_t out_head, int64_t cos_h, int64_t sin_h);
+/* paged int32 (guarded) / int64 context; out_head < 0 = layers only. */
+int64_t imie_net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d, int64_t dff,
+                        int64_t cap, int64_t frac, int64_t eps, int64_t inv_sqrt, const int64_t *wq, const int64_t *wk,
+                        const int64_t *wv, const int64_t *wo, const int64_t *w1, const int64_t *wu, const int64_t *w2,
+                        const int64_t *n1g, const int64_t *n2g, const int64_t *qng, const int64_t *kng,
+                        int64_t finalg, int64_t out_head, int64_t cos_h, int64_t sin_h, int64_t page, int kv32);
+/* bonsai_q1_gpu.cu:3565-3584 `bonsai_decode_ctx_seed_seq` (gpu_native.py:509-521). */
+int bonsai_decode_ctx_seed_seq(int64_t ctx, int64_t b, const int64_t *k, const int64_t *v, int64_t Lb);
+/* bonsai_q1_gpu.cu:3588-3647 `bonsai_decode_step` (gpu_native.py:524-538). */
+int bonsai_decode_step(int64_t ctx, const int64_t *x_in, const int64_t *pos, int64_t *out);
+/* bonsai_q1_gpu.cu `bonsai_decode_ctx_free` (gpu_native.py:541-546). */
+void bonsai_decode_ctx_free(int64_t ctx);
+int imie_net_forward_dev(int64_t ctx, int64_t *x_dev, const int64_t *starts, int64_t M, void *stream);
+int imie_net_head_dev(int64_t ctx, const int64_t *x_dev, int64_t rows, int64_t *logits_dev, int64_t *ids_dev,
+                      void *stream);
+int imie_net_status(int64_t ctx, int clear, void *stream);
+int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int64_t *k_out, int64_t *v_out);
+/* Q1 embedding rows sign*scale (reference_bonsai.py:138-146) from device tables. */
+int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
+                   void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,34 @@ SIGNATURES = {
     "imie_q1_weight_info": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
     "imie_q1_linear_simple_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                           c_void_p, c_void_p]),
+    # RMSNorm / element-wise
+    "bonsai_rmsnorm_gpu": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_rmsnorm_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
+    "bonsai_silu_gpu": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
+    "imie_rope_neox_gpu": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
+                                   c_int64, c_void_p]),
+    "imie_argmax_gpu": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
+    # attention
+    "bonsai_attention_prefill_gpu": (c_int, [c_void_p] * 3 + [c_int64] * 8 + [c_void_p]),
+    "bonsai_attention_decode_batched_gpu": (c_int, [c_void_p] * 4 + [c_int64] * 7 + [c_void_p]),
+    "imie_attention_scores_probe": (c_int, [c_void_p] * 2 + [c_int64] * 8 + [c_void_p] * 2 + [c_int, c_void_p]),
+    # resident model / decode context
+    "bonsai_buf_upload_i64": (c_int64, [c_void_p, c_int64]),
+    "imie_buf_device_ptr": (c_void_p, [c_int64]),
+    "imie_buf_free_all": (None, []),
+    "bonsai_prefill_forward_gpu": (c_int, [c_void_p] + [c_int64] * 10 + [c_void_p] * 11 + [c_int64] * 4
+                                   + [c_void_p] * 3),
+    "bonsai_decode_ctx_create": (c_int64, [c_int64] * 12 + [c_void_p] * 11 + [c_int64] * 4),
+    "imie_net_create": (c_int64, [c_int64] * 11 + [c_void_p] * 11 + [c_int64] * 5 + [c_int]),
+    "bonsai_decode_ctx_seed_seq": (c_int, [c_int64, c_int64, c_void_p, c_void_p, c_int64]),
+    "bonsai_decode_step": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
+    "bonsai_decode_ctx_free": (None, [c_int64]),
+    "imie_net_forward_dev": (c_int, [c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
+    "imie_net_head_dev": (c_int, [c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+    "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),
+    "imie_net_export_kv": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_embed_dev": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
 }
 
 

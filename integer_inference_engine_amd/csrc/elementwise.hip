@@ -1,0 +1,280 @@
+// Element-wise integer kernels around the Q1 matmuls (gfx950).
+//   RoPE NeoX apply         bonsai/src/trinote/model/rope_v2.py:92-117 (+ guard rope.py:26-39)
+//   SiLU / SiLU*up          reference_bonsai.py:245-264, :611-614 over fixedpoint.py:143-174 (wrap mod 2^64)
+//   residual add            reference_bonsai.py:960-964 (wrap)
+//   embedding rows          reference_bonsai.py:138-146 (sign * scale, no shift)
+//   lowest-index argmax     reference_bonsai.py:812-827 (numpy first-max)
+#include "imie_common.h"
+#include "imie_kernels.h"
+
+namespace {
+
+typedef unsigned __int128 u128;
+
+__device__ inline int64_t rshift_np(int64_t a, int64_t s) {   // numpy int64 `a >> s` incl. out-of-range counts
+  if (s < 0 || s >= 64) return a < 0 ? -1 : 0;
+  return a >> s;
+}
+
+__device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
+  const int64_t fp = (int64_t)1 << frac;
+  const int64_t k = u >> frac, f = u & (fp - 1);
+  const int sh = 16 - frac;
+  int64_t c0, c1, c2, c3;
+  if (sh >= 0) { c0 = 65536 >> sh; c1 = 45426 >> sh; c2 = 15743 >> sh; c3 = 3638 >> sh; }
+  else { c0 = (int64_t)65536 << -sh; c1 = (int64_t)45426 << -sh; c2 = (int64_t)15743 << -sh; c3 = (int64_t)3638 << -sh; }
+  const int64_t f2 = (int64_t)((uint64_t)f * (uint64_t)f) >> frac;
+  const int64_t f3 = (int64_t)((uint64_t)f2 * (uint64_t)f) >> frac;
+  int64_t poly = c0 - ((int64_t)((uint64_t)c1 * (uint64_t)f) >> frac) + ((int64_t)((uint64_t)c2 * (uint64_t)f2) >> frac) -
+                 ((int64_t)((uint64_t)c3 * (uint64_t)f3) >> frac);
+  if (poly < 0) poly = 0;
+  return rshift_np(poly, k < 63 ? k : 63);
+}
+
+__device__ inline int64_t sigmoid_fixed(int64_t x, int frac, int64_t log2e, int64_t dclip) {
+  const int64_t m = x > 0 ? x : 0;
+  int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
+  if (d0 > dclip) d0 = dclip;
+  if (d1 > dclip) d1 = dclip;
+  const int64_t e0 = exp2_neg_fixed((int64_t)((uint64_t)d0 * (uint64_t)log2e) >> frac, frac);
+  const int64_t e1 = exp2_neg_fixed((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> frac, frac);
+  const int64_t z = e0 + e1;
+  if (z == 0) return 0;
+  return (int64_t)(((uint64_t)e1 << frac) / (uint64_t)z);   // e1 << frac >= 0 and fits (e1 <= c0 + c2)
+}
+
+__global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t* __restrict__ up, int64_t n, int frac,
+                                int64_t log2e, int64_t dclip, int64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t g = gate[i];
+  const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
+  out[i] = up ? (int64_t)((uint64_t)silu * (uint64_t)up[i]) >> frac : silu;
+}
+
+__global__ void add_kernel(int64_t* __restrict__ x, const int64_t* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = (int64_t)((uint64_t)x[i] + (uint64_t)y[i]);
+}
+
+__device__ inline void atomic_max_u64(uint64_t* p, uint64_t v) {
+  atomicMax((unsigned long long*)p, (unsigned long long)v);
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(const int64_t* __restrict__ x, int64_t rows, int64_t nh, int64_t hd,
+                                                   const int64_t* __restrict__ pos, int64_t pos0,
+                                                   const int64_t* __restrict__ cs, const int64_t* __restrict__ sn,
+                                                   int frac, int64_t* __restrict__ out, uint64_t* __restrict__ guard) {
+  const int64_t half = hd / 2;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t mx = 0, mc = 0;
+  if (i < rows * nh * half) {
+    const int64_t j = i % half, h = (i / half) % nh, r = i / (half * nh);
+    const int64_t p = pos ? pos[r] : pos0 + r;
+    const int64_t* xv = x + (r * nh + h) * hd;
+    const int64_t x0 = xv[j], x1 = xv[j + half];
+    const int64_t c = cs[p * half + j], s = sn[p * half + j];
+    int64_t* o = out + (r * nh + h) * hd;
+    o[j] = (int64_t)((uint64_t)x0 * (uint64_t)c - (uint64_t)x1 * (uint64_t)s) >> frac;
+    o[j + half] = (int64_t)((uint64_t)x0 * (uint64_t)s + (uint64_t)x1 * (uint64_t)c) >> frac;
+    const uint64_t a0 = imie_absu64(x0), a1 = imie_absu64(x1), ac = imie_absu64(c), as = imie_absu64(s);
+    mx = a0 > a1 ? a0 : a1;
+    mc = ac > as ? ac : as;
+  }
+  // wave-level max, one atomic per wave
+  mx = imie_wave_max_u64(mx);
+  mc = imie_wave_max_u64(mc);
+  if ((threadIdx.x & 63) == 0) {
+    atomic_max_u64(&guard[0], mx);
+    atomic_max_u64(&guard[1], mc);
+  }
+}
+
+__global__ void rope_guard_kernel(const uint64_t* __restrict__ guard, int* __restrict__ status) {
+  const u128 b = (u128)2 * guard[0] * guard[1];
+  if (b > (u128)INT64_MAX) atomicOr(status, IMIE_EOVF);
+}
+
+__global__ void embed_kernel(const uint8_t* __restrict__ bits, const int64_t* __restrict__ scale, int64_t nb,
+                             const int64_t* __restrict__ ids, int64_t T, int64_t* __restrict__ out) {
+  const int64_t d = nb * 128;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * d) return;
+  const int64_t t = i / d, k = i % d, id = ids[t];
+  const int bit = (bits[(id * nb + k / 128) * 16 + (k % 128) / 8] >> (k % 8)) & 1;
+  const int64_t sc = scale[id * nb + k / 128];
+  out[i] = bit ? sc : (int64_t)(0 - (uint64_t)sc);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const int64_t* __restrict__ logits, int64_t cols,
+                                                     int64_t* __restrict__ ids) {
+  __shared__ int64_t sv[256];
+  __shared__ int64_t si[256];
+  const int64_t row = blockIdx.x;
+  const int64_t* lr = logits + row * cols;
+  int64_t bv = INT64_MIN, bi = 0x7FFFFFFFFFFFFFFFll;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const int64_t v = lr[c];
+    if (v > bv) { bv = v; bi = c; }      // ascending c per thread: first max wins
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const int64_t v2 = sv[threadIdx.x + o], i2 = si[threadIdx.x + o];
+      if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+        sv[threadIdx.x] = v2;
+        si[threadIdx.x] = i2;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) ids[row] = si[0];
+}
+
+}  // namespace
+
+int imie_rope_launch(const int64_t* x, int64_t rows, int64_t nh, int64_t hd, const int64_t* pos, int64_t pos0,
+                     const int64_t* cos, const int64_t* sin, int64_t frac, int64_t* out, uint64_t* guard,
+                     hipStream_t st) {
+  const int64_t n = rows * nh * (hd / 2);
+  if (n <= 0) return IMIE_OK;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, rows, nh, hd, pos, pos0,
+                     cos, sin, (int)frac, out, guard);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_rope_guard_check(const uint64_t* guard, int* status, hipStream_t st) {
+  hipLaunchKernelGGL(rope_guard_kernel, dim3(1), dim3(1), 0, st, guard, status);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+static void silu_consts(int64_t frac, int64_t* log2e, int64_t* dclip) {
+  const int64_t sh = 16 - frac;
+  *log2e = sh >= 0 ? (94548 >> sh) : ((int64_t)94548 << -sh);
+  const int64_t a = ((frac + 2) << (2 * frac)) / *log2e, b = ((int64_t)1 << 62) / *log2e;
+  *dclip = a < b ? a : b;
+}
+
+int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int64_t frac, int64_t* out,
+                         hipStream_t st) {
+  if (n <= 0) return IMIE_OK;
+  int64_t log2e, dclip;
+  silu_consts(frac, &log2e, &dclip);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gate, up, n, (int)frac,
+                     log2e, dclip, out);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_silu_launch(const int64_t* x, int64_t n, int64_t frac, int64_t* out, hipStream_t st) {
+  return imie_silu_mul_launch(x, nullptr, n, frac, out, st);
+}
+
+int imie_add_launch(int64_t* x, const int64_t* y, int64_t n, hipStream_t st) {
+  if (n <= 0) return IMIE_OK;
+  hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_embed_launch(const uint8_t* bits, const int64_t* scale, int64_t nb, const int64_t* ids, int64_t T,
+                      int64_t* out, hipStream_t st) {
+  const int64_t n = T * nb * 128;
+  if (n <= 0) return IMIE_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bits, scale, nb, ids, T, out);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, hipStream_t st) {
+  if (rows <= 0) return IMIE_OK;
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, st, logits, cols, ids);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+namespace {
+struct EwWs {
+  DevBuf a, b, c, status;
+} g_ews;
+}  // namespace
+
+extern "C" {
+
+// bonsai_q1_gpu.cu:848-864 / bonsai_q1_kernel.c:1729-1767 `bonsai_silu_i64` semantics on the GPU:
+// out = (x * sigmoid(x)) >> frac, wrapping mod 2^64. Host pointers, synchronous.
+int bonsai_silu_gpu(const int64_t* x, int64_t n, int64_t frac, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!x || !out || n < 0 || frac < 1 || frac > 29) return IMIE_EARG;
+  if (n == 0) return IMIE_OK;
+  if (imie_device_ready() != 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const size_t b = (size_t)n * 8;
+  if (g_ews.a.ensure(b) || g_ews.b.ensure(b)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(g_ews.a.p, x, b, hipMemcpyHostToDevice, st));
+  int rc = imie_silu_launch((const int64_t*)g_ews.a.p, n, frac, (int64_t*)g_ews.b.p, st);
+  if (rc) return rc;
+  IMIE_HIP(hipMemcpyAsync(out, g_ews.b.p, b, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
+
+// NeoX RoPE apply (rope_v2.py:92-117) over x (rows, nh, hd) where row r uses table row pos[r]; cos/sin
+// (n_pos, hd/2). Host pointers, synchronous; rc 2 where the oracle raises (2*max|x|*max|cs| > INT64_MAX).
+int imie_rope_neox_gpu(const int64_t* x, int64_t rows, int64_t nh, int64_t hd, const int64_t* pos,
+                       const int64_t* cos, const int64_t* sin, int64_t n_pos, int64_t frac, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!x || !out || !pos || !cos || !sin || rows < 0 || nh <= 0 || hd <= 0 || (hd & 1) || n_pos <= 0 || frac < 0 ||
+      frac > 62)
+    return IMIE_EARG;
+  for (int64_t r = 0; r < rows; ++r)
+    if (pos[r] < 0 || pos[r] >= n_pos) return IMIE_EARG;
+  if (rows == 0) return IMIE_OK;
+  if (imie_device_ready() != 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const size_t xb = (size_t)(rows * nh * hd) * 8, tb = (size_t)(n_pos * hd / 2) * 8;
+  if (g_ews.a.ensure(xb + (size_t)rows * 8) || g_ews.b.ensure(xb) || g_ews.c.ensure(2 * tb) ||
+      g_ews.status.ensure(64))
+    return IMIE_EARG;
+  char* a = (char*)g_ews.a.p;
+  char* c = (char*)g_ews.c.p;
+  IMIE_HIP(hipMemcpyAsync(a, x, xb, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(a + xb, pos, (size_t)rows * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(c, cos, tb, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(c + tb, sin, tb, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemsetAsync(g_ews.status.p, 0, 64, st));
+  uint64_t* guard = (uint64_t*)((char*)g_ews.status.p + 16);
+  int rc = imie_rope_launch((const int64_t*)a, rows, nh, hd, (const int64_t*)(a + xb), 0, (const int64_t*)c,
+                            (const int64_t*)(c + tb), frac, (int64_t*)g_ews.b.p, guard, st);
+  if (rc) return rc;
+  rc = imie_rope_guard_check(guard, (int*)g_ews.status.p, st);
+  if (rc) return rc;
+  int stat = 0;
+  IMIE_HIP(hipMemcpyAsync(&stat, g_ews.status.p, 4, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipMemcpyAsync(out, g_ews.b.p, xb, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return stat ? IMIE_EOVF : IMIE_OK;
+}
+
+// Lowest-index argmax over rows of int64 logits (reference_bonsai.py:812-827). Host pointers, synchronous.
+int imie_argmax_gpu(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!logits || !ids || rows < 0 || cols <= 0) return IMIE_EARG;
+  if (rows == 0) return IMIE_OK;
+  if (imie_device_ready() != 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const size_t b = (size_t)(rows * cols) * 8;
+  if (g_ews.a.ensure(b) || g_ews.b.ensure((size_t)rows * 8)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(g_ews.a.p, logits, b, hipMemcpyHostToDevice, st));
+  int rc = imie_argmax_launch((const int64_t*)g_ews.a.p, rows, cols, (int64_t*)g_ews.b.p, st);
+  if (rc) return rc;
+  IMIE_HIP(hipMemcpyAsync(ids, g_ews.b.p, (size_t)rows * 8, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
+
+}  // extern "C"

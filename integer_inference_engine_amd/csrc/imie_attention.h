@@ -1,0 +1,30 @@
+// Attention problem descriptor shared by the attention kernels and the layer pipelines.
+#pragma once
+#include "imie_common.h"
+
+struct AttnDesc {
+  int64_t B, H, Hkv, hd, M;        // query rows (b, h, m): q[b*qsb + h*qsh + m*qsm + c]
+  int64_t qsb, qsh, qsm;           // element strides of q and out (out uses the same strides)
+  const int64_t* q;
+  const void* K;                   // paged pools (see attention.hip)
+  const void* V;
+  int kv32;                        // 1: int32 KV elements, 0: int64
+  const int64_t* pt;               // page table [B][mp]
+  int64_t P, mp;                   // tokens per page, pages per sequence
+  const int64_t* lengths;          // decode: keys per sequence (starts == nullptr)
+  const int64_t* starts;           // causal: first new position per sequence (M new rows)
+  int64_t Lmax;                    // score row stride (>= max visible keys)
+  int frac;
+  int64_t inv_sqrt, log2e, dclip;
+  int64_t* out;
+  int* status;
+  // scratch (imie_attn_bind_scratch)
+  int64_t* scores;
+  uint64_t* acc;
+  int64_t* rowmax;
+  uint64_t *maxq, *maxp, *maxk, *maxv;
+};
+
+size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax);
+void imie_attn_bind_scratch(AttnDesc& d, void* scratch);
+int imie_attention_launch(AttnDesc d, hipStream_t st);

@@ -1,0 +1,33 @@
+// Internal launchers shared by the C-ABI files (device pointers, asynchronous on `st`).
+#pragma once
+#include "imie_common.h"
+
+// status word bits (device int, OR-ed by kernels): IMIE_EOVF (2) attention / RoPE / int32-KV envelope,
+// IMIE_ERMS (4) RMSNorm envelope.
+
+int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                        const int64_t* gain, int64_t* out, int* status, hipStream_t st);
+
+// Q1 apply on a registered handle. accumulate != 0 adds the result into out (residual add fused).
+int imie_q1_launch(int64_t handle, const int64_t* x, int64_t T, int64_t frac, int64_t* out, int accumulate,
+                   hipStream_t st);
+int imie_q1_dims(int64_t handle, int64_t* N, int64_t* nb);
+
+// NeoX RoPE on rows x (rows, nh, hd); row r uses table row pos[r] (pos == nullptr: pos0 + r).
+// The fail-loud envelope 2*max|x|*max|cos,sin| <= INT64_MAX is checked exactly via `guard` scratch
+// (2 x uint64, zeroed by the caller) and reported in `status` by imie_rope_guard_check.
+int imie_rope_launch(const int64_t* x, int64_t rows, int64_t nh, int64_t hd, const int64_t* pos, int64_t pos0,
+                     const int64_t* cos, const int64_t* sin, int64_t frac, int64_t* out, uint64_t* guard,
+                     hipStream_t st);
+int imie_rope_guard_check(const uint64_t* guard, int* status, hipStream_t st);
+
+// h = ((silu(gate) * up) >> frac) with the bonsai wrap semantics (reference_bonsai.py:245-264, 611-614)
+int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int64_t frac, int64_t* out,
+                         hipStream_t st);
+int imie_silu_launch(const int64_t* x, int64_t n, int64_t frac, int64_t* out, hipStream_t st);
+int imie_add_launch(int64_t* x, const int64_t* y, int64_t n, hipStream_t st);
+// embedding rows: out[t] = sign(bits[ids[t]]) * scale[ids[t]] (no frac shift), natural Q1 layout
+int imie_embed_launch(const uint8_t* bits, const int64_t* scale, int64_t nb, const int64_t* ids, int64_t T,
+                      int64_t* out, hipStream_t st);
+// lowest-index argmax per row of (rows, cols) int64
+int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, hipStream_t st);

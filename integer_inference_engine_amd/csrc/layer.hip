@@ -1,0 +1,511 @@
+// Resident Qwen3-dense (Bonsai) forward over packed Q1_0 weights: the per-layer pipeline, a paged integer KV
+// cache, and the reference's monolith / decode-context ABIs on top of them.
+//
+// Per layer (reference_bonsai.py:941-966, :656-720, :603-615):
+//   n1 = rmsnorm(x, n1g); q,k,v = Q1(n1); q,k = head-rmsnorm(q/k); q,k = rope(q/k, pos); cache <- (k, v)
+//   x += Q1(attention(q, cache), wo); n2 = rmsnorm(x, n2g); x += Q1((silu(Q1(n2,w1)) * Q1(n2,wu)) >> f, w2)
+// Residual adds are fused into the Q1 epilogue (accumulate mode). Positions of the B*M new rows are
+// pos = start_b + m; the attention is causal over each sequence's cache.
+//
+// KV cache: per layer a pool of pages [page][Hkv][P][hd] (int32 or int64); page table [B][mp] shared by the
+// layers. int32 storage is guarded: a value that does not fit sets status bit 2 (the caller re-runs with an
+// int64 cache). A dense reference cache (B, Hkv, cap, hd) is the case P = cap, mp = 1.
+#include "imie_common.h"
+#include "imie_kernels.h"
+#include "imie_attention.h"
+#include <string.h>
+
+namespace {
+
+// ---- device buffer registry (bonsai_buf_upload_i64) ---------------------------------------------------------
+struct BufEntry {
+  int64_t* p = nullptr;
+  int64_t n = 0;
+};
+std::vector<BufEntry>& bufs() {
+  static std::vector<BufEntry> b;
+  return b;
+}
+const int64_t* buf_get(int64_t h, int64_t need) {
+  if (h < 0 || h >= (int64_t)bufs().size() || !bufs()[(size_t)h].p) return nullptr;
+  if (bufs()[(size_t)h].n < need) return nullptr;
+  return bufs()[(size_t)h].p;
+}
+
+__global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t st) {
+  if (n <= 0) return IMIE_OK;
+  hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n, v);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+template <typename KT>
+__global__ void kv_append_kernel(const int64_t* __restrict__ k, const int64_t* __restrict__ v,
+                                 const int64_t* __restrict__ pos, int64_t rows, int64_t M, int64_t Hkv, int64_t hd,
+                                 const int64_t* __restrict__ pt, int64_t P, int64_t mp, KT* __restrict__ kpool,
+                                 KT* __restrict__ vpool, int* __restrict__ status) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * Hkv * hd) return;
+  const int64_t c = i % hd, kv = (i / hd) % Hkv, r = i / (hd * Hkv);
+  const int64_t b = r / M, j = pos[r];
+  const int64_t off = pt[b * mp + j / P] * (Hkv * P * hd) + kv * P * hd + (j % P) * hd + c;
+  const int64_t kval = k[i], vval = v[i];
+  if (sizeof(KT) == 4) {
+    if (kval != (int64_t)(int32_t)kval || vval != (int64_t)(int32_t)vval) atomicOr(status, IMIE_EOVF);
+  }
+  kpool[off] = (KT)kval;
+  vpool[off] = (KT)vval;
+}
+
+struct LayerW {
+  int64_t w[7];                       // wq, wk, wv, wo, w1, wu, w2 Q1 handles
+  const int64_t *n1g, *n2g, *qng, *kng;
+};
+
+struct Net {
+  int64_t B = 0, d = 0, H = 0, Hkv = 0, hd = 0, dff = 0, nl = 0, vocab = 0, frac = 16, eps = 1, inv_sqrt = 0;
+  std::vector<LayerW> layers;
+  const int64_t* finalg = nullptr;
+  int64_t out_head = -1;
+  const int64_t *cos = nullptr, *sin = nullptr;
+  // KV
+  int kv32 = 0;
+  int64_t P = 0, mp = 0, npages = 0;
+  std::vector<void*> kpool, vpool;    // per layer
+  int64_t* pt = nullptr;              // device [B][mp]
+  std::vector<int64_t> len;           // host lengths per sequence
+  // workspace
+  DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx;
+  bool live = false;
+};
+
+std::vector<Net*>& nets() {
+  static std::vector<Net*> v;
+  return v;
+}
+
+Net* net_get(int64_t h) {
+  if (h < 0 || h >= (int64_t)nets().size()) return nullptr;
+  Net* n = nets()[(size_t)h];
+  return (n && n->live) ? n : nullptr;
+}
+
+void net_free(Net* n) {
+  if (!n) return;
+  (void)hipStreamSynchronize(imie_stream());
+  for (auto p : n->kpool) if (p) (void)hipFree(p);
+  for (auto p : n->vpool) if (p) (void)hipFree(p);
+  if (n->pt) (void)hipFree(n->pt);
+  DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
+                  &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx};
+  for (auto b : bs) b->release();
+  n->live = false;
+}
+
+// Allocate the paged cache: every sequence gets ceil(cap / P) pages (page table = identity blocks).
+int net_alloc_kv(Net& n, int64_t cap, int64_t P, int kv32) {
+  n.kv32 = kv32;
+  n.P = P;
+  n.mp = (cap + P - 1) / P;
+  n.npages = n.B * n.mp;
+  const size_t esz = kv32 ? 4 : 8;
+  const size_t bytes = (size_t)(n.npages * n.Hkv * P * n.hd) * esz;
+  n.kpool.assign((size_t)n.nl, nullptr);
+  n.vpool.assign((size_t)n.nl, nullptr);
+  for (int64_t l = 0; l < n.nl; ++l) {
+    if (hipMalloc(&n.kpool[(size_t)l], bytes) != hipSuccess) return IMIE_EARG;
+    if (hipMalloc(&n.vpool[(size_t)l], bytes) != hipSuccess) return IMIE_EARG;
+  }
+  std::vector<int64_t> pt((size_t)n.npages);
+  for (int64_t i = 0; i < n.npages; ++i) pt[(size_t)i] = i;
+  IMIE_HIP(hipMalloc((void**)&n.pt, (size_t)n.npages * 8));
+  IMIE_HIP(hipMemcpy(n.pt, pt.data(), (size_t)n.npages * 8, hipMemcpyHostToDevice));
+  n.len.assign((size_t)n.B, 0);
+  return IMIE_OK;
+}
+
+// Run all layers over M new tokens for each of the B sequences. x: device (B*M, d), updated in place.
+// starts: host (B), the first new position per sequence (== its current cache length).
+int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st) {
+  const int64_t rows = n.B * M;
+  int64_t lmax = 0;
+  for (int64_t b = 0; b < n.B; ++b) {
+    if (starts[b] < 0 || starts[b] + M > n.mp * n.P) return IMIE_EARG;
+    lmax = starts[b] + M > lmax ? starts[b] + M : lmax;
+  }
+  const int64_t qd = n.H * n.hd, kd = n.Hkv * n.hd;
+  if (n.n.ensure((size_t)(rows * n.d) * 8) || n.q.ensure((size_t)(rows * qd) * 8) ||
+      n.k.ensure((size_t)(rows * kd) * 8) || n.v.ensure((size_t)(rows * kd) * 8) ||
+      n.qn.ensure((size_t)(rows * qd) * 8) || n.kn.ensure((size_t)(rows * kd) * 8) ||
+      n.att.ensure((size_t)(rows * qd) * 8) || n.gate.ensure((size_t)(rows * n.dff) * 8) ||
+      n.up.ensure((size_t)(rows * n.dff) * 8) || n.h.ensure((size_t)(rows * n.dff) * 8) ||
+      n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure(64) ||
+      n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)))
+    return IMIE_EARG;
+  std::vector<int64_t> pos((size_t)rows);
+  for (int64_t r = 0; r < rows; ++r) pos[(size_t)r] = starts[r / M] + r % M;
+  IMIE_HIP(hipMemcpyAsync(n.pos.p, pos.data(), (size_t)rows * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(n.starts.p, starts, (size_t)n.B * 8, hipMemcpyHostToDevice, st));
+  int rc = 0;
+#define CK(call) do { rc = (call); if (rc) return rc; } while (0)
+  int64_t *xn = (int64_t*)n.n.p, *q = (int64_t*)n.q.p, *k = (int64_t*)n.k.p, *v = (int64_t*)n.v.p;
+  int64_t *qn = (int64_t*)n.qn.p, *kn = (int64_t*)n.kn.p, *att = (int64_t*)n.att.p;
+  int64_t *gate = (int64_t*)n.gate.p, *up = (int64_t*)n.up.p, *hh = (int64_t*)n.h.p;
+  const int64_t* posd = (const int64_t*)n.pos.p;
+  uint64_t* guard = (uint64_t*)n.guard.p;
+  int* status = (int*)n.status.p;
+  for (int64_t l = 0; l < n.nl; ++l) {
+    const LayerW& L = n.layers[(size_t)l];
+    CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n1g, xn, status, st));
+    CK(imie_q1_launch(L.w[0], xn, rows, n.frac, q, 0, st));
+    CK(imie_q1_launch(L.w[1], xn, rows, n.frac, k, 0, st));
+    CK(imie_q1_launch(L.w[2], xn, rows, n.frac, v, 0, st));
+    CK(imie_rmsnorm_launch(q, rows * n.H, n.hd, n.frac, n.eps, L.qng, qn, status, st));
+    CK(imie_rmsnorm_launch(k, rows * n.Hkv, n.hd, n.frac, n.eps, L.kng, kn, status, st));
+    CK(fill_i64((int64_t*)guard, 2, 0, st));
+    CK(imie_rope_launch(qn, rows, n.H, n.hd, posd, 0, n.cos, n.sin, n.frac, q, guard, st));
+    CK(imie_rope_guard_check(guard, status, st));
+    CK(fill_i64((int64_t*)guard, 2, 0, st));
+    CK(imie_rope_launch(kn, rows, n.Hkv, n.hd, posd, 0, n.cos, n.sin, n.frac, k, guard, st));
+    CK(imie_rope_guard_check(guard, status, st));
+    const int64_t na = rows * kd;
+    if (n.kv32)
+      hipLaunchKernelGGL(kv_append_kernel<int32_t>, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, st, k, v, posd,
+                         rows, M, n.Hkv, n.hd, n.pt, n.P, n.mp, (int32_t*)n.kpool[(size_t)l],
+                         (int32_t*)n.vpool[(size_t)l], status);
+    else
+      hipLaunchKernelGGL(kv_append_kernel<int64_t>, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, st, k, v, posd,
+                         rows, M, n.Hkv, n.hd, n.pt, n.P, n.mp, (int64_t*)n.kpool[(size_t)l],
+                         (int64_t*)n.vpool[(size_t)l], status);
+    IMIE_HIP(hipGetLastError());
+    AttnDesc d = {};
+    d.B = n.B; d.H = n.H; d.Hkv = n.Hkv; d.hd = n.hd; d.M = M;
+    d.qsb = M * qd; d.qsh = n.hd; d.qsm = qd;
+    d.q = q; d.K = n.kpool[(size_t)l]; d.V = n.vpool[(size_t)l]; d.kv32 = n.kv32;
+    d.pt = n.pt; d.P = n.P; d.mp = n.mp;
+    d.starts = (const int64_t*)n.starts.p; d.lengths = nullptr;
+    d.Lmax = lmax; d.frac = (int)n.frac; d.inv_sqrt = n.inv_sqrt;
+    d.out = att; d.status = status;
+    imie_attn_bind_scratch(d, n.attn.p);
+    CK(imie_attention_launch(d, st));
+    CK(imie_q1_launch(L.w[3], att, rows, n.frac, x, 1, st));
+    CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n2g, xn, status, st));
+    CK(imie_q1_launch(L.w[4], xn, rows, n.frac, gate, 0, st));
+    CK(imie_q1_launch(L.w[5], xn, rows, n.frac, up, 0, st));
+    CK(imie_silu_mul_launch(gate, up, rows * n.dff, n.frac, hh, st));
+    CK(imie_q1_launch(L.w[6], hh, rows, n.frac, x, 1, st));
+  }
+#undef CK
+  for (int64_t b = 0; b < n.B; ++b) n.len[(size_t)b] = starts[b] + M;
+  return IMIE_OK;
+}
+
+// final norm of selected rows + output head (+ argmax). rows_idx: host list of row indices into x.
+int net_head(Net& n, const int64_t* x, const std::vector<int64_t>& rows_idx, int64_t* logits, int64_t* ids,
+             hipStream_t st) {
+  const int64_t R = (int64_t)rows_idx.size();
+  if (n.out_head < 0 || R == 0) return IMIE_EARG;
+  if (n.lastx.ensure((size_t)(R * n.d) * 8) || n.n.ensure((size_t)(R * n.d) * 8)) return IMIE_EARG;
+  for (int64_t i = 0; i < R; ++i)
+    IMIE_HIP(hipMemcpyAsync((int64_t*)n.lastx.p + i * n.d, x + rows_idx[(size_t)i] * n.d, (size_t)n.d * 8,
+                            hipMemcpyDeviceToDevice, st));
+  int rc = imie_rmsnorm_launch((const int64_t*)n.lastx.p, R, n.d, n.frac, n.eps, n.finalg, (int64_t*)n.n.p,
+                               (int*)n.status.p, st);
+  if (rc) return rc;
+  rc = imie_q1_launch(n.out_head, (const int64_t*)n.n.p, R, n.frac, logits, 0, st);
+  if (rc) return rc;
+  if (ids) rc = imie_argmax_launch(logits, R, n.vocab, ids, st);
+  return rc;
+}
+
+int read_status(Net& n, hipStream_t st, int* stat) {
+  IMIE_HIP(hipMemcpyAsync(stat, n.status.p, 4, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
+
+int64_t net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d, int64_t dff,
+                   int64_t cap, int64_t vocab, int64_t frac, int64_t eps, int64_t inv_sqrt, const int64_t* wq,
+                   const int64_t* wk, const int64_t* wv, const int64_t* wo, const int64_t* w1, const int64_t* wu,
+                   const int64_t* w2, const int64_t* n1g, const int64_t* n2g, const int64_t* qng, const int64_t* kng,
+                   int64_t finalg, int64_t out_head, int64_t cos_h, int64_t sin_h, int64_t page, int kv32) {
+  if (B <= 0 || n_layers <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd > 128 || (hd & 1) || d <= 0 ||
+      dff <= 0 || cap <= 0 || frac < 1 || frac > 29 || eps < 0 || imie_device_ready() != 0)
+    return -1;
+  Net* n = new Net();
+  n->B = B; n->d = d; n->H = H; n->Hkv = Hkv; n->hd = hd; n->dff = dff; n->nl = n_layers; n->vocab = vocab;
+  n->frac = frac; n->eps = eps; n->inv_sqrt = inv_sqrt;
+  const int64_t* arrs[] = {wq, wk, wv, wo, w1, wu, w2};
+  for (int64_t l = 0; l < n_layers; ++l) {
+    LayerW L;
+    for (int i = 0; i < 7; ++i) L.w[i] = arrs[i][l];
+    // shape checks: q (H*hd, d), k/v (Hkv*hd, d), o (d, H*hd), w1/wu (dff, d), w2 (d, dff)
+    const int64_t want[7][2] = {{H * hd, d}, {Hkv * hd, d}, {Hkv * hd, d}, {d, H * hd}, {dff, d}, {dff, d}, {d, dff}};
+    for (int i = 0; i < 7; ++i) {
+      int64_t N = 0, nb = 0;
+      if (imie_q1_dims(L.w[i], &N, &nb) || N != want[i][0] || nb * 128 != want[i][1]) { delete n; return -1; }
+    }
+    L.n1g = buf_get(n1g[l], d); L.n2g = buf_get(n2g[l], d); L.qng = buf_get(qng[l], hd); L.kng = buf_get(kng[l], hd);
+    if (!L.n1g || !L.n2g || !L.qng || !L.kng) { delete n; return -1; }
+    n->layers.push_back(L);
+  }
+  n->finalg = finalg >= 0 ? buf_get(finalg, d) : nullptr;
+  n->out_head = out_head;
+  if (out_head >= 0) {
+    int64_t N = 0, nb = 0;
+    if (imie_q1_dims(out_head, &N, &nb) || nb * 128 != d || (vocab > 0 && N != vocab) || !n->finalg) { delete n; return -1; }
+    n->vocab = N;
+  }
+  n->cos = buf_get(cos_h, cap * (hd / 2));
+  n->sin = buf_get(sin_h, cap * (hd / 2));
+  if (!n->cos || !n->sin) { delete n; return -1; }
+  n->live = true;
+  if (net_alloc_kv(*n, cap, page, kv32)) { net_free(n); delete n; return -1; }
+  nets().push_back(n);
+  return (int64_t)nets().size() - 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+// gpu_native.py:549-556 / bonsai_q1_gpu.cu `bonsai_buf_upload_i64`: upload an int64 array once -> handle.
+int64_t bonsai_buf_upload_i64(const int64_t* host, int64_t n) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!host || n <= 0 || imie_device_ready() != 0) return -1;
+  BufEntry e;
+  if (hipMalloc((void**)&e.p, (size_t)n * 8) != hipSuccess) return -1;
+  if (hipMemcpy(e.p, host, (size_t)n * 8, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(e.p); return -1; }
+  e.n = n;
+  bufs().push_back(e);
+  return (int64_t)bufs().size() - 1;
+}
+
+// Device address of an uploaded buffer (device-pointer pipelines).
+const int64_t* imie_buf_device_ptr(int64_t handle) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  return buf_get(handle, 0);
+}
+
+void imie_buf_free_all(void) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  (void)hipStreamSynchronize(imie_stream());
+  for (auto& e : bufs()) if (e.p) (void)hipFree(e.p);
+  bufs().clear();
+}
+
+// gpu_native.py:559-595 / bonsai_q1_gpu.cu:3694-3819 `bonsai_prefill_forward_gpu`: whole prefill on the device,
+// last-row logits (vocab,) out; optional KV export (n_layers, Hkv, T, hd) int64 (post-RoPE K, raw V).
+int bonsai_prefill_forward_gpu(const int64_t* x_embed, int64_t T, int64_t d, int64_t n_layers, int64_t H, int64_t Hkv,
+                               int64_t hd, int64_t dff, int64_t frac, int64_t eps, int64_t inv_sqrt,
+                               const int64_t* wq, const int64_t* wk, const int64_t* wv, const int64_t* wo,
+                               const int64_t* w1, const int64_t* wu, const int64_t* w2, const int64_t* n1g,
+                               const int64_t* n2g, const int64_t* qng, const int64_t* kng, int64_t finalg,
+                               int64_t out_head, int64_t cos_h, int64_t sin_h, int64_t* out_logits, int64_t* out_k,
+                               int64_t* out_v) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!x_embed || !out_logits || T <= 0 || !wq || !wk || !wv || !wo || !w1 || !wu || !w2 || !n1g || !n2g || !qng ||
+      !kng)
+    return IMIE_EARG;
+  const int64_t h = net_create(1, n_layers, H, Hkv, hd, d, dff, T, 0, frac, eps, inv_sqrt, wq, wk, wv, wo, w1, wu,
+                               w2, n1g, n2g, qng, kng, finalg, out_head, cos_h, sin_h, T, 0);
+  if (h < 0) return IMIE_EARG;
+  Net& n = *nets()[(size_t)h];
+  hipStream_t st = imie_stream();
+  int rc = IMIE_OK;
+  do {
+    if (n.x.ensure((size_t)(T * d) * 8) || n.logits.ensure((size_t)n.vocab * 8)) { rc = IMIE_EARG; break; }
+    if (hipMemcpyAsync(n.x.p, x_embed, (size_t)(T * d) * 8, hipMemcpyHostToDevice, st) != hipSuccess) { rc = IMIE_EARG; break; }
+    if (n.status.ensure(64) || fill_i64((int64_t*)n.status.p, 1, 0, st)) { rc = IMIE_EARG; break; }
+    const int64_t start = 0;
+    if ((rc = net_run(n, (int64_t*)n.x.p, &start, T, st))) break;
+    if ((rc = net_head(n, (const int64_t*)n.x.p, {T - 1}, (int64_t*)n.logits.p, nullptr, st))) break;
+    int stat = 0;
+    if ((rc = read_status(n, st, &stat))) break;
+    if (stat) { rc = stat & IMIE_ERMS ? IMIE_ERMS : IMIE_EOVF; break; }
+    if (hipMemcpy(out_logits, n.logits.p, (size_t)n.vocab * 8, hipMemcpyDeviceToHost) != hipSuccess) { rc = IMIE_EARG; break; }
+    if (out_k && out_v) {
+      // dense int64 cache with P = T: layer pool is exactly (Hkv, T, hd)
+      const size_t lb = (size_t)(Hkv * T * hd) * 8;
+      for (int64_t l = 0; l < n_layers; ++l) {
+        if (hipMemcpy((char*)out_k + l * lb, n.kpool[(size_t)l], lb, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy((char*)out_v + l * lb, n.vpool[(size_t)l], lb, hipMemcpyDeviceToHost) != hipSuccess) {
+          rc = IMIE_EARG;
+          break;
+        }
+      }
+    }
+  } while (0);
+  net_free(&n);
+  delete nets()[(size_t)h];
+  nets()[(size_t)h] = nullptr;
+  return rc;
+}
+
+// gpu_native.py:483-506 / bonsai_q1_gpu.cu:3517-3562 `bonsai_decode_ctx_create`: B sequences, int64 cache of
+// capacity cap per sequence. Returns a context handle >= 0 or -1.
+int64_t bonsai_decode_ctx_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d,
+                                 int64_t dff, int64_t cap, int64_t vocab, int64_t frac, int64_t eps, int64_t inv_sqrt,
+                                 const int64_t* wq, const int64_t* wk, const int64_t* wv, const int64_t* wo,
+                                 const int64_t* w1, const int64_t* wu, const int64_t* w2, const int64_t* n1g,
+                                 const int64_t* n2g, const int64_t* qng, const int64_t* kng, int64_t finalg,
+                                 int64_t out_head, int64_t cos_h, int64_t sin_h) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!wq || !wk || !wv || !wo || !w1 || !wu || !w2 || !n1g || !n2g || !qng || !kng) return -1;
+  return net_create(B, n_layers, H, Hkv, hd, d, dff, cap, vocab, frac, eps, inv_sqrt, wq, wk, wv, wo, w1, wu, w2, n1g,
+                    n2g, qng, kng, finalg, out_head, cos_h, sin_h, cap, 0);
+}
+
+// Extended context (no reference counterpart): int32 (kv32 = 1, guarded) or int64 paged cache with `page`
+// tokens per page; out_head < 0 builds a layers-only context.
+int64_t imie_net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d, int64_t dff,
+                        int64_t cap, int64_t frac, int64_t eps, int64_t inv_sqrt, const int64_t* wq, const int64_t* wk,
+                        const int64_t* wv, const int64_t* wo, const int64_t* w1, const int64_t* wu, const int64_t* w2,
+                        const int64_t* n1g, const int64_t* n2g, const int64_t* qng, const int64_t* kng,
+                        int64_t finalg, int64_t out_head, int64_t cos_h, int64_t sin_h, int64_t page, int kv32) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!wq || !wk || !wv || !wo || !w1 || !wu || !w2 || !n1g || !n2g || !qng || !kng || page <= 0) return -1;
+  return net_create(B, n_layers, H, Hkv, hd, d, dff, cap, 0, frac, eps, inv_sqrt, wq, wk, wv, wo, w1, wu, w2, n1g,
+                    n2g, qng, kng, finalg, out_head, cos_h, sin_h, page, kv32);
+}
+
+// gpu_native.py:509-521 / bonsai_q1_gpu.cu:3565-3584 `bonsai_decode_ctx_seed_seq`: k/v (n_layers, Hkv, Lb, hd).
+int bonsai_decode_ctx_seed_seq(int64_t ctx, int64_t b, const int64_t* k, const int64_t* v, int64_t Lb) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !k || !v || b < 0 || b >= n->B || Lb < 0 || Lb > n->mp * n->P) return IMIE_EARG;
+  const size_t esz = n->kv32 ? 4 : 8;
+  std::vector<char> kb((size_t)(n->mp * n->Hkv * n->P * n->hd) * esz), vb(kb.size());
+  int bad = 0;
+  for (int64_t l = 0; l < n->nl; ++l) {
+    memset(kb.data(), 0, kb.size());
+    memset(vb.data(), 0, vb.size());
+    for (int64_t kv = 0; kv < n->Hkv; ++kv)
+      for (int64_t j = 0; j < Lb; ++j)
+        for (int64_t c = 0; c < n->hd; ++c) {
+          const int64_t src = ((l * n->Hkv + kv) * Lb + j) * n->hd + c;
+          const int64_t dst = (j / n->P) * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + (j % n->P) * n->hd + c;
+          if (n->kv32) {
+            if (k[src] != (int64_t)(int32_t)k[src] || v[src] != (int64_t)(int32_t)v[src]) bad = 1;
+            ((int32_t*)kb.data())[dst] = (int32_t)k[src];
+            ((int32_t*)vb.data())[dst] = (int32_t)v[src];
+          } else {
+            ((int64_t*)kb.data())[dst] = k[src];
+            ((int64_t*)vb.data())[dst] = v[src];
+          }
+        }
+    if (bad) return IMIE_EOVF;                      // transactional: nothing of sequence b was written
+    const size_t off = (size_t)(b * n->mp * n->Hkv * n->P * n->hd) * esz;
+    IMIE_HIP(hipMemcpy((char*)n->kpool[(size_t)l] + off, kb.data(), kb.size(), hipMemcpyHostToDevice));
+    IMIE_HIP(hipMemcpy((char*)n->vpool[(size_t)l] + off, vb.data(), vb.size(), hipMemcpyHostToDevice));
+  }
+  n->len[(size_t)b] = Lb;
+  return IMIE_OK;
+}
+
+// gpu_native.py:524-538 / bonsai_q1_gpu.cu:3588-3647 `bonsai_decode_step`: x_in (B, d) new-token residuals, pos (B,)
+// absolute positions; out (B, vocab) logits. Host pointers, synchronous.
+int bonsai_decode_step(int64_t ctx, const int64_t* x_in, const int64_t* pos, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !x_in || !pos || !out || n->out_head < 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const size_t xb = (size_t)(n->B * n->d) * 8;
+  if (n->x.ensure(xb) || n->logits.ensure((size_t)(n->B * n->vocab) * 8) || n->status.ensure(64)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(n->x.p, x_in, xb, hipMemcpyHostToDevice, st));
+  int rc = fill_i64((int64_t*)n->status.p, 1, 0, st);
+  if (rc) return rc;
+  if ((rc = net_run(*n, (int64_t*)n->x.p, pos, 1, st))) return rc;
+  std::vector<int64_t> rows((size_t)n->B);
+  for (int64_t b = 0; b < n->B; ++b) rows[(size_t)b] = b;
+  if ((rc = net_head(*n, (const int64_t*)n->x.p, rows, (int64_t*)n->logits.p, nullptr, st))) return rc;
+  int stat = 0;
+  if ((rc = read_status(*n, st, &stat))) return rc;
+  if (stat) return stat & IMIE_ERMS ? IMIE_ERMS : IMIE_EOVF;
+  IMIE_HIP(hipMemcpy(out, n->logits.p, (size_t)(n->B * n->vocab) * 8, hipMemcpyDeviceToHost));
+  return IMIE_OK;
+}
+
+void bonsai_decode_ctx_free(int64_t ctx) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n) return;
+  net_free(n);
+  delete n;
+  nets()[(size_t)ctx] = nullptr;
+}
+
+// Device-pointer forward (no reference counterpart): x_dev (B*M, d) updated in place through all layers for M new
+// tokens per sequence at positions starts[b] .. starts[b] + M - 1 (host array). Asynchronous on `stream`;
+// the status word (imie_net_status) reports envelope refusals.
+int imie_net_forward_dev(int64_t ctx, int64_t* x_dev, const int64_t* starts, int64_t M, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !x_dev || !starts || M <= 0) return IMIE_EARG;
+  return net_run(*n, x_dev, starts, M, (hipStream_t)stream);
+}
+
+// Final norm + output head (+ lowest-index argmax when ids_dev != NULL) for rows [0, rows) of x_dev.
+int imie_net_head_dev(int64_t ctx, const int64_t* x_dev, int64_t rows, int64_t* logits_dev, int64_t* ids_dev,
+                      void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !x_dev || !logits_dev || rows <= 0) return IMIE_EARG;
+  std::vector<int64_t> r((size_t)rows);
+  for (int64_t i = 0; i < rows; ++i) r[(size_t)i] = i;
+  return net_head(*n, x_dev, r, logits_dev, ids_dev, (hipStream_t)stream);
+}
+
+// Clear (0) or read the context status word: 0 ok, bit 2 attention / RoPE / int32-KV envelope, bit 4 RMSNorm.
+int imie_net_status(int64_t ctx, int clear, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || n->status.ensure(64)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  if (clear) return fill_i64((int64_t*)n->status.p, 1, 0, st) ? -1 : 0;
+  int stat = 0;
+  if (read_status(*n, st, &stat)) return -1;
+  return stat;
+}
+
+// Copy sequence b's cached K/V of `layer` for positions [0, count) to host (Hkv, count, hd) int64.
+int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int64_t* k_out, int64_t* v_out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !k_out || !v_out || layer < 0 || layer >= n->nl || b < 0 || b >= n->B || count < 0 ||
+      count > n->mp * n->P)
+    return IMIE_EARG;
+  IMIE_HIP(hipStreamSynchronize(imie_stream()));
+  IMIE_HIP(hipDeviceSynchronize());
+  const size_t esz = n->kv32 ? 4 : 8;
+  const size_t seq = (size_t)(n->mp * n->Hkv * n->P * n->hd);
+  std::vector<char> kb(seq * esz), vb(seq * esz);
+  const size_t off = (size_t)b * seq * esz;
+  IMIE_HIP(hipMemcpy(kb.data(), (char*)n->kpool[(size_t)layer] + off, kb.size(), hipMemcpyDeviceToHost));
+  IMIE_HIP(hipMemcpy(vb.data(), (char*)n->vpool[(size_t)layer] + off, vb.size(), hipMemcpyDeviceToHost));
+  for (int64_t kv = 0; kv < n->Hkv; ++kv)
+    for (int64_t j = 0; j < count; ++j)
+      for (int64_t c = 0; c < n->hd; ++c) {
+        const size_t src = (size_t)((j / n->P) * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + (j % n->P) * n->hd + c);
+        const size_t dst = (size_t)((kv * count + j) * n->hd + c);
+        k_out[dst] = n->kv32 ? (int64_t)((int32_t*)kb.data())[src] : ((int64_t*)kb.data())[src];
+        v_out[dst] = n->kv32 ? (int64_t)((int32_t*)vb.data())[src] : ((int64_t*)vb.data())[src];
+      }
+  return IMIE_OK;
+}
+
+// Q1 embedding rows on the device: out (T, nb*128) = sign * scale of rows ids (device int64) of a natural-layout
+// table (bits (V, nb, 16), scale (V, nb) int64, both device pointers).
+int imie_embed_dev(const uint8_t* bits, const int64_t* scale, int64_t nb, const int64_t* ids, int64_t T, int64_t* out,
+                   void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!bits || !scale || !ids || !out || nb <= 0 || T < 0) return IMIE_EARG;
+  return imie_embed_launch(bits, scale, nb, ids, T, out, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -17,6 +17,7 @@
 //     all 64 lanes busy, in int32 when max|x| <= 2^23 and in wrapping int64 otherwise.
 // MFMA int32 accumulation is exact: each D entry is at most 128 * 128 * 2^7 in magnitude.
 #include "imie_common.h"
+#include "imie_kernels.h"
 #include <string.h>
 #include <stdlib.h>
 
@@ -265,7 +266,8 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
       v += (uint64_t)__shfl_xor((int64_t)v, 32, 64);
       const int64_t row = (tile0 + r) * kTileRows + n;
       if (g == 0 && tile0 + r < ntiles && row < N) {
-        if (atomic_out) atomicAdd((unsigned long long*)&out[(int64_t)t * N + row], (unsigned long long)v);
+        if (atomic_out == 1) atomicAdd((unsigned long long*)&out[(int64_t)t * N + row], (unsigned long long)v);
+        else if (atomic_out == 2) out[(int64_t)t * N + row] = (int64_t)((uint64_t)out[(int64_t)t * N + row] + v);
         else out[(int64_t)t * N + row] = (int64_t)v;
       }
     }
@@ -307,7 +309,7 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
 // Launch helpers
 // ------------------------------------------------------------------------------------------------------
 static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int64_t frac, int64_t* out_dev,
-                        hipStream_t st) {
+                        hipStream_t st, int accumulate = 0) {
   if (T <= 0) return IMIE_OK;
   const int64_t nbp = w.nslabs * kSlabBlocks;
   if (g_ws.xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || g_ws.totals.ensure((size_t)T * nbp * 8) ||
@@ -342,12 +344,13 @@ static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int6
     const uint4* xq = (const uint4*)g_ws.xq.p + t0 * kMaxLimbs * nbp * 8;
     const int64_t* tot = (const int64_t*)g_ws.totals.p + t0 * nbp;
     const int* ls = (const int*)g_ws.lslab.p + t0 * w.nslabs;
-    if (ksplit > 1)
+    const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
+    if (ksplit > 1 && !accumulate)
       hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((tn * w.N + 255) / 256)), dim3(256), 0, st, o,
                          (int64_t)tn * w.N);
 #define IMIE_Q1_LAUNCH(S64_, R_, TT_)                                                                        \
   hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, R_, TT_>), grid, dim3(256), lds, st, w.bits, w.scale, xq, tot, ls, \
-                     w.N, w.ntiles, w.nslabs, nbp, tn, fr, spk, Lcap, ksplit > 1 ? 1 : 0, o)
+                     w.N, w.ntiles, w.nslabs, nbp, tn, fr, spk, Lcap, mode, o)
 #define IMIE_Q1_LAUNCH_R(S64_, TT_)                                                                          \
   if (R == 4) IMIE_Q1_LAUNCH(S64_, 4, TT_); else if (R == 2) IMIE_Q1_LAUNCH(S64_, 2, TT_); else IMIE_Q1_LAUNCH(S64_, 1, TT_)
 #define IMIE_Q1_LAUNCH_T(S64_)                                                                               \
@@ -409,6 +412,21 @@ static int q1_host_apply(const Q1Weight& w, const int64_t* x, int64_t T, int64_t
   if (rc) return rc;
   IMIE_HIP(hipMemcpyAsync(out, g_ws.out.p, ob, hipMemcpyDeviceToHost, st));
   IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
+
+int imie_q1_launch(int64_t handle, const int64_t* x, int64_t T, int64_t frac, int64_t* out, int accumulate,
+                   hipStream_t st) {
+  const Q1Weight* w = q1_get(handle);
+  if (!w) return IMIE_EARG;
+  return q1_apply_dev(*w, x, T, frac, out, st, accumulate);
+}
+
+int imie_q1_dims(int64_t handle, int64_t* N, int64_t* nb) {
+  const Q1Weight* w = q1_get(handle);
+  if (!w) return IMIE_EARG;
+  *N = w->N;
+  *nb = w->nb;
   return IMIE_OK;
 }
 

@@ -1,0 +1,88 @@
+"""Device-resident Bonsai forward (layers + optional head) over a paged integer KV cache.
+
+Host-side wrapper of the ``imie_net_*`` C-ABI (no reference counterpart; the reference's decode context,
+``gpu_native.decode_ctx_*``, is the host-pointer special case). Activations stay in HBM between calls; torch is
+used only to own device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+_ORDER = ("wq", "wk", "wv", "wo", "w1", "wu", "w2", "n1g", "n2g", "qng", "kng")
+
+
+class ResidentNet:
+    """B sequences, ``cap`` positions each, ``page`` tokens per KV page, int32 (guarded) or int64 KV."""
+
+    def __init__(self, *, B: int, n_layers: int, H: int, Hkv: int, hd: int, d: int, dff: int, cap: int, w: dict,
+                 g: dict, frac: int = 16, eps: int = 1, inv_sqrt: int | None = None, page: int = 64,
+                 kv32: bool = True):
+        import torch  # device memory owner
+        self.torch = torch
+        self.lib = _lib.lib()
+        if inv_sqrt is None:
+            inv_sqrt = int(round((1.0 / np.sqrt(hd)) * (1 << frac)))
+        arrs = {k: np.ascontiguousarray(np.asarray(v, dtype=np.int64)) for k, v in
+                dict(wq=w["wq"], wk=w["wk"], wv=w["wv"], wo=w["wo"], w1=w["w1"], wu=w["wu"], w2=w["w2"],
+                     n1g=g["n1g"], n2g=g["n2g"], qng=g["qng"], kng=g["kng"]).items()}
+        h = self.lib.imie_net_create(B, n_layers, H, Hkv, hd, d, dff, cap, frac, eps, inv_sqrt,
+                                     *[arrs[k].ctypes.data for k in _ORDER], int(g.get("finalg", -1)),
+                                     int(w.get("out_head", -1)), int(g["cos_h"]), int(g["sin_h"]), page,
+                                     1 if kv32 else 0)
+        if h < 0:
+            raise RuntimeError(f"imie_net_create failed: {_lib.last_error()}")
+        self.h = int(h)
+        self.B, self.d, self.nl, self.Hkv, self.hd = B, d, n_layers, Hkv, hd
+        self.vocab = int(w.get("out_head_vocab", 0))
+        self.stream = torch.cuda.Stream()
+
+    def _sp(self):
+        return ctypes.c_void_p(self.stream.cuda_stream)
+
+    def seed(self, b: int, k: np.ndarray, v: np.ndarray) -> None:
+        """k/v (n_layers, Hkv, Lb, hd) int64."""
+        k = np.ascontiguousarray(k, dtype=np.int64)
+        v = np.ascontiguousarray(v, dtype=np.int64)
+        rc = self.lib.bonsai_decode_ctx_seed_seq(self.h, b, k.ctypes.data, v.ctypes.data, k.shape[2])
+        if rc != 0:
+            raise RuntimeError(f"seed rc={rc}")
+
+    def forward(self, x, starts, M: int):
+        """x: torch int64 (B*M, d) on the device, updated in place. Returns the status word (0 = exact)."""
+        st = np.ascontiguousarray(np.asarray(starts, dtype=np.int64))
+        self.lib.imie_net_status(self.h, 1, self._sp())
+        rc = self.lib.imie_net_forward_dev(self.h, ctypes.c_void_p(x.data_ptr()), st.ctypes.data, int(M), self._sp())
+        if rc != 0:
+            raise RuntimeError(f"forward rc={rc}: {_lib.last_error()}")
+        return self.lib.imie_net_status(self.h, 0, self._sp())
+
+    def head(self, x, rows: int, *, argmax: bool = True):
+        t = self.torch
+        logits = t.empty((rows, self.vocab), dtype=t.int64, device="cuda")
+        ids = t.empty((rows,), dtype=t.int64, device="cuda") if argmax else None
+        rc = self.lib.imie_net_head_dev(self.h, ctypes.c_void_p(x.data_ptr()), rows,
+                                        ctypes.c_void_p(logits.data_ptr()),
+                                        ctypes.c_void_p(ids.data_ptr()) if ids is not None else None, self._sp())
+        if rc != 0:
+            raise RuntimeError(f"head rc={rc}")
+        self.stream.synchronize()
+        return logits, ids
+
+    def export_kv(self, layer: int, b: int, count: int):
+        k = np.empty((self.Hkv, count, self.hd), dtype=np.int64)
+        v = np.empty_like(k)
+        self.stream.synchronize()
+        rc = self.lib.imie_net_export_kv(self.h, layer, b, count, k.ctypes.data, v.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"export rc={rc}")
+        return k, v
+
+    def close(self) -> None:
+        if self.h >= 0:
+            self.stream.synchronize()
+            self.lib.bonsai_decode_ctx_free(self.h)
+            self.h = -1
