@@ -69,8 +69,19 @@ SIGNATURES = {
 }
 
 
+def _single_hip_runtime() -> None:
+    """PyTorch-ROCm bundles its own ``libamdhip64.so.7`` (same soname as /opt/rocm's). Whichever copy is loaded
+    first serves the whole process; if ours came first, torch would load a second runtime that sees no device.
+    Importing torch (when installed) before the library makes both share torch's runtime."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 @lru_cache(maxsize=1)
 def lib() -> ctypes.CDLL:
+    _single_hip_runtime()
     if not LIB_PATH.exists():
         raise ImportError(f"{LIB_PATH} is missing: build it with `python -m integer_inference_engine_amd.build`")
     so = ctypes.CDLL(str(LIB_PATH))
