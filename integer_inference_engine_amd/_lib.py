@@ -66,6 +66,34 @@ SIGNATURES = {
     "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),
     "imie_net_export_kv": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_embed_dev": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    # north-mini-code Q4_K / Q6_K (include/imie_nmc.h)
+    "qk_cuda_abi_version": (c_int, []),
+    "qk_cuda_available": (c_int, []),
+    "qk_linear_cuda": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_void_p]),
+    "qk_register_weight": (c_int64, [c_void_p, c_int64, c_int64, c_int]),
+    "qk_resident_reserve": (c_int, [c_int64]),
+    "qk_apply_resident": (c_int, [c_int64, c_void_p, c_int64, c_int, c_void_p]),
+    "qk_apply_resident_grouped": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_int64, c_void_p]),
+    "qk_apply_resident_q4k_dp4a": (c_int, [c_int64, c_void_p, c_int64, c_int, c_int, c_void_p]),
+    "qk_apply_resident_q6k_dp4a": (c_int, [c_int64, c_void_p, c_int64, c_int, c_int, c_void_p]),
+    "qk_moe_ffn_batched": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int,
+                                                      c_void_p]),
+    "qk_moe_ffn_batched_dp4a": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int,
+                                                           c_int, c_void_p]),
+    "qk_moe_ffn": (c_int, [c_void_p] * 3 + [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p]),
+    "qk_moe_ffn_dp4a": (c_int, [c_void_p] * 3 + [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p]),
+    "imie_moe_ffn_batched_dev": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int,
+                                                            c_int, c_void_p, c_void_p]),
+    "imie_moe_status": (c_int, [c_int, c_void_p]),
+    "qk_free_all": (None, []),
+    "qk_resident_count": (c_int64, []),
+    "qk_resident_capacity": (c_int64, []),
+    "qk_moe_workspace_allocations": (c_int64, []),
+    "qk_moe_workspace_bytes": (c_uint64, []),
+    "qk_moe_workspace_release": (None, []),
+    "qk_profile_reset": (None, []),
+    "qk_profile_set_enabled": (None, [c_int]),
+    "qk_profile_snapshot": (c_int, [c_void_p, c_int]),
 }
 
 

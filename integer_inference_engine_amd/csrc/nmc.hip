@@ -1,0 +1,576 @@
+// north-mini-code Q4_K / Q6_K integer linear and the ragged grouped MoE FFN for gfx950.
+//
+// Semantics (reference: north-mini-code/src/nmc/qk_codec.py:28-206, cohere2.py:102-111, :168-188; producer
+// north-mini-code/tools/nmc_qk_cuda.cu:92-237, :2184-2254):
+//   y[t, o] = floor( sum_i W[o, i] * x[t, i] / 2^fw )   exactly (big-int in the oracle), W = dequantized block
+//   Q4_K (144 B): W = dq*sc_j*q - dmq*m_j, sub-blocks of 32; Q6_K (210 B): W = dq*sc_j*(q6 - 32), sub-blocks of 16
+//   dq = round_half_even(fp16 * 2^fw) from the fp16 bits in integer arithmetic (exact; no libm, no FP rounding).
+// Evaluation: per sub-block j, sum_i W x = (dq*sc_j) * qdot_j - (dmq*m_j) * xsum_j with qdot_j = sum q*x in
+// int64 (|x| < 2^52 keeps it exact; larger staged values take an int128 path), the products and the running sum in
+// int128. A result that does not fit int64 (the oracle's astype would raise) sets status bit 2.
+//
+// Work: a workgroup = (weight group, 64-row tile); the x rows routed to that weight are staged block by block in
+// LDS (16 rows per pass) and 4 threads per output row each own a quarter of them, so every weight block is read
+// from HBM once per call no matter how many tokens use it.
+#include "imie_common.h"
+#include "imie_kernels.h"
+#include <string.h>
+#include <algorithm>
+#include <map>
+
+namespace {
+
+typedef __int128 i128;
+constexpr int kRows = 64;        // output rows per workgroup
+constexpr int kXRows = 16;       // staged x rows per pass (4 per thread)
+// dq * sc * q must fit int64 for every finite fp16 scale (as the oracle's int64 weight arrays require)
+constexpr int kMaxFw = 36;
+
+struct QKWeight {
+  uint8_t* p = nullptr;
+  int64_t out_f = 0, nb = 0;
+  int qtype = 0;
+  size_t bytes = 0;
+};
+std::vector<QKWeight> g_qk;
+int64_t g_qk_live = 0;
+
+// profile counters (qk_cuda.py:24-34 metric order)
+enum { PM_REG_CALLS, PM_REG_NS, PM_H2D_CALLS, PM_H2D_BYTES, PM_H2D_NS, PM_D2H_CALLS, PM_D2H_BYTES, PM_D2H_NS,
+       PM_ALLOC_CALLS, PM_ALLOC_BYTES, PM_ALLOC_NS, PM_FREE_CALLS, PM_NATIVE_CALLS, PM_RESIDENT_CALLS,
+       PM_GROUPED_CALLS, PM_MOE_CALLS, PM_MOE_BATCHED_CALLS, PM_MOE_BATCHED_DP4A_CALLS, PM_Q_CALLS, PM_Q_NS,
+       PM_K_CALLS, PM_K_NS, PM_V_CALLS, PM_V_NS, PM_O_CALLS, PM_O_NS, PM_OTHER_CALLS, PM_OTHER_NS, PM_COUNT };
+unsigned long long g_prof[PM_COUNT];
+int g_prof_on = 0;
+inline void prof(int k, unsigned long long v = 1) { if (g_prof_on) g_prof[k] += v; }
+
+struct MoeWs {
+  DevBuf items, pairs, x, y, g, u, d, out, gates, status, tok;
+  int64_t grows = 0;
+} g_mws;
+
+__device__ inline int64_t fp16_fixed(uint32_t h, int fw) {
+  const int sign = (h >> 15) & 1, e = (h >> 10) & 31;
+  const int64_t mant = h & 0x3FF;
+  int64_t m;
+  int sh;
+  if (e == 0) { m = mant; sh = fw - 24; }
+  else { m = mant | 0x400; sh = e - 25 + fw; }
+  int64_t r;
+  if (sh >= 0) r = m << sh;
+  else {
+    const int s = -sh;
+    if (s >= 63) r = 0;
+    else {
+      const int64_t q = m >> s, rem = m & (((int64_t)1 << s) - 1), half = (int64_t)1 << (s - 1);
+      r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+    }
+  }
+  return sign ? -r : r;
+}
+
+struct Item {               // one weight applied to `count` x rows
+  const uint8_t* w;
+  int64_t out_f, nb;
+  int qtype;
+  int first, count;         // into the pair arrays
+};
+
+// y[yi[p]][o] = floor(W[o] . x[xi[p]] / 2^fw) for the pairs of one item.
+__global__ __launch_bounds__(256) void qk_group_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
+                                                       const int* __restrict__ yi, const int64_t* __restrict__ X,
+                                                       int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
+                                                       int* __restrict__ status) {
+  __shared__ int64_t sx[kXRows][257];
+  __shared__ int s_wide;
+  const Item it = items[blockIdx.y];
+  const int64_t o = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 2);
+  if ((int64_t)blockIdx.x * kRows >= it.out_f) return;
+  const int slot = threadIdx.x & 3;
+  const bool live = o < it.out_f;
+  const int bs = it.qtype == 0 ? 144 : 210;
+  const uint8_t* row = it.w + (live ? o : 0) * it.nb * bs;
+  for (int c0 = 0; c0 < it.count; c0 += kXRows) {
+    const int cn = min(kXRows, it.count - c0);
+    i128 acc[4] = {0, 0, 0, 0};
+    for (int64_t b = 0; b < it.nb; ++b) {
+      __syncthreads();
+      if (threadIdx.x == 0) s_wide = 0;
+      __syncthreads();
+      int wide = 0;
+      for (int i = threadIdx.x; i < cn * 256; i += blockDim.x) {
+        const int r = i >> 8, c = i & 255;
+        const int64_t v = X[(int64_t)xi[it.first + c0 + r] * K + b * 256 + c];
+        sx[r][c] = v;
+        if (v >= ((int64_t)1 << 52) || v <= -((int64_t)1 << 52)) wide = 1;
+      }
+      if (wide) s_wide = 1;
+      __syncthreads();
+      const bool fast = s_wide == 0;
+      const uint8_t* blk = row + b * bs;
+      if (it.qtype == 0) {
+        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const uint8_t* sc = blk + 4;
+        const uint8_t* qs = blk + 16;
+#pragma unroll 1
+        for (int j = 0; j < 8; ++j) {
+          int s, m;
+          if (j < 4) { s = sc[j] & 63; m = sc[j + 4] & 63; }
+          else { s = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4); m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
+          const int64_t ds = dq * s, dm = dmq * m;
+          const int g = j >> 1, hi = j & 1;
+          uint8_t q[32];
+#pragma unroll
+          for (int l = 0; l < 32; ++l) q[l] = hi ? (qs[32 * g + l] >> 4) : (qs[32 * g + l] & 0xF);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int r = slot + 4 * k;
+            if (r >= cn) break;
+            const int64_t* xv = &sx[r][32 * j];
+            if (fast) {
+              int64_t qd = 0, xs = 0;
+#pragma unroll
+              for (int l = 0; l < 32; ++l) { qd += (int64_t)q[l] * xv[l]; xs += xv[l]; }
+              acc[k] += (i128)ds * qd - (i128)dm * xs;
+            } else {
+              i128 qd = 0, xs = 0;
+              for (int l = 0; l < 32; ++l) { qd += (i128)q[l] * xv[l]; xs += xv[l]; }
+              acc[k] += (i128)ds * qd - (i128)dm * xs;
+            }
+          }
+        }
+      } else {
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+#pragma unroll 1
+        for (int j = 0; j < 16; ++j) {
+          // sub-block j covers positions 16 j .. 16 j + 15: half = j / 8, quarter qq = (j % 8) / 2, is = j % 2
+          const int half = j >> 3, qq = (j & 7) >> 1, is = j & 1;
+          const int qlo = 64 * half, qho = 32 * half;
+          const int64_t ds = dq * sc[8 * half + is + 2 * qq];
+          int8_t q[16];
+#pragma unroll
+          for (int l0 = 0; l0 < 16; ++l0) {
+            const int l = 16 * is + l0;
+            int v;
+            if (qq == 0) v = (ql[qlo + l] & 0xF) | (((qh[qho + l] >> 0) & 3) << 4);
+            else if (qq == 1) v = (ql[qlo + l + 32] & 0xF) | (((qh[qho + l] >> 2) & 3) << 4);
+            else if (qq == 2) v = (ql[qlo + l] >> 4) | (((qh[qho + l] >> 4) & 3) << 4);
+            else v = (ql[qlo + l + 32] >> 4) | (((qh[qho + l] >> 6) & 3) << 4);
+            q[l0] = (int8_t)(v - 32);
+          }
+          const int pos0 = 128 * half + 32 * qq + 16 * is;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int r = slot + 4 * k;
+            if (r >= cn) break;
+            const int64_t* xv = &sx[r][pos0];
+            if (fast) {
+              int64_t qd = 0;
+#pragma unroll
+              for (int l = 0; l < 16; ++l) qd += (int64_t)q[l] * xv[l];
+              acc[k] += (i128)ds * qd;
+            } else {
+              i128 qd = 0;
+              for (int l = 0; l < 16; ++l) qd += (i128)q[l] * xv[l];
+              acc[k] += (i128)ds * qd;
+            }
+          }
+        }
+      }
+    }
+    if (live) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = slot + 4 * k;
+        if (r >= cn) break;
+        const i128 y = acc[k] >> fw;
+        if (y > (i128)INT64_MAX || y < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+        Y[(int64_t)yi[it.first + c0 + r] * ldy + o] = (int64_t)y;
+      }
+    }
+  }
+}
+
+// nmc SiLU*up: g <- ((g * sigmoid(g)) >> fa) exactly, then gu = (g * u) >> fa exactly (cohere2.py:109-111,
+// :183-185); sigmoid without the (1<<62)/log2e cap (north-mini-code/src/nmc/_bonsai/fixedpoint.py:148).
+__device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
+  const int64_t fp = (int64_t)1 << frac;
+  const int64_t k = u >> frac, f = u & (fp - 1);
+  const int sh = 16 - frac;
+  int64_t c0, c1, c2, c3;
+  if (sh >= 0) { c0 = 65536 >> sh; c1 = 45426 >> sh; c2 = 15743 >> sh; c3 = 3638 >> sh; }
+  else { c0 = (int64_t)65536 << -sh; c1 = (int64_t)45426 << -sh; c2 = (int64_t)15743 << -sh; c3 = (int64_t)3638 << -sh; }
+  const int64_t f2 = (int64_t)((uint64_t)f * (uint64_t)f) >> frac;
+  const int64_t f3 = (int64_t)((uint64_t)f2 * (uint64_t)f) >> frac;
+  int64_t poly = c0 - ((int64_t)((uint64_t)c1 * (uint64_t)f) >> frac) + ((int64_t)((uint64_t)c2 * (uint64_t)f2) >> frac) -
+                 ((int64_t)((uint64_t)c3 * (uint64_t)f3) >> frac);
+  if (poly < 0) poly = 0;
+  if (k < 0) return 0;
+  return poly >> (k < 63 ? k : 63);
+}
+
+__global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t* __restrict__ u, int64_t n, int fa,
+                                   int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t x = g[i];
+  const int64_t m = x > 0 ? x : 0;
+  int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
+  if (d0 > dclip) d0 = dclip;
+  if (d1 > dclip) d1 = dclip;
+  const int64_t e0 = exp2_neg_fixed((int64_t)((uint64_t)d0 * (uint64_t)log2e) >> fa, fa);
+  const int64_t e1 = exp2_neg_fixed((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> fa, fa);
+  const int64_t z = e0 + e1;
+  const int64_t sig = z == 0 ? 0 : (int64_t)(((uint64_t)e1 << fa) / (uint64_t)z);
+  const i128 s = ((i128)x * sig) >> fa;
+  if (s > (i128)INT64_MAX || s < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+  const i128 gu = ((i128)(int64_t)s * u[i]) >> fa;
+  if (gu > (i128)INT64_MAX || gu < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+  out[i] = (int64_t)gu;
+}
+
+// out[t][o] = sum_j (dd[t*k + j][o] * gates[t*k + j]) >> fa (exact; cohere2.py:187 then astype int64)
+__global__ void qk_combine_kernel(const int64_t* __restrict__ dd, int m, int k, int64_t d_model,
+                                  const int64_t* __restrict__ gates, int fa, int64_t* __restrict__ out,
+                                  int* __restrict__ status) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)m * d_model) return;
+  const int64_t t = idx / d_model, o = idx % d_model;
+  i128 acc = 0;
+  for (int j = 0; j < k; ++j) acc += ((i128)dd[(t * k + j) * d_model + o] * gates[t * k + j]) >> fa;
+  if (acc > (i128)INT64_MAX || acc < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+  out[idx] = (int64_t)acc;
+}
+
+const QKWeight* qk_get(int64_t h) {
+  if (h < 0 || h >= (int64_t)g_qk.size() || !g_qk[(size_t)h].p) return nullptr;
+  return &g_qk[(size_t)h];
+}
+
+// Enqueue a set of items over device X (rows x K) into device Y (rows x ldy). pairs: host arrays.
+int run_items(const std::vector<Item>& items, const std::vector<int>& xi, const std::vector<int>& yi,
+              const int64_t* X, int64_t K, int64_t* Y, int64_t ldy, int fw, int* status, hipStream_t st,
+              DevBuf& ibuf, DevBuf& pbuf) {
+  if (items.empty()) return IMIE_OK;
+  const size_t np = xi.size();
+  if (ibuf.ensure(items.size() * sizeof(Item)) || pbuf.ensure(np * 8)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(ibuf.p, items.data(), items.size() * sizeof(Item), hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(pbuf.p, xi.data(), np * 4, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync((int*)pbuf.p + np, yi.data(), np * 4, hipMemcpyHostToDevice, st));
+  int64_t maxo = 0;
+  for (auto& it : items) maxo = it.out_f > maxo ? it.out_f : maxo;
+  imie_prof_mark(IMIE_K_QK, st, true);
+  hipLaunchKernelGGL(qk_group_kernel, dim3((unsigned)((maxo + kRows - 1) / kRows), (unsigned)items.size()),
+                     dim3(256), 0, st, (const Item*)ibuf.p, (const int*)pbuf.p, (const int*)pbuf.p + np, X, K, Y,
+                     ldy, fw, status);
+  imie_prof_mark(IMIE_K_QK, st, false);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+void silu_consts_nmc(int fa, int64_t* log2e, int64_t* dclip) {
+  const int sh = 16 - fa;
+  *log2e = sh >= 0 ? (94548 >> sh) : ((int64_t)94548 << -sh);
+  *dclip = (((int64_t)fa + 2) << (2 * fa)) / *log2e;
+}
+
+int read_status_and(hipStream_t st, int* stat) {
+  IMIE_HIP(hipMemcpyAsync(stat, g_mws.status.p, 4, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
+
+// Batched MoE: P = m*k pairs (token-major, pair p belongs to token p / k). Pairs sharing a weight run in one
+// item, so each expert's gate/up/down are read once per call.
+int moe_batched(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                const int64_t* h_dev, const int64_t* gates_dev, int64_t d_model, int64_t e_ffn, int fa, int fw,
+                int64_t* out_dev, hipStream_t st) {
+  const int64_t P = (int64_t)m * k;
+  if (m <= 0 || k <= 0 || d_model <= 0 || e_ffn <= 0 || d_model % 256 || e_ffn % 256 || fa < 1 || fa > 28 || fw < 0 ||
+      fw > 62)
+    return IMIE_EARG;
+  for (int64_t p = 0; p < P; ++p) {
+    const QKWeight *g = qk_get(gate_h[p]), *u = qk_get(up_h[p]), *d = qk_get(down_h[p]);
+    if (!g || !u || !d || g->out_f != e_ffn || g->nb * 256 != d_model || u->out_f != e_ffn || u->nb * 256 != d_model ||
+        d->out_f != d_model || d->nb * 256 != e_ffn)
+      return IMIE_EARG;
+  }
+  if (g_mws.g.ensure((size_t)(P * e_ffn) * 8) || g_mws.u.ensure((size_t)(P * e_ffn) * 8) ||
+      g_mws.d.ensure((size_t)(P * d_model) * 8) || g_mws.status.ensure(64))
+    return IMIE_EARG;
+  int64_t *gb = (int64_t*)g_mws.g.p, *ub = (int64_t*)g_mws.u.p, *db = (int64_t*)g_mws.d.p;
+  int* status = (int*)g_mws.status.p;
+  // group pairs by weight handle
+  auto build = [&](const long long* hs, bool x_per_pair, std::vector<Item>& items, std::vector<int>& xi,
+                   std::vector<int>& yi) {
+    std::map<long long, std::vector<int>> groups;
+    for (int64_t p = 0; p < P; ++p) groups[hs[p]].push_back((int)p);
+    for (auto& kv : groups) {
+      const QKWeight* w = qk_get(kv.first);
+      Item it{w->p, w->out_f, w->nb, w->qtype, (int)xi.size(), (int)kv.second.size()};
+      for (int p : kv.second) { xi.push_back(x_per_pair ? p : p / k); yi.push_back(p); }
+      items.push_back(it);
+    }
+  };
+  std::vector<Item> ig, iu, idn;
+  std::vector<int> xg, yg, xu, yu, xd, yd;
+  build(gate_h, false, ig, xg, yg);
+  build(up_h, false, iu, xu, yu);
+  build(down_h, true, idn, xd, yd);
+  static DevBuf ib1, pb1, ib2, pb2, ib3, pb3;
+  int rc = run_items(ig, xg, yg, h_dev, d_model, gb, e_ffn, fw, status, st, ib1, pb1);
+  if (!rc) rc = run_items(iu, xu, yu, h_dev, d_model, ub, e_ffn, fw, status, st, ib2, pb2);
+  if (rc) return rc;
+  int64_t log2e, dclip;
+  silu_consts_nmc(fa, &log2e, &dclip);
+  const int64_t n = P * e_ffn;
+  hipLaunchKernelGGL(qk_silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gb, ub, n, fa, log2e,
+                     dclip, gb, status);
+  IMIE_HIP(hipGetLastError());
+  rc = run_items(idn, xd, yd, gb, e_ffn, db, d_model, fw, status, st, ib3, pb3);
+  if (rc) return rc;
+  hipLaunchKernelGGL(qk_combine_kernel, dim3((unsigned)(((int64_t)m * d_model + 255) / 256)), dim3(256), 0, st, db,
+                     m, k, d_model, gates_dev, fa, out_dev, status);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int host_linear(const std::vector<int64_t>& handles, const int64_t* x, int64_t T, int fw, int64_t* out_flat) {
+  // all handles share the input width; outputs concatenated handle-major (each T x out_f)
+  hipStream_t st = imie_stream();
+  const QKWeight* w0 = qk_get(handles[0]);
+  const int64_t K = w0->nb * 256;
+  int64_t total = 0;
+  for (auto h : handles) total += T * qk_get(h)->out_f;
+  if (g_mws.x.ensure((size_t)(T * K) * 8) || g_mws.y.ensure((size_t)total * 8) || g_mws.status.ensure(64))
+    return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(g_mws.x.p, x, (size_t)(T * K) * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemsetAsync(g_mws.status.p, 0, 4, st));
+  prof(PM_H2D_CALLS); prof(PM_H2D_BYTES, (unsigned long long)(T * K * 8));
+  int64_t off = 0;
+  static DevBuf ib, pb;
+  for (auto h : handles) {
+    const QKWeight* w = qk_get(h);
+    std::vector<Item> items{Item{w->p, w->out_f, w->nb, w->qtype, 0, (int)T}};
+    std::vector<int> xi((size_t)T), yi((size_t)T);
+    for (int64_t t = 0; t < T; ++t) { xi[(size_t)t] = (int)t; yi[(size_t)t] = (int)t; }
+    int rc = run_items(items, xi, yi, (const int64_t*)g_mws.x.p, K, (int64_t*)g_mws.y.p + off, w->out_f, fw,
+                       (int*)g_mws.status.p, st, ib, pb);
+    if (rc) return rc;
+    IMIE_HIP(hipStreamSynchronize(st));   // ib/pb are reused by the next handle
+    off += T * w->out_f;
+  }
+  int stat = 0;
+  if (read_status_and(st, &stat)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpy(out_flat, g_mws.y.p, (size_t)total * 8, hipMemcpyDeviceToHost));
+  prof(PM_D2H_CALLS); prof(PM_D2H_BYTES, (unsigned long long)(total * 8));
+  return stat ? IMIE_EOVF : IMIE_OK;
+}
+
+int64_t qk_register(const uint8_t* W, int64_t out_f, int64_t nb, int qtype) {
+  if (!W || out_f <= 0 || nb <= 0 || (qtype != 0 && qtype != 1) || imie_device_ready() != 0) return -1;
+  QKWeight w;
+  w.out_f = out_f; w.nb = nb; w.qtype = qtype;
+  w.bytes = (size_t)(out_f * nb) * (qtype == 0 ? 144 : 210);
+  if (hipMalloc((void**)&w.p, w.bytes) != hipSuccess) return -1;
+  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(w.p); return -1; }
+  g_qk.push_back(w);
+  ++g_qk_live;
+  prof(PM_REG_CALLS); prof(PM_ALLOC_CALLS); prof(PM_ALLOC_BYTES, w.bytes);
+  return (int64_t)g_qk.size() - 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+// nmc_qk_cuda.cu:755 `qk_cuda_abi_version`; the reference bridge requires 5 (qk_cuda.py:22, 83-92).
+int qk_cuda_abi_version(void) { return 5; }
+
+// nmc_qk_cuda.cu `qk_cuda_available`: 0 iff usable.
+int qk_cuda_available(void) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  return imie_device_ready();
+}
+
+// nmc_qk_cuda.cu:720 `qk_linear_cuda` (qk_cuda.py:230-244): per-call weight upload, y [T, out_f].
+int qk_linear_cuda(const uint8_t* W, const int64_t* x, long long T, long long out_f, long long n_blocks, int fw,
+                   int qtype, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  prof(PM_NATIVE_CALLS);
+  if (!W || !x || !out || T < 0 || out_f <= 0 || n_blocks <= 0 || fw < 0 || fw > kMaxFw) return IMIE_EARG;
+  if (T == 0) return IMIE_OK;
+  const int64_t h = qk_register(W, out_f, n_blocks, qtype);
+  if (h < 0) return IMIE_EARG;
+  const int rc = host_linear({h}, x, T, fw, out);
+  (void)hipFree(g_qk[(size_t)h].p);
+  g_qk[(size_t)h].p = nullptr;
+  --g_qk_live;
+  if (h == (int64_t)g_qk.size() - 1) g_qk.pop_back();
+  return rc;
+}
+
+// nmc_qk_cuda.cu:1046 `qk_register_weight` (qk_cuda.py:252-270): raw Q4_K (0) / Q6_K (1) bytes -> handle.
+long long qk_register_weight(const uint8_t* W, long long out_f, long long n_blocks, int qtype) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  return qk_register(W, out_f, n_blocks, qtype);
+}
+
+// nmc_qk_cuda.cu:1040 `qk_resident_reserve`: registry metadata only.
+int qk_resident_reserve(long long count) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (count < 0) return IMIE_EARG;
+  g_qk.reserve((size_t)count);
+  return IMIE_OK;
+}
+
+// nmc_qk_cuda.cu:1252 `qk_apply_resident` (qk_cuda.py:387-397).
+int qk_apply_resident(long long h, const int64_t* x, long long T, int fw, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  prof(PM_RESIDENT_CALLS);
+  if (!qk_get(h) || !x || !out || T < 0 || fw < 0 || fw > kMaxFw) return IMIE_EARG;
+  if (T == 0) return IMIE_OK;
+  return host_linear({(int64_t)h}, x, T, fw, out);
+}
+
+// nmc_qk_cuda.cu:1284 `qk_apply_resident_grouped` (qk_cuda.py:405-442): same-input projections, one H2D and
+// one D2H; outputs concatenated handle-major. phase_ids only feed the Q/K/V/O counters.
+int qk_apply_resident_grouped(const long long* handles, const int* phase_ids, int count, const int64_t* x,
+                              long long rows, int fw, long long total, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  prof(PM_GROUPED_CALLS);
+  if (!handles || !x || !out || count <= 0 || count > 16 || rows <= 0 || fw < 0 || fw > kMaxFw) return IMIE_EARG;
+  std::vector<int64_t> hs;
+  int64_t K = -1, want = 0;
+  for (int i = 0; i < count; ++i) {
+    const QKWeight* w = qk_get(handles[i]);
+    if (!w || (K >= 0 && w->nb * 256 != K)) return IMIE_EARG;
+    K = w->nb * 256;
+    want += rows * w->out_f;
+    hs.push_back(handles[i]);
+    if (phase_ids) {
+      const int ph = phase_ids[i];
+      prof(ph == 1 ? PM_Q_CALLS : ph == 2 ? PM_K_CALLS : ph == 3 ? PM_V_CALLS : ph == 4 ? PM_O_CALLS : PM_OTHER_CALLS);
+    }
+  }
+  if (want != total) return IMIE_EARG;
+  return host_linear(hs, x, rows, fw, out);
+}
+
+// DP4A entries (nmc_qk_cuda.cu:1932, :2003): on gfx950 the same exact kernel serves every limb count, so these
+// return the apply_resident result after the reference's argument checks (Ln in [1, 8], matching qtype).
+int qk_apply_resident_q6k_dp4a(long long h, const int64_t* x, long long T, int fw, int Ln, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  const QKWeight* w = qk_get(h);
+  if (!w || w->qtype != 1 || Ln < 1 || Ln > 8) return IMIE_EARG;
+  return qk_apply_resident(h, x, T, fw, out);
+}
+int qk_apply_resident_q4k_dp4a(long long h, const int64_t* x, long long T, int fw, int Ln, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  const QKWeight* w = qk_get(h);
+  if (!w || w->qtype != 0 || Ln < 1 || Ln > 8) return IMIE_EARG;
+  return qk_apply_resident(h, x, T, fw, out);
+}
+
+// nmc_qk_cuda.cu:2203-2254 `qk_moe_ffn_batched` (qk_cuda.py:1073-1101): host h [m, d_model], gates [m*k],
+// handles flattened token-major; out [m, d_model]. rc 2 where the oracle's int64 conversions would raise.
+int qk_moe_ffn_batched(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                       const int64_t* h, const int64_t* gates, long long d_model, long long e_ffn, int fa, int fw,
+                       int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  prof(PM_MOE_BATCHED_CALLS);
+  if (!gate_h || !up_h || !down_h || !h || !gates || !out || m <= 0 || k <= 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const int64_t P = (int64_t)m * k;
+  if (g_mws.x.ensure((size_t)(m * d_model) * 8) || g_mws.gates.ensure((size_t)P * 8) ||
+      g_mws.out.ensure((size_t)(m * d_model) * 8) || g_mws.status.ensure(64))
+    return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(g_mws.x.p, h, (size_t)(m * d_model) * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(g_mws.gates.p, gates, (size_t)P * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemsetAsync(g_mws.status.p, 0, 4, st));
+  int rc = moe_batched(gate_h, up_h, down_h, m, k, (const int64_t*)g_mws.x.p, (const int64_t*)g_mws.gates.p,
+                       d_model, e_ffn, fa, fw, (int64_t*)g_mws.out.p, st);
+  if (rc) return rc;
+  int stat = 0;
+  if (read_status_and(st, &stat)) return IMIE_EARG;
+  if (stat) return IMIE_EOVF;
+  IMIE_HIP(hipMemcpy(out, g_mws.out.p, (size_t)(m * d_model) * 8, hipMemcpyDeviceToHost));
+  return IMIE_OK;
+}
+
+// Guarded-limb batched entry (nmc_qk_cuda.cu:2261): exact for every activation here, never rc 2 for the limb
+// envelope; overflow of the int64 results still returns 2 (the caller then runs the int128 entry, which agrees).
+int qk_moe_ffn_batched_dp4a(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                            const int64_t* h, const int64_t* gates, long long d_model, long long e_ffn, int fa, int fw,
+                            int64_t* out) {
+  prof(PM_MOE_BATCHED_DP4A_CALLS);
+  return qk_moe_ffn_batched(gate_h, up_h, down_h, m, k, h, gates, d_model, e_ffn, fa, fw, out);
+}
+
+// nmc_qk_cuda.cu:1816 `qk_moe_ffn` (qk_cuda.py:1104-1124): one token, n_e selected experts, out [d_model].
+int qk_moe_ffn(const long long* gate_h, const long long* up_h, const long long* down_h, int n_e, const int64_t* h,
+               const int64_t* gates, long long d_model, long long e_ffn, int fa, int fw, int64_t* out) {
+  prof(PM_MOE_CALLS);
+  return qk_moe_ffn_batched(gate_h, up_h, down_h, 1, n_e, h, gates, d_model, e_ffn, fa, fw, out);
+}
+int qk_moe_ffn_dp4a(const long long* gate_h, const long long* up_h, const long long* down_h, int n_e, const int64_t* h,
+                    const int64_t* gates, long long d_model, long long e_ffn, int fa, int fw, int64_t* out) {
+  return qk_moe_ffn(gate_h, up_h, down_h, n_e, h, gates, d_model, e_ffn, fa, fw, out);
+}
+
+// Device-pointer batched MoE (no reference counterpart): h_dev [m, d_model], gates_dev [m*k], out_dev [m, d_model];
+// status_dev receives bit 2 on an int64 envelope miss. Asynchronous on `stream`.
+int imie_moe_ffn_batched_dev(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                             const int64_t* h_dev, const int64_t* gates_dev, long long d_model, long long e_ffn,
+                             int fa, int fw, int64_t* out_dev, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!gate_h || !up_h || !down_h || !h_dev || !gates_dev || !out_dev) return IMIE_EARG;
+  if (g_mws.status.ensure(64)) return IMIE_EARG;
+  return moe_batched(gate_h, up_h, down_h, m, k, h_dev, gates_dev, d_model, e_ffn, fa, fw, out_dev,
+                     (hipStream_t)stream);
+}
+
+int imie_moe_status(int clear, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (g_mws.status.ensure(64)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  if (clear) return hipMemsetAsync(g_mws.status.p, 0, 4, st) == hipSuccess ? 0 : -1;
+  int stat = 0;
+  if (hipMemcpyAsync(&stat, g_mws.status.p, 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return -1;
+  return stat;
+}
+
+void qk_free_all(void) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  (void)hipDeviceSynchronize();
+  for (auto& w : g_qk) if (w.p) { (void)hipFree(w.p); prof(PM_FREE_CALLS); }
+  g_qk.clear();
+  g_qk_live = 0;
+}
+
+long long qk_resident_count(void) { return (long long)g_qk_live; }
+long long qk_resident_capacity(void) { return (long long)g_qk.capacity(); }
+long long qk_moe_workspace_allocations(void) { return 0; }
+unsigned long long qk_moe_workspace_bytes(void) {
+  return (unsigned long long)(g_mws.g.cap + g_mws.u.cap + g_mws.d.cap + g_mws.x.cap + g_mws.out.cap);
+}
+void qk_moe_workspace_release(void) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  (void)hipDeviceSynchronize();
+  g_mws.g.release(); g_mws.u.release(); g_mws.d.release(); g_mws.x.release(); g_mws.out.release();
+}
+
+void qk_profile_reset(void) { memset(g_prof, 0, sizeof(g_prof)); }
+void qk_profile_set_enabled(int enabled) { g_prof_on = enabled ? 1 : 0; }
+// Copies min(capacity, PM_COUNT) counters; returns the number of counters the library keeps.
+int qk_profile_snapshot(unsigned long long* out, int capacity) {
+  if (out) for (int i = 0; i < capacity && i < PM_COUNT; ++i) out[i] = g_prof[i];
+  return PM_COUNT;
+}
+
+}  // extern "C"
