@@ -267,6 +267,8 @@ __global__ void attn_final_kernel(AttnDesc d) {
     const RowInfo ri = row_info(d, r);
     const u128 pv = (u128)d.maxp[r] * d.maxv[ri.b * d.Hkv + ri.kv];
     if (pv > (u128)(INT64_MAX / ri.lv)) atomicOr(d.status, IMIE_EOVF);
+    const u128 qk = (u128)d.maxq[r] * d.maxk[ri.b * d.Hkv + ri.kv];
+    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
   }
 }
 
@@ -278,18 +280,208 @@ __global__ void attn_init_kernel(AttnDesc d) {
   if (i < d.B * d.Hkv) { d.maxk[i] = 0; d.maxv[i] = 0; }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Decode fast path (M == 1): one query per (b, head); the rep = H / Hkv heads of a KV group share every K/V read.
+//   D1 scores : wave = 4 keys x 16 lanes (8 dims per lane, coalesced 512 B rows), rep dots per key, 16-lane
+//               shuffle reduction; scores[(b,h)][j]; per-head max via atomicMax
+//   D2 exp    : thread per key: e_j = 2^-(...) for each head (stored in place), Z by wave sums + atomicAdd
+//   D3 PV     : WG per (b, kv, 256-key chunk): p_j = (e_j << f) / Z through a 2^64 / Z reciprocal with one
+//               correction step (exact for e_j << f < 2^40), staged in LDS; lanes split head_dim; int64 partial
+//               sums added into acc atomically
+//   final     : the shared attn_final_kernel
+// ---------------------------------------------------------------------------------------------------------
+constexpr int kDecChunk = 256;
+constexpr int kMaxRep = 8;
+
+__device__ inline int64_t page_off(const AttnDesc& d, int64_t b, int64_t kv, int64_t j) {
+  const int64_t pg = d.pt[b * d.mp + j / d.P];
+  return pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + (j % d.P) * d.hd;
+}
+
+template <typename KT, int REP>
+__global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
+  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
+  const int64_t j0 = (int64_t)blockIdx.y * kDecChunk;
+  if (j0 >= L) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane >> 4, l16 = lane & 15;          // key within the 4-key group, lane within the key
+  const bool dims = l16 * 8 < d.hd;
+  // this lane's 8 dims of the group's REP query rows
+  int64_t q[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const int64_t* qr = d.q + b * d.qsb + (kv * REP + r) * d.qsh;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) q[r][c] = dims ? qr[l16 * 8 + c] : 0;
+  }
+  if (blockIdx.y == 0 && wave == 0 && sub == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      uint64_t m = 0;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) { const uint64_t a = imie_absu64(q[r][c]); m = a > m ? a : m; }
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) { const uint64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
+      if (l16 == 0) d.maxq[b * d.H + kv * REP + r] = m;
+    }
+  }
+  int64_t smax[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) smax[r] = INT64_MIN;
+  uint64_t mk = 0;
+  const int64_t jend = min(j0 + kDecChunk, L);
+  for (int64_t jj = j0 + wave * 4; jj < jend; jj += 16) {
+    const int64_t j = jj + sub;
+    const bool live = j < jend;
+    int64_t kvv[8];
+    if (live && dims) {
+      const KT* kp = (const KT*)d.K + page_off(d, b, kv, j) + l16 * 8;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kvv[c] = (int64_t)kp[c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kvv[c] = 0;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) { const uint64_t a = imie_absu64(kvv[c]); mk = a > mk ? a : mk; }
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      uint64_t dot = 0;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dot += (uint64_t)q[r][c] * (uint64_t)kvv[c];
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) dot += (uint64_t)__shfl_xor((int64_t)dot, o, 64);
+      if (live) {
+        int64_t sc = (int64_t)dot >> d.frac;
+        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+        if (l16 == 0) d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] = sc;
+        smax[r] = sc > smax[r] ? sc : smax[r];
+      }
+    }
+  }
+  mk = imie_wave_max_u64(mk);
+  if (lane == 0) amax_u64(&d.maxk[bkv], mk);
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    int64_t m = smax[r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
+    if (lane == 0 && m != INT64_MIN) amax_i64(&d.rowmax[b * d.H + kv * REP + r], m);
+  }
+}
+
+__global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
+  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int rep = (int)(d.H / d.Hkv);
+  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
+  const int64_t j = (int64_t)blockIdx.y * kDecChunk + threadIdx.x;
+  if ((int64_t)blockIdx.y * kDecChunk >= L) return;
+  const int lane = threadIdx.x & 63;
+  for (int r = 0; r < rep; ++r) {
+    const int64_t row = b * d.H + kv * rep + r;
+    uint64_t e = 0;
+    if (j < L) {
+      int64_t dd = (int64_t)((uint64_t)d.rowmax[row] - (uint64_t)d.scores[row * d.Lmax + j]);
+      if (dd > d.dclip) dd = d.dclip;
+      e = (uint64_t)exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+      d.scores[row * d.Lmax + j] = (int64_t)e;
+    }
+    uint64_t z = e;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
+    if (lane == 0 && z) atomicAdd((unsigned long long*)&d.acc[d.B * d.H * d.M * d.hd + row], (unsigned long long)z);
+  }
+}
+
+template <typename KT>
+__global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
+  __shared__ int64_t sp[kMaxRep][kDecChunk];
+  __shared__ uint64_t red[4][kMaxRep][128];
+  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int rep = (int)(d.H / d.Hkv);
+  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
+  const int64_t j0 = (int64_t)blockIdx.y * kDecChunk;
+  if (j0 >= L) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t* Zs = d.acc + d.B * d.H * d.M * d.hd;
+  // p for this chunk (exact floor((e << f) / Z) via reciprocal + one correction), max|p| per head
+  for (int r = 0; r < rep; ++r) {
+    const int64_t row = b * d.H + kv * rep + r;
+    const uint64_t Z = Zs[row];
+    const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
+    const int64_t j = j0 + tid;
+    int64_t p = 0;
+    if (j < L && Z != 0) {
+      const uint64_t num = (uint64_t)d.scores[row * d.Lmax + j] << d.frac;
+      if (Z == 1) p = (int64_t)num;
+      else {
+        uint64_t qq = __umul64hi(num, rz);
+        if (num - qq * Z >= Z) ++qq;
+        p = (int64_t)qq;
+      }
+    }
+    sp[r][tid] = p;
+    uint64_t m = (uint64_t)p;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const uint64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
+    if (lane == 0 && m) amax_u64(&d.maxp[row], m);
+  }
+  __syncthreads();
+  // PV: wave w takes keys j0 + w, w + 4, ...; lane covers dims 2*lane, 2*lane+1
+  uint64_t acc[kMaxRep][2];
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) acc[r][0] = acc[r][1] = 0;
+  uint64_t mv = 0;
+  const int c0 = 2 * lane;
+  for (int i = wave; i < kDecChunk && j0 + i < L; i += 4) {
+    const int64_t j = j0 + i;
+    const KT* vp = (const KT*)d.V + page_off(d, b, kv, j);
+    const int64_t v0 = c0 < d.hd ? (int64_t)vp[c0] : 0, v1 = c0 + 1 < d.hd ? (int64_t)vp[c0 + 1] : 0;
+    const uint64_t a0 = imie_absu64(v0), a1 = imie_absu64(v1);
+    mv = a0 > mv ? a0 : mv;
+    mv = a1 > mv ? a1 : mv;
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r >= rep) break;
+      const uint64_t pp = (uint64_t)sp[r][i];
+      acc[r][0] += pp * (uint64_t)v0;
+      acc[r][1] += pp * (uint64_t)v1;
+    }
+  }
+  mv = imie_wave_max_u64(mv);
+  if (lane == 0) amax_u64(&d.maxv[bkv], mv);
+  for (int r = 0; r < rep; ++r) {
+    if (c0 < 128) { red[wave][r][c0] = acc[r][0]; if (c0 + 1 < 128) red[wave][r][c0 + 1] = acc[r][1]; }
+  }
+  __syncthreads();
+  for (int i = tid; i < rep * d.hd; i += blockDim.x) {
+    const int r = i / (int)d.hd, c = i % (int)d.hd;
+    const uint64_t v = red[0][r][c] + red[1][r][c] + red[2][r][c] + red[3][r][c];
+    if (v) atomicAdd((unsigned long long*)&d.acc[(b * d.H + kv * rep + r) * d.hd + c], (unsigned long long)v);
+  }
+}
+
+__global__ void dec_init_kernel(AttnDesc d) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t rows = d.B * d.H;
+  if (i < rows * d.hd + rows) d.acc[i] = 0;          // PV accumulators then the Z sums
+  if (i < rows) { d.rowmax[i] = INT64_MIN; d.maxp[i] = 0; }
+  if (i < d.B * d.Hkv) { d.maxk[i] = 0; d.maxv[i] = 0; }
+}
+
 }  // namespace
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax) {
   const int64_t rows = B * H * M;
-  return (size_t)(rows * Lmax + rows * hd + 3 * rows + 2 * B * Hkv) * 8 + 256;
+  return (size_t)(rows * Lmax + rows * hd + rows + 3 * rows + 2 * B * Hkv) * 8 + 256;
 }
 
 void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
   const int64_t rows = d.B * d.H * d.M;
   int64_t* p = (int64_t*)scratch;
   d.scores = p;            p += rows * d.Lmax;
-  d.acc = (uint64_t*)p;    p += rows * d.hd;
+  d.acc = (uint64_t*)p;    p += rows * d.hd + rows;   // + Z sums of the decode path
   d.rowmax = p;            p += rows;
   d.maxq = (uint64_t*)p;   p += rows;
   d.maxp = (uint64_t*)p;   p += rows;
@@ -309,6 +501,33 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
   const int64_t nkt = (d.Lmax + kKeyTile - 1) / kKeyTile;
   const int64_t ninit = rows * d.hd > d.B * d.Hkv ? rows * d.hd : d.B * d.Hkv;
   imie_prof_mark(IMIE_K_ATTN, st, true);
+  const int64_t rp = d.H / d.Hkv;
+  if (d.M == 1 && (rp == 1 || rp == 2 || rp == 4 || rp == 8) && d.hd <= 128) {
+    const int64_t nch = (d.Lmax + kDecChunk - 1) / kDecChunk;
+    const dim3 gd((unsigned)(d.B * d.Hkv), (unsigned)nch);
+    const int64_t ni = rows * d.hd + rows;
+    hipLaunchKernelGGL(dec_init_kernel, dim3((unsigned)((ni + 255) / 256)), dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    const int rep = (int)(d.H / d.Hkv);
+#define IMIE_DEC_SCORES(KT_, R_) hipLaunchKernelGGL((dec_scores_kernel<KT_, R_>), gd, dim3(256), 0, st, d)
+#define IMIE_DEC_SCORES_R(KT_)                                                                             \
+    if (rep == 1) IMIE_DEC_SCORES(KT_, 1); else if (rep == 2) IMIE_DEC_SCORES(KT_, 2);                     \
+    else if (rep <= 4 && rep % 4 == 0) IMIE_DEC_SCORES(KT_, 4); else IMIE_DEC_SCORES(KT_, 8)
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return IMIE_EARG;
+    if (d.kv32) { IMIE_DEC_SCORES_R(int32_t); } else { IMIE_DEC_SCORES_R(int64_t); }
+#undef IMIE_DEC_SCORES_R
+#undef IMIE_DEC_SCORES
+    IMIE_HIP(hipGetLastError());
+    hipLaunchKernelGGL(dec_exp_kernel, gd, dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    if (d.kv32) hipLaunchKernelGGL(dec_pv_kernel<int32_t>, gd, dim3(256), 0, st, d);
+    else hipLaunchKernelGGL(dec_pv_kernel<int64_t>, gd, dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_final_kernel, dim3((unsigned)((rows * d.hd + 255) / 256)), dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    imie_prof_mark(IMIE_K_ATTN, st, false);
+    return IMIE_OK;
+  }
   hipLaunchKernelGGL(attn_init_kernel, dim3((unsigned)((ninit + 255) / 256)), dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());
   const dim3 g2((unsigned)(d.B * d.Hkv * nrt), (unsigned)nkt);
