@@ -90,3 +90,30 @@ def test_moe_grouped_equals_per_token_and_c_linear():
     rawc = {e: {n: (r[n], *shapes[n]) for n in r} for e, r in raws.items()}
     lin = lambda x, w, fw: c_oracle.qk_linear(w[0], x, w[1], w[2], fw, w[3])
     assert np.array_equal(qk.moe_ffn_grouped(h, sel, gates, rawc, 16, 24, lin), ref)
+
+
+def test_moe_composition_tracks_float_math():
+    """The integer MoE equals the real-valued formula sum_j g_j * down(silu(gate h) * up h) within fixed-point
+    rounding (the reference gates its MoE the same way: int vs float, north-mini-code/tests/test_cohere2_moe.py:
+    44-51, rel < 5e-3). A dropped term, a sign error or a transposed weight fails by orders of magnitude."""
+    E, k, d, e_ffn, T, fa, fw = 5, 2, 256, 256, 4, 16, 24
+    raws = {e: dict(gate=qk.random_blocks(2, 200 + 3 * e, e_ffn, 1, 0), up=qk.random_blocks(2, 201 + 3 * e, e_ffn, 1, 0),
+                    down=qk.random_blocks(2, 202 + 3 * e, d, 1, 1)) for e in range(E)}
+    deq = {e: {n: qk.dequant(r[n], e_ffn if n != "down" else d, 1, 0 if n != "down" else 1, fw) for n in r}
+           for e, r in raws.items()}
+    rng = np.random.default_rng(3)
+    h = rng.integers(-(1 << 19), 1 << 19, size=(T, d), dtype=np.int64)
+    logits = rng.integers(-(1 << 17), 1 << 17, size=(T, E), dtype=np.int64)
+    sel, gates = qk.moe_route(logits, k, fa)
+    got = qk.moe_ffn(h, sel, gates, deq, fa, fw).astype(np.float64) / 2.0 ** fa
+    hf = h.astype(np.float64) / 2.0 ** fa
+    want = np.zeros((T, d))
+    for t in range(T):
+        for j, e in enumerate(sel[t]):
+            W = {n: deq[int(e)][n].astype(np.float64) / 2.0 ** fw for n in ("gate", "up", "down")}
+            g, u = W["gate"] @ hf[t], W["up"] @ hf[t]
+            a = g / (1.0 + np.exp(-g)) * u
+            gate = 1.0 / (1.0 + np.exp(-logits[t, e] / 2.0 ** fa))
+            want[t] += gate * (W["down"] @ a)
+    rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
+    assert rel < 5e-3, rel
