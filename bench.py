@@ -13,6 +13,7 @@ oracle/_ref, timed on this host's cores on a bounded sample).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import subprocess
@@ -73,6 +74,93 @@ def cpu_worker(npz: str, seconds: float) -> None:
     print(json.dumps({"value": gbs, "unit": "GB/s", "kind": kind, "calls": n, "seconds": el, "match": match}))
 
 
+def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, vocab: int = 151936) -> dict:
+    """Bonsai-8B-shape greedy decode at batch 1: embed -> 36 layers over a paged int32 KV cache holding ``ctx``
+    positions -> final RMSNorm + Q1_0 LM head (151936x4096) -> lowest-index argmax -> next embed, all on device.
+
+    Weights are seeded random Q1_0 of the 8B shapes; the 36 layers are 36 separately resident copies of one
+    random layer (the HBM traffic per token is that of 36 distinct layers). The timed loop is ``tokens`` decode
+    steps back to back on one stream with no host synchronisation. Byte-exactness of this path against the
+    oracle is what tests/test_gpu_decode_8b.py checks."""
+    from integer_inference_engine_amd import gpu_native as gn
+    from integer_inference_engine_amd.resident import ResidentNet
+    from integer_inference_engine_amd.rope_tables import bonsai8b_tables
+    d, H, Hkv, hd, dff = 4096, 32, 8, 128, 12288
+    rng = np.random.default_rng(8)
+    shapes = {"wq": (H * hd, d), "wk": (Hkv * hd, d), "wv": (Hkv * hd, d), "wo": (d, H * hd),
+              "w1": (dff, d), "wu": (dff, d), "w2": (d, dff)}
+    layer = {k: (rng.integers(0, 256, size=(o, i // 128, 16), dtype=np.uint8),
+                 rng.integers(1, 4097, size=(o, i // 128), dtype=np.int64)) for k, (o, i) in shapes.items()}
+    gains = {k: rng.integers(1 << 15, (1 << 17) + 1, size=(n,), dtype=np.int64)
+             for k, n in (("n1g", d), ("n2g", d), ("qng", hd), ("kng", hd))}
+    w = {k: np.array([gn.q1_register_weight(*layer[k]) for _ in range(n_layers)], dtype=np.int64) for k in shapes}
+    g = {k: np.array([gn.buf_upload_i64(v) for _ in range(n_layers)], dtype=np.int64) for k, v in gains.items()}
+    assert all((v >= 0).all() for v in list(w.values()) + list(g.values())), _lib_err()
+    hbits = rng.integers(0, 256, size=(vocab, d // 128, 16), dtype=np.uint8)
+    hscale = rng.integers(1, 4097, size=(vocab, d // 128), dtype=np.int64)
+    w["out_head"], w["out_head_vocab"] = gn.q1_register_weight(hbits, hscale), vocab
+    g["finalg"] = gn.buf_upload_i64(rng.integers(1 << 15, (1 << 17) + 1, size=(d,), dtype=np.int64))
+    cap = ctx + max(64, tokens)
+    cos, sin = bonsai8b_tables(cap)
+    g["cos_h"], g["sin_h"] = gn.buf_upload_i64(cos), gn.buf_upload_i64(sin)
+    net = ResidentNet(B=1, n_layers=n_layers, H=H, Hkv=Hkv, hd=hd, d=d, dff=dff, cap=cap, w=w, g=g, page=64,
+                      kv32=True)
+    k1 = rng.integers(-(1 << 20), 1 << 20, size=(Hkv, ctx, hd), dtype=np.int64)
+    v1 = rng.integers(-(1 << 20), 1 << 20, size=(Hkv, ctx, hd), dtype=np.int64)
+    net.seed(0, np.broadcast_to(k1, (n_layers,) + k1.shape), np.broadcast_to(v1, (n_layers,) + v1.shape))
+    del k1, v1
+    ebits = torch.from_numpy(hbits).cuda()
+    escale = torch.from_numpy(hscale).cuda()
+    ids = torch.tensor([7], dtype=torch.int64, device="cuda")
+    x = torch.empty((1, d), dtype=torch.int64, device="cuda")
+    logits = torch.empty((1, vocab), dtype=torch.int64, device="cuda")
+    sp = ctypes.c_void_p(net.stream.cuda_stream)
+    out_ids = []
+
+    def token(pos):
+        assert so.imie_embed_dev(ctypes.c_void_p(ebits.data_ptr()), ctypes.c_void_p(escale.data_ptr()), d // 128,
+                                 ctypes.c_void_p(ids.data_ptr()), 1, ctypes.c_void_p(x.data_ptr()), sp) == 0
+        st = np.array([pos], dtype=np.int64)
+        assert so.imie_net_forward_dev(net.h, ctypes.c_void_p(x.data_ptr()), st.ctypes.data, 1, sp) == 0
+        assert so.imie_net_head_dev(net.h, ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(logits.data_ptr()),
+                                    ctypes.c_void_p(ids.data_ptr()), sp) == 0
+
+    so.imie_net_status(net.h, 1, sp)
+    token(ctx)                                   # warm-up token (not timed)
+    net.stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    so.imie_profile_begin()
+    e0.record(net.stream)
+    t0 = time.perf_counter()
+    for i in range(tokens):
+        token(ctx + 1 + i)
+    e1.record(net.stream)
+    t_host = time.perf_counter() - t0
+    net.stream.synchronize()
+    ms = e0.elapsed_time(e1)
+    prof = {}
+    for kid, name in ((0, "q1_prep"), (1, "q1_gemv"), (3, "attention")):
+        kms, kcnt = ctypes.c_double(), ctypes.c_int64()
+        so.imie_profile_read(kid, ctypes.byref(kms), ctypes.byref(kcnt))
+        prof[name + "_ms_per_token"] = round(kms.value / tokens, 4)
+    so.imie_profile_end()
+    status = int(so.imie_net_status(net.h, 0, sp))
+    last = int(ids.item())
+    net.close()
+    wbytes = sum(o * (i // 128) * (16 + 4) for o, i in shapes.values()) * n_layers + vocab * (d // 128) * 20
+    kvbytes = n_layers * 2 * Hkv * ctx * hd * 4
+    return {"tok_s": round(tokens / (ms / 1e3), 2), "ms_per_token": round(ms / tokens, 3),
+            "host_enqueue_ms_per_token": round(t_host * 1e3 / tokens, 3), "tokens": tokens, "context": ctx,
+            "layers": n_layers, "vocab": vocab, "kv": "int32 paged (64-token pages)", "status": status,
+            "last_token": last, "weight_plus_kv_GB_per_token": round((wbytes + kvbytes) / 1e9, 3),
+            "effective_GB_s": round((wbytes + kvbytes) / (ms / tokens / 1e3) / 1e9, 1), **prof}
+
+
+def _lib_err():
+    from integer_inference_engine_amd import _lib
+    return _lib.last_error()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,7 +169,10 @@ def main() -> int:
     ap.add_argument("--replicas", type=int, default=384)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-tokens", type=int, default=32, help="8B-shape b=1 decode leg (0 = skip)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     args = ap.parse_args()
     if args.cpu_worker:
         cpu_worker(args.cpu_worker, args.cpu_seconds)
@@ -94,6 +185,14 @@ def main() -> int:
     import ctypes
     import torch
     from integer_inference_engine_amd import _lib
+    if args.copy_calibration:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 1 << 30, "launches": 3}))
+        return 0
     so = _lib.lib()
     assert _lib.device_available(), "no usable gfx950 device"
     R = args.replicas
@@ -173,6 +272,13 @@ def main() -> int:
             else:
                 print(r.stderr[-2000:], file=sys.stderr)
 
+    dec = None
+    if args.decode_tokens > 0:
+        del bits, scale
+        so.bonsai_q1_free_weights()
+        print("[bench] 8B-shape decode leg", file=sys.stderr, flush=True)
+        dec = decode_leg(so, torch, args.decode_tokens)
+
     line = {
         "metric": "Q1 matvec HBM GB/s (% of peak); 8B-shape decode tok/s b=1; byte-exact",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -188,6 +294,7 @@ def main() -> int:
                      "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,
+        "decode_8b_b1": dec,
     }
     print(json.dumps(line))
     return 0
