@@ -127,6 +127,12 @@ int imie_net_head_dev(int64_t ctx, const int64_t *x_dev, int64_t rows, int64_t *
                       void *stream);
 int imie_net_status(int64_t ctx, int clear, void *stream);
 int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int64_t *k_out, int64_t *v_out);
+/* Greedy decode of `steps` tokens on the device: embed -> all layers -> final norm + LM head -> lowest-index
+ * argmax, per step (the host-driven loop of reference_bonsai.py:1200-1310 moved onto the GPU; no single
+ * reference entry point). ids_dev (B) in/out, logits_dev (B, vocab) = last step's logits, hist_dev (steps, B)
+ * optional; use_graph replays a captured HIP graph of one step after the first. */
+int imie_net_decode_dev(int64_t ctx, const uint8_t *ebits, const int64_t *escale, int64_t *ids_dev,
+                        int64_t *logits_dev, int64_t *hist_dev, int64_t steps, int use_graph, void *stream);
 /* Q1 embedding rows sign*scale (reference_bonsai.py:138-146) from device tables. */
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);

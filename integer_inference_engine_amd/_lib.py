@@ -66,6 +66,8 @@ SIGNATURES = {
     "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),
     "imie_net_export_kv": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_embed_dev": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "imie_net_decode_dev": (c_int, [c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int,
+                                    c_void_p]),
     # north-mini-code Q4_K / Q6_K (include/imie_nmc.h)
     "qk_cuda_abi_version": (c_int, []),
     "qk_cuda_available": (c_int, []),

@@ -282,15 +282,19 @@ __global__ void attn_init_kernel(AttnDesc d) {
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode fast path (M == 1): one query per (b, head); the rep = H / Hkv heads of a KV group share every K/V read.
-//   D1 scores : wave = 4 keys x 16 lanes (8 dims per lane, coalesced 512 B rows), rep dots per key, 16-lane
-//               shuffle reduction; scores[(b,h)][j]; per-head max via atomicMax
-//   D2 exp    : thread per key: e_j = 2^-(...) for each head (stored in place), Z by wave sums + atomicAdd
-//   D3 PV     : WG per (b, kv, 256-key chunk): p_j = (e_j << f) / Z through a 2^64 / Z reciprocal with one
-//               correction step (exact for e_j << f < 2^40), staged in LDS; lanes split head_dim; int64 partial
-//               sums added into acc atomically
-//   final     : the shared attn_final_kernel
+// The keys of each (b, kv) are split into nch chunks of `chunk` keys (a multiple of 64, sized so the grid has
+// ~2048 workgroups); grid = (B * Hkv, nch). Every cross-chunk quantity (row max, Z, max|K|, max|V|, max|p|, the
+// PV sums) is written per chunk and reduced by its consumer: no same-address atomics, which serialize across
+// the XCDs' L2 slices.
+//   D1 scores : wave = 4 keys x 16 lanes (8 dims per lane, 32 B vector loads), rep dots per key, 16-lane shuffle
+//               reduction; scores[(b,h)][j]; chunk max per head -> cmax[chunk][row], chunk max|K| -> ckm
+//   D2 exp    : row max = max over cmax; e_j = 2^-(...) stored in place; chunk Z -> cz[chunk][row]
+//   D3 PV     : Z = sum over cz; per 256-key tile p_j = (e_j << f) / Z through a 2^64 / Z reciprocal with a
+//               correction loop (exact for every e_j << f < 2^64), staged in LDS; a wave covers 2 keys per step
+//               (32 lanes x 4 dims); chunk PV sums -> part[chunk][row][dim], chunk max|p| / max|V| -> cmp / cvm
+//   D4 final  : out = (sum over chunks of part) >> f, plus the bound checks from the chunk maxima
 // ---------------------------------------------------------------------------------------------------------
-constexpr int kDecChunk = 256;
+constexpr int kDecTile = 256;
 constexpr int kMaxRep = 8;
 
 __device__ inline int64_t page_off(const AttnDesc& d, int64_t b, int64_t kv, int64_t j) {
@@ -298,16 +302,45 @@ __device__ inline int64_t page_off(const AttnDesc& d, int64_t b, int64_t kv, int
   return pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + (j % d.P) * d.hd;
 }
 
+__device__ inline int64_t dec_len(const AttnDesc& d, int64_t b) { return d.starts ? d.starts[b] + 1 : d.lengths[b]; }
+
+// 8 consecutive KV elements as int64 (two 16 B loads for int32, four for int64); p is 32 B aligned
+template <typename KT>
+__device__ inline void load8(const KT* p, int64_t v[8]);
+template <>
+__device__ inline void load8<int32_t>(const int32_t* p, int64_t v[8]) {
+  const v4i a = ((const v4i*)p)[0], b = ((const v4i*)p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <>
+__device__ inline void load8<int64_t>(const int64_t* p, int64_t v[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) v[c] = p[c];
+}
+template <typename KT>
+__device__ inline void load4(const KT* p, int64_t v[4]);
+template <>
+__device__ inline void load4<int32_t>(const int32_t* p, int64_t v[4]) {
+  const v4i w = *(const v4i*)p;
+  v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+}
+template <>
+__device__ inline void load4<int64_t>(const int64_t* p, int64_t v[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) v[c] = p[c];
+}
+
 template <typename KT, int REP>
 __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
+  __shared__ int64_t s_max[4][REP];
+  __shared__ uint64_t s_mk[4];
   const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
-  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
-  const int64_t j0 = (int64_t)blockIdx.y * kDecChunk;
-  if (j0 >= L) return;
+  const int64_t rows = d.B * d.H;
+  const int64_t L = dec_len(d, b);
+  const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane >> 4, l16 = lane & 15;          // key within the 4-key group, lane within the key
   const bool dims = l16 * 8 < d.hd;
-  // this lane's 8 dims of the group's REP query rows
   int64_t q[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
@@ -330,19 +363,12 @@ __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
 #pragma unroll
   for (int r = 0; r < REP; ++r) smax[r] = INT64_MIN;
   uint64_t mk = 0;
-  const int64_t jend = min(j0 + kDecChunk, L);
+  const int64_t jend = min(j0 + d.chunk, L);
   for (int64_t jj = j0 + wave * 4; jj < jend; jj += 16) {
     const int64_t j = jj + sub;
     const bool live = j < jend;
-    int64_t kvv[8];
-    if (live && dims) {
-      const KT* kp = (const KT*)d.K + page_off(d, b, kv, j) + l16 * 8;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) kvv[c] = (int64_t)kp[c];
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) kvv[c] = 0;
-    }
+    int64_t kvv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (live && dims) load8<KT>((const KT*)d.K + page_off(d, b, kv, j) + l16 * 8, kvv);
 #pragma unroll
     for (int c = 0; c < 8; ++c) { const uint64_t a = imie_absu64(kvv[c]); mk = a > mk ? a : mk; }
 #pragma unroll
@@ -361,120 +387,249 @@ __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
     }
   }
   mk = imie_wave_max_u64(mk);
-  if (lane == 0) amax_u64(&d.maxk[bkv], mk);
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     int64_t m = smax[r];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) { const int64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
-    if (lane == 0 && m != INT64_MIN) amax_i64(&d.rowmax[b * d.H + kv * REP + r], m);
+    smax[r] = m;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) s_max[wave][r] = smax[r];
+    s_mk[wave] = mk;
+  }
+  __syncthreads();
+  if (threadIdx.x < REP) {
+    const int r = threadIdx.x;
+    int64_t m = s_max[0][r];
+    for (int w = 1; w < 4; ++w) m = s_max[w][r] > m ? s_max[w][r] : m;
+    d.cmax[blockIdx.y * rows + b * d.H + kv * REP + r] = m;          // INT64_MIN for an empty chunk
+  }
+  if (threadIdx.x == 0) {
+    uint64_t m = s_mk[0];
+    for (int w = 1; w < 4; ++w) m = s_mk[w] > m ? s_mk[w] : m;
+    d.ckm[blockIdx.y * d.B * d.Hkv + bkv] = m;
   }
 }
 
+template <int REP>
 __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
+  __shared__ int64_t s_rmax[REP];
+  __shared__ uint64_t s_z[4][REP];
   const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
-  const int rep = (int)(d.H / d.Hkv);
-  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
-  const int64_t j = (int64_t)blockIdx.y * kDecChunk + threadIdx.x;
-  if ((int64_t)blockIdx.y * kDecChunk >= L) return;
-  const int lane = threadIdx.x & 63;
-  for (int r = 0; r < rep; ++r) {
-    const int64_t row = b * d.H + kv * rep + r;
-    uint64_t e = 0;
-    if (j < L) {
-      int64_t dd = (int64_t)((uint64_t)d.rowmax[row] - (uint64_t)d.scores[row * d.Lmax + j]);
-      if (dd > d.dclip) dd = d.dclip;
-      e = (uint64_t)exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
-      d.scores[row * d.Lmax + j] = (int64_t)e;
+  const int64_t rows = d.B * d.H;
+  const int64_t L = dec_len(d, b);
+  const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (j0 >= L) {
+    if (threadIdx.x < REP) d.cz[blockIdx.y * rows + b * d.H + kv * REP + threadIdx.x] = 0;
+    return;
+  }
+  // row max over the chunks that hold keys (wave r reduces row r)
+  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  for (int r = wave; r < REP; r += 4) {
+    int64_t m = INT64_MIN;
+    for (int64_t c = lane; c < nlive; c += 64) {
+      const int64_t v = d.cmax[c * rows + b * d.H + kv * REP + r];
+      m = v > m ? v : m;
     }
-    uint64_t z = e;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
+    if (lane == 0) s_rmax[r] = m;
+  }
+  __syncthreads();
+  const int64_t jend = min(j0 + d.chunk, L);
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const int64_t row = b * d.H + kv * REP + r;
+    const int64_t mx = s_rmax[r];
+    uint64_t z = 0;
+    for (int64_t j = j0 + threadIdx.x; j < jend; j += blockDim.x) {
+      int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)d.scores[row * d.Lmax + j]);
+      if (dd > d.dclip) dd = d.dclip;
+      const uint64_t e = (uint64_t)exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+      d.scores[row * d.Lmax + j] = (int64_t)e;
+      z += e;
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
-    if (lane == 0 && z) atomicAdd((unsigned long long*)&d.acc[d.B * d.H * d.M * d.hd + row], (unsigned long long)z);
+    if (lane == 0) s_z[wave][r] = z;
+  }
+  __syncthreads();
+  if (threadIdx.x < REP) {
+    const int r = threadIdx.x;
+    d.cz[blockIdx.y * rows + b * d.H + kv * REP + r] = s_z[0][r] + s_z[1][r] + s_z[2][r] + s_z[3][r];
   }
 }
 
-template <typename KT>
+template <typename KT, int REP>
 __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
-  __shared__ int64_t sp[kMaxRep][kDecChunk];
-  __shared__ uint64_t red[4][kMaxRep][128];
+  __shared__ int64_t sp[REP][kDecTile];
+  __shared__ uint64_t red[4][REP][128];
+  __shared__ uint64_t s_z[REP], s_mp[4][REP], s_mv[4];
   const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
-  const int rep = (int)(d.H / d.Hkv);
-  const int64_t L = d.starts ? d.starts[b] + 1 : d.lengths[b];
-  const int64_t j0 = (int64_t)blockIdx.y * kDecChunk;
-  if (j0 >= L) return;
+  const int64_t L = dec_len(d, b);
+  const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint64_t* Zs = d.acc + d.B * d.H * d.M * d.hd;
-  // p for this chunk (exact floor((e << f) / Z) via reciprocal + one correction), max|p| per head
-  for (int r = 0; r < rep; ++r) {
-    const int64_t row = b * d.H + kv * rep + r;
-    const uint64_t Z = Zs[row];
-    const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
-    const int64_t j = j0 + tid;
-    int64_t p = 0;
-    if (j < L && Z != 0) {
-      const uint64_t num = (uint64_t)d.scores[row * d.Lmax + j] << d.frac;
-      if (Z == 1) p = (int64_t)num;
-      else {
-        uint64_t qq = __umul64hi(num, rz);
-        if (num - qq * Z >= Z) ++qq;
-        p = (int64_t)qq;
+  const int half = lane >> 5, c0 = (lane & 31) * 4;     // key parity within the wave step, first dim
+  const bool dims = c0 < d.hd;
+  const int64_t rows = d.B * d.H;
+  uint64_t* part = d.part + (int64_t)blockIdx.y * rows * d.hd;
+  if (j0 >= L) {                                      // an empty chunk still owns its partial slots
+    for (int i = tid; i < REP * d.hd; i += blockDim.x)
+      part[(b * d.H + kv * REP + i / d.hd) * d.hd + i % d.hd] = 0;
+    if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
+    if (tid == 0) d.cvm[blockIdx.y * d.B * d.Hkv + bkv] = 0;
+    return;
+  }
+  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  for (int r = wave; r < REP; r += 4) {
+    uint64_t z = 0;
+    for (int64_t c = lane; c < nlive; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
+    if (lane == 0) s_z[r] = z;
+  }
+  __syncthreads();
+  const int64_t jend = min(j0 + d.chunk, L);
+  uint64_t Z[REP], rz[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    Z[r] = s_z[r];
+    rz[r] = Z[r] > 1 ? (~(uint64_t)0) / Z[r] : 0;
+  }
+  uint64_t acc[REP][4];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0;
+  uint64_t mp[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) mp[r] = 0;
+  uint64_t mv = 0;
+  for (int64_t t0 = j0; t0 < jend; t0 += kDecTile) {
+    const int64_t tn = min((int64_t)kDecTile, jend - t0);
+    __syncthreads();                                  // previous tile's sp fully consumed
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const int64_t row = b * d.H + kv * REP + r;
+      int64_t p = 0;
+      if (tid < tn && Z[r] != 0) {
+        const uint64_t num = (uint64_t)d.scores[row * d.Lmax + t0 + tid] << d.frac;
+        if (Z[r] == 1) p = (int64_t)num;
+        else {
+          uint64_t qq = __umul64hi(num, rz[r]);
+          uint64_t rem = num - qq * Z[r];
+          while (rem >= Z[r]) { ++qq; rem -= Z[r]; }
+          p = (int64_t)qq;
+        }
+      }
+      sp[r][tid] = p;
+      mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
+    }
+    __syncthreads();
+    for (int i = 2 * wave + half; i < tn; i += 8) {
+      int64_t v[4] = {0, 0, 0, 0};
+      if (dims) load4<KT>((const KT*)d.V + page_off(d, b, kv, t0 + i) + c0, v);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) { const uint64_t a = imie_absu64(v[c]); mv = a > mv ? a : mv; }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const uint64_t pp = (uint64_t)sp[r][i];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] += pp * (uint64_t)v[c];
       }
     }
-    sp[r][tid] = p;
-    uint64_t m = (uint64_t)p;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) { const uint64_t w = __shfl_xor(m, o, 64); m = w > m ? w : m; }
-    if (lane == 0 && m) amax_u64(&d.maxp[row], m);
   }
-  __syncthreads();
-  // PV: wave w takes keys j0 + w, w + 4, ...; lane covers dims 2*lane, 2*lane+1
-  uint64_t acc[kMaxRep][2];
 #pragma unroll
-  for (int r = 0; r < kMaxRep; ++r) acc[r][0] = acc[r][1] = 0;
-  uint64_t mv = 0;
-  const int c0 = 2 * lane;
-  for (int i = wave; i < kDecChunk && j0 + i < L; i += 4) {
-    const int64_t j = j0 + i;
-    const KT* vp = (const KT*)d.V + page_off(d, b, kv, j);
-    const int64_t v0 = c0 < d.hd ? (int64_t)vp[c0] : 0, v1 = c0 + 1 < d.hd ? (int64_t)vp[c0 + 1] : 0;
-    const uint64_t a0 = imie_absu64(v0), a1 = imie_absu64(v1);
-    mv = a0 > mv ? a0 : mv;
-    mv = a1 > mv ? a1 : mv;
-#pragma unroll
-    for (int r = 0; r < kMaxRep; ++r) {
-      if (r >= rep) break;
-      const uint64_t pp = (uint64_t)sp[r][i];
-      acc[r][0] += pp * (uint64_t)v0;
-      acc[r][1] += pp * (uint64_t)v1;
-    }
+  for (int r = 0; r < REP; ++r) {
+    const uint64_t m = imie_wave_max_u64(mp[r]);
+    if (lane == 0) s_mp[wave][r] = m;
   }
   mv = imie_wave_max_u64(mv);
-  if (lane == 0) amax_u64(&d.maxv[bkv], mv);
-  for (int r = 0; r < rep; ++r) {
-    if (c0 < 128) { red[wave][r][c0] = acc[r][0]; if (c0 + 1 < 128) red[wave][r][c0 + 1] = acc[r][1]; }
+  if (lane == 0) s_mv[wave] = mv;
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[r][c] += (uint64_t)__shfl_xor((int64_t)acc[r][c], 32, 64);
+  if (half == 0 && dims) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[wave][r][c0 + c] = acc[r][c];
   }
   __syncthreads();
-  for (int i = tid; i < rep * d.hd; i += blockDim.x) {
+  for (int i = tid; i < REP * d.hd; i += blockDim.x) {
     const int r = i / (int)d.hd, c = i % (int)d.hd;
-    const uint64_t v = red[0][r][c] + red[1][r][c] + red[2][r][c] + red[3][r][c];
-    if (v) atomicAdd((unsigned long long*)&d.acc[(b * d.H + kv * rep + r) * d.hd + c], (unsigned long long)v);
+    part[(b * d.H + kv * REP + r) * d.hd + c] = red[0][r][c] + red[1][r][c] + red[2][r][c] + red[3][r][c];
+  }
+  if (tid < REP) {
+    uint64_t m = s_mp[0][tid];
+    for (int w = 1; w < 4; ++w) m = s_mp[w][tid] > m ? s_mp[w][tid] : m;
+    d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = m;
+  }
+  if (tid == 0) {
+    uint64_t m = s_mv[0];
+    for (int w = 1; w < 4; ++w) m = s_mv[w] > m ? s_mv[w] : m;
+    d.cvm[blockIdx.y * d.B * d.Hkv + bkv] = m;
   }
 }
 
-__global__ void dec_init_kernel(AttnDesc d) {
+// thread per (row, dim): sums the chunk partials (8 independent accumulators for load ILP)
+__global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t rows = d.B * d.H;
-  if (i < rows * d.hd + rows) d.acc[i] = 0;          // PV accumulators then the Z sums
-  if (i < rows) { d.rowmax[i] = INT64_MIN; d.maxp[i] = 0; }
-  if (i < d.B * d.Hkv) { d.maxk[i] = 0; d.maxv[i] = 0; }
+  if (i >= rows * d.hd) return;
+  const int64_t r = i / d.hd;
+  const int64_t b = r / d.H, kv = (r % d.H) / (d.H / d.Hkv);
+  const int64_t L = dec_len(d, b);
+  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  const int64_t stride = rows * d.hd;
+  uint64_t s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t c = 0;
+  for (; c + 8 <= nlive; c += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s[u] += d.part[(c + u) * stride + i];
+  }
+  for (; c < nlive; ++c) s[0] += d.part[c * stride + i];
+  const uint64_t tot = s[0] + s[1] + s[2] + s[3] + s[4] + s[5] + s[6] + s[7];
+  d.out[qoff(d, r) + i % d.hd] = (int64_t)tot >> d.frac;
+  if (i % d.hd == 0 && L > 0) {
+    uint64_t mp = 0, mv = 0, mk = 0;
+    for (int64_t cc = 0; cc < nlive; ++cc) {
+      const uint64_t a = d.cmp[cc * rows + r], v = d.cvm[cc * d.B * d.Hkv + b * d.Hkv + kv],
+                     k = d.ckm[cc * d.B * d.Hkv + b * d.Hkv + kv];
+      mp = a > mp ? a : mp;
+      mv = v > mv ? v : mv;
+      mk = k > mk ? k : mk;
+    }
+    const u128 pv = (u128)mp * mv;
+    if (pv > (u128)(INT64_MAX / L)) atomicOr(d.status, IMIE_EOVF);
+    const u128 qk = (u128)d.maxq[r] * mk;
+    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+  }
+}
+
+// decode chunking: ~2048 workgroups over the (b, kv) groups, chunks of >= 64 keys (multiple of 64)
+void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t* nch) {
+  const int64_t groups = B * Hkv;
+  int64_t want = 2048 / (groups > 0 ? groups : 1);
+  if (want < 1) want = 1;
+  int64_t c = (Lmax + want - 1) / want;
+  c = ((c + 63) / 64) * 64;
+  if (c < 64) c = 64;
+  *chunk = c;
+  *nch = (Lmax + c - 1) / c;
+  if (*nch < 1) *nch = 1;
 }
 
 }  // namespace
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax) {
   const int64_t rows = B * H * M;
-  return (size_t)(rows * Lmax + rows * hd + rows + 3 * rows + 2 * B * Hkv) * 8 + 256;
+  int64_t chunk = 0, nch = 0;
+  dec_geometry(B, Hkv, Lmax, &chunk, &nch);
+  const int64_t part = M == 1 ? nch * (rows * hd + 3 * rows + 2 * B * Hkv) : 0;
+  return (size_t)(rows * Lmax + rows * hd + rows + 3 * rows + 2 * B * Hkv + part) * 8 + 256;
 }
 
 void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
@@ -486,7 +641,16 @@ void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
   d.maxq = (uint64_t*)p;   p += rows;
   d.maxp = (uint64_t*)p;   p += rows;
   d.maxk = (uint64_t*)p;   p += d.B * d.Hkv;
-  d.maxv = (uint64_t*)p;
+  d.maxv = (uint64_t*)p;   p += d.B * d.Hkv;
+  // decode per-chunk partials (sized by imie_attn_scratch_bytes for M == 1)
+  int64_t chunk = 0, nch = 0;
+  dec_geometry(d.B, d.Hkv, d.Lmax, &chunk, &nch);
+  d.part = (uint64_t*)p;   p += nch * rows * d.hd;
+  d.cmax = p;              p += nch * rows;
+  d.cz = (uint64_t*)p;     p += nch * rows;
+  d.cmp = (uint64_t*)p;    p += nch * rows;
+  d.ckm = (uint64_t*)p;    p += nch * d.B * d.Hkv;
+  d.cvm = (uint64_t*)p;
 }
 
 int imie_attention_launch(AttnDesc d, hipStream_t st) {
@@ -502,28 +666,26 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
   const int64_t ninit = rows * d.hd > d.B * d.Hkv ? rows * d.hd : d.B * d.Hkv;
   imie_prof_mark(IMIE_K_ATTN, st, true);
   const int64_t rp = d.H / d.Hkv;
-  if (d.M == 1 && (rp == 1 || rp == 2 || rp == 4 || rp == 8) && d.hd <= 128) {
-    const int64_t nch = (d.Lmax + kDecChunk - 1) / kDecChunk;
-    const dim3 gd((unsigned)(d.B * d.Hkv), (unsigned)nch);
-    const int64_t ni = rows * d.hd + rows;
-    hipLaunchKernelGGL(dec_init_kernel, dim3((unsigned)((ni + 255) / 256)), dim3(256), 0, st, d);
+  if (d.M == 1 && (rp == 1 || rp == 2 || rp == 4 || rp == 8) && d.hd <= 128 && d.hd % 8 == 0) {
+    dec_geometry(d.B, d.Hkv, d.Lmax, &d.chunk, &d.nch);
+    const dim3 gd((unsigned)(d.B * d.Hkv), (unsigned)d.nch);
+    const int rep = (int)rp;
+#define IMIE_DEC(K_, KT_, R_) hipLaunchKernelGGL((K_<KT_, R_>), gd, dim3(256), 0, st, d)
+#define IMIE_DEC_R(K_, KT_)                                                                                \
+    if (rep == 1) IMIE_DEC(K_, KT_, 1); else if (rep == 2) IMIE_DEC(K_, KT_, 2);                           \
+    else if (rep == 4) IMIE_DEC(K_, KT_, 4); else IMIE_DEC(K_, KT_, 8)
+    if (d.kv32) { IMIE_DEC_R(dec_scores_kernel, int32_t); } else { IMIE_DEC_R(dec_scores_kernel, int64_t); }
     IMIE_HIP(hipGetLastError());
-    const int rep = (int)(d.H / d.Hkv);
-#define IMIE_DEC_SCORES(KT_, R_) hipLaunchKernelGGL((dec_scores_kernel<KT_, R_>), gd, dim3(256), 0, st, d)
-#define IMIE_DEC_SCORES_R(KT_)                                                                             \
-    if (rep == 1) IMIE_DEC_SCORES(KT_, 1); else if (rep == 2) IMIE_DEC_SCORES(KT_, 2);                     \
-    else if (rep <= 4 && rep % 4 == 0) IMIE_DEC_SCORES(KT_, 4); else IMIE_DEC_SCORES(KT_, 8)
-    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return IMIE_EARG;
-    if (d.kv32) { IMIE_DEC_SCORES_R(int32_t); } else { IMIE_DEC_SCORES_R(int64_t); }
-#undef IMIE_DEC_SCORES_R
-#undef IMIE_DEC_SCORES
+    if (rep == 1) hipLaunchKernelGGL(dec_exp_kernel<1>, gd, dim3(256), 0, st, d);
+    else if (rep == 2) hipLaunchKernelGGL(dec_exp_kernel<2>, gd, dim3(256), 0, st, d);
+    else if (rep == 4) hipLaunchKernelGGL(dec_exp_kernel<4>, gd, dim3(256), 0, st, d);
+    else hipLaunchKernelGGL(dec_exp_kernel<8>, gd, dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(dec_exp_kernel, gd, dim3(256), 0, st, d);
+    if (d.kv32) { IMIE_DEC_R(dec_pv_kernel, int32_t); } else { IMIE_DEC_R(dec_pv_kernel, int64_t); }
+#undef IMIE_DEC_R
+#undef IMIE_DEC
     IMIE_HIP(hipGetLastError());
-    if (d.kv32) hipLaunchKernelGGL(dec_pv_kernel<int32_t>, gd, dim3(256), 0, st, d);
-    else hipLaunchKernelGGL(dec_pv_kernel<int64_t>, gd, dim3(256), 0, st, d);
-    IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_final_kernel, dim3((unsigned)((rows * d.hd + 255) / 256)), dim3(256), 0, st, d);
+    hipLaunchKernelGGL(dec_final_kernel, dim3((unsigned)((rows * d.hd + 255) / 256)), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
     imie_prof_mark(IMIE_K_ATTN, st, false);
     return IMIE_OK;

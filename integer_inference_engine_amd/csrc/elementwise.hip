@@ -106,31 +106,46 @@ __global__ void embed_kernel(const uint8_t* __restrict__ bits, const int64_t* __
   out[i] = bit ? sc : (int64_t)(0 - (uint64_t)sc);
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const int64_t* __restrict__ logits, int64_t cols,
-                                                     int64_t* __restrict__ ids) {
-  __shared__ int64_t sv[256];
-  __shared__ int64_t si[256];
-  const int64_t row = blockIdx.x;
-  const int64_t* lr = logits + row * cols;
-  int64_t bv = INT64_MIN, bi = 0x7FFFFFFFFFFFFFFFll;
-  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-    const int64_t v = lr[c];
-    if (v > bv) { bv = v; bi = c; }      // ascending c per thread: first max wins
-  }
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
+// lowest-index argmax: stage 1 reduces a contiguous column range per workgroup to (value, index); stage 2
+// reduces the partials of a row. Ties keep the lower index at every level, which is numpy's first-max rule.
+__device__ inline void amx_merge(int64_t& v, int64_t& i, int64_t v2, int64_t i2) {
+  if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+
+__device__ inline void amx_block(int64_t& v, int64_t& i, int64_t* sv, int64_t* si) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amx_merge(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) { sv[wave] = v; si[wave] = i; }
   __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if (threadIdx.x < o) {
-      const int64_t v2 = sv[threadIdx.x + o], i2 = si[threadIdx.x + o];
-      if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
-        sv[threadIdx.x] = v2;
-        si[threadIdx.x] = i2;
-      }
-    }
-    __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < nw; ++w) amx_merge(v, i, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const int64_t* __restrict__ logits, int64_t cols,
+                                                          int64_t per, int64_t* __restrict__ part, int nparts) {
+  __shared__ int64_t sv[4], si[4];
+  const int64_t row = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * per, c1 = min(cols, c0 + per);
+  const int64_t* lr = logits + row * cols;
+  int64_t bv = INT64_MIN, bi = INT64_MAX;
+  for (int64_t c = c0 + threadIdx.x; c < c1; c += blockDim.x) amx_merge(bv, bi, lr[c], c);
+  amx_block(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    part[(row * nparts + blockIdx.x) * 2] = bv;
+    part[(row * nparts + blockIdx.x) * 2 + 1] = bi;
   }
-  if (threadIdx.x == 0) ids[row] = si[0];
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const int64_t* __restrict__ part, int nparts,
+                                                           int64_t* __restrict__ ids) {
+  __shared__ int64_t sv[4], si[4];
+  const int64_t row = blockIdx.x;
+  int64_t bv = INT64_MIN, bi = INT64_MAX;
+  for (int p = threadIdx.x; p < nparts; p += blockDim.x)
+    amx_merge(bv, bi, part[(row * nparts + p) * 2], part[(row * nparts + p) * 2 + 1]);
+  amx_block(bv, bi, sv, si);
+  if (threadIdx.x == 0) ids[row] = bi == INT64_MAX ? 0 : bi;
 }
 
 }  // namespace
@@ -190,9 +205,17 @@ int imie_embed_launch(const uint8_t* bits, const int64_t* scale, int64_t nb, con
   return IMIE_OK;
 }
 
-int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, hipStream_t st) {
+int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, int64_t* scratch,
+                       hipStream_t st) {
   if (rows <= 0) return IMIE_OK;
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, st, logits, cols, ids);
+  if (cols <= 0 || !scratch) return IMIE_EARG;
+  int64_t per = 2048;
+  int nparts = (int)((cols + per - 1) / per);
+  if (nparts > kArgmaxParts) { nparts = kArgmaxParts; per = (cols + nparts - 1) / nparts; }
+  hipLaunchKernelGGL(argmax_part_kernel, dim3((unsigned)nparts, (unsigned)rows), dim3(256), 0, st, logits, cols, per,
+                     scratch, nparts);
+  IMIE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(256), 0, st, scratch, nparts, ids);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
@@ -270,7 +293,8 @@ int imie_argmax_gpu(const int64_t* logits, int64_t rows, int64_t cols, int64_t* 
   const size_t b = (size_t)(rows * cols) * 8;
   if (g_ews.a.ensure(b) || g_ews.b.ensure((size_t)rows * 8)) return IMIE_EARG;
   IMIE_HIP(hipMemcpyAsync(g_ews.a.p, logits, b, hipMemcpyHostToDevice, st));
-  int rc = imie_argmax_launch((const int64_t*)g_ews.a.p, rows, cols, (int64_t*)g_ews.b.p, st);
+  if (g_ews.c.ensure(imie_argmax_scratch_bytes(rows))) return IMIE_EARG;
+  int rc = imie_argmax_launch((const int64_t*)g_ews.a.p, rows, cols, (int64_t*)g_ews.b.p, (int64_t*)g_ews.c.p, st);
   if (rc) return rc;
   IMIE_HIP(hipMemcpyAsync(ids, g_ews.b.p, (size_t)rows * 8, hipMemcpyDeviceToHost, st));
   IMIE_HIP(hipStreamSynchronize(st));

@@ -23,6 +23,11 @@ struct AttnDesc {
   uint64_t* acc;
   int64_t* rowmax;
   uint64_t *maxq, *maxp, *maxk, *maxv;
+  uint64_t* part;                  // decode: per-chunk PV partials [nch][B*H][hd]
+  int64_t* cmax;                   // decode: per-chunk row max of the scores [nch][B*H]
+  uint64_t *cz, *cmp;              // decode: per-chunk Z and max p [nch][B*H]
+  uint64_t *ckm, *cvm;             // decode: per-chunk max|K|, max|V| [nch][B*Hkv]
+  int64_t chunk, nch;              // decode key chunking (set by the launcher)
 };
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax);

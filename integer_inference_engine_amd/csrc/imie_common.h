@@ -80,4 +80,5 @@ __device__ __forceinline__ int64_t imie_wave_sum_i64(int64_t v) {
 enum { IMIE_K_Q1_PREP = 0, IMIE_K_Q1_GEMV = 1, IMIE_K_Q1_GEMM = 2, IMIE_K_ATTN = 3, IMIE_K_QK = 4,
        IMIE_K_COUNT = 16 };
 bool imie_prof_on();
+bool imie_prof_suspend(bool off);
 void imie_prof_mark(int kernel, hipStream_t st, bool begin);

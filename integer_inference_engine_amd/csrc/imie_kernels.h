@@ -12,6 +12,15 @@ int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t fr
 int imie_q1_launch(int64_t handle, const int64_t* x, int64_t T, int64_t frac, int64_t* out, int accumulate,
                    hipStream_t st);
 int imie_q1_dims(int64_t handle, int64_t* N, int64_t* nb);
+// Per-caller Q1 activation workspace (digit table, block totals, limb counts). A caller that captures its launches
+// into a graph owns one, so no other call can reallocate the buffers the graph points at.
+struct Q1Ws {
+  DevBuf xq, totals, lslab;
+};
+// Up to 3 weights with the same n_blocks applied to the same x in one prep + one matvec launch (wk == nullptr:
+// the library's shared workspace).
+int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int64_t T, int64_t frac,
+                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st);
 
 // NeoX RoPE on rows x (rows, nh, hd); row r uses table row pos[r] (pos == nullptr: pos0 + r).
 // The fail-loud envelope 2*max|x|*max|cos,sin| <= INT64_MAX is checked exactly via `guard` scratch
@@ -30,4 +39,8 @@ int imie_add_launch(int64_t* x, const int64_t* y, int64_t n, hipStream_t st);
 int imie_embed_launch(const uint8_t* bits, const int64_t* scale, int64_t nb, const int64_t* ids, int64_t T,
                       int64_t* out, hipStream_t st);
 // lowest-index argmax per row of (rows, cols) int64
-int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, hipStream_t st);
+// scratch: device buffer of imie_argmax_scratch_bytes(rows) bytes (two-stage reduction partials)
+constexpr int kArgmaxParts = 256;
+inline size_t imie_argmax_scratch_bytes(int64_t rows) { return (size_t)rows * kArgmaxParts * 16; }
+int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, int64_t* scratch,
+                       hipStream_t st);

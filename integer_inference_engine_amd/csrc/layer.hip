@@ -80,7 +80,11 @@ struct Net {
   int64_t* pt = nullptr;              // device [B][mp]
   std::vector<int64_t> len;           // host lengths per sequence
   // workspace
-  DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx;
+  DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx, amx, stepc;
+  Q1Ws q1w;                           // this net's Q1 workspace (graph-stable addresses)
+  // captured greedy decode step (imie_net_decode_dev): valid for the pointer key it was captured with
+  hipGraphExec_t gexec = nullptr;
+  const void* gkey[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   bool live = false;
 };
 
@@ -101,8 +105,10 @@ void net_free(Net* n) {
   for (auto p : n->kpool) if (p) (void)hipFree(p);
   for (auto p : n->vpool) if (p) (void)hipFree(p);
   if (n->pt) (void)hipFree(n->pt);
+  if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
-                  &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx};
+                  &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx, &n->amx,
+                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab};
   for (auto b : bs) b->release();
   n->live = false;
 }
@@ -129,15 +135,9 @@ int net_alloc_kv(Net& n, int64_t cap, int64_t P, int kv32) {
   return IMIE_OK;
 }
 
-// Run all layers over M new tokens for each of the B sequences. x: device (B*M, d), updated in place.
-// starts: host (B), the first new position per sequence (== its current cache length).
-int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st) {
+// Workspace for rows = B * M new rows attending over at most lmax keys.
+int net_ensure(Net& n, int64_t M, int64_t lmax) {
   const int64_t rows = n.B * M;
-  int64_t lmax = 0;
-  for (int64_t b = 0; b < n.B; ++b) {
-    if (starts[b] < 0 || starts[b] + M > n.mp * n.P) return IMIE_EARG;
-    lmax = starts[b] + M > lmax ? starts[b] + M : lmax;
-  }
   const int64_t qd = n.H * n.hd, kd = n.Hkv * n.hd;
   if (n.n.ensure((size_t)(rows * n.d) * 8) || n.q.ensure((size_t)(rows * qd) * 8) ||
       n.k.ensure((size_t)(rows * kd) * 8) || n.v.ensure((size_t)(rows * kd) * 8) ||
@@ -147,10 +147,15 @@ int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st
       n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure(64) ||
       n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)))
     return IMIE_EARG;
-  std::vector<int64_t> pos((size_t)rows);
-  for (int64_t r = 0; r < rows; ++r) pos[(size_t)r] = starts[r / M] + r % M;
-  IMIE_HIP(hipMemcpyAsync(n.pos.p, pos.data(), (size_t)rows * 8, hipMemcpyHostToDevice, st));
-  IMIE_HIP(hipMemcpyAsync(n.starts.p, starts, (size_t)n.B * 8, hipMemcpyHostToDevice, st));
+  return IMIE_OK;
+}
+
+// All layers over M new tokens per sequence; positions come from the device buffers n.pos (B*M) and n.starts
+// (B), so the launch sequence is independent of the positions (graph-capturable). lmax bounds the keys any row
+// sees and fixes the attention geometry. x: device (B*M, d), updated in place.
+int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
+  const int64_t rows = n.B * M;
+  const int64_t qd = n.H * n.hd, kd = n.Hkv * n.hd;
   int rc = 0;
 #define CK(call) do { rc = (call); if (rc) return rc; } while (0)
   int64_t *xn = (int64_t*)n.n.p, *q = (int64_t*)n.q.p, *k = (int64_t*)n.k.p, *v = (int64_t*)n.v.p;
@@ -162,9 +167,10 @@ int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st
   for (int64_t l = 0; l < n.nl; ++l) {
     const LayerW& L = n.layers[(size_t)l];
     CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n1g, xn, status, st));
-    CK(imie_q1_launch(L.w[0], xn, rows, n.frac, q, 0, st));
-    CK(imie_q1_launch(L.w[1], xn, rows, n.frac, k, 0, st));
-    CK(imie_q1_launch(L.w[2], xn, rows, n.frac, v, 0, st));
+    {
+      int64_t* outs[3] = {q, k, v};
+      CK(imie_q1_launch_multi(L.w, 3, xn, rows, n.frac, outs, 0, &n.q1w, st));
+    }
     CK(imie_rmsnorm_launch(q, rows * n.H, n.hd, n.frac, n.eps, L.qng, qn, status, st));
     CK(imie_rmsnorm_launch(k, rows * n.Hkv, n.hd, n.frac, n.eps, L.kng, kn, status, st));
     CK(fill_i64((int64_t*)guard, 2, 0, st));
@@ -193,16 +199,52 @@ int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st
     d.out = att; d.status = status;
     imie_attn_bind_scratch(d, n.attn.p);
     CK(imie_attention_launch(d, st));
-    CK(imie_q1_launch(L.w[3], att, rows, n.frac, x, 1, st));
+    CK(imie_q1_launch_multi(&L.w[3], 1, att, rows, n.frac, &x, 1, &n.q1w, st));
     CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n2g, xn, status, st));
-    CK(imie_q1_launch(L.w[4], xn, rows, n.frac, gate, 0, st));
-    CK(imie_q1_launch(L.w[5], xn, rows, n.frac, up, 0, st));
+    {
+      int64_t* outs[2] = {gate, up};
+      CK(imie_q1_launch_multi(&L.w[4], 2, xn, rows, n.frac, outs, 0, &n.q1w, st));
+    }
     CK(imie_silu_mul_launch(gate, up, rows * n.dff, n.frac, hh, st));
-    CK(imie_q1_launch(L.w[6], hh, rows, n.frac, x, 1, st));
+    CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st));
   }
 #undef CK
+  return IMIE_OK;
+}
+
+// Run all layers over M new tokens for each of the B sequences. x: device (B*M, d), updated in place.
+// starts: host (B), the first new position per sequence (== its current cache length).
+int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st) {
+  const int64_t rows = n.B * M;
+  int64_t lmax = 0;
+  for (int64_t b = 0; b < n.B; ++b) {
+    if (starts[b] < 0 || starts[b] + M > n.mp * n.P) return IMIE_EARG;
+    lmax = starts[b] + M > lmax ? starts[b] + M : lmax;
+  }
+  if (net_ensure(n, M, lmax)) return IMIE_EARG;
+  std::vector<int64_t> pos((size_t)rows);
+  for (int64_t r = 0; r < rows; ++r) pos[(size_t)r] = starts[r / M] + r % M;
+  IMIE_HIP(hipMemcpyAsync(n.pos.p, pos.data(), (size_t)rows * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(n.starts.p, starts, (size_t)n.B * 8, hipMemcpyHostToDevice, st));
+  const int rc = net_run_core(n, x, M, lmax, st);
+  if (rc) return rc;
   for (int64_t b = 0; b < n.B; ++b) n.len[(size_t)b] = starts[b] + M;
   return IMIE_OK;
+}
+
+// After a greedy step: hist[step * B + b] = ids[b]; every sequence advances one position (starts, pos); step++.
+__global__ void decode_advance_kernel(const int64_t* __restrict__ ids, int64_t* __restrict__ hist,
+                                      int64_t* __restrict__ stepc, int64_t* __restrict__ starts,
+                                      int64_t* __restrict__ pos, int64_t B) {
+  const int64_t s = *stepc;
+  for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
+    if (hist) hist[s * B + b] = ids[b];
+    const int64_t p = starts[b] + 1;
+    starts[b] = p;
+    pos[b] = p;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *stepc = s + 1;
 }
 
 // final norm of selected rows + output head (+ argmax). rows_idx: host list of row indices into x.
@@ -211,15 +253,23 @@ int net_head(Net& n, const int64_t* x, const std::vector<int64_t>& rows_idx, int
   const int64_t R = (int64_t)rows_idx.size();
   if (n.out_head < 0 || R == 0) return IMIE_EARG;
   if (n.lastx.ensure((size_t)(R * n.d) * 8) || n.n.ensure((size_t)(R * n.d) * 8)) return IMIE_EARG;
-  for (int64_t i = 0; i < R; ++i)
-    IMIE_HIP(hipMemcpyAsync((int64_t*)n.lastx.p + i * n.d, x + rows_idx[(size_t)i] * n.d, (size_t)n.d * 8,
-                            hipMemcpyDeviceToDevice, st));
-  int rc = imie_rmsnorm_launch((const int64_t*)n.lastx.p, R, n.d, n.frac, n.eps, n.finalg, (int64_t*)n.n.p,
-                               (int*)n.status.p, st);
+  bool ident = true;
+  for (int64_t i = 0; i < R; ++i) ident = ident && rows_idx[(size_t)i] == i;
+  const int64_t* src = x;
+  if (!ident) {
+    for (int64_t i = 0; i < R; ++i)
+      IMIE_HIP(hipMemcpyAsync((int64_t*)n.lastx.p + i * n.d, x + rows_idx[(size_t)i] * n.d, (size_t)n.d * 8,
+                              hipMemcpyDeviceToDevice, st));
+    src = (const int64_t*)n.lastx.p;
+  }
+  int rc = imie_rmsnorm_launch(src, R, n.d, n.frac, n.eps, n.finalg, (int64_t*)n.n.p, (int*)n.status.p, st);
   if (rc) return rc;
-  rc = imie_q1_launch(n.out_head, (const int64_t*)n.n.p, R, n.frac, logits, 0, st);
+  rc = imie_q1_launch_multi(&n.out_head, 1, (const int64_t*)n.n.p, R, n.frac, &logits, 0, &n.q1w, st);
   if (rc) return rc;
-  if (ids) rc = imie_argmax_launch(logits, R, n.vocab, ids, st);
+  if (ids) {
+    if (n.amx.ensure(imie_argmax_scratch_bytes(R))) return IMIE_EARG;
+    rc = imie_argmax_launch(logits, R, n.vocab, ids, (int64_t*)n.amx.p, st);
+  }
   return rc;
 }
 
@@ -459,6 +509,74 @@ int imie_net_head_dev(int64_t ctx, const int64_t* x_dev, int64_t rows, int64_t* 
   std::vector<int64_t> r((size_t)rows);
   for (int64_t i = 0; i < rows; ++i) r[(size_t)i] = i;
   return net_head(*n, x_dev, r, logits_dev, ids_dev, (hipStream_t)stream);
+}
+
+// Greedy decode on the device (no reference counterpart; the reference's decode loop drives
+// bonsai_decode_step from the host, reference_bonsai.py:1200-1310): `steps` times, embed ids_dev (B) from the
+// natural-layout Q1 embedding (ebits, escale), run every layer at the sequences' current lengths, final norm +
+// LM head into logits_dev (B, vocab), lowest-index argmax back into ids_dev, and hist_dev[step * B + b] (when
+// non-null) records the token. use_graph != 0 runs the first step eagerly and replays a captured HIP graph of
+// one step for the rest (the graph is kept for the same pointer set). Asynchronous on `stream`; envelope
+// refusals set the status word (imie_net_status).
+int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale, int64_t* ids_dev,
+                        int64_t* logits_dev, int64_t* hist_dev, int64_t steps, int use_graph, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !ebits || !escale || !ids_dev || !logits_dev || steps <= 0 || n->out_head < 0) return IMIE_EARG;
+  const int64_t cap = n->mp * n->P;
+  for (int64_t b = 0; b < n->B; ++b)
+    if (n->len[(size_t)b] + steps > cap) return IMIE_EARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (net_ensure(*n, 1, cap) || n->amx.ensure(imie_argmax_scratch_bytes(n->B)) || n->stepc.ensure(64) ||
+      n->lastx.ensure((size_t)(n->B * n->d) * 8))
+    return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(n->starts.p, n->len.data(), (size_t)n->B * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(n->pos.p, n->len.data(), (size_t)n->B * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipStreamSynchronize(st));                 // the host length vector is read by the copies above
+  if (fill_i64((int64_t*)n->stepc.p, 1, 0, st)) return IMIE_EARG;
+  std::vector<int64_t> rows((size_t)n->B);
+  for (int64_t b = 0; b < n->B; ++b) rows[(size_t)b] = b;
+  auto step = [&]() -> int {
+    int rc = imie_embed_launch(ebits, escale, n->d / 128, ids_dev, n->B, (int64_t*)n->x.p, st);
+    if (rc) return rc;
+    if ((rc = net_run_core(*n, (int64_t*)n->x.p, 1, cap, st))) return rc;
+    if ((rc = net_head(*n, (const int64_t*)n->x.p, rows, logits_dev, ids_dev, st))) return rc;
+    hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(256), 0, st, ids_dev, hist_dev, (int64_t*)n->stepc.p,
+                       (int64_t*)n->starts.p, (int64_t*)n->pos.p, n->B);
+    IMIE_HIP(hipGetLastError());
+    return IMIE_OK;
+  };
+  if (n->x.ensure((size_t)(n->B * n->d) * 8)) return IMIE_EARG;
+  int rc = step();                                    // eager: also sizes every workspace the graph will use
+  if (rc) return rc;
+  if (steps > 1) {
+    if (!use_graph) {
+      for (int64_t s = 1; s < steps && !rc; ++s) rc = step();
+      if (rc) return rc;
+    } else {
+      const void* key[5] = {ebits, escale, ids_dev, logits_dev, hist_dev};
+      if (n->gexec && memcmp(key, n->gkey, sizeof(key)) != 0) {
+        (void)hipGraphExecDestroy(n->gexec);
+        n->gexec = nullptr;
+      }
+      if (!n->gexec) {
+        const bool prof = imie_prof_suspend(true);
+        hipGraph_t g = nullptr;
+        IMIE_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        rc = step();
+        const hipError_t ec = hipStreamEndCapture(st, &g);
+        imie_prof_suspend(prof);
+        if (rc || ec != hipSuccess || !g) { if (g) (void)hipGraphDestroy(g); return rc ? rc : IMIE_EARG; }
+        const hipError_t ei = hipGraphInstantiate(&n->gexec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ei != hipSuccess) { n->gexec = nullptr; return IMIE_EARG; }
+        memcpy(n->gkey, key, sizeof(key));
+      }
+      for (int64_t s = 1; s < steps; ++s) IMIE_HIP(hipGraphLaunch(n->gexec, st));
+    }
+  }
+  for (int64_t b = 0; b < n->B; ++b) n->len[(size_t)b] += steps;
+  return IMIE_OK;
 }
 
 // Clear (0) or read the context status word: 0 ok, bit 2 attention / RoPE / int32-KV envelope, bit 4 RMSNorm.

@@ -26,6 +26,7 @@ namespace {
 constexpr int kTileRows = 16;      // output rows per MFMA tile
 constexpr int kSlabBlocks = 4;     // 128-blocks per slab (= K 512 per wave step)
 constexpr int kMaxLimbs = 8;
+constexpr int kMaxSegs = 3;        // weights sharing one activation in a single matvec launch
 
 // ------------------------------------------------------------------------------------------------------
 // Registry of resident Q1 weights (process-global, handle = index). Layout per weight:
@@ -49,7 +50,8 @@ std::vector<Q1Weight>& registry() {
 uint64_t g_resident_bytes = 0;
 
 struct Workspace {
-  DevBuf x, out, xq, totals, lslab;
+  DevBuf x, out;
+  Q1Ws w;
 } g_ws;
 
 }  // namespace
@@ -86,12 +88,24 @@ extern "C" int imie_q1_repack_host(const uint8_t* bits, const int64_t* scale, in
 // c = 0..3, as bytes c). Lane layout: g = lane>>4 (block of slab), s = lane&7, dh = (lane>>3)&1 covering
 // d in {2dh, 2dh+1}: 8 positions per lane.
 // ------------------------------------------------------------------------------------------------------
+struct Q1Zero {                    // outputs the prep kernel clears (K-split matvecs add into them atomically)
+  int64_t* p[kMaxSegs];
+  int64_t n[kMaxSegs];
+  int cnt;
+};
+
 __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__ x, int64_t K, int64_t nb,
                                                       int64_t nbp, int64_t nslabs, uint32_t* __restrict__ xq,
-                                                      int64_t* __restrict__ totals, int* __restrict__ lslab) {
+                                                      int64_t* __restrict__ totals, int* __restrict__ lslab,
+                                                      Q1Zero zero) {
   const int lane = threadIdx.x;
   const int64_t sl = blockIdx.x;
   const int64_t t = blockIdx.y;
+  {
+    const int64_t wg = t * nslabs + sl, nwg = (int64_t)gridDim.y * nslabs;
+    for (int z = 0; z < zero.cnt; ++z)
+      for (int64_t e = wg * 64 + lane; e < zero.n[z]; e += nwg * 64) zero.p[z][e] = 0;
+  }
   const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
   const int64_t blk = sl * kSlabBlocks + g;
   int64_t v[8];
@@ -140,15 +154,23 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 //   * grid.y splits K: with ksplit > 1 the waves add their int64 partials into a zeroed output with 64-bit
 //     atomics (integer addition: order-free and exact).
 // ------------------------------------------------------------------------------------------------------
+struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) applied to the same activations
+  const uint4* bits[kMaxSegs];
+  const void* scale[kMaxSegs];
+  int64_t N[kMaxSegs], ntiles[kMaxSegs];
+  int64_t* out[kMaxSegs];
+  int64_t gbegin[kMaxSegs + 1];    // first tile group of each segment (groups of R tiles)
+  int cnt;
+};
+
 template <bool S64, int R, int TT>
 __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
-    const uint4* __restrict__ bitsT, const void* __restrict__ scaleT, const uint4* __restrict__ xq,
-    const int64_t* __restrict__ totals, const int* __restrict__ lslab, int64_t N, int64_t ntiles, int64_t nslabs,
-    int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, int64_t* __restrict__ out) {
+    Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
+    int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: keeps the segment scalar
   const int64_t s0 = (int64_t)blockIdx.y * spk;
   const int64_t s1 = min(nslabs, s0 + spk);
   const int64_t nsl = s1 - s0;
@@ -165,8 +187,18 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     }
   __syncthreads();
 
-  const int64_t tile0 = ((int64_t)blockIdx.x * 4 + wave) * R;
-  if (tile0 >= ntiles) return;
+  // this wave's tile group -> (segment, first tile)
+  const int64_t gi = (int64_t)blockIdx.x * 4 + wave;
+  if (gi >= sg.gbegin[sg.cnt]) return;
+  int seg = 0;
+#pragma unroll
+  for (int z = 1; z < kMaxSegs; ++z)
+    if (z < sg.cnt && gi >= sg.gbegin[z]) seg = z;
+  const uint4* __restrict__ bitsT = sg.bits[seg];
+  const void* __restrict__ scaleT = sg.scale[seg];
+  const int64_t N = sg.N[seg], ntiles = sg.ntiles[seg];
+  int64_t* __restrict__ out = sg.out[seg];
+  const int64_t tile0 = (gi - sg.gbegin[seg]) * R;
   const int g = lane >> 4;       // block within the slab
   const int n = lane & 15;       // output row within the tile
   const bool aact = (n >> 2) == g;
@@ -274,11 +306,6 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   }
 }
 
-__global__ void q1_zero_kernel(int64_t* __restrict__ out, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = 0;
-}
-
 // Straightforward exact kernel (thread per output): used for shapes the MFMA path declines and as an
 // in-library cross-check. Reads the natural (N, nb, 16) layout.
 __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uint8_t* __restrict__ bits,
@@ -308,54 +335,77 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
 // ------------------------------------------------------------------------------------------------------
 // Launch helpers
 // ------------------------------------------------------------------------------------------------------
-static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int64_t frac, int64_t* out_dev,
-                        hipStream_t st, int accumulate = 0) {
+// One prep (digit table of x, shared by every segment) and one matvec launch over up to kMaxSegs weights with
+// the same n_blocks and scale width; outs[i] receives (T, N_i). accumulate != 0 adds into the outputs.
+static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
+                          int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
   if (T <= 0) return IMIE_OK;
-  const int64_t nbp = w.nslabs * kSlabBlocks;
-  if (g_ws.xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || g_ws.totals.ensure((size_t)T * nbp * 8) ||
-      g_ws.lslab.ensure((size_t)T * w.nslabs * 4))
+  if (cnt < 1 || cnt > kMaxSegs) return IMIE_EARG;
+  const Q1Weight& w0 = *ws[0];
+  for (int i = 1; i < cnt; ++i)
+    if (ws[i]->nb != w0.nb || ws[i]->scale64 != w0.scale64) return IMIE_EARG;
+  const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks;
+  if (wk.xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || wk.totals.ensure((size_t)T * nbp * 8) ||
+      wk.lslab.ensure((size_t)T * nslabs * 4))
     return IMIE_EARG;
-  const int64_t K = w.nb * 128;
-  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
-  hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)w.nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w.nb, nbp,
-                     w.nslabs, (uint32_t*)g_ws.xq.p, (int64_t*)g_ws.totals.p, (int*)g_ws.lslab.p);
-  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
-  IMIE_HIP(hipGetLastError());
   // Work split: waves = tile groups of R tiles; grid.y splits the slabs when there are too few tile groups
   // to keep ~8 waves per CU busy (decode-sized matvecs).
-  const int R = w.ntiles >= 4 * 16384 ? 4 : (w.ntiles >= 2 * 8192 ? 2 : 1);
-  const int64_t groups = (w.ntiles + R - 1) / R;
+  int64_t ntiles_all = 0;
+  for (int i = 0; i < cnt; ++i) ntiles_all += ws[i]->ntiles;
+  const int R = ntiles_all >= 4 * 16384 ? 4 : (ntiles_all >= 2 * 8192 ? 2 : 1);
+  Q1Segs sg = {};
+  sg.cnt = cnt;
+  int64_t groups = 0;
+  for (int i = 0; i < cnt; ++i) {
+    sg.bits[i] = ws[i]->bits;
+    sg.scale[i] = ws[i]->scale;
+    sg.N[i] = ws[i]->N;
+    sg.ntiles[i] = ws[i]->ntiles;
+    sg.gbegin[i] = groups;
+    groups += (ws[i]->ntiles + R - 1) / R;
+  }
+  sg.gbegin[cnt] = groups;
   int64_t ksplit = 1;
-  while (groups * ksplit < 8 * 1024 && ksplit * 2 <= w.nslabs && ksplit < 8) ksplit *= 2;
-  const int64_t spk = (w.nslabs + ksplit - 1) / ksplit;
-  ksplit = (w.nslabs + spk - 1) / spk;
+  while (groups * ksplit < 8 * 1024 && ksplit * 2 <= nslabs && ksplit < 8) ksplit *= 2;
+  const int64_t spk = (nslabs + ksplit - 1) / ksplit;
+  ksplit = (nslabs + spk - 1) / spk;
   const int TT = T <= 1 ? 1 : (T <= 2 ? 2 : 4);
   const int Tc = TT;
+  // the prep kernel clears the outputs when the matvec adds into them (K-split) and no residual is kept
+  Q1Zero zero = {};
+  if (ksplit > 1 && !accumulate) {
+    zero.cnt = cnt;
+    for (int i = 0; i < cnt; ++i) { zero.p[i] = outs[i]; zero.n[i] = T * ws[i]->N; }
+  }
+  const int64_t K = w0.nb * 128;
+  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
+  hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w0.nb, nbp,
+                     nslabs, (uint32_t*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, zero);
+  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
+  IMIE_HIP(hipGetLastError());
   const size_t budget = 48 * 1024;
   int Lcap = (int)(budget / ((size_t)Tc * spk * 512));
   Lcap = Lcap < 1 ? 1 : (Lcap > kMaxLimbs ? kMaxLimbs : Lcap);
   const size_t lds = (size_t)Tc * spk * Lcap * 512;
   const int fr = (int)(frac > 63 ? 63 : frac);
   const dim3 grid((unsigned)((groups + 3) / 4), (unsigned)ksplit);
+  const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
   imie_prof_mark(IMIE_K_Q1_GEMV, st, true);
   for (int64_t t0 = 0; t0 < T; t0 += Tc) {
     const int tn = (int)(T - t0 < Tc ? T - t0 : Tc);
-    int64_t* o = out_dev + t0 * w.N;
-    const uint4* xq = (const uint4*)g_ws.xq.p + t0 * kMaxLimbs * nbp * 8;
-    const int64_t* tot = (const int64_t*)g_ws.totals.p + t0 * nbp;
-    const int* ls = (const int*)g_ws.lslab.p + t0 * w.nslabs;
-    const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
-    if (ksplit > 1 && !accumulate)
-      hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((tn * w.N + 255) / 256)), dim3(256), 0, st, o,
-                         (int64_t)tn * w.N);
+    Q1Segs sgt = sg;
+    for (int i = 0; i < cnt; ++i) sgt.out[i] = outs[i] + t0 * ws[i]->N;
+    const uint4* xq = (const uint4*)wk.xq.p + t0 * kMaxLimbs * nbp * 8;
+    const int64_t* tot = (const int64_t*)wk.totals.p + t0 * nbp;
+    const int* ls = (const int*)wk.lslab.p + t0 * nslabs;
 #define IMIE_Q1_LAUNCH(S64_, R_, TT_)                                                                        \
-  hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, R_, TT_>), grid, dim3(256), lds, st, w.bits, w.scale, xq, tot, ls, \
-                     w.N, w.ntiles, w.nslabs, nbp, tn, fr, spk, Lcap, mode, o)
+  hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, R_, TT_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs,  \
+                     nbp, tn, fr, spk, Lcap, mode)
 #define IMIE_Q1_LAUNCH_R(S64_, TT_)                                                                          \
   if (R == 4) IMIE_Q1_LAUNCH(S64_, 4, TT_); else if (R == 2) IMIE_Q1_LAUNCH(S64_, 2, TT_); else IMIE_Q1_LAUNCH(S64_, 1, TT_)
 #define IMIE_Q1_LAUNCH_T(S64_)                                                                               \
   if (TT == 1) { IMIE_Q1_LAUNCH_R(S64_, 1); } else if (TT == 2) { IMIE_Q1_LAUNCH_R(S64_, 2); } else { IMIE_Q1_LAUNCH_R(S64_, 4); }
-    if (w.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
+    if (w0.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
 #undef IMIE_Q1_LAUNCH_T
 #undef IMIE_Q1_LAUNCH_R
 #undef IMIE_Q1_LAUNCH
@@ -363,6 +413,13 @@ static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int6
   imie_prof_mark(IMIE_K_Q1_GEMV, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
+}
+
+static int q1_apply_dev(const Q1Weight& w, const int64_t* x_dev, int64_t T, int64_t frac, int64_t* out_dev,
+                        hipStream_t st, int accumulate = 0) {
+  const Q1Weight* ws[1] = {&w};
+  int64_t* outs[1] = {out_dev};
+  return q1_apply_multi(ws, 1, x_dev, T, frac, outs, accumulate, g_ws.w, st);
 }
 
 static int64_t q1_register(const uint8_t* bits, const void* scale, int64_t N, int64_t nb, int src32) {
@@ -420,6 +477,23 @@ int imie_q1_launch(int64_t handle, const int64_t* x, int64_t T, int64_t frac, in
   const Q1Weight* w = q1_get(handle);
   if (!w) return IMIE_EARG;
   return q1_apply_dev(*w, x, T, frac, out, st, accumulate);
+}
+
+int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int64_t T, int64_t frac,
+                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st) {
+  if (cnt < 1 || cnt > kMaxSegs) return IMIE_EARG;
+  const Q1Weight* ws[kMaxSegs];
+  for (int i = 0; i < cnt; ++i)
+    if (!(ws[i] = q1_get(handles[i]))) return IMIE_EARG;
+  bool same = true;
+  for (int i = 1; i < cnt; ++i) same = same && ws[i]->nb == ws[0]->nb && ws[i]->scale64 == ws[0]->scale64;
+  Q1Ws& w = wk ? *wk : g_ws.w;
+  if (same) return q1_apply_multi(ws, cnt, x, T, frac, outs, accumulate, w, st);
+  for (int i = 0; i < cnt; ++i) {
+    const int rc = q1_apply_multi(&ws[i], 1, x, T, frac, &outs[i], accumulate, w, st);
+    if (rc) return rc;
+  }
+  return IMIE_OK;
 }
 
 int imie_q1_dims(int64_t handle, int64_t* N, int64_t* nb) {

@@ -117,13 +117,19 @@ struct ProfSlot {
   size_t used = 0;
 };
 bool g_prof = false;
+bool g_prof_suspended = false;     // set while a launch sequence is being captured into a graph
 ProfSlot g_slots[IMIE_K_COUNT];
 }  // namespace
 
 bool imie_prof_on() { return g_prof; }
+bool imie_prof_suspend(bool off) {   // returns the previous state; no events are recorded while suspended
+  const bool prev = g_prof_suspended;
+  g_prof_suspended = off;
+  return prev;
+}
 
 void imie_prof_mark(int kernel, hipStream_t st, bool begin) {
-  if (!g_prof || kernel < 0 || kernel >= IMIE_K_COUNT) return;
+  if (!g_prof || g_prof_suspended || kernel < 0 || kernel >= IMIE_K_COUNT) return;
   ProfSlot& s = g_slots[kernel];
   if (begin && s.used + 2 > s.ev.size()) {
     hipEvent_t a, b;

@@ -72,6 +72,29 @@ class ResidentNet:
         self.stream.synchronize()
         return logits, ids
 
+    def decode(self, embed_bits, embed_scale, ids, steps: int, *, graph: bool = True, hist=None, logits=None):
+        """Greedy decode ``steps`` tokens on the device. embed_bits (vocab, nb, 16) uint8 and embed_scale
+        (vocab, nb) int64 torch tensors on the device; ids (B,) int64 device tensor, overwritten with the last
+        token. Returns (logits of the last step (B, vocab), hist (steps, B)) as device tensors."""
+        t = self.torch
+        if logits is None:
+            logits = t.empty((self.B, self.vocab), dtype=t.int64, device="cuda")
+        if hist is None:
+            hist = t.empty((steps, self.B), dtype=t.int64, device="cuda")
+        rc = self.lib.imie_net_decode_dev(self.h, ctypes.c_void_p(embed_bits.data_ptr()),
+                                          ctypes.c_void_p(embed_scale.data_ptr()), ctypes.c_void_p(ids.data_ptr()),
+                                          ctypes.c_void_p(logits.data_ptr()), ctypes.c_void_p(hist.data_ptr()),
+                                          int(steps), 1 if graph else 0, self._sp())
+        if rc != 0:
+            raise RuntimeError(f"decode rc={rc}: {_lib.last_error()}")
+        return logits, hist
+
+    def status(self) -> int:
+        return int(self.lib.imie_net_status(self.h, 0, self._sp()))
+
+    def clear_status(self) -> None:
+        self.lib.imie_net_status(self.h, 1, self._sp())
+
     def export_kv(self, layer: int, b: int, count: int):
         k = np.empty((self.Hkv, count, self.hd), dtype=np.int64)
         v = np.empty_like(k)

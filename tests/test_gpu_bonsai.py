@@ -166,3 +166,67 @@ def test_decode_ctx_greedy_generation_matches_oracle(gpu):
         nxt = [int(v) for v in np.argmax(logits, axis=1)]
         pos = [p + 1 for p in pos]
     gpu.decode_ctx_free(ctx)
+
+
+@pytest.mark.parametrize("graph", [0, 1])
+def test_device_greedy_decode_matches_oracle(gpu, graph):
+    """imie_net_decode_dev: embed -> layers -> head -> argmax on the device for B=3 ragged sequences; the graph
+    variant replays one captured step, so steps 2.. exercise the replay (positions advance on the device)."""
+    import ctypes
+    import torch
+    from integer_inference_engine_amd import _lib
+    model = workloads.small_bonsai(seed=43)
+    cfg = model["cfg"]
+    w, g = register_model(gpu, model)
+    B, T0, steps = 3, [5, 9, 2], 7
+    prompts = [prng.uniform_int(43, 300 + b, (T0[b],), 0, cfg["vocab"]) for b in range(B)]
+    c = {"H": cfg["H"], "Hkv": cfg["Hkv"], "hd": cfg["hd"]}
+    ctx = gpu.decode_ctx_create((B, cfg["n_layers"], cfg["H"], cfg["Hkv"], cfg["hd"], cfg["d"], cfg["dff"],
+                                 cfg["vocab"]), w, g, 16, 1, fx.inv_sqrt_fp(cfg["hd"], 16), 64)
+    assert ctx is not None
+    caches, first = [], []
+    for b in range(B):
+        x, ks, vs = _oracle_prefill(model, prompts[b])
+        assert gpu.decode_ctx_seed_seq(ctx, b, ks, vs)
+        caches.append(([ks[li] for li in range(len(ks))], [vs[li] for li in range(len(vs))]))
+        first.append(int(np.argmax(obm.head_logits(model, x[-1:], 16)[0])))
+    # oracle greedy continuation
+    want_tok, nxt, pos = [], list(first), list(T0)
+    for _ in range(steps):
+        x_in = q1_rows(*model["embed"], nxt)
+        logits = []
+        for b in range(B):
+            xb = x_in[b:b + 1]
+            kc, vc = caches[b]
+            for li, layer in enumerate(model["layers"]):
+                xb, kn, vn = obm.layer_forward(xb, layer, c, model["cos"], model["sin"], 16, kc[li], vc[li], pos[b])
+                kc[li] = np.concatenate([kc[li], kn], axis=1)
+                vc[li] = np.concatenate([vc[li], vn], axis=1)
+            logits.append(obm.head_logits(model, xb, 16)[0])
+        nxt = [int(np.argmax(lg)) for lg in logits]
+        want_tok.append(nxt)
+        pos = [p + 1 for p in pos]
+    so = _lib.lib()
+    eb = torch.from_numpy(np.ascontiguousarray(model["embed"][0])).cuda()
+    es = torch.from_numpy(np.ascontiguousarray(model["embed"][1])).cuda()
+    ids = torch.tensor(first, dtype=torch.int64, device="cuda")
+    lg = torch.empty((B, cfg["vocab"]), dtype=torch.int64, device="cuda")
+    hist = torch.full((steps, B), -1, dtype=torch.int64, device="cuda")
+    s = torch.cuda.Stream()
+    sp = ctypes.c_void_p(s.cuda_stream)
+    so.imie_net_status(ctx, 1, sp)
+    rc = so.imie_net_decode_dev(ctx, ctypes.c_void_p(eb.data_ptr()), ctypes.c_void_p(es.data_ptr()),
+                                ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(lg.data_ptr()),
+                                ctypes.c_void_p(hist.data_ptr()), steps, graph, sp)
+    assert rc == 0, _lib.last_error()
+    assert so.imie_net_status(ctx, 0, sp) == 0
+    s.synchronize()
+    assert hist.cpu().numpy().tolist() == want_tok
+    assert_same(lg.cpu().numpy(), np.stack(logits), "last-step logits")
+    for b in range(B):
+        for li in range(cfg["n_layers"]):
+            k = np.empty((cfg["Hkv"], T0[b] + steps, cfg["hd"]), dtype=np.int64)
+            v = np.empty_like(k)
+            assert so.imie_net_export_kv(ctx, li, b, T0[b] + steps, k.ctypes.data, v.ctypes.data) == 0
+            assert np.array_equal(k, caches[b][0][li][:, :T0[b] + steps]) and np.array_equal(v, caches[b][1][li][:, :T0[b] + steps])
+    gpu.decode_ctx_free(ctx)

@@ -44,9 +44,7 @@ def oracle_decode(model, kc, vc, first_id):
 @pytest.mark.gpu
 @pytest.mark.timeout(400)
 def test_8b_decode_36_layers_byte_exact(gpu):
-    import ctypes
     import torch
-    from integer_inference_engine_amd import _lib
     from integer_inference_engine_amd.resident import ResidentNet
     from tests.bonsai_gpu_harness import register_model
     model = _model()
@@ -59,21 +57,17 @@ def test_8b_decode_36_layers_byte_exact(gpu):
                       kv32=True)
     try:
         net.seed(0, np.broadcast_to(kc, (NL,) + kc.shape), np.broadcast_to(vc, (NL,) + vc.shape))
-        so = _lib.lib()
         eb = torch.from_numpy(np.ascontiguousarray(model["embed"][0])).cuda()
         es = torch.from_numpy(np.ascontiguousarray(model["embed"][1])).cuda()
         ids = torch.tensor([7], dtype=torch.int64, device="cuda")
-        x = torch.empty((1, D), dtype=torch.int64, device="cuda")
-        sp = ctypes.c_void_p(net.stream.cuda_stream)
-        for s, (wl, wt, wkv) in enumerate(want):
-            assert so.imie_embed_dev(ctypes.c_void_p(eb.data_ptr()), ctypes.c_void_p(es.data_ptr()), D // 128,
-                                     ctypes.c_void_p(ids.data_ptr()), 1, ctypes.c_void_p(x.data_ptr()), sp) == 0
-            assert net.forward(x, [CTX + s], 1) == 0
-            logits, dev_ids = net.head(x, 1)
-            got = logits.cpu().numpy()[0]
-            assert np.array_equal(got, wl), f"step {s}: {np.count_nonzero(got != wl)} logits differ"
-            assert int(dev_ids.item()) == wt
-            ids.copy_(dev_ids)
+        net.clear_status()
+        logits, hist = net.decode(eb, es, ids, STEPS, graph=True)   # step 1 eager, steps 2.. graph replays
+        assert net.status() == 0
+        net.stream.synchronize()
+        assert hist.cpu().numpy()[:, 0].tolist() == [t for _, t, _ in want]
+        got = logits.cpu().numpy()[0]
+        wl = want[-1][0]
+        assert np.array_equal(got, wl), f"{np.count_nonzero(got != wl)} last-step logits differ"
         for li in (0, NL // 2, NL - 1):
             k, v = net.export_kv(li, 0, CTX + STEPS)
             assert np.array_equal(k[:, :CTX], kc) and np.array_equal(v[:, :CTX], vc)
