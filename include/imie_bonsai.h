@@ -133,6 +133,11 @@ int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int
  * optional; use_graph replays a captured HIP graph of one step after the first. */
 int imie_net_decode_dev(int64_t ctx, const uint8_t *ebits, const int64_t *escale, int64_t *ids_dev,
                         int64_t *logits_dev, int64_t *hist_dev, int64_t steps, int use_graph, void *stream);
+/* CPU test hooks for the exact RMSNorm arithmetic (no reference counterpart): floor(sqrt(hi*2^64 + lo)),
+ * floor((2^64 - 1) / d), low 64 bits of floor((hi*2^64 + lo) / d). */
+uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo);
+uint64_t imie_fx_recip_u64(uint64_t d);
+uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d);
 /* Q1 embedding rows sign*scale (reference_bonsai.py:138-146) from device tables. */
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);

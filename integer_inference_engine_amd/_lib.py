@@ -7,7 +7,7 @@ by ``device_available()`` (the reference's ``bonsai_gpu_available`` probe).
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_int, c_int64, c_uint64, c_void_p
+from ctypes import c_int, c_int64, c_uint32, c_uint64, c_void_p
 from functools import lru_cache
 from pathlib import Path
 
@@ -66,6 +66,9 @@ SIGNATURES = {
     "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),
     "imie_net_export_kv": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_embed_dev": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "imie_fx_isqrt_u128": (c_uint64, [c_uint64, c_uint64]),
+    "imie_fx_recip_u64": (c_uint64, [c_uint64]),
+    "imie_fx_div_u128": (c_uint64, [c_uint64, c_uint64, c_uint32]),
     "imie_net_decode_dev": (c_int, [c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int,
                                     c_void_p]),
     # north-mini-code Q4_K / Q6_K (include/imie_nmc.h)

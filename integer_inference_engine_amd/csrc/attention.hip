@@ -21,6 +21,7 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_attention.h"
+#include <stdlib.h>
 
 namespace {
 
@@ -51,16 +52,26 @@ __device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
 __device__ inline void amax_u64(uint64_t* p, uint64_t v) { atomicMax((unsigned long long*)p, (unsigned long long)v); }
 __device__ inline void amax_i64(int64_t* p, int64_t v) { atomicMax((long long*)p, (long long)v); }
 
+// RoPE envelope of the fused head stage: 2 * max|x| * max|cos, sin| <= INT64_MAX for q ([0], [1]) and k
+// ([2], [3]) (rope.py:26-39)
+__device__ inline void check_rope_guard(const AttnDesc& d) {
+  if (!d.rope_guard) return;
+  for (int t = 0; t < 2; ++t) {
+    const u128 b = (u128)2 * d.rope_guard[2 * t] * d.rope_guard[2 * t + 1];
+    if (b > (u128)INT64_MAX) atomicOr(d.status, IMIE_EOVF);
+  }
+}
+
 struct RowInfo {
   int64_t b, h, m, kv, lv, len;   // len = keys cached for (b): the max|K|/max|V| range
 };
 
 __device__ inline RowInfo row_info(const AttnDesc& d, int64_t r) {
   RowInfo ri;
-  ri.m = r % d.M;
-  ri.h = (r / d.M) % d.H;
-  ri.b = r / (d.M * d.H);
-  ri.kv = ri.h / (d.H / d.Hkv);
+  ri.m = imie_umod32(r, d.M);
+  ri.h = imie_umod32(imie_udiv32(r, d.M), d.H);
+  ri.b = imie_udiv32(r, d.M * d.H);
+  ri.kv = imie_udiv32(ri.h, d.H / d.Hkv);
   if (d.starts) {
     ri.lv = d.starts[ri.b] + ri.m + 1;
     ri.len = d.starts[ri.b] + d.M;
@@ -71,22 +82,36 @@ __device__ inline RowInfo row_info(const AttnDesc& d, int64_t r) {
   return ri;
 }
 
+// key j -> (page index within the sequence, slot in the page); positions are below 2^31
+__device__ inline void page_split(const AttnDesc& d, int64_t j, int64_t& pi, int64_t& in) {
+  if (d.pshift >= 0) {
+    pi = j >> d.pshift;
+    in = j & ((int64_t)1 << d.pshift) - 1;
+  } else {
+    const uint32_t jj = (uint32_t)j, P = (uint32_t)d.P, q = jj / P;
+    pi = q;
+    in = jj - q * P;
+  }
+}
+
 template <typename KT>
 __device__ inline const KT* key_ptr(const AttnDesc& d, const void* pool, int64_t b, int64_t kv, int64_t j) {
-  const int64_t pg = d.pt[b * d.mp + j / d.P];
-  return (const KT*)pool + pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + (j % d.P) * d.hd;
+  int64_t pi, in;
+  page_split(d, j, pi, in);
+  const int64_t pg = d.pt[b * d.mp + pi];
+  return (const KT*)pool + pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + in * d.hd;
 }
 
 // rows of one (b, kv) group are ordered h-major: row index within the group g = (h - kv*rep) * M + m.
 __device__ inline int64_t group_row(const AttnDesc& d, int64_t b, int64_t kv, int64_t gr) {
   const int64_t rep = d.H / d.Hkv;
-  const int64_t hh = gr / d.M, m = gr % d.M;
+  const int64_t hh = imie_udiv32(gr, d.M), m = imie_umod32(gr, d.M);
   return (b * d.H + kv * rep + hh) * d.M + m;
 }
 
 // element offset of query row r = ((b * H) + h) * M + m
 __device__ inline int64_t qoff(const AttnDesc& d, int64_t r) {
-  const int64_t m = r % d.M, h = (r / d.M) % d.H, b = r / (d.M * d.H);
+  const int64_t m = imie_umod32(r, d.M), h = imie_umod32(imie_udiv32(r, d.M), d.H), b = imie_udiv32(r, d.M * d.H);
   return b * d.qsb + h * d.qsh + m * d.qsm;
 }
 
@@ -98,7 +123,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDesc d) {
   const int64_t grows = rep * d.M;
   const int64_t nrt = (grows + kRowTile - 1) / kRowTile;
   const int64_t bkv = blockIdx.x / nrt, rt = blockIdx.x % nrt;
-  const int64_t b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t j0 = (int64_t)blockIdx.y * kKeyTile;
   const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
   if (j0 >= len) return;
@@ -108,7 +133,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDesc d) {
     int64_t mmax = -1;
     for (int i = 0; i < kRowTile; ++i) {
       const int64_t gr = rt * kRowTile + i;
-      if (gr < grows) mmax = max(mmax, gr % d.M);
+      if (gr < grows) mmax = max(mmax, imie_umod32(gr, d.M));
     }
     vis = d.starts[b] + mmax + 1;
   }
@@ -116,13 +141,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDesc d) {
   const int tid = threadIdx.x;
   // stage q rows and the key tile; max|q| per row, max|K| over cached keys
   for (int i = tid; i < kRowTile * d.hd; i += blockDim.x) {
-    const int ri = i / d.hd, c = i % d.hd;
+    const int ri = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
     const int64_t gr = rt * kRowTile + ri;
     sq[ri][c] = gr < grows ? d.q[qoff(d, group_row(d, b, kv, gr)) + c] : 0;
   }
   uint64_t mk = 0;
   for (int i = tid; i < kKeyTile * d.hd; i += blockDim.x) {
-    const int ki = i / d.hd, c = i % d.hd;
+    const int ki = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
     const int64_t j = j0 + ki;
     int64_t v = 0;
     if (j < len) {
@@ -152,7 +177,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDesc d) {
     const int64_t j = j0 + ki;
     if (gr >= grows) continue;
     const int64_t r = group_row(d, b, kv, gr);
-    const int64_t lv = d.starts ? d.starts[b] + (gr % d.M) + 1 : len;
+    const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
     if (j >= lv) continue;
     uint64_t dot = 0;
     for (int c = 0; c < d.hd; ++c) dot += (uint64_t)sq[ri][c] * (uint64_t)sk[ki][c];
@@ -214,7 +239,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDesc d) {
   const int64_t grows = rep * d.M;
   const int64_t nrt = (grows + kRowTile - 1) / kRowTile;
   const int64_t bkv = blockIdx.x / nrt, rt = blockIdx.x % nrt;
-  const int64_t b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t j0 = (int64_t)blockIdx.y * kKeyTile;
   const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
   if (j0 >= len) return;
@@ -222,7 +247,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDesc d) {
   // max|V| over all cached keys (every key tile of the sequence is visited by row tile 0)
   uint64_t mv = 0;
   for (int i = tid; i < kKeyTile * d.hd; i += blockDim.x) {
-    const int ki = i / d.hd, c = i % d.hd;
+    const int ki = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
     const int64_t j = j0 + ki;
     int64_t v = 0;
     if (j < len) {
@@ -241,14 +266,14 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDesc d) {
     const int64_t j = j0 + ki;
     int64_t p = 0;
     if (gr < grows) {
-      const int64_t lv = d.starts ? d.starts[b] + (gr % d.M) + 1 : len;
+      const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
       if (j < lv) { p = d.scores[group_row(d, b, kv, gr) * d.Lmax + j]; any = 1; }
     }
     sp[ri][ki] = p;
   }
   if (!__syncthreads_or(any)) return;
   for (int i = tid; i < kRowTile * d.hd; i += blockDim.x) {
-    const int ri = i / d.hd, c = i % d.hd;
+    const int ri = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
     const int64_t gr = rt * kRowTile + ri;
     if (gr >= grows) continue;
     uint64_t acc = 0;
@@ -261,9 +286,10 @@ __global__ void attn_final_kernel(AttnDesc d) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t rows = d.B * d.H * d.M;
   if (i >= rows * d.hd) return;
-  const int64_t r = i / d.hd;
-  d.out[qoff(d, r) + i % d.hd] = (int64_t)d.acc[i] >> d.frac;
-  if (i % d.hd == 0) {
+  const int64_t r = imie_udiv32(i, d.hd), c = imie_umod32(i, d.hd);
+  if (i == 0) check_rope_guard(d);
+  d.out[qoff(d, r) + c] = (int64_t)d.acc[i] >> d.frac;
+  if (c == 0) {
     const RowInfo ri = row_info(d, r);
     const u128 pv = (u128)d.maxp[r] * d.maxv[ri.b * d.Hkv + ri.kv];
     if (pv > (u128)(INT64_MAX / ri.lv)) atomicOr(d.status, IMIE_EOVF);
@@ -294,12 +320,20 @@ __global__ void attn_init_kernel(AttnDesc d) {
 //               (32 lanes x 4 dims); chunk PV sums -> part[chunk][row][dim], chunk max|p| / max|V| -> cmp / cvm
 //   D4 final  : out = (sum over chunks of part) >> f, plus the bound checks from the chunk maxima
 // ---------------------------------------------------------------------------------------------------------
-constexpr int kDecTile = 256;
 constexpr int kMaxRep = 8;
 
 __device__ inline int64_t page_off(const AttnDesc& d, int64_t b, int64_t kv, int64_t j) {
-  const int64_t pg = d.pt[b * d.mp + j / d.P];
-  return pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + (j % d.P) * d.hd;
+  int64_t pi, in;
+  page_split(d, j, pi, in);
+  const int64_t pg = d.pt[b * d.mp + pi];
+  return pg * (d.Hkv * d.P * d.hd) + kv * d.P * d.hd + in * d.hd;
+}
+
+// element offsets of the keys r0 .. r0+63 of (b, kv) into s_off (threads 0..63; the caller synchronizes)
+__device__ inline void round_offsets(const AttnDesc& d, int64_t b, int64_t kv, int64_t r0, int64_t jend,
+                                     int64_t* s_off) {
+  const int t = threadIdx.x;
+  if (t < 64) s_off[t] = r0 + t < jend ? page_off(d, b, kv, r0 + t) : 0;
 }
 
 __device__ inline int64_t dec_len(const AttnDesc& d, int64_t b) { return d.starts ? d.starts[b] + 1 : d.lengths[b]; }
@@ -334,7 +368,8 @@ template <typename KT, int REP>
 __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
   __shared__ int64_t s_max[4][REP];
   __shared__ uint64_t s_mk[4];
-  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  __shared__ int64_t s_off[64];
+  const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t rows = d.B * d.H;
   const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
@@ -364,25 +399,39 @@ __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
   for (int r = 0; r < REP; ++r) smax[r] = INT64_MIN;
   uint64_t mk = 0;
   const int64_t jend = min(j0 + d.chunk, L);
-  for (int64_t jj = j0 + wave * 4; jj < jend; jj += 16) {
-    const int64_t j = jj + sub;
-    const bool live = j < jend;
-    int64_t kvv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (live && dims) load8<KT>((const KT*)d.K + page_off(d, b, kv, j) + l16 * 8, kvv);
+  // rounds of 64 keys: wave w owns keys 16w .. 16w+15 of the round as 4 groups of 4; all 4 groups' K slices
+  // are loaded before any dot product (4 loads in flight per lane)
+  for (int64_t r0 = j0; r0 < jend; r0 += 64) {
+    __syncthreads();                                  // previous round's offsets consumed
+    round_offsets(d, b, kv, r0, jend, s_off);
+    __syncthreads();
+    int64_t kvv[4][8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) { const uint64_t a = imie_absu64(kvv[c]); mk = a > mk ? a : mk; }
+    for (int gq = 0; gq < 4; ++gq) {
+      const int64_t j = r0 + wave * 16 + gq * 4 + sub;
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      uint64_t dot = 0;
+      for (int c = 0; c < 8; ++c) kvv[gq][c] = 0;
+      if (j < jend && dims) load8<KT>((const KT*)d.K + s_off[j - r0] + l16 * 8, kvv[gq]);
+    }
 #pragma unroll
-      for (int c = 0; c < 8; ++c) dot += (uint64_t)q[r][c] * (uint64_t)kvv[c];
+    for (int gq = 0; gq < 4; ++gq) {
+      const int64_t j = r0 + wave * 16 + gq * 4 + sub;
+      const bool live = j < jend;
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) dot += (uint64_t)__shfl_xor((int64_t)dot, o, 64);
-      if (live) {
-        int64_t sc = (int64_t)dot >> d.frac;
-        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
-        if (l16 == 0) d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] = sc;
-        smax[r] = sc > smax[r] ? sc : smax[r];
+      for (int c = 0; c < 8; ++c) { const uint64_t a = imie_absu64(kvv[gq][c]); mk = a > mk ? a : mk; }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        uint64_t dot = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dot += (uint64_t)q[r][c] * (uint64_t)kvv[gq][c];
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) dot += (uint64_t)__shfl_xor((int64_t)dot, o, 64);
+        if (live) {
+          int64_t sc = (int64_t)dot >> d.frac;
+          sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+          if (l16 == 0) d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] = sc;
+          smax[r] = sc > smax[r] ? sc : smax[r];
+        }
       }
     }
   }
@@ -417,7 +466,7 @@ template <int REP>
 __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
   __shared__ int64_t s_rmax[REP];
   __shared__ uint64_t s_z[4][REP];
-  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t rows = d.B * d.H;
   const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
@@ -427,7 +476,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     return;
   }
   // row max over the chunks that hold keys (wave r reduces row r)
-  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   for (int r = wave; r < REP; r += 4) {
     int64_t m = INT64_MIN;
     for (int64_t c = lane; c < nlive; c += 64) {
@@ -465,10 +514,11 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
 
 template <typename KT, int REP>
 __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
-  __shared__ int64_t sp[REP][kDecTile];
+  __shared__ int64_t sp[REP][64];
   __shared__ uint64_t red[4][REP][128];
+  __shared__ int64_t s_off[64];
   __shared__ uint64_t s_z[REP], s_mp[4][REP], s_mv[4];
-  const int64_t bkv = blockIdx.x, b = bkv / d.Hkv, kv = bkv % d.Hkv;
+  const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -478,12 +528,12 @@ __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
   uint64_t* part = d.part + (int64_t)blockIdx.y * rows * d.hd;
   if (j0 >= L) {                                      // an empty chunk still owns its partial slots
     for (int i = tid; i < REP * d.hd; i += blockDim.x)
-      part[(b * d.H + kv * REP + i / d.hd) * d.hd + i % d.hd] = 0;
+      part[(b * d.H + kv * REP + imie_udiv32(i, d.hd)) * d.hd + imie_umod32(i, d.hd)] = 0;
     if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
     if (tid == 0) d.cvm[blockIdx.y * d.B * d.Hkv + bkv] = 0;
     return;
   }
-  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   for (int r = wave; r < REP; r += 4) {
     uint64_t z = 0;
     for (int64_t c = lane; c < nlive; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
@@ -506,37 +556,50 @@ __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
 #pragma unroll
   for (int r = 0; r < REP; ++r) mp[r] = 0;
   uint64_t mv = 0;
-  for (int64_t t0 = j0; t0 < jend; t0 += kDecTile) {
-    const int64_t tn = min((int64_t)kDecTile, jend - t0);
-    __syncthreads();                                  // previous tile's sp fully consumed
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      const int64_t row = b * d.H + kv * REP + r;
-      int64_t p = 0;
-      if (tid < tn && Z[r] != 0) {
-        const uint64_t num = (uint64_t)d.scores[row * d.Lmax + t0 + tid] << d.frac;
-        if (Z[r] == 1) p = (int64_t)num;
-        else {
-          uint64_t qq = __umul64hi(num, rz[r]);
-          uint64_t rem = num - qq * Z[r];
-          while (rem >= Z[r]) { ++qq; rem -= Z[r]; }
-          p = (int64_t)qq;
+  // rounds of 64 keys: p for the round's keys is staged in LDS (thread t: key t % 64, rows t / 64 + 4k); wave w
+  // owns keys 16w .. 16w+15, 2 per step (lane halves), all 8 steps' V slices loaded before accumulating
+  for (int64_t t0 = j0; t0 < jend; t0 += 64) {
+    const int64_t tn = min((int64_t)64, jend - t0);
+    __syncthreads();                                  // previous round's sp / offsets fully consumed
+    round_offsets(d, b, kv, t0, jend, s_off);
+    {
+      const int kk = tid & 63;
+      for (int r = tid >> 6; r < REP; r += 4) {
+        const int64_t row = b * d.H + kv * REP + r;
+        int64_t p = 0;
+        if (kk < tn && Z[r] != 0) {
+          const uint64_t num = (uint64_t)d.scores[row * d.Lmax + t0 + kk] << d.frac;
+          if (Z[r] == 1) p = (int64_t)num;
+          else {
+            uint64_t qq = __umul64hi(num, rz[r]);
+            uint64_t rem = num - qq * Z[r];
+            while (rem >= Z[r]) { ++qq; rem -= Z[r]; }
+            p = (int64_t)qq;
+          }
         }
+        sp[r][kk] = p;
+        mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
       }
-      sp[r][tid] = p;
-      mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
     }
     __syncthreads();
-    for (int i = 2 * wave + half; i < tn; i += 8) {
-      int64_t v[4] = {0, 0, 0, 0};
-      if (dims) load4<KT>((const KT*)d.V + page_off(d, b, kv, t0 + i) + c0, v);
+    int64_t v[8][4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) { const uint64_t a = imie_absu64(v[c]); mv = a > mv ? a : mv; }
+    for (int u = 0; u < 8; ++u) {
+      const int i = wave * 16 + 2 * u + half;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[u][c] = 0;
+      if (dims && i < tn) load4<KT>((const KT*)d.V + s_off[i] + c0, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = wave * 16 + 2 * u + half;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) { const uint64_t a = imie_absu64(v[u][c]); mv = a > mv ? a : mv; }
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
-        const uint64_t pp = (uint64_t)sp[r][i];
+        const uint64_t pp = (uint64_t)sp[r][i];      // 0 beyond tn (and v is 0 there)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] += pp * (uint64_t)v[c];
+        for (int c = 0; c < 4; ++c) acc[r][c] += pp * (uint64_t)v[u][c];
       }
     }
   }
@@ -574,33 +637,58 @@ __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
   }
 }
 
-// thread per (row, dim): sums the chunk partials (8 independent accumulators for load ILP)
+// WG = 32 consecutive outputs (within one row) x 8 chunk groups: thread (o, g) sums chunks g, g + 8, ... of
+// output o (all loads issued together), the 8 group sums are added through LDS. The first WG of a row also
+// reduces the chunk maxima for the bound checks (same split).
 __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ uint64_t s_sum[8][32];
+  __shared__ uint64_t s_mx[3][8];
+  const int t = threadIdx.x, o = t & 31, g = t >> 5;
+  const int64_t i = (int64_t)blockIdx.x * 32 + o;
   const int64_t rows = d.B * d.H;
-  if (i >= rows * d.hd) return;
-  const int64_t r = i / d.hd;
-  const int64_t b = r / d.H, kv = (r % d.H) / (d.H / d.Hkv);
+  const int64_t r = imie_udiv32((int64_t)blockIdx.x * 32, d.hd);
+  const int64_t b = imie_udiv32(r, d.H), kv = imie_udiv32(imie_umod32(r, d.H), d.H / d.Hkv);
   const int64_t L = dec_len(d, b);
-  const int64_t nlive = (L + d.chunk - 1) / d.chunk;
+  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   const int64_t stride = rows * d.hd;
-  uint64_t s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int64_t c = 0;
-  for (; c + 8 <= nlive; c += 8) {
+  uint64_t acc = 0;
+  if (i < rows * d.hd) {
+    uint64_t s4[4] = {0, 0, 0, 0};
+    int64_t c = g;
+    for (; c + 24 < nlive; c += 32) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s[u] += d.part[(c + u) * stride + i];
+      for (int u = 0; u < 4; ++u) s4[u] += d.part[(c + 8 * u) * stride + i];
+    }
+    for (; c < nlive; c += 8) s4[0] += d.part[c * stride + i];
+    acc = s4[0] + s4[1] + s4[2] + s4[3];
   }
-  for (; c < nlive; ++c) s[0] += d.part[c * stride + i];
-  const uint64_t tot = s[0] + s[1] + s[2] + s[3] + s[4] + s[5] + s[6] + s[7];
-  d.out[qoff(d, r) + i % d.hd] = (int64_t)tot >> d.frac;
-  if (i % d.hd == 0 && L > 0) {
+  s_sum[g][o] = acc;
+  const bool head = imie_umod32((int64_t)blockIdx.x * 32, d.hd) == 0;
+  if (head && o == 0) {
     uint64_t mp = 0, mv = 0, mk = 0;
-    for (int64_t cc = 0; cc < nlive; ++cc) {
-      const uint64_t a = d.cmp[cc * rows + r], v = d.cvm[cc * d.B * d.Hkv + b * d.Hkv + kv],
-                     k = d.ckm[cc * d.B * d.Hkv + b * d.Hkv + kv];
+    for (int64_t c = g; c < nlive; c += 8) {
+      const uint64_t a = d.cmp[c * rows + r], v = d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv],
+                     k = d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv];
       mp = a > mp ? a : mp;
       mv = v > mv ? v : mv;
       mk = k > mk ? k : mk;
+    }
+    s_mx[0][g] = mp; s_mx[1][g] = mv; s_mx[2][g] = mk;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && t == 0) check_rope_guard(d);
+  if (t < 32 && i < rows * d.hd) {
+    uint64_t tot = 0;
+#pragma unroll
+    for (int gg = 0; gg < 8; ++gg) tot += s_sum[gg][t];
+    d.out[qoff(d, r) + imie_umod32(i, d.hd)] = (int64_t)tot >> d.frac;
+  }
+  if (head && t == 0 && L > 0) {
+    uint64_t mp = 0, mv = 0, mk = 0;
+    for (int gg = 0; gg < 8; ++gg) {
+      mp = s_mx[0][gg] > mp ? s_mx[0][gg] : mp;
+      mv = s_mx[1][gg] > mv ? s_mx[1][gg] : mv;
+      mk = s_mx[2][gg] > mk ? s_mx[2][gg] : mk;
     }
     const u128 pv = (u128)mp * mv;
     if (pv > (u128)(INT64_MAX / L)) atomicOr(d.status, IMIE_EOVF);
@@ -611,8 +699,13 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
 
 // decode chunking: ~2048 workgroups over the (b, kv) groups, chunks of >= 64 keys (multiple of 64)
 void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t* nch) {
+  static const int64_t target = [] {               // workgroups to aim for (IMIE_DEC_WGS overrides, tuning)
+    const char* e = getenv("IMIE_DEC_WGS");
+    const long v = e ? atol(e) : 0;
+    return v > 0 ? (int64_t)v : (int64_t)2048;
+  }();
   const int64_t groups = B * Hkv;
-  int64_t want = 2048 / (groups > 0 ? groups : 1);
+  int64_t want = target / (groups > 0 ? groups : 1);
   if (want < 1) want = 1;
   int64_t c = (Lmax + want - 1) / want;
   c = ((c + 63) / 64) * 64;
@@ -623,6 +716,11 @@ void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t*
 }
 
 }  // namespace
+
+static void attn_set_pshift(AttnDesc& d) {
+  d.pshift = -1;
+  if (d.P > 0 && (d.P & (d.P - 1)) == 0) { d.pshift = 0; while (((int64_t)1 << d.pshift) < d.P) ++d.pshift; }
+}
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax) {
   const int64_t rows = B * H * M;
@@ -655,6 +753,7 @@ void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
 
 int imie_attention_launch(AttnDesc d, hipStream_t st) {
   if (d.frac < 1 || d.frac > 29 || d.H % d.Hkv != 0 || d.hd > 128 || d.hd <= 0) return IMIE_EARG;
+  attn_set_pshift(d);
   const int64_t sh = 16 - d.frac;
   d.log2e = sh >= 0 ? (94548 >> sh) : ((int64_t)94548 << -sh);
   const int64_t a = (((int64_t)d.frac + 2) << (2 * d.frac)) / d.log2e, bb = ((int64_t)1 << 62) / d.log2e;
@@ -666,7 +765,7 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
   const int64_t ninit = rows * d.hd > d.B * d.Hkv ? rows * d.hd : d.B * d.Hkv;
   imie_prof_mark(IMIE_K_ATTN, st, true);
   const int64_t rp = d.H / d.Hkv;
-  if (d.M == 1 && (rp == 1 || rp == 2 || rp == 4 || rp == 8) && d.hd <= 128 && d.hd % 8 == 0) {
+  if (d.M == 1 && (rp == 1 || rp == 2 || rp == 4 || rp == 8) && d.hd <= 128 && d.hd % 32 == 0) {
     dec_geometry(d.B, d.Hkv, d.Lmax, &d.chunk, &d.nch);
     const dim3 gd((unsigned)(d.B * d.Hkv), (unsigned)d.nch);
     const int rep = (int)rp;
@@ -685,7 +784,7 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
 #undef IMIE_DEC_R
 #undef IMIE_DEC
     IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(dec_final_kernel, dim3((unsigned)((rows * d.hd + 255) / 256)), dim3(256), 0, st, d);
+    hipLaunchKernelGGL(dec_final_kernel, dim3((unsigned)((rows * d.hd + 31) / 32)), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
     imie_prof_mark(IMIE_K_ATTN, st, false);
     return IMIE_OK;
@@ -838,6 +937,7 @@ int imie_attention_scores_probe(const int64_t* q, const int64_t* k, int64_t H, i
   d.starts = (const int64_t*)g_aws.meta.p;
   d.Lmax = L; d.frac = (int)frac; d.inv_sqrt = inv_sqrt;
   d.status = (int*)g_aws.status.p;
+  attn_set_pshift(d);
   imie_attn_bind_scratch(d, g_aws.scratch.p);
   const int64_t rows = H * M, grows = (H / Hkv) * M;
   const int64_t nrt = (grows + kRowTile - 1) / kRowTile, nkt = (L + kKeyTile - 1) / kKeyTile;

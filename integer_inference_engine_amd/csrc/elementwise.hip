@@ -40,7 +40,14 @@ __device__ inline int64_t sigmoid_fixed(int64_t x, int frac, int64_t log2e, int6
   const int64_t e1 = exp2_neg_fixed((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> frac, frac);
   const int64_t z = e0 + e1;
   if (z == 0) return 0;
-  return (int64_t)(((uint64_t)e1 << frac) / (uint64_t)z);   // e1 << frac >= 0 and fits (e1 <= c0 + c2)
+  const uint64_t num = (uint64_t)e1 << frac;               // e1 << frac >= 0 and fits (e1 <= c0 + c2)
+  if (num < ((uint64_t)1 << 52)) {                         // exact double quotient estimate, +-1 integer fix
+    uint64_t q = (uint64_t)((double)num / (double)z);
+    if (q * (uint64_t)z > num) --q;
+    else if (num - q * (uint64_t)z >= (uint64_t)z) ++q;
+    return (int64_t)q;
+  }
+  return (int64_t)(num / (uint64_t)z);
 }
 
 __global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t* __restrict__ up, int64_t n, int frac,
@@ -50,6 +57,30 @@ __global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t*
   const int64_t g = gate[i];
   const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
   out[i] = up ? (int64_t)((uint64_t)silu * (uint64_t)up[i]) >> frac : silu;
+}
+
+// silu_mul for one (token, 512-slab): thread per element into LDS, then wave 0 builds the slab's digit table
+__global__ __launch_bounds__(512) void silu_mul_prep_kernel(const int64_t* __restrict__ gate,
+                                                            const int64_t* __restrict__ up, int64_t n, int frac,
+                                                            int64_t log2e, int64_t dclip, int64_t* __restrict__ out,
+                                                            imie_q1::Q1PrepOut po) {
+  __shared__ int64_t sh[512];
+  const int64_t sl = blockIdx.x, t = blockIdx.y;
+  const int64_t p = sl * 512 + threadIdx.x;
+  int64_t h = 0;
+  if (p < n) {
+    const int64_t g = gate[t * n + p];
+    const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
+    h = (int64_t)((uint64_t)silu * (uint64_t)up[t * n + p]) >> frac;
+    out[t * n + p] = h;
+  }
+  sh[threadIdx.x] = h;
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  int64_t v[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = sh[imie_q1::prep_pos(threadIdx.x, 0, q)];
+  imie_q1::prep_slab(v, po, t, sl);
 }
 
 __global__ void add_kernel(int64_t* __restrict__ x, const int64_t* __restrict__ y, int64_t n) {
@@ -181,6 +212,18 @@ int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int6
   silu_consts(frac, &log2e, &dclip);
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gate, up, n, (int)frac,
                      log2e, dclip, out);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_silu_mul_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
+                              int64_t* out, const imie_q1::Q1PrepOut& po, hipStream_t st) {
+  if (T <= 0) return IMIE_OK;
+  if (!up || n != po.nb * 128) return IMIE_EARG;
+  int64_t log2e, dclip;
+  silu_consts(frac, &log2e, &dclip);
+  hipLaunchKernelGGL(silu_mul_prep_kernel, dim3((unsigned)po.nslabs, (unsigned)T), dim3(512), 0, st, gate, up, n,
+                     (int)frac, log2e, dclip, out, po);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

@@ -11,6 +11,7 @@ struct AttnDesc {
   int kv32;                        // 1: int32 KV elements, 0: int64
   const int64_t* pt;               // page table [B][mp]
   int64_t P, mp;                   // tokens per page, pages per sequence
+  int pshift;                      // log2(P) when P is a power of two, else -1 (set by the launcher)
   const int64_t* lengths;          // decode: keys per sequence (starts == nullptr)
   const int64_t* starts;           // causal: first new position per sequence (M new rows)
   int64_t Lmax;                    // score row stride (>= max visible keys)
@@ -18,6 +19,7 @@ struct AttnDesc {
   int64_t inv_sqrt, log2e, dclip;
   int64_t* out;
   int* status;
+  const uint64_t* rope_guard;      // optional: q/k RoPE envelope maxima (4 x u64), checked by the final kernel
   // scratch (imie_attn_bind_scratch)
   int64_t* scores;
   uint64_t* acc;

@@ -1,6 +1,7 @@
 // Internal launchers shared by the C-ABI files (device pointers, asynchronous on `st`).
 #pragma once
 #include "imie_common.h"
+#include "imie_q1prep.h"
 
 // status word bits (device int, OR-ed by kernels): IMIE_EOVF (2) attention / RoPE / int32-KV envelope,
 // IMIE_ERMS (4) RMSNorm envelope.
@@ -19,8 +20,21 @@ struct Q1Ws {
 };
 // Up to 3 weights with the same n_blocks applied to the same x in one prep + one matvec launch (wk == nullptr:
 // the library's shared workspace).
+// prepped != 0: the digit table is already in wk (written by a fused producer through imie_q1_prep_target) and
+// the non-accumulated outputs are already zero.
 int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int64_t T, int64_t frac,
-                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st);
+                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st, int prepped = 0);
+// Size wk for T tokens of nb blocks and describe it for a producer that writes the digit table itself.
+int imie_q1_prep_target(Q1Ws* wk, int64_t nb, int64_t T, imie_q1::Q1PrepOut* po);
+// RMSNorm rows of cols = nb * 128 (<= 4096) that also write the Q1 digit table of the output (po) and clear
+// the zero list, for a following matvec launched with prepped = 1.
+int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                             const int64_t* gain, int64_t* out, int* status, const imie_q1::Q1PrepOut& po,
+                             const imie_q1::Q1Zero& zero, hipStream_t st);
+// h = silu(gate) * up >> frac (as imie_silu_mul_launch) for T rows of n = nb * 128 that also writes the digit
+// table of h (po).
+int imie_silu_mul_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
+                              int64_t* out, const imie_q1::Q1PrepOut& po, hipStream_t st);
 
 // NeoX RoPE on rows x (rows, nh, hd); row r uses table row pos[r] (pos == nullptr: pos0 + r).
 // The fail-loud envelope 2*max|x|*max|cos,sin| <= INT64_MAX is checked exactly via `guard` scratch
@@ -44,3 +58,19 @@ constexpr int kArgmaxParts = 256;
 inline size_t imie_argmax_scratch_bytes(int64_t rows) { return (size_t)rows * kArgmaxParts * 16; }
 int imie_argmax_launch(const int64_t* logits, int64_t rows, int64_t cols, int64_t* ids, int64_t* scratch,
                        hipStream_t st);
+
+// Fused head RMSNorm + RoPE + KV-cache append for rows = B * M new rows (see qkhead.hip). q, k, v: projection
+// outputs (rows, H|Hkv, hd); qo receives the rotated q; k (rotated) and v go to the paged cache at pos[row].
+struct QkHeadArgs {
+  const int64_t *q, *k, *v;
+  int64_t* qo;
+  const int64_t *qng, *kng, *pos, *cos, *sin;
+  int64_t rows, H, Hkv, hd, M, eps;
+  int frac;
+  const int64_t* pt;
+  int64_t P, mp;
+  void *kpool, *vpool;
+  uint64_t* guard;                 // 4 x u64, zeroed before the launch (RoPE envelope maxima)
+  int* status;
+};
+int imie_qk_head_launch(const QkHeadArgs& a, int kv32, hipStream_t st);

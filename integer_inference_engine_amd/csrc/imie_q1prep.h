@@ -1,0 +1,78 @@
+// Q1_0 activation "prep": the balanced base-256 digit table of x that the MFMA matvec consumes, computed by one
+// full wave per (token t, 512-wide slab). Shared by the stand-alone prep kernel and by the producers that fuse it
+// into their epilogue (RMSNorm, SiLU * up), so a matvec can start from a table written by the kernel before it.
+//
+// Lane layout: g = lane >> 4 (block of the slab), s = lane & 7, dh = (lane >> 3) & 1; the lane's 8 positions are
+// block * 128 + 32 d + 8 c + s for d in {2 dh, 2 dh + 1}, c = 0..3. Outputs per (t, slab): the limb count L (from
+// the slab's max|x|), per-block totals, and xq[t][l][block][s] (uint4: dword d packs the digits of positions
+// 32 d + 8 c + s as bytes c).
+#pragma once
+#include "imie_common.h"
+
+namespace imie_q1 {
+
+constexpr int kSlabBlocks = 4;     // 128-blocks per slab (= K 512 per wave step)
+constexpr int kMaxLimbs = 8;
+constexpr int kMaxSegs = 3;        // weights sharing one activation in a single matvec launch
+
+struct Q1PrepOut {                 // where a prep writes its table (sized for T tokens of nb blocks)
+  uint32_t* xq;
+  int64_t* totals;
+  int* lslab;
+  int64_t nb, nbp, nslabs;
+};
+
+struct Q1Zero {                    // outputs a producer clears before a K-split matvec adds into them
+  int64_t* p[kMaxSegs];
+  int64_t n[kMaxSegs];
+  int cnt;
+};
+
+__device__ inline int64_t prep_pos(int lane, int64_t sl, int q) {
+  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
+  const int d = 2 * dh + (q >> 2), c = q & 3;
+  return (sl * kSlabBlocks + g) * 128 + 32 * d + 8 * c + s;
+}
+
+// v[q] = x at prep_pos(lane, sl, q) (0 for blocks >= nb); every lane of the wave participates.
+__device__ inline void prep_slab(int64_t v[8], const Q1PrepOut& po, int64_t t, int64_t sl) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
+  const int64_t blk = sl * kSlabBlocks + g;
+  uint64_t mx = 0;
+  int64_t part = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint64_t a = imie_absu64(v[q]);
+    mx = a > mx ? a : mx;
+    part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
+  }
+  mx = imie_wave_max_u64(mx);
+  const int L = imie_limbs_needed(mx);
+  // block total: sum over the 16 lanes of group g (xor 1,2,4,8 stays inside the group)
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
+  if ((lane & 15) == 0) po.totals[t * po.nbp + blk] = part;
+  if (lane == 0) po.lslab[t * po.nslabs + sl] = L;
+  for (int l = 0; l < L; ++l) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t dig = ((v[q] + 128) & 255) - 128;          // balanced digit in [-128, 127]
+      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;  // exact: v - dig is a multiple of 256
+      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
+      if (q < 4) w0 |= byte; else w1 |= byte;
+    }
+    uint32_t* dst = po.xq + ((((t * kMaxLimbs + l) * po.nbp + blk) * 8 + s) * 4);
+    dst[2 * dh] = w0;
+    dst[2 * dh + 1] = w1;
+  }
+}
+
+// workgroup `wg` of `nwg` clears its share of the zero list (threads tid of nthreads)
+__device__ inline void zero_share(const Q1Zero& z, int64_t wg, int64_t nwg, int tid, int nthreads) {
+  for (int i = 0; i < z.cnt; ++i)
+    for (int64_t e = wg * nthreads + tid; e < z.n[i]; e += nwg * nthreads) z.p[i][e] = 0;
+}
+
+}  // namespace imie_q1

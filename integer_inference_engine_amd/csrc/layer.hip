@@ -44,24 +44,6 @@ int fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t st) {
   return IMIE_OK;
 }
 
-template <typename KT>
-__global__ void kv_append_kernel(const int64_t* __restrict__ k, const int64_t* __restrict__ v,
-                                 const int64_t* __restrict__ pos, int64_t rows, int64_t M, int64_t Hkv, int64_t hd,
-                                 const int64_t* __restrict__ pt, int64_t P, int64_t mp, KT* __restrict__ kpool,
-                                 KT* __restrict__ vpool, int* __restrict__ status) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * Hkv * hd) return;
-  const int64_t c = i % hd, kv = (i / hd) % Hkv, r = i / (hd * Hkv);
-  const int64_t b = r / M, j = pos[r];
-  const int64_t off = pt[b * mp + j / P] * (Hkv * P * hd) + kv * P * hd + (j % P) * hd + c;
-  const int64_t kval = k[i], vval = v[i];
-  if (sizeof(KT) == 4) {
-    if (kval != (int64_t)(int32_t)kval || vval != (int64_t)(int32_t)vval) atomicOr(status, IMIE_EOVF);
-  }
-  kpool[off] = (KT)kval;
-  vpool[off] = (KT)vval;
-}
-
 struct LayerW {
   int64_t w[7];                       // wq, wk, wv, wo, w1, wu, w2 Q1 handles
   const int64_t *n1g, *n2g, *qng, *kng;
@@ -144,10 +126,35 @@ int net_ensure(Net& n, int64_t M, int64_t lmax) {
       n.qn.ensure((size_t)(rows * qd) * 8) || n.kn.ensure((size_t)(rows * kd) * 8) ||
       n.att.ensure((size_t)(rows * qd) * 8) || n.gate.ensure((size_t)(rows * n.dff) * 8) ||
       n.up.ensure((size_t)(rows * n.dff) * 8) || n.h.ensure((size_t)(rows * n.dff) * 8) ||
-      n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure(64) ||
+      n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure((size_t)n.nl * 32) ||
       n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)))
     return IMIE_EARG;
   return IMIE_OK;
+}
+
+// RMSNorm of `rows` rows of x (gain g) into xn, then the matvec(s) `hs` of xn into outs. When d is a multiple of
+// 128 up to 4096, the norm kernel also writes the matvec's digit table and clears its outputs (one kernel fewer).
+int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, int64_t* xn, const int64_t* hs,
+                     int cnt, int64_t* const* outs, hipStream_t st) {
+  int* status = (int*)n.status.p;
+  if (n.d % 128 == 0 && n.d <= 4096) {
+    imie_q1::Q1PrepOut po;
+    int rc = imie_q1_prep_target(&n.q1w, n.d / 128, rows, &po);
+    if (rc) return rc;
+    imie_q1::Q1Zero z = {};
+    z.cnt = cnt;
+    for (int i = 0; i < cnt; ++i) {
+      int64_t N = 0, nb = 0;
+      if (imie_q1_dims(hs[i], &N, &nb)) return IMIE_EARG;
+      z.p[i] = outs[i];
+      z.n[i] = rows * N;
+    }
+    if ((rc = imie_rmsnorm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, po, z, st))) return rc;
+    return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, 1);
+  }
+  int rc = imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, st);
+  if (rc) return rc;
+  return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st);
 }
 
 // All layers over M new tokens per sequence; positions come from the device buffers n.pos (B*M) and n.starts
@@ -164,49 +171,46 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
   const int64_t* posd = (const int64_t*)n.pos.p;
   uint64_t* guard = (uint64_t*)n.guard.p;
   int* status = (int*)n.status.p;
+  CK(fill_i64((int64_t*)guard, 4 * n.nl, 0, st));   // per-layer RoPE envelope maxima
   for (int64_t l = 0; l < n.nl; ++l) {
     const LayerW& L = n.layers[(size_t)l];
-    CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n1g, xn, status, st));
     {
       int64_t* outs[3] = {q, k, v};
-      CK(imie_q1_launch_multi(L.w, 3, xn, rows, n.frac, outs, 0, &n.q1w, st));
+      CK(norm_into_matvec(n, x, rows, L.n1g, xn, L.w, 3, outs, st));
     }
-    CK(imie_rmsnorm_launch(q, rows * n.H, n.hd, n.frac, n.eps, L.qng, qn, status, st));
-    CK(imie_rmsnorm_launch(k, rows * n.Hkv, n.hd, n.frac, n.eps, L.kng, kn, status, st));
-    CK(fill_i64((int64_t*)guard, 2, 0, st));
-    CK(imie_rope_launch(qn, rows, n.H, n.hd, posd, 0, n.cos, n.sin, n.frac, q, guard, st));
-    CK(imie_rope_guard_check(guard, status, st));
-    CK(fill_i64((int64_t*)guard, 2, 0, st));
-    CK(imie_rope_launch(kn, rows, n.Hkv, n.hd, posd, 0, n.cos, n.sin, n.frac, k, guard, st));
-    CK(imie_rope_guard_check(guard, status, st));
-    const int64_t na = rows * kd;
-    if (n.kv32)
-      hipLaunchKernelGGL(kv_append_kernel<int32_t>, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, st, k, v, posd,
-                         rows, M, n.Hkv, n.hd, n.pt, n.P, n.mp, (int32_t*)n.kpool[(size_t)l],
-                         (int32_t*)n.vpool[(size_t)l], status);
-    else
-      hipLaunchKernelGGL(kv_append_kernel<int64_t>, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, st, k, v, posd,
-                         rows, M, n.Hkv, n.hd, n.pt, n.P, n.mp, (int64_t*)n.kpool[(size_t)l],
-                         (int64_t*)n.vpool[(size_t)l], status);
-    IMIE_HIP(hipGetLastError());
+    {
+      QkHeadArgs a = {};
+      a.q = q; a.k = k; a.v = v; a.qo = qn;
+      a.qng = L.qng; a.kng = L.kng; a.pos = posd; a.cos = n.cos; a.sin = n.sin;
+      a.rows = rows; a.H = n.H; a.Hkv = n.Hkv; a.hd = n.hd; a.M = M; a.eps = n.eps; a.frac = (int)n.frac;
+      a.pt = n.pt; a.P = n.P; a.mp = n.mp; a.kpool = n.kpool[(size_t)l]; a.vpool = n.vpool[(size_t)l];
+      a.guard = guard + 4 * l; a.status = status;
+      CK(imie_qk_head_launch(a, n.kv32, st));
+    }
     AttnDesc d = {};
     d.B = n.B; d.H = n.H; d.Hkv = n.Hkv; d.hd = n.hd; d.M = M;
     d.qsb = M * qd; d.qsh = n.hd; d.qsm = qd;
-    d.q = q; d.K = n.kpool[(size_t)l]; d.V = n.vpool[(size_t)l]; d.kv32 = n.kv32;
+    d.q = qn; d.K = n.kpool[(size_t)l]; d.V = n.vpool[(size_t)l]; d.kv32 = n.kv32;
     d.pt = n.pt; d.P = n.P; d.mp = n.mp;
     d.starts = (const int64_t*)n.starts.p; d.lengths = nullptr;
     d.Lmax = lmax; d.frac = (int)n.frac; d.inv_sqrt = n.inv_sqrt;
-    d.out = att; d.status = status;
+    d.out = att; d.status = status; d.rope_guard = guard + 4 * l;
     imie_attn_bind_scratch(d, n.attn.p);
     CK(imie_attention_launch(d, st));
     CK(imie_q1_launch_multi(&L.w[3], 1, att, rows, n.frac, &x, 1, &n.q1w, st));
-    CK(imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, L.n2g, xn, status, st));
     {
       int64_t* outs[2] = {gate, up};
-      CK(imie_q1_launch_multi(&L.w[4], 2, xn, rows, n.frac, outs, 0, &n.q1w, st));
+      CK(norm_into_matvec(n, x, rows, L.n2g, xn, &L.w[4], 2, outs, st));
     }
-    CK(imie_silu_mul_launch(gate, up, rows * n.dff, n.frac, hh, st));
-    CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st));
+    if (n.dff % 128 == 0) {
+      imie_q1::Q1PrepOut po;
+      CK(imie_q1_prep_target(&n.q1w, n.dff / 128, rows, &po));
+      CK(imie_silu_mul_prep_launch(gate, up, rows, n.dff, n.frac, hh, po, st));
+      CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st, 1));
+    } else {
+      CK(imie_silu_mul_launch(gate, up, rows * n.dff, n.frac, hh, st));
+      CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st));
+    }
   }
 #undef CK
   return IMIE_OK;
@@ -262,9 +266,7 @@ int net_head(Net& n, const int64_t* x, const std::vector<int64_t>& rows_idx, int
                               hipMemcpyDeviceToDevice, st));
     src = (const int64_t*)n.lastx.p;
   }
-  int rc = imie_rmsnorm_launch(src, R, n.d, n.frac, n.eps, n.finalg, (int64_t*)n.n.p, (int*)n.status.p, st);
-  if (rc) return rc;
-  rc = imie_q1_launch_multi(&n.out_head, 1, (const int64_t*)n.n.p, R, n.frac, &logits, 0, &n.q1w, st);
+  int rc = norm_into_matvec(n, src, R, n.finalg, (int64_t*)n.n.p, &n.out_head, 1, &logits, st);
   if (rc) return rc;
   if (ids) {
     if (n.amx.ensure(imie_argmax_scratch_bytes(R))) return IMIE_EARG;

@@ -6,98 +6,52 @@
 // One workgroup per row; the 128-bit sum is reduced by wave shuffles and LDS, the isqrt / mean run on one lane.
 #include "imie_common.h"
 #include "imie_kernels.h"
+#include "imie_fixed.h"
+#include <stdlib.h>
 
 namespace {
 
+using namespace imie_fx;
 typedef unsigned __int128 u128;
 
-__device__ inline u128 div_u128_u32(u128 v, uint32_t d) {
-  const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
-  const uint64_t qh = hi / d, r0 = hi % d;
-  const uint64_t mid = (r0 << 32) | (lo >> 32);
-  const uint64_t qm = mid / d, r1 = mid % d;
-  const uint64_t low = (r1 << 32) | (lo & 0xFFFFFFFFu);
-  const uint64_t ql = low / d;
-  return ((u128)qh << 64) | ((u128)qm << 32) | (u128)ql;
-}
-
-// floor(sqrt(v)) for v < 2^128: a double-precision estimate narrowed by an exact integer binary search over
-// [est - 2^12, est + 2^12] (the estimate is within ~2^-52 * 2^64 of the root); full 64-step search otherwise.
-__device__ inline uint64_t isqrt_u128(u128 v) {
-  const double fv = (double)(uint64_t)(v >> 64) * 18446744073709551616.0 + (double)(uint64_t)v;
-  double fe = sqrt(fv);
-  uint64_t est = fe >= 18446744073709549568.0 ? ~(uint64_t)0 : (uint64_t)fe;
-  uint64_t lo = est > 4096 ? est - 4096 : 0;
-  uint64_t hi = est < ~(uint64_t)0 - 4096 ? est + 4096 : ~(uint64_t)0;
-  auto sq_le = [&](uint64_t c) { return (u128)c * c <= v; };
-  if (!sq_le(lo) || (hi != ~(uint64_t)0 && sq_le(hi + 1))) { lo = 0; hi = ~(uint64_t)0; }
-  while (lo < hi) {                                 // invariant: lo^2 <= v, answer in [lo, hi]
-    const uint64_t mid = lo + (hi - lo + 1) / 2;
-    if (sq_le(mid)) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
-// floor(num / d) for |num| < 2^127 given as sign + 128-bit magnitude, d > 0 (bitwise long division; rare path)
-__device__ inline int64_t floor_div_mag128(bool neg, u128 mag, uint64_t d, bool* fits) {
-  u128 q = 0, r = 0;
-  for (int b = 127; b >= 0; --b) {
-    r = (r << 1) | ((mag >> b) & 1);
-    if (r >= d) { r -= d; q |= (u128)1 << b; }
-  }
-  if (neg && r != 0) q += 1;
-  if (!neg) { *fits = q <= (u128)INT64_MAX; return (int64_t)(uint64_t)q; }
-  *fits = q <= ((u128)1 << 63);
-  return (int64_t)(0 - (uint64_t)q);
-}
-
-// n = floor((x << frac) / rms); *fits false if the quotient leaves int64. rinv = floor((2^64 - 1) / rms): for
-// num < 2^64, umulhi(num, rinv) is at most 2 below floor(num / rms), fixed by the correction loop.
-__device__ inline int64_t norm_elem(int64_t x, int frac, uint64_t rms, uint64_t rinv, bool* fits) {
-  const uint64_t ax = imie_absu64(x);
-  const bool neg = x < 0;
-  *fits = true;
-  if (frac < 63 && ax < ((uint64_t)1 << (63 - frac))) {
-    const uint64_t num = ax << frac;
-    uint64_t q = __umul64hi(num, rinv);
-    uint64_t r = num - q * rms;
-    while (r >= rms) { ++q; r -= rms; }
-    if (neg) return -(int64_t)(q + (r != 0));
-    return (int64_t)q;
-  }
-  return floor_div_mag128(neg, (u128)ax << frac, rms, fits);
-}
-
-// 128-bit sums across a wave: (hi, lo) limbs with the carry folded into hi
-__device__ inline void wave_sum_u128(uint64_t& hi, uint64_t& lo, int& bad) {
+// One workgroup (nt = 64..256 threads) per row. Rows of up to kNormPer * nt columns are loaded once and kept in
+// registers (x and gain); longer rows are re-read. Each wave reduces its partials by shuffles; after one barrier
+// every wave combines the per-wave partials from LDS itself (no single-lane serial phase). Steps: (1) 128-bit sum
+// of squares -> rms, (2) n = floor((x << f) / rms) with max|n| and max|gain| for the envelope, (3) y = (n * g) >> f.
+// Q1 digit table of a row staged in LDS: wave w takes slabs w, w + nw, ...; then this workgroup's zero-list share.
+__device__ inline void prep_row(const int64_t* s_y, int64_t row, const imie_q1::Q1PrepOut& po,
+                                const imie_q1::Q1Zero& zero, int tid, int nt) {
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+  const int64_t cols = po.nb * 128;
+  for (int64_t sl = wave; sl < po.nslabs; sl += nw) {
+    int64_t v[8];
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint64_t l2 = __shfl_xor(lo, o, 64), h2 = __shfl_xor(hi, o, 64);
-    const int b2 = __shfl_xor(bad, o, 64);
-    const uint64_t nl = lo + l2;
-    const uint64_t c = nl < lo ? 1 : 0;
-    const uint64_t nh = hi + h2;
-    bad |= b2 | (nh < hi ? 1 : 0) | (nh + c < nh ? 1 : 0);
-    hi = nh + c;
-    lo = nl;
+    for (int q = 0; q < 8; ++q) {
+      const int64_t p = imie_q1::prep_pos(lane, sl, q);
+      v[q] = p < cols ? s_y[p] : 0;
+    }
+    imie_q1::prep_slab(v, po, row, sl);
   }
+  imie_q1::zero_share(zero, row, (int64_t)gridDim.x, tid, nt);
 }
 
-// One workgroup (nt threads, 64..1024) per row; per-thread partials reduced by wave shuffles, then across the
-// waves through LDS. Rows of up to 4 * nt columns are loaded once and kept in registers (x and gain); longer rows
-// are re-read. Steps: (1) 128-bit sum of squares; (2) n = floor((x << f) / rms) with max|n| and max|gain| for
-// the envelope; (3) y = (n * gain) >> f.
-constexpr int kNormPer = 4;
+// NT threads with PER cached columns each (the per-thread serial work is what bounds a single-row launch, so
+// wide rows get many threads). PREP: the row (cols = nb * 128 <= NT * PER) is also staged in LDS and turned
+// into the Q1 digit table (one wave per 512-slab), and the workgroups clear the zero list of the next matvec.
+constexpr int kPrepCols = 4096;
 
-__global__ __launch_bounds__(1024) void rmsnorm_kernel(const int64_t* __restrict__ x, int64_t cols, int frac,
-                                                        int64_t eps, const int64_t* __restrict__ gain,
-                                                        int64_t* __restrict__ out, int* __restrict__ status) {
-  __shared__ uint64_t s_hi[16], s_lo[16], s_mn[16], s_mg[16];
-  __shared__ int s_bad[16];
-  __shared__ uint64_t s_rms, s_rinv;
-  __shared__ int s_ok;
+template <bool PREP, int NT, int kNormPer>
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__ x, int64_t cols, int frac,
+                                                      int64_t eps, const int64_t* __restrict__ gain,
+                                                      int64_t* __restrict__ out, int* __restrict__ status,
+                                                      imie_q1::Q1PrepOut po, imie_q1::Q1Zero zero) {
+  constexpr int NW = NT / 64;
+  __shared__ int64_t s_y[PREP ? kPrepCols : 1];
+  __shared__ uint64_t s_hi[NW], s_lo[NW], s_mn[NW], s_mg[NW];
+  __shared__ int s_bad[NW], s_fit[NW];
   const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+  const int tid = threadIdx.x, nt = NT, lane = tid & 63, wave = tid >> 6, nw = NW;
   const int64_t* xr = x + row * cols;
   const bool cached = cols <= (int64_t)kNormPer * nt;
   int64_t xv[kNormPer], gv[kNormPer];
@@ -131,29 +85,21 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const int64_t* __restrict
   wave_sum_u128(hi, lo, bad);
   if (lane == 0) { s_hi[wave] = hi; s_lo[wave] = lo; s_bad[wave] = bad; }
   __syncthreads();
-  if (tid == 0) {
-    uint64_t H = 0, Lo = 0;
-    int B = 0;
-    for (int w = 0; w < nw; ++w) {
-      const uint64_t nl = Lo + s_lo[w];
-      const uint64_t cy = nl < Lo ? 1 : 0;
-      const uint64_t nh = H + s_hi[w];
-      B |= s_bad[w] | (nh < H ? 1 : 0) | (nh + cy < nh ? 1 : 0);
-      H = nh + cy;
-      Lo = nl;
-    }
-    uint64_t rms = 0;
-    if (!B) {
-      const u128 mean = div_u128_u32(((u128)H << 64) | Lo, (uint32_t)cols);
-      if (mean <= ~(u128)0 - (u128)(uint64_t)eps) rms = isqrt_u128(mean + (u128)(uint64_t)eps);
-    }
-    s_rms = rms;
-    s_rinv = rms ? (~(uint64_t)0) / rms : 0;
-    if (rms == 0) atomicOr(status, IMIE_ERMS);
+  // every wave: combine the per-wave sums (lane w holds wave w's) and derive rms / reciprocal redundantly
+  hi = lane < nw ? s_hi[lane] : 0;
+  lo = lane < nw ? s_lo[lane] : 0;
+  bad = lane < nw ? s_bad[lane] : 0;
+  wave_sum_u128(hi, lo, bad);
+  uint64_t rms = 0;
+  if (!bad) {
+    const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)cols);
+    if (mean <= ~(u128)0 - (u128)(uint64_t)eps) rms = isqrt_u128(mean + (u128)(uint64_t)eps);
   }
-  __syncthreads();
-  const uint64_t rms = s_rms, rinv = s_rinv;
-  if (rms == 0) return;
+  if (rms == 0) {
+    if (tid == 0) atomicOr(status, IMIE_ERMS);
+    return;
+  }
+  const uint64_t rinv = recip_u64(rms);
   uint64_t mxn = 0, mxg = 0;
   int nfit = 1;
   int64_t nvk[kNormPer];
@@ -168,6 +114,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const int64_t* __restrict
       mxg = ag > mxg ? ag : mxg;
     } else {
       out[row * cols + c] = nv;
+      if (PREP) s_y[c] = nv;
     }
     if (keep) *keep = nv;
   };
@@ -182,34 +129,37 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const int64_t* __restrict
   }
   if (!gain) {
     if (!nfit) atomicOr(status, IMIE_ERMS);
+    if (PREP) prep_row(s_y, row, po, zero, tid, nt);
     return;
   }
   mxn = imie_wave_max_u64(mxn);
   mxg = imie_wave_max_u64(mxg);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) nfit &= __shfl_xor(nfit, o, 64);
-  if (lane == 0) { s_mn[wave] = mxn; s_mg[wave] = mxg; s_bad[wave] = nfit; }
+  if (lane == 0) { s_mn[wave] = mxn; s_mg[wave] = mxg; s_fit[wave] = nfit; }
   __syncthreads();
-  if (tid == 0) {
-    uint64_t mn = 0, mg = 0;
-    int ok = 1;
-    for (int w = 0; w < nw; ++w) {
-      mn = s_mn[w] > mn ? s_mn[w] : mn;
-      mg = s_mg[w] > mg ? s_mg[w] : mg;
-      ok &= s_bad[w];
-    }
-    if (ok && mn != 0 && mg > (uint64_t)INT64_MAX / mn) ok = 0;
-    if (!ok) atomicOr(status, IMIE_ERMS);
-    s_ok = ok;
+  mxn = lane < nw ? s_mn[lane] : 0;
+  mxg = lane < nw ? s_mg[lane] : 0;
+  nfit = lane < nw ? s_fit[lane] : 1;
+  mxn = imie_wave_max_u64(mxn);
+  mxg = imie_wave_max_u64(mxg);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) nfit &= __shfl_xor(nfit, o, 64);
+  if (!nfit || (mxn != 0 && mxg > (uint64_t)INT64_MAX / mxn)) {
+    if (tid == 0) atomicOr(status, IMIE_ERMS);
+    return;
   }
-  __syncthreads();
-  if (!s_ok) return;
   if (cached) {
 #pragma unroll
     for (int k = 0; k < kNormPer; ++k) {
       const int64_t c = tid + (int64_t)k * nt;
-      if (c < cols) out[row * cols + c] = imie_floor_shift((int64_t)((uint64_t)nvk[k] * (uint64_t)gv[k]), frac);
+      if (c < cols) {
+        const int64_t y = imie_floor_shift((int64_t)((uint64_t)nvk[k] * (uint64_t)gv[k]), frac);
+        out[row * cols + c] = y;
+        if (PREP) s_y[c] = y;
+      }
     }
+    if (PREP) prep_row(s_y, row, po, zero, tid, nt);
   } else {
     for (int64_t c = tid; c < cols; c += nt) {
       bool fits;
@@ -224,11 +174,39 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const int64_t* __restrict
 int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
                         const int64_t* gain, int64_t* out, int* status, hipStream_t st) {
   if (rows <= 0) return IMIE_OK;
-  // one thread per 4 columns up to 1024 threads; at least one wave
-  int nt = (int)((cols + 3) / 4);
-  nt = nt < 64 ? 64 : (nt > 1024 ? 1024 : ((nt + 63) / 64) * 64);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(nt), 0, st, x, cols, (int)frac, eps, gain, out,
-                     status);
+  const imie_q1::Q1PrepOut po = {};
+  const imie_q1::Q1Zero z = {};
+  static const int force_nt = [] { const char* e = getenv("IMIE_NORM_NT"); return e ? atoi(e) : 0; }();  // tuning
+  if (force_nt == 64)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, z);
+  else if (force_nt == 256)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, z);
+  else if (cols <= 256)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, z);
+  else if (cols <= 1024)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, z);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, z);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                             const int64_t* gain, int64_t* out, int* status, const imie_q1::Q1PrepOut& po,
+                             const imie_q1::Q1Zero& zero, hipStream_t st) {
+  if (rows <= 0) return IMIE_OK;
+  if (cols != po.nb * 128 || cols > kPrepCols) return IMIE_EARG;
+  if (cols <= 1024)
+    hipLaunchKernelGGL((rmsnorm_kernel<true, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, zero);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<true, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, zero);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
@@ -265,6 +243,14 @@ int bonsai_rmsnorm_gpu(const int64_t* x, int64_t rows, int64_t cols, int64_t fra
   IMIE_HIP(hipMemcpyAsync(out, g_nws.out.p, xb, hipMemcpyDeviceToHost, st));
   IMIE_HIP(hipStreamSynchronize(st));
   return stat ? IMIE_ERMS : IMIE_OK;
+}
+
+// Host evaluation of the RMSNorm kernels' exact helpers (CPU test hooks, no reference counterpart):
+// floor(sqrt(hi * 2^64 + lo)), floor((2^64 - 1) / d) and floor((hi * 2^64 + lo) / d) (low 64 bits).
+uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo) { return imie_fx::isqrt_u128(((imie_fx::u128)hi << 64) | lo); }
+uint64_t imie_fx_recip_u64(uint64_t d) { return imie_fx::recip_u64(d); }
+uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d) {
+  return (uint64_t)imie_fx::div_u128_cols(((imie_fx::u128)hi << 64) | lo, d);
 }
 
 // Device-pointer RMSNorm; status (device int) receives bit 4 on refusal. Asynchronous on `stream`.

@@ -18,15 +18,14 @@
 // MFMA int32 accumulation is exact: each D entry is at most 128 * 128 * 2^7 in magnitude.
 #include "imie_common.h"
 #include "imie_kernels.h"
+#include "imie_q1prep.h"
 #include <string.h>
 #include <stdlib.h>
 
 namespace {
 
+using namespace imie_q1;
 constexpr int kTileRows = 16;      // output rows per MFMA tile
-constexpr int kSlabBlocks = 4;     // 128-blocks per slab (= K 512 per wave step)
-constexpr int kMaxLimbs = 8;
-constexpr int kMaxSegs = 3;        // weights sharing one activation in a single matvec launch
 
 // ------------------------------------------------------------------------------------------------------
 // Registry of resident Q1 weights (process-global, handle = index). Layout per weight:
@@ -82,65 +81,20 @@ extern "C" int imie_q1_repack_host(const uint8_t* bits, const int64_t* scale, in
   return IMIE_OK;
 }
 
-// ------------------------------------------------------------------------------------------------------
-// Activation prep: per (token t, slab) one wave computes max|x| -> limb count L, the per-block totals and
-// the digit operand table xq[t][l][block][s] (uint4: dword d packs digits of positions 32d + 8c + s,
-// c = 0..3, as bytes c). Lane layout: g = lane>>4 (block of slab), s = lane&7, dh = (lane>>3)&1 covering
-// d in {2dh, 2dh+1}: 8 positions per lane.
-// ------------------------------------------------------------------------------------------------------
-struct Q1Zero {                    // outputs the prep kernel clears (K-split matvecs add into them atomically)
-  int64_t* p[kMaxSegs];
-  int64_t n[kMaxSegs];
-  int cnt;
-};
-
-__global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__ x, int64_t K, int64_t nb,
-                                                      int64_t nbp, int64_t nslabs, uint32_t* __restrict__ xq,
-                                                      int64_t* __restrict__ totals, int* __restrict__ lslab,
+// Stand-alone activation prep (see imie_q1prep.h): grid (nslabs, T), one wave per (token, slab); the
+// workgroups also clear the zero list for a following K-split matvec.
+__global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__ x, int64_t K, Q1PrepOut po,
                                                       Q1Zero zero) {
   const int lane = threadIdx.x;
-  const int64_t sl = blockIdx.x;
-  const int64_t t = blockIdx.y;
-  {
-    const int64_t wg = t * nslabs + sl, nwg = (int64_t)gridDim.y * nslabs;
-    for (int z = 0; z < zero.cnt; ++z)
-      for (int64_t e = wg * 64 + lane; e < zero.n[z]; e += nwg * 64) zero.p[z][e] = 0;
-  }
-  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
-  const int64_t blk = sl * kSlabBlocks + g;
+  const int64_t sl = blockIdx.x, t = blockIdx.y;
+  zero_share(zero, t * po.nslabs + sl, (int64_t)gridDim.y * po.nslabs, lane, 64);
   int64_t v[8];
-  uint64_t mx = 0;
-  int64_t part = 0;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const int d = 2 * dh + (q >> 2), c = q & 3;
-    const int64_t pos = blk * 128 + 32 * d + 8 * c + s;
-    const int64_t xv = (blk < nb) ? x[t * K + pos] : 0;
-    v[q] = xv;
-    const uint64_t a = imie_absu64(xv);
-    mx = a > mx ? a : mx;
-    part = (int64_t)((uint64_t)part + (uint64_t)xv);
+    const int64_t pos = prep_pos(lane, sl, q);
+    v[q] = (pos < po.nb * 128) ? x[t * K + pos] : 0;
   }
-  mx = imie_wave_max_u64(mx);
-  const int L = imie_limbs_needed(mx);
-  // block total: sum over the 16 lanes of group g (xor 1,2,4,8 stays inside the group)
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
-  if ((lane & 15) == 0) totals[t * nbp + blk] = part;
-  if (lane == 0) lslab[t * nslabs + sl] = L;
-  for (int l = 0; l < L; ++l) {
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t dig = ((v[q] + 128) & 255) - 128;          // balanced digit in [-128, 127]
-      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;  // exact: v - dig is a multiple of 256
-      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
-      if (q < 4) w0 |= byte; else w1 |= byte;
-    }
-    uint32_t* dst = xq + ((((t * kMaxLimbs + l) * nbp + blk) * 8 + s) * 4);
-    dst[2 * dh] = w0;
-    dst[2 * dh + 1] = w1;
-  }
+  prep_slab(v, po, t, sl);
 }
 
 // ------------------------------------------------------------------------------------------------------
@@ -337,8 +291,10 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
 // ------------------------------------------------------------------------------------------------------
 // One prep (digit table of x, shared by every segment) and one matvec launch over up to kMaxSegs weights with
 // the same n_blocks and scale width; outs[i] receives (T, N_i). accumulate != 0 adds into the outputs.
+// prepped != 0: the caller's producer already wrote the digit table into wk (imie_q1_prep_target) and cleared
+// every non-accumulated output, so no prep kernel is launched.
 static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
-                          int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
+                          int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st, int prepped = 0) {
   if (T <= 0) return IMIE_OK;
   if (cnt < 1 || cnt > kMaxSegs) return IMIE_EARG;
   const Q1Weight& w0 = *ws[0];
@@ -379,8 +335,10 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   }
   const int64_t K = w0.nb * 128;
   imie_prof_mark(IMIE_K_Q1_PREP, st, true);
-  hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w0.nb, nbp,
-                     nslabs, (uint32_t*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, zero);
+  if (!prepped) {
+    Q1PrepOut po = {(uint32_t*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, w0.nb, nbp, nslabs};
+    hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, po, zero);
+  }
   imie_prof_mark(IMIE_K_Q1_PREP, st, false);
   IMIE_HIP(hipGetLastError());
   const size_t budget = 48 * 1024;
@@ -480,7 +438,7 @@ int imie_q1_launch(int64_t handle, const int64_t* x, int64_t T, int64_t frac, in
 }
 
 int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int64_t T, int64_t frac,
-                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st) {
+                         int64_t* const* outs, int accumulate, Q1Ws* wk, hipStream_t st, int prepped) {
   if (cnt < 1 || cnt > kMaxSegs) return IMIE_EARG;
   const Q1Weight* ws[kMaxSegs];
   for (int i = 0; i < cnt; ++i)
@@ -488,11 +446,21 @@ int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int6
   bool same = true;
   for (int i = 1; i < cnt; ++i) same = same && ws[i]->nb == ws[0]->nb && ws[i]->scale64 == ws[0]->scale64;
   Q1Ws& w = wk ? *wk : g_ws.w;
-  if (same) return q1_apply_multi(ws, cnt, x, T, frac, outs, accumulate, w, st);
+  if (same) return q1_apply_multi(ws, cnt, x, T, frac, outs, accumulate, w, st, prepped);
   for (int i = 0; i < cnt; ++i) {
-    const int rc = q1_apply_multi(&ws[i], 1, x, T, frac, &outs[i], accumulate, w, st);
+    const int rc = q1_apply_multi(&ws[i], 1, x, T, frac, &outs[i], accumulate, w, st, prepped);
     if (rc) return rc;
   }
+  return IMIE_OK;
+}
+
+int imie_q1_prep_target(Q1Ws* wk, int64_t nb, int64_t T, Q1PrepOut* po) {
+  if (!wk || !po || nb <= 0 || T <= 0) return IMIE_EARG;
+  const int64_t nslabs = (nb + kSlabBlocks - 1) / kSlabBlocks, nbp = nslabs * kSlabBlocks;
+  if (wk->xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || wk->totals.ensure((size_t)T * nbp * 8) ||
+      wk->lslab.ensure((size_t)T * nslabs * 4))
+    return IMIE_EARG;
+  *po = Q1PrepOut{(uint32_t*)wk->xq.p, (int64_t*)wk->totals.p, (int*)wk->lslab.p, nb, nbp, nslabs};
   return IMIE_OK;
 }
 

@@ -47,3 +47,27 @@ def test_q1_repack_host_layout():
                     assert st[tile, sl, lane] == scale[row, blk]
                 else:
                     assert not bt[tile, sl, lane].any() and st[tile, sl, lane] == 0
+
+
+def test_exact_norm_helpers_host():
+    """isqrt / reciprocal / 128-by-32 division used by the RMSNorm kernels, against Python big integers on
+    random magnitudes and the edges (perfect squares and their neighbours, 2^64 - 1, power-of-two divisors)."""
+    import math
+    so = _lib.lib()
+    rng = np.random.default_rng(7)
+    vals = [0, 1, 2, 3, 4, (1 << 64) - 1, 1 << 64, (1 << 100) - 1, 1 << 100, (1 << 128) - 1]
+    for r in [1, 2, 3, 1 << 20, (1 << 32) + 1, (1 << 50) - 3, (1 << 64) - 1]:
+        vals += [r * r - 1, r * r, r * r + 1]
+    for bits in range(1, 129, 3):
+        vals += [int(rng.integers(0, 1 << 62)) << (bits - 62) if bits > 62 else int(rng.integers(0, 1 << bits))
+                 for _ in range(6)]
+    for v in vals:
+        v &= (1 << 128) - 1
+        assert so.imie_fx_isqrt_u128(v >> 64, v & ((1 << 64) - 1)) == math.isqrt(v), v
+    for d in [1, 2, 3, 5, 7, 255, 4096, 12345, (1 << 32) - 1, 1 << 40, (1 << 63) + 11, (1 << 64) - 1] + \
+             [int(x) for x in rng.integers(1, 1 << 62, size=200)]:
+        assert so.imie_fx_recip_u64(d) == ((1 << 64) - 1) // d, d
+    for d in [1, 3, 128, 4096, 4095, 12288, (1 << 32) - 1]:
+        for v in vals[:40]:
+            v &= (1 << 128) - 1
+            assert so.imie_fx_div_u128(v >> 64, v & ((1 << 64) - 1), d) == (v // d) & ((1 << 64) - 1), (v, d)
