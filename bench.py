@@ -155,6 +155,56 @@ def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, voca
             "effective_GB_s": round((wbytes + kvbytes) / (ms / tokens / 1e3) / 1e9, 1), **prof}
 
 
+def prefill_leg(so, torch, T: int = 2048) -> dict:
+    """Config 3: one Bonsai-8B-shape decoder layer in prefill over a T-token prompt (causal attention over all T
+    positions, int32 paged KV). Seeded random Q1_0 weights and activations; timed on one stream with HIP events.
+    The Q1 projections run as int8-MFMA GEMMs (tokens in M); `q1_gemm_alg_TOPS` counts 2*T*N*K ops of the
+    projections over the GEMM kernels' time (each +-1 weight times an int64 activation counted as one MAC)."""
+    from integer_inference_engine_amd import gpu_native as gn
+    from integer_inference_engine_amd.resident import ResidentNet
+    from integer_inference_engine_amd.rope_tables import bonsai8b_tables
+    d, H, Hkv, hd, dff = 4096, 32, 8, 128, 12288
+    rng = np.random.default_rng(3)
+    shapes = {"wq": (H * hd, d), "wk": (Hkv * hd, d), "wv": (Hkv * hd, d), "wo": (d, H * hd),
+              "w1": (dff, d), "wu": (dff, d), "w2": (d, dff)}
+    w = {k: np.array([gn.q1_register_weight(rng.integers(0, 256, size=(o, i // 128, 16), dtype=np.uint8),
+                                            rng.integers(1, 4097, size=(o, i // 128), dtype=np.int64))],
+                     dtype=np.int64) for k, (o, i) in shapes.items()}
+    g = {k: np.array([gn.buf_upload_i64(rng.integers(1 << 15, (1 << 17) + 1, size=(n,), dtype=np.int64))],
+                     dtype=np.int64) for k, n in (("n1g", d), ("n2g", d), ("qng", hd), ("kng", hd))}
+    w["out_head"], w["out_head_vocab"], g["finalg"] = -1, 0, -1
+    cos, sin = bonsai8b_tables(T + 64)
+    g["cos_h"], g["sin_h"] = gn.buf_upload_i64(cos), gn.buf_upload_i64(sin)
+    net = ResidentNet(B=1, n_layers=1, H=H, Hkv=Hkv, hd=hd, d=d, dff=dff, cap=T + 64, w=w, g=g, page=64, kv32=True)
+    x0 = torch.from_numpy(rng.integers(-(1 << 20), 1 << 20, size=(T, d), dtype=np.int64)).cuda()
+    x = torch.empty_like(x0)
+    torch.cuda.set_stream(net.stream)
+    x.copy_(x0)
+    st = net.forward(x, [0], T)                    # warm-up (sizes workspaces)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    x.copy_(x0)
+    net.stream.synchronize()
+    so.imie_profile_begin()
+    e0.record(net.stream)
+    st = net.forward(x, [0], T)
+    e1.record(net.stream)
+    net.stream.synchronize()
+    ms = e0.elapsed_time(e1)
+    prof = {}
+    for kid, name in ((0, "q1_prep"), (2, "q1_gemm"), (3, "attention")):
+        kms, kcnt = ctypes.c_double(), ctypes.c_int64()
+        so.imie_profile_read(kid, ctypes.byref(kms), ctypes.byref(kcnt))
+        prof[name + "_ms"] = round(kms.value, 3)
+    so.imie_profile_end()
+    net.close()
+    so.bonsai_q1_free_weights()
+    ops = 2 * T * sum(o * i for o, i in shapes.values())
+    gemm_ms = prof["q1_gemm_ms"]
+    return {"tokens": T, "layer_ms": round(ms, 3), "tok_s": round(T / (ms / 1e3), 1), "status": int(st),
+            "q1_gemm_alg_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1) if gemm_ms > 0 else None,
+            "q1_gemm_frac_of_int8_peak": round(ops / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None, **prof}
+
+
 def _lib_err():
     from integer_inference_engine_amd import _lib
     return _lib.last_error()
@@ -169,6 +219,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=32, help="8B-shape b=1 decode leg (0 = skip)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048, help="config-3 layer prefill leg (0 = skip)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
@@ -278,6 +329,11 @@ def main() -> int:
         print("[bench] 8B-shape decode leg", file=sys.stderr, flush=True)
         dec = decode_leg(so, torch, args.decode_tokens)
 
+    pre = None
+    if args.prefill_tokens > 0:
+        print("[bench] config-3 prefill leg", file=sys.stderr, flush=True)
+        pre = prefill_leg(so, torch, args.prefill_tokens)
+
     line = {
         "metric": "Q1 matvec HBM GB/s (% of peak); 8B-shape decode tok/s b=1; byte-exact",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -294,6 +350,7 @@ def main() -> int:
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,
         "decode_8b_b1": dec,
+        "prefill_8b_layer": pre,
     }
     print(json.dumps(line))
     return 0

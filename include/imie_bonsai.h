@@ -133,6 +133,14 @@ int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int
  * optional; use_graph replays a captured HIP graph of one step after the first. */
 int imie_net_decode_dev(int64_t ctx, const uint8_t *ebits, const int64_t *escale, int64_t *ids_dev,
                         int64_t *logits_dev, int64_t *hist_dev, int64_t steps, int use_graph, void *stream);
+/* Ragged paged cache: sequence b gets room for caps[b] positions; the cache is replaced (lengths restart at 0).
+ * No reference counterpart (the reference decode context is dense). */
+int imie_net_set_caps(int64_t ctx, const int64_t *caps);
+/* Seeded synthetic K/V for lens[b] positions per sequence, generated on the device (benchmark / large-context
+ * test workloads; no reference counterpart). Values uniform in [lo, hi); seq_ids (nullable) keys each
+ * sequence's draw. */
+int imie_net_fill_kv(int64_t ctx, uint64_t seed, const int64_t *lens, const int64_t *seq_ids, int64_t lo,
+                     int64_t hi);
 /* CPU test hooks for the exact RMSNorm arithmetic (no reference counterpart): floor(sqrt(hi*2^64 + lo)),
  * floor((2^64 - 1) / d), low 64 bits of floor((hi*2^64 + lo) / d). */
 uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo);

@@ -69,6 +69,8 @@ SIGNATURES = {
     "imie_fx_isqrt_u128": (c_uint64, [c_uint64, c_uint64]),
     "imie_fx_recip_u64": (c_uint64, [c_uint64]),
     "imie_fx_div_u128": (c_uint64, [c_uint64, c_uint64, c_uint32]),
+    "imie_net_set_caps": (c_int, [c_int64, c_void_p]),
+    "imie_net_fill_kv": (c_int, [c_int64, c_uint64, c_void_p, c_void_p, c_int64, c_int64]),
     "imie_net_decode_dev": (c_int, [c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int,
                                     c_void_p]),
     # north-mini-code Q4_K / Q6_K (include/imie_nmc.h)

@@ -23,6 +23,9 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     # packed FP32 instructions are disabled for every HIP object (no packed-fp32 codegen on this pool)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the integer kernels rework every MFMA result with VALU ops (limb shifts,
+    # recombination), which the AGPR form would route through v_accvgpr_read / write copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
 ]
 

@@ -21,6 +21,7 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_attention.h"
+#include "imie_kvfmt.h"
 #include <stdlib.h>
 
 namespace {
@@ -667,8 +668,9 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
   if (head && o == 0) {
     uint64_t mp = 0, mv = 0, mk = 0;
     for (int64_t c = g; c < nlive; c += 8) {
-      const uint64_t a = d.cmp[c * rows + r], v = d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv],
-                     k = d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv];
+      const uint64_t a = d.cmp[c * rows + r];
+      const uint64_t v = d.run_k ? 0 : d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv];
+      const uint64_t k = d.run_k ? 0 : d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv];
       mp = a > mp ? a : mp;
       mv = v > mv ? v : mv;
       mk = k > mk ? k : mk;
@@ -690,10 +692,569 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
       mv = s_mx[1][gg] > mv ? s_mx[1][gg] : mv;
       mk = s_mx[2][gg] > mk ? s_mx[2][gg] : mk;
     }
+    if (d.run_k) { mk = d.run_k[b * d.Hkv + kv]; mv = d.run_v[b * d.Hkv + kv]; }
     const u128 pv = (u128)mp * mv;
     if (pv > (u128)(INT64_MAX / L)) atomicOr(d.status, IMIE_EOVF);
     const u128 qk = (u128)d.maxq[r] * mk;
     if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+  }
+}
+
+
+// ---------------------------------------------------------------------------------------------------------
+// kv8 cache (imie_kvfmt.h): the dot products run as int8 MFMAs on the stored digit bytes.
+//   scores: A = balanced base-256 digits of q (limb lq), B = K digit plane b; sum_c q k = sum_{lq,b} 256^(lq+b) D
+//   PV    : A = digits of p (limb lp, keys on the K axis), B = V digit plane b (keys x dims)
+// MFMA int32 sums are exact (|D| <= 64 * 128 * 128 per MFMA; partial sums bounded below 2^31 as noted); every
+// recombination into the int64 result wraps mod 2^64 like the oracle's int64 arithmetic.
+// max|K| / max|V| for the fail-loud bounds are the running maxima kept by the cache writes (run_k / run_v).
+// ---------------------------------------------------------------------------------------------------------
+__device__ inline int64_t bal_digit(int64_t x, int l) {
+  for (int i = 0; i < l; ++i) {
+    const int64_t dg = ((x + 128) & 255) - 128;
+    x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+  }
+  return ((x + 128) & 255) - 128;
+}
+
+__device__ inline v4i pack16(const int8_t* v) {
+  v4i r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    r[k] = (int)((uint32_t)(uint8_t)v[4 * k] | ((uint32_t)(uint8_t)v[4 * k + 1] << 8) |
+                 ((uint32_t)(uint8_t)v[4 * k + 2] << 16) | ((uint32_t)(uint8_t)v[4 * k + 3] << 24));
+  return r;
+}
+
+__device__ inline v4i mfma8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+
+// keep the first n (0..16) bytes of a 16-byte operand
+__device__ inline v4i keep_bytes(v4i v, int n) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int nb = n - 4 * k;
+    const uint32_t mk = nb >= 4 ? 0xFFFFFFFFu : (nb <= 0 ? 0u : ((1u << (8 * nb)) - 1u));
+    v[k] = (int)((uint32_t)v[k] & mk);
+  }
+  return v;
+}
+
+__device__ inline int64_t kv8_row_base(const AttnDesc& d, int64_t b, int64_t kv, int64_t j, int64_t* slot) {
+  int64_t pi, in;
+  page_split(d, j, pi, in);
+  *slot = in;
+  return imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+}
+
+// Decode scores (M == 1). Workgroup = (b, kv, chunk); wave w takes 16-key tiles w, w + 4, ... MFMA rows are
+// (head r, limb lq): row 4 (r % 4) + (lq % 4) of row block (r / 4, lq / 4); a D lane (g, n) then holds the 4
+// limbs of head 4 * hb + g for key n and recombines them in place.
+template <int REP>
+__global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
+  constexpr int RBH = (REP + 3) / 4;
+  __shared__ int64_t s_max[4][REP];
+  __shared__ uint64_t s_mq[4];
+  __shared__ __align__(16) int8_t sQd[RBH][2][16][128];
+  const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
+  const int64_t rows = d.B * d.H;
+  const int64_t L = dec_len(d, b);
+  const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  const int64_t* qg = d.q + b * d.qsb + kv * REP * d.qsh;
+  uint64_t mq = 0;
+  for (int i = tid; i < REP * d.hd; i += 256) {
+    const uint64_t a = imie_absu64(qg[imie_udiv32(i, d.hd) * d.qsh + imie_umod32(i, d.hd)]);
+    mq = a > mq ? a : mq;
+  }
+  mq = imie_wave_max_u64(mq);
+  if (lane == 0) s_mq[wave] = mq;
+  if (blockIdx.y == 0 && tid < REP) {
+    uint64_t mr = 0;
+    for (int c = 0; c < d.hd; ++c) { const uint64_t a = imie_absu64(qg[tid * d.qsh + c]); mr = a > mr ? a : mr; }
+    d.maxq[b * d.H + kv * REP + tid] = mr;
+  }
+  __syncthreads();
+  uint64_t mqa = s_mq[0];
+  for (int w = 1; w < 4; ++w) mqa = s_mq[w] > mqa ? s_mq[w] : mqa;
+  const int Lq = imie_limbs_needed(mqa), LB = (Lq + 3) / 4;
+  const int KS = (int)((d.hd + 63) / 64);
+  // digits of every q element once (thread per element) into LDS rows [head block][4 (r % 4) + lq % 4][limb
+  // block][dim]; each lane then reads its 16-byte A operands directly
+  for (int i = tid; i < RBH * 2 * 16 * 128; i += 256) (&sQd[0][0][0][0])[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < REP * d.hd; i += 256) {
+    const int r = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
+    int64_t x = qg[r * d.qsh + c];
+    for (int lq = 0; lq < Lq; ++lq) {
+      const int64_t dg = ((x + 128) & 255) - 128;
+      x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+      sQd[r >> 2][lq >> 2][4 * (r & 3) + (lq & 3)][c] = (int8_t)dg;
+    }
+  }
+  __syncthreads();
+  v4i av[RBH][2][2];
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+    for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
+  int64_t smax[RBH];
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb) smax[hb] = INT64_MIN;
+  const int64_t jend = min(j0 + d.chunk, L);
+  const int8_t* Kb = (const int8_t*)d.K;
+  for (int64_t t = j0 + 16 * wave; t < jend; t += 64) {
+    const int64_t j = t + m;
+    const bool valid = j < jend;
+    v4i bk[4][2];
+    int64_t base = 0, slot = 0;
+    if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
+                        ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
+                        : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb) {
+      uint64_t S = 0;
+      for (int lb = 0; lb < LB; ++lb)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          v4i D = mfma8(av[hb][lb][0], bk[db][0], v4i{0, 0, 0, 0});
+          if (KS > 1) D = mfma8(av[hb][lb][1], bk[db][1], D);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S += (uint64_t)(int64_t)D[i] << (8 * (4 * lb + i + db));
+        }
+      const int r = 4 * hb + g;
+      if (valid && r < REP) {
+        int64_t sc = (int64_t)S >> d.frac;
+        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+        d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] = sc;
+        smax[hb] = sc > smax[hb] ? sc : smax[hb];
+      }
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb) {
+    int64_t mx = smax[hb];
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) { const int64_t w2 = __shfl_xor(mx, o, 64); mx = w2 > mx ? w2 : mx; }
+    const int r = 4 * hb + g;
+    if (m == 0 && r < REP) s_max[wave][r] = mx;
+  }
+  __syncthreads();
+  if (tid < REP) {
+    int64_t mx = s_max[0][tid];
+    for (int w = 1; w < 4; ++w) mx = s_max[w][tid] > mx ? s_max[w][tid] : mx;
+    d.cmax[blockIdx.y * rows + b * d.H + kv * REP + tid] = mx;
+  }
+}
+
+// Decode PV (M == 1). Workgroup = (b, kv, chunk); per 64-key step the p digits of the REP heads are staged in LDS
+// as the A operand (row 4 (r % 4) + lp of head block r / 4); wave w owns dim tiles w and w + 4.
+template <int REP>
+__global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
+  constexpr int RBH = (REP + 3) / 4;
+  __shared__ __align__(16) int8_t sPd[RBH][16][64];
+  __shared__ uint64_t s_z[REP], s_rz[REP], s_mp[4][REP];
+  const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
+  const int64_t L = dec_len(d, b);
+  const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  const int64_t rows = d.B * d.H;
+  uint64_t* part = d.part + (int64_t)blockIdx.y * rows * d.hd;
+  if (j0 >= L) {
+    for (int i = tid; i < REP * d.hd; i += blockDim.x)
+      part[(b * d.H + kv * REP + imie_udiv32(i, d.hd)) * d.hd + imie_umod32(i, d.hd)] = 0;
+    if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
+    return;
+  }
+  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
+  for (int r = wave; r < REP; r += 4) {
+    uint64_t z = 0;
+    for (int64_t c = lane; c < nlive; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
+    if (lane == 0) { s_z[r] = z; s_rz[r] = z > 1 ? (~(uint64_t)0) / z : 0; }
+  }
+  for (int i = tid; i < RBH * 16 * 64; i += 256) (&sPd[0][0][0])[i] = 0;
+  __syncthreads();
+  const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
+  const int64_t jend = min(j0 + d.chunk, L);
+  const int DT = (int)(d.hd / 16);
+  uint64_t mp[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) mp[r] = 0;
+  v4i acc[RBH][4][2];
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[hb][db][0] = acc[hb][db][1] = v4i{0, 0, 0, 0};
+  const int8_t* Vb = (const int8_t*)d.V;
+  for (int64_t t0 = j0; t0 < jend; t0 += 64) {
+    const int64_t tn = min((int64_t)64, jend - t0);
+    __syncthreads();                                  // previous step's digits consumed
+    {
+      const int kk = tid & 63;
+      for (int r = tid >> 6; r < REP; r += 4) {
+        const int64_t row = b * d.H + kv * REP + r;
+        const uint64_t Z = s_z[r];
+        int64_t p = 0;
+        if (kk < tn && Z != 0) {
+          const uint64_t num = (uint64_t)d.scores[row * d.Lmax + t0 + kk] << d.frac;
+          if (Z == 1) p = (int64_t)num;
+          else {
+            const uint64_t rz = s_rz[r];
+            uint64_t qq = __umul64hi(num, rz);
+            uint64_t rem = num - qq * Z;
+            while (rem >= Z) { ++qq; rem -= Z; }
+            p = (int64_t)qq;
+          }
+        }
+        mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
+        int64_t x = p;
+        for (int lp = 0; lp < 4; ++lp) {
+          const int64_t dg = ((x + 128) & 255) - 128;
+          x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+          sPd[r >> 2][4 * (r & 3) + lp][kk] = lp < Lp ? (int8_t)dg : (int8_t)0;
+        }
+      }
+    }
+    __syncthreads();
+    int64_t pi, slot0;
+    page_split(d, t0, pi, slot0);
+    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+    v4i av[RBH];
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb) av[hb] = *(const v4i*)&sPd[hb][m][16 * g];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tile = wave + 4 * tt;
+      if (tile >= DT) continue;
+      const int64_t c = 16 * tile + m;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const v4i bv = *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, c, d.hd, d.P));
+#pragma unroll
+        for (int hb = 0; hb < RBH; ++hb) acc[hb][db][tt] = mfma8(av[hb], bv, acc[hb][db][tt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const uint64_t mm = imie_wave_max_u64(mp[r]);
+    if (lane == 0) s_mp[wave][r] = mm;
+  }
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tile = wave + 4 * tt;
+      const int r = 4 * hb + g;
+      if (tile >= DT || r >= REP) continue;
+      uint64_t o = 0;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o += (uint64_t)(int64_t)acc[hb][db][tt][i] << (8 * (i + db));
+      part[(b * d.H + kv * REP + r) * d.hd + 16 * tile + m] = o;
+    }
+  __syncthreads();
+  if (tid < REP) {
+    uint64_t mm = s_mp[0][tid];
+    for (int w = 1; w < 4; ++w) mm = s_mp[w][tid] > mm ? s_mp[w][tid] : mm;
+    d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = mm;
+  }
+}
+
+// Prefill scores (M > 1, causal). Workgroup = (b, kv, 16 group rows, 256 keys); wave w takes keys 64w .. 64w+63
+// as 4 MFMA tiles of 16. MFMA rows are the 16 query rows; each limb lq is a separate A operand and the products
+// are summed per exponent e = lq + b in int32 (|T_e| <= 4 * 2 * 2^20), then S = sum_e T_e << 8e in int64.
+constexpr int kPfKeys = 256;
+__global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
+  __shared__ __align__(16) int8_t sQ[8][16][128];
+  __shared__ uint64_t s_mq[16];
+  __shared__ int64_t s_pm[4][16];
+  const int64_t rep = d.H / d.Hkv, grows = rep * d.M;
+  const int64_t nrt = (grows + 15) / 16;
+  const int64_t bkv = imie_udiv32(blockIdx.x, nrt), rt = imie_umod32(blockIdx.x, nrt);
+  const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
+  const int64_t rows = d.B * d.H * d.M;
+  const int64_t j0 = (int64_t)blockIdx.y * kPfKeys;
+  const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  int64_t vismax = 0;
+  for (int i = 0; i < 16; ++i) {
+    const int64_t gr = rt * 16 + i;
+    if (gr < grows) {
+      const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
+      vismax = lv > vismax ? lv : vismax;
+    }
+  }
+  if (j0 >= vismax) return;
+  // q rows: thread -> row tid / 16, dims 8 * (tid % 16) .. + 7
+  const int qi = tid >> 4, qc = 8 * (tid & 15);
+  const int64_t qgr = rt * 16 + qi;
+  const bool qrow = qgr < grows;
+  const int64_t qr = qrow ? group_row(d, b, kv, qgr) : 0;
+  int64_t qv[8];
+  uint64_t mq = 0;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    qv[c] = (qrow && qc + c < d.hd) ? d.q[qoff(d, qr) + qc + c] : 0;
+    const uint64_t a = imie_absu64(qv[c]);
+    mq = a > mq ? a : mq;
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) { const uint64_t w2 = __shfl_xor(mq, o, 64); mq = w2 > mq ? w2 : mq; }
+  if ((tid & 15) == 0) s_mq[qi] = mq;
+  __syncthreads();
+  if (blockIdx.y == 0 && (tid & 15) == 0 && qrow) d.maxq[qr] = mq;
+  uint64_t mqa = 0;
+  for (int i = 0; i < 16; ++i) mqa = s_mq[i] > mqa ? s_mq[i] : mqa;
+  const int Lq = imie_limbs_needed(mqa);
+  for (int lq = 0; lq < Lq; ++lq)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int64_t x = qv[c];
+      sQ[lq][qi][qc + c] = (int8_t)bal_digit(x, lq);
+    }
+  __syncthreads();
+  const int KS = (int)((d.hd + 63) / 64);
+  // rows of this lane's D values: 4g + i
+  int64_t rr[4], lvr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t gr = rt * 16 + 4 * g + i;
+    rr[i] = gr < grows ? group_row(d, b, kv, gr) : -1;
+    lvr[i] = gr < grows ? (d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len) : 0;
+  }
+  int64_t pm[4] = {INT64_MIN, INT64_MIN, INT64_MIN, INT64_MIN};
+  const int8_t* Kb = (const int8_t*)d.K;
+  for (int st = 0; st < 4; ++st) {
+    const int64_t t = j0 + 64 * wave + 16 * st;
+    if (t >= vismax) break;
+    const int64_t j = t + m;
+    const bool valid = j < len;
+    v4i bk[4][2];
+    int64_t base = 0, slot = 0;
+    if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
+                        ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
+                        : v4i{0, 0, 0, 0};
+    v4i T[11];
+#pragma unroll
+    for (int e = 0; e < 11; ++e) T[e] = v4i{0, 0, 0, 0};
+    for (int lq = 0; lq < Lq; ++lq) {
+      v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
+      v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
+      if (16 * g >= d.hd) a0 = v4i{0, 0, 0, 0};
+      if (64 + 16 * g >= d.hd) a1 = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        v4i x = mfma8(a0, bk[db][0], T[lq + db]);
+        if (KS > 1) x = mfma8(a1, bk[db][1], x);
+        T[lq + db] = x;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint64_t S = 0;
+      for (int e = 0; e < Lq + 3; ++e) S += (uint64_t)(int64_t)T[e][i] << (8 * e);
+      if (rr[i] >= 0 && j < lvr[i]) {
+        int64_t sc = (int64_t)S >> d.frac;
+        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+        d.scores[rr[i] * d.Lmax + j] = sc;
+        pm[i] = sc > pm[i] ? sc : pm[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int64_t mx = pm[i];
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) { const int64_t w2 = __shfl_xor(mx, o, 64); mx = w2 > mx ? w2 : mx; }
+    if (m == 0) s_pm[wave][4 * g + i] = mx;
+  }
+  __syncthreads();
+  if (tid < 16) {
+    const int64_t gr = rt * 16 + tid;
+    if (gr < grows) {
+      int64_t mx = s_pm[0][tid];
+      for (int w = 1; w < 4; ++w) mx = s_pm[w][tid] > mx ? s_pm[w][tid] : mx;
+      d.pmax[blockIdx.y * rows + group_row(d, b, kv, gr)] = mx;
+    }
+  }
+}
+
+// Prefill softmax (kv8): workgroup per query row; row max from the score kernel's per-256-key maxima; exact e_j, Z,
+// p_j = floor((e_j << f) / Z) by a 2^64 / Z reciprocal with correction; p written as Lp digit planes pd[lp][r][j].
+__global__ __launch_bounds__(256) void pf_softmax8_kernel(AttnDesc d) {
+  __shared__ uint64_t red[256];
+  __shared__ int64_t s_m;
+  const int64_t r = blockIdx.x;
+  const RowInfo ri = row_info(d, r);
+  const int tid = threadIdx.x;
+  const int64_t rows = d.B * d.H * d.M;
+  const int64_t bkv = ri.b * d.Hkv + ri.kv;
+  if (tid == 0) {
+    const u128 qk = (u128)d.maxq[r] * d.run_k[bkv];
+    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+  }
+  const int64_t nkt = (ri.lv + kPfKeys - 1) / kPfKeys;
+  int64_t mx = INT64_MIN;
+  for (int64_t kt = tid; kt < nkt; kt += 256) { const int64_t v = d.pmax[kt * rows + r]; mx = v > mx ? v : mx; }
+  red[tid] = (uint64_t)mx;
+  __syncthreads();
+  if (tid == 0) {
+    int64_t m2 = INT64_MIN;
+    for (int i = 0; i < 256; ++i) m2 = (int64_t)red[i] > m2 ? (int64_t)red[i] : m2;
+    s_m = m2;
+  }
+  __syncthreads();
+  const int64_t m = s_m;
+  int64_t* s = d.scores + r * d.Lmax;
+  uint64_t z = 0;
+  for (int64_t j = tid; j < ri.lv; j += 256) {
+    int64_t dd = (int64_t)((uint64_t)m - (uint64_t)s[j]);
+    if (dd > d.dclip) dd = d.dclip;
+    const int64_t e = exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+    s[j] = e;
+    z += (uint64_t)e;
+  }
+  z = (uint64_t)imie_wave_sum_i64((int64_t)z);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = z;
+  __syncthreads();
+  const uint64_t Z = red[0] + red[1] + red[2] + red[3];
+  const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
+  const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
+  uint64_t mp = 0;
+  for (int64_t j = tid; j < ri.lv; j += 256) {
+    int64_t p = 0;
+    if (Z != 0) {
+      const uint64_t num = (uint64_t)s[j] << d.frac;
+      if (Z == 1) p = (int64_t)num;
+      else {
+        uint64_t qq = __umul64hi(num, rz);
+        uint64_t rem = num - qq * Z;
+        while (rem >= Z) { ++qq; rem -= Z; }
+        p = (int64_t)qq;
+      }
+    }
+    mp = (uint64_t)p > mp ? (uint64_t)p : mp;
+    int64_t x = p;
+    for (int lp = 0; lp < Lp; ++lp) {
+      const int64_t dg = ((x + 128) & 255) - 128;
+      x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+      d.pd[((int64_t)lp * rows + r) * d.pdL + j] = (int8_t)dg;
+    }
+  }
+  mp = imie_wave_max_u64(mp);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = mp;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t a = red[0];
+    for (int w = 1; w < 4; ++w) a = red[w] > a ? red[w] : a;
+    d.maxp[r] = a;
+  }
+}
+
+// Prefill PV (kv8) + final: workgroup = (b, kv, 16 group rows); wave w owns dim tiles w and w + 4. Per 64-key
+// step: A = p digit plane lp of the 16 rows (keys past a row's causal limit masked to 0), B = V digit plane b;
+// T_e (e = lp + b) in int32, folded into int64 every 4096 keys (|T_e| < 2^27 before a fold).
+__global__ __launch_bounds__(256) void pf_pv8_kernel(AttnDesc d) {
+  const int64_t rep = d.H / d.Hkv, grows = rep * d.M;
+  const int64_t nrt = (grows + 15) / 16;
+  const int64_t bkv = imie_udiv32(blockIdx.x, nrt), rt = imie_umod32(blockIdx.x, nrt);
+  const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
+  const int64_t rows = d.B * d.H * d.M;
+  const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  if (blockIdx.x == 0 && tid == 0) check_rope_guard(d);
+  const int64_t agr = rt * 16 + m;                    // A row of this lane
+  const bool arow = agr < grows;
+  const int64_t ar = arow ? group_row(d, b, kv, agr) : 0;
+  const int64_t alv = arow ? (d.starts ? d.starts[b] + imie_umod32(agr, d.M) + 1 : len) : 0;
+  int64_t vismax = 0;
+  for (int i = 0; i < 16; ++i) {
+    const int64_t gr = rt * 16 + i;
+    if (gr < grows) {
+      const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
+      vismax = lv > vismax ? lv : vismax;
+    }
+  }
+  const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
+  const int DT = (int)(d.hd / 16);
+  v4i T[7][2];
+  uint64_t O[2][4];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+    for (int e = 0; e < 7; ++e) T[e][tt] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[tt][i] = 0;
+  }
+  auto fold = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int e = 0; e < 7; ++e) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[tt][i] += (uint64_t)(int64_t)T[e][tt][i] << (8 * e);
+        T[e][tt] = v4i{0, 0, 0, 0};
+      }
+  };
+  const int8_t* Vb = (const int8_t*)d.V;
+  int steps = 0;
+  for (int64_t t0 = 0; t0 < vismax; t0 += 64) {
+    int64_t pi, slot0;
+    page_split(d, t0, pi, slot0);
+    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+    const int nv = (int)max((int64_t)0, min((int64_t)16, alv - (t0 + 16 * g)));
+    for (int lp = 0; lp < Lp; ++lp) {
+      v4i a = nv > 0 ? *(const v4i*)(d.pd + ((int64_t)lp * rows + ar) * d.pdL + t0 + 16 * g) : v4i{0, 0, 0, 0};
+      a = keep_bytes(a, nv);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tile = wave + 4 * tt;
+        if (tile >= DT) continue;
+        const int64_t c = 16 * tile + m;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const v4i bv = *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, c, d.hd, d.P));
+          T[lp + db][tt] = mfma8(a, bv, T[lp + db][tt]);
+        }
+      }
+    }
+    if (++steps == 64) { fold(); steps = 0; }
+  }
+  fold();
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tile = wave + 4 * tt;
+    if (tile >= DT) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t gr = rt * 16 + 4 * g + i;
+      if (gr >= grows) continue;
+      const int64_t r = group_row(d, b, kv, gr);
+      d.out[qoff(d, r) + 16 * tile + m] = (int64_t)O[tt][i] >> d.frac;
+      if (tile == 0 && m == 0) {
+        const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
+        const u128 pv = (u128)d.maxp[r] * d.run_v[bkv];
+        if (pv > (u128)(INT64_MAX / lv)) atomicOr(d.status, IMIE_EOVF);
+      }
+    }
   }
 }
 
@@ -710,6 +1271,7 @@ void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t*
   int64_t c = (Lmax + want - 1) / want;
   c = ((c + 63) / 64) * 64;
   if (c < 64) c = 64;
+  if (c > 8192) c = 8192;                            // kv8 PV: int32 sums stay below 2^27 per chunk
   *chunk = c;
   *nch = (Lmax + c - 1) / c;
   if (*nch < 1) *nch = 1;
@@ -727,7 +1289,10 @@ size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int
   int64_t chunk = 0, nch = 0;
   dec_geometry(B, Hkv, Lmax, &chunk, &nch);
   const int64_t part = M == 1 ? nch * (rows * hd + 3 * rows + 2 * B * Hkv) : 0;
-  return (size_t)(rows * Lmax + rows * hd + rows + 3 * rows + 2 * B * Hkv + part) * 8 + 256;
+  // prefill kv8: per-256-key row maxima + 4 digit planes of p (bytes)
+  const int64_t pdL = (Lmax + 15) / 16 * 16;
+  const int64_t pf = M > 1 ? ((Lmax + kPfKeys - 1) / kPfKeys) * rows + (4 * rows * pdL + 7) / 8 + 2 : 0;
+  return (size_t)(rows * Lmax + rows * hd + rows + 3 * rows + 2 * B * Hkv + part + pf) * 8 + 256;
 }
 
 void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
@@ -749,6 +1314,12 @@ void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
   d.cmp = (uint64_t*)p;    p += nch * rows;
   d.ckm = (uint64_t*)p;    p += nch * d.B * d.Hkv;
   d.cvm = (uint64_t*)p;
+  if (d.M > 1) {                                      // prefill kv8 (decode partials are not used)
+    p = (int64_t*)d.part;
+    d.pmax = p;            p += ((d.Lmax + kPfKeys - 1) / kPfKeys) * rows;
+    d.pd = (int8_t*)(((uintptr_t)p + 15) & ~(uintptr_t)15);
+    d.pdL = (d.Lmax + 15) / 16 * 16;
+  }
 }
 
 int imie_attention_launch(AttnDesc d, hipStream_t st) {
@@ -773,14 +1344,28 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
 #define IMIE_DEC_R(K_, KT_)                                                                                \
     if (rep == 1) IMIE_DEC(K_, KT_, 1); else if (rep == 2) IMIE_DEC(K_, KT_, 2);                           \
     else if (rep == 4) IMIE_DEC(K_, KT_, 4); else IMIE_DEC(K_, KT_, 8)
-    if (d.kv32) { IMIE_DEC_R(dec_scores_kernel, int32_t); } else { IMIE_DEC_R(dec_scores_kernel, int64_t); }
+    if (d.kv32) {
+      if (rep == 1) hipLaunchKernelGGL(dec_scores8_kernel<1>, gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL(dec_scores8_kernel<2>, gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL(dec_scores8_kernel<4>, gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL(dec_scores8_kernel<8>, gd, dim3(256), 0, st, d);
+    } else {
+      IMIE_DEC_R(dec_scores_kernel, int64_t);
+    }
     IMIE_HIP(hipGetLastError());
     if (rep == 1) hipLaunchKernelGGL(dec_exp_kernel<1>, gd, dim3(256), 0, st, d);
     else if (rep == 2) hipLaunchKernelGGL(dec_exp_kernel<2>, gd, dim3(256), 0, st, d);
     else if (rep == 4) hipLaunchKernelGGL(dec_exp_kernel<4>, gd, dim3(256), 0, st, d);
     else hipLaunchKernelGGL(dec_exp_kernel<8>, gd, dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
-    if (d.kv32) { IMIE_DEC_R(dec_pv_kernel, int32_t); } else { IMIE_DEC_R(dec_pv_kernel, int64_t); }
+    if (d.kv32) {
+      if (rep == 1) hipLaunchKernelGGL(dec_pv8_kernel<1>, gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL(dec_pv8_kernel<2>, gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL(dec_pv8_kernel<4>, gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL(dec_pv8_kernel<8>, gd, dim3(256), 0, st, d);
+    } else {
+      IMIE_DEC_R(dec_pv_kernel, int64_t);
+    }
 #undef IMIE_DEC_R
 #undef IMIE_DEC
     IMIE_HIP(hipGetLastError());
@@ -789,16 +1374,26 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
     imie_prof_mark(IMIE_K_ATTN, st, false);
     return IMIE_OK;
   }
+  if (d.kv32) {                                      // kv8 prefill: MFMA scores, softmax to p digits, MFMA PV
+    if (d.hd % 16 != 0 || !d.run_k || !d.run_v) return IMIE_EARG;
+    const int64_t nrt16 = (grows + 15) / 16, nkt8 = (d.Lmax + kPfKeys - 1) / kPfKeys;
+    hipLaunchKernelGGL(pf_scores8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16), (unsigned)nkt8), dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pf_softmax8_kernel, dim3((unsigned)rows), dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pf_pv8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16)), dim3(256), 0, st, d);
+    IMIE_HIP(hipGetLastError());
+    imie_prof_mark(IMIE_K_ATTN, st, false);
+    return IMIE_OK;
+  }
   hipLaunchKernelGGL(attn_init_kernel, dim3((unsigned)((ninit + 255) / 256)), dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());
   const dim3 g2((unsigned)(d.B * d.Hkv * nrt), (unsigned)nkt);
-  if (d.kv32) hipLaunchKernelGGL(attn_scores_kernel<int32_t>, g2, dim3(256), 0, st, d);
-  else hipLaunchKernelGGL(attn_scores_kernel<int64_t>, g2, dim3(256), 0, st, d);
+  hipLaunchKernelGGL(attn_scores_kernel<int64_t>, g2, dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());
   hipLaunchKernelGGL(attn_softmax_kernel, dim3((unsigned)rows), dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());
-  if (d.kv32) hipLaunchKernelGGL(attn_pv_kernel<int32_t>, g2, dim3(256), 0, st, d);
-  else hipLaunchKernelGGL(attn_pv_kernel<int64_t>, g2, dim3(256), 0, st, d);
+  hipLaunchKernelGGL(attn_pv_kernel<int64_t>, g2, dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());
   hipLaunchKernelGGL(attn_final_kernel, dim3((unsigned)((rows * d.hd + 255) / 256)), dim3(256), 0, st, d);
   IMIE_HIP(hipGetLastError());

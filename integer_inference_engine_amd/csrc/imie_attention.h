@@ -8,7 +8,8 @@ struct AttnDesc {
   const int64_t* q;
   const void* K;                   // paged pools (see attention.hip)
   const void* V;
-  int kv32;                        // 1: int32 KV elements, 0: int64
+  int kv32;                        // 1: kv8 digit-plane cache (imie_kvfmt.h), 0: int64 elements
+  const uint64_t *run_k, *run_v;   // kv8: running max|K|, max|V| per (sequence, kv head) [B*Hkv]
   const int64_t* pt;               // page table [B][mp]
   int64_t P, mp;                   // tokens per page, pages per sequence
   int pshift;                      // log2(P) when P is a power of two, else -1 (set by the launcher)
@@ -30,6 +31,9 @@ struct AttnDesc {
   uint64_t *cz, *cmp;              // decode: per-chunk Z and max p [nch][B*H]
   uint64_t *ckm, *cvm;             // decode: per-chunk max|K|, max|V| [nch][B*Hkv]
   int64_t chunk, nch;              // decode key chunking (set by the launcher)
+  int64_t* pmax;                   // prefill kv8: per-256-key row maxima [nkt][rows]
+  int8_t* pd;                      // prefill kv8: digit planes of p [4][rows][pdL]
+  int64_t pdL;                     // row stride of pd (Lmax rounded up to 16)
 };
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax);

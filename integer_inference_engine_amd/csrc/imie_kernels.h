@@ -72,5 +72,12 @@ struct QkHeadArgs {
   void *kpool, *vpool;
   uint64_t* guard;                 // 4 x u64, zeroed before the launch (RoPE envelope maxima)
   int* status;
+  // kv8 cache only: max|k|, max|v| of the appended rows per (row, kv head) [rows][Hkv] (M > 1), or folded
+  // straight into the running per-(sequence, kv head) maxima run_k / run_v [B][Hkv] (M == 1)
+  uint64_t *rowk, *rowv, *run_k, *run_v;
 };
-int imie_qk_head_launch(const QkHeadArgs& a, int kv32, hipStream_t st);
+// kv8 = 1: the digit-plane cache of imie_kvfmt.h; 0: int64 rows
+int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
+// kv8 cache: fold the appended rows' maxima (rowk / rowv, M rows per sequence) into run_k / run_v
+int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
+                          uint64_t* run_k, uint64_t* run_v, hipStream_t st);

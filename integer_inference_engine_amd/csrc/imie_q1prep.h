@@ -14,6 +14,7 @@ namespace imie_q1 {
 constexpr int kSlabBlocks = 4;     // 128-blocks per slab (= K 512 per wave step)
 constexpr int kMaxLimbs = 8;
 constexpr int kMaxSegs = 3;        // weights sharing one activation in a single matvec launch
+constexpr int kGemmMinT = 8;       // from this many tokens the Q1 linear runs as an MFMA GEMM (own digit layout)
 
 struct Q1PrepOut {                 // where a prep writes its table (sized for T tokens of nb blocks)
   uint32_t* xq;

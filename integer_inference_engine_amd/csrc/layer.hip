@@ -13,7 +13,9 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_attention.h"
+#include "imie_kvfmt.h"
 #include <string.h>
+#include <algorithm>
 
 namespace {
 
@@ -44,6 +46,48 @@ int fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t st) {
   return IMIE_OK;
 }
 
+// Seeded synthetic cache contents: element i (flattened (kv, j, c) of the (Hkv, len, hd) tensor of one layer,
+// kind 0 = K / 1 = V, and sequence b) is uniform in [lo, lo + span) from the counter-based SplitMix64 stream keyed
+// by (seed, 100000 + 1024 layer + 512 kind + sequence id) -- the same draw as the host generator's uniform_int.
+__device__ inline uint64_t sm_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void kv_fill_kernel(void* pool, const int64_t* __restrict__ pt, int64_t mp,
+                                                      int64_t P, int pshift, int64_t Hkv, int64_t hd,
+                                                      const int64_t* __restrict__ lens, const int64_t* __restrict__ sid,
+                                                      uint64_t seed, int64_t layer, int kind, int64_t lo,
+                                                      uint64_t span, int kv8, uint64_t* __restrict__ run) {
+  const int64_t b = blockIdx.z, kv = blockIdx.y;
+  const int64_t len = lens[b];
+  const int64_t n = len * hd;
+  const uint64_t tid = (uint64_t)(100000 + 1024 * layer + 512 * kind + sid[b]);
+  const uint64_t key = sm_mix(seed * 0x100000001B3ull + tid * 0x9E3779B1ull + 0x632BE59BD9B4E019ull);
+  uint64_t mx = 0;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t j = e / hd, c = e - j * hd;
+    const uint64_t i = (uint64_t)(kv * len * hd + e);
+    const int64_t v = (int64_t)(sm_mix(key + (i + 1) * 0x9E3779B97F4A7C15ull) % span) + lo;
+    const uint64_t a = imie_absu64(v);
+    mx = a > mx ? a : mx;
+    const int64_t pg = pt[b * mp + (j >> pshift)], slot = j & (P - 1);
+    if (kv8) {
+      int8_t* blk = (int8_t*)pool + imie_kv8::block_base(pg, kv, Hkv, hd, P);
+      const uint32_t w = imie_kv8::encode(v);
+      for (int db = 0; db < 4; ++db) {
+        const int64_t off = kind == 0 ? imie_kv8::k_off(slot, db, c, hd) : imie_kv8::v_off(slot, db, c, hd, P);
+        blk[off] = (int8_t)(w >> (8 * db));
+      }
+    } else {
+      ((int64_t*)pool)[pg * (Hkv * P * hd) + kv * P * hd + slot * hd + c] = v;
+    }
+  }
+  mx = imie_wave_max_u64(mx);
+  if (run && (threadIdx.x & 63) == 0 && mx) atomicMax((unsigned long long*)&run[b * Hkv + kv], (unsigned long long)mx);
+}
+
 struct LayerW {
   int64_t w[7];                       // wq, wk, wv, wo, w1, wu, w2 Q1 handles
   const int64_t *n1g, *n2g, *qng, *kng;
@@ -56,13 +100,16 @@ struct Net {
   int64_t out_head = -1;
   const int64_t *cos = nullptr, *sin = nullptr;
   // KV
-  int kv32 = 0;
-  int64_t P = 0, mp = 0, npages = 0;
+  int kv32 = 0;                       // 1: kv8 digit-plane cache (imie_kvfmt.h), 0: int64 rows
+  int64_t P = 0, mp = 0, npages = 0;  // page size, page-table row length (max pages of a sequence), pool pages
+  std::vector<int64_t> pg0, npg;      // per sequence: first pool page and page count (its pages are contiguous)
   std::vector<void*> kpool, vpool;    // per layer
   int64_t* pt = nullptr;              // device [B][mp]
   std::vector<int64_t> len;           // host lengths per sequence
   // workspace
   DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx, amx, stepc;
+  DevBuf kvrun;                       // kv8: running max|K|, max|V| per (layer, sequence, kv head): [nl][2][B*Hkv]
+  DevBuf kvrow;                       // kv8: appended rows' maxima [2][rows*Hkv]
   Q1Ws q1w;                           // this net's Q1 workspace (graph-stable addresses)
   // captured greedy decode step (imie_net_decode_dev): valid for the pointer key it was captured with
   hipGraphExec_t gexec = nullptr;
@@ -81,26 +128,46 @@ Net* net_get(int64_t h) {
   return (n && n->live) ? n : nullptr;
 }
 
+void net_free_kv(Net& n) {
+  for (auto p : n.kpool) if (p) (void)hipFree(p);
+  for (auto p : n.vpool) if (p) (void)hipFree(p);
+  n.kpool.clear();
+  n.vpool.clear();
+  if (n.pt) (void)hipFree(n.pt);
+  n.pt = nullptr;
+}
+
 void net_free(Net* n) {
   if (!n) return;
   (void)hipStreamSynchronize(imie_stream());
-  for (auto p : n->kpool) if (p) (void)hipFree(p);
-  for (auto p : n->vpool) if (p) (void)hipFree(p);
-  if (n->pt) (void)hipFree(n->pt);
+  net_free_kv(*n);
   if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
                   &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx, &n->amx,
-                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab};
+                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow};
   for (auto b : bs) b->release();
   n->live = false;
 }
 
-// Allocate the paged cache: every sequence gets ceil(cap / P) pages (page table = identity blocks).
-int net_alloc_kv(Net& n, int64_t cap, int64_t P, int kv32) {
+// Allocate the paged cache: sequence b gets ceil(caps[b] / P) pages, contiguous in the pool; its page-table row
+// (mp = the largest page count) lists them and repeats its first page past its own count (never addressed).
+int net_alloc_kv(Net& n, const std::vector<int64_t>& caps, int64_t P, int kv32) {
+  if (P <= 0 || (kv32 && P % 64 != 0)) return IMIE_EARG;   // kv8 MFMA steps take 64 slots of one page
   n.kv32 = kv32;
   n.P = P;
-  n.mp = (cap + P - 1) / P;
-  n.npages = n.B * n.mp;
+  n.pg0.assign((size_t)n.B, 0);
+  n.npg.assign((size_t)n.B, 0);
+  int64_t tot = 0, mp = 1;
+  for (int64_t b = 0; b < n.B; ++b) {
+    if (caps[(size_t)b] <= 0) return IMIE_EARG;
+    const int64_t np = (caps[(size_t)b] + P - 1) / P;
+    n.pg0[(size_t)b] = tot;
+    n.npg[(size_t)b] = np;
+    tot += np;
+    mp = np > mp ? np : mp;
+  }
+  n.mp = mp;
+  n.npages = tot;
   const size_t esz = kv32 ? 4 : 8;
   const size_t bytes = (size_t)(n.npages * n.Hkv * P * n.hd) * esz;
   n.kpool.assign((size_t)n.nl, nullptr);
@@ -109,13 +176,25 @@ int net_alloc_kv(Net& n, int64_t cap, int64_t P, int kv32) {
     if (hipMalloc(&n.kpool[(size_t)l], bytes) != hipSuccess) return IMIE_EARG;
     if (hipMalloc(&n.vpool[(size_t)l], bytes) != hipSuccess) return IMIE_EARG;
   }
-  std::vector<int64_t> pt((size_t)n.npages);
-  for (int64_t i = 0; i < n.npages; ++i) pt[(size_t)i] = i;
-  IMIE_HIP(hipMalloc((void**)&n.pt, (size_t)n.npages * 8));
-  IMIE_HIP(hipMemcpy(n.pt, pt.data(), (size_t)n.npages * 8, hipMemcpyHostToDevice));
+  std::vector<int64_t> pt((size_t)(n.B * mp));
+  for (int64_t b = 0; b < n.B; ++b)
+    for (int64_t i = 0; i < mp; ++i)
+      pt[(size_t)(b * mp + i)] = n.pg0[(size_t)b] + (i < n.npg[(size_t)b] ? i : 0);
+  IMIE_HIP(hipMalloc((void**)&n.pt, pt.size() * 8));
+  IMIE_HIP(hipMemcpy(n.pt, pt.data(), pt.size() * 8, hipMemcpyHostToDevice));
   n.len.assign((size_t)n.B, 0);
+  if (kv32) {
+    const size_t rb = (size_t)(n.nl * 2 * n.B * n.Hkv) * 8;
+    if (n.kvrun.ensure(rb)) return IMIE_EARG;
+    IMIE_HIP(hipMemset(n.kvrun.p, 0, rb));
+  }
   return IMIE_OK;
 }
+
+int64_t seq_cap(const Net& n, int64_t b) { return n.npg[(size_t)b] * n.P; }
+
+uint64_t* run_k(Net& n, int64_t l) { return (uint64_t*)n.kvrun.p + (l * 2) * n.B * n.Hkv; }
+uint64_t* run_v(Net& n, int64_t l) { return (uint64_t*)n.kvrun.p + (l * 2 + 1) * n.B * n.Hkv; }
 
 // Workspace for rows = B * M new rows attending over at most lmax keys.
 int net_ensure(Net& n, int64_t M, int64_t lmax) {
@@ -127,7 +206,8 @@ int net_ensure(Net& n, int64_t M, int64_t lmax) {
       n.att.ensure((size_t)(rows * qd) * 8) || n.gate.ensure((size_t)(rows * n.dff) * 8) ||
       n.up.ensure((size_t)(rows * n.dff) * 8) || n.h.ensure((size_t)(rows * n.dff) * 8) ||
       n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure((size_t)n.nl * 32) ||
-      n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)))
+      n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)) ||
+      n.kvrow.ensure((size_t)(2 * rows * n.Hkv) * 8))
     return IMIE_EARG;
   return IMIE_OK;
 }
@@ -137,7 +217,7 @@ int net_ensure(Net& n, int64_t M, int64_t lmax) {
 int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, int64_t* xn, const int64_t* hs,
                      int cnt, int64_t* const* outs, hipStream_t st) {
   int* status = (int*)n.status.p;
-  if (n.d % 128 == 0 && n.d <= 4096) {
+  if (n.d % 128 == 0 && n.d <= 4096 && rows < imie_q1::kGemmMinT) {
     imie_q1::Q1PrepOut po;
     int rc = imie_q1_prep_target(&n.q1w, n.d / 128, rows, &po);
     if (rc) return rc;
@@ -185,7 +265,12 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       a.rows = rows; a.H = n.H; a.Hkv = n.Hkv; a.hd = n.hd; a.M = M; a.eps = n.eps; a.frac = (int)n.frac;
       a.pt = n.pt; a.P = n.P; a.mp = n.mp; a.kpool = n.kpool[(size_t)l]; a.vpool = n.vpool[(size_t)l];
       a.guard = guard + 4 * l; a.status = status;
+      if (n.kv32) {
+        a.rowk = (uint64_t*)n.kvrow.p; a.rowv = (uint64_t*)n.kvrow.p + rows * n.Hkv;
+        a.run_k = run_k(n, l); a.run_v = run_v(n, l);
+      }
       CK(imie_qk_head_launch(a, n.kv32, st));
+      if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));
     }
     AttnDesc d = {};
     d.B = n.B; d.H = n.H; d.Hkv = n.Hkv; d.hd = n.hd; d.M = M;
@@ -195,6 +280,7 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
     d.starts = (const int64_t*)n.starts.p; d.lengths = nullptr;
     d.Lmax = lmax; d.frac = (int)n.frac; d.inv_sqrt = n.inv_sqrt;
     d.out = att; d.status = status; d.rope_guard = guard + 4 * l;
+    if (n.kv32) { d.run_k = run_k(n, l); d.run_v = run_v(n, l); }
     imie_attn_bind_scratch(d, n.attn.p);
     CK(imie_attention_launch(d, st));
     CK(imie_q1_launch_multi(&L.w[3], 1, att, rows, n.frac, &x, 1, &n.q1w, st));
@@ -202,7 +288,7 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       int64_t* outs[2] = {gate, up};
       CK(norm_into_matvec(n, x, rows, L.n2g, xn, &L.w[4], 2, outs, st));
     }
-    if (n.dff % 128 == 0) {
+    if (n.dff % 128 == 0 && rows < imie_q1::kGemmMinT) {
       imie_q1::Q1PrepOut po;
       CK(imie_q1_prep_target(&n.q1w, n.dff / 128, rows, &po));
       CK(imie_silu_mul_prep_launch(gate, up, rows, n.dff, n.frac, hh, po, st));
@@ -222,7 +308,7 @@ int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st
   const int64_t rows = n.B * M;
   int64_t lmax = 0;
   for (int64_t b = 0; b < n.B; ++b) {
-    if (starts[b] < 0 || starts[b] + M > n.mp * n.P) return IMIE_EARG;
+    if (starts[b] < 0 || starts[b] + M > seq_cap(n, b)) return IMIE_EARG;
     lmax = starts[b] + M > lmax ? starts[b] + M : lmax;
   }
   if (net_ensure(n, M, lmax)) return IMIE_EARG;
@@ -317,7 +403,7 @@ int64_t net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t 
   n->sin = buf_get(sin_h, cap * (hd / 2));
   if (!n->cos || !n->sin) { delete n; return -1; }
   n->live = true;
-  if (net_alloc_kv(*n, cap, page, kv32)) { net_free(n); delete n; return -1; }
+  if (net_alloc_kv(*n, std::vector<int64_t>((size_t)B, cap), page, kv32)) { net_free(n); delete n; return -1; }
   nets().push_back(n);
   return (int64_t)nets().size() - 1;
 }
@@ -430,10 +516,23 @@ int64_t imie_net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int
 int bonsai_decode_ctx_seed_seq(int64_t ctx, int64_t b, const int64_t* k, const int64_t* v, int64_t Lb) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   Net* n = net_get(ctx);
-  if (!n || !k || !v || b < 0 || b >= n->B || Lb < 0 || Lb > n->mp * n->P) return IMIE_EARG;
+  if (!n || !k || !v || b < 0 || b >= n->B || Lb < 0 || Lb > seq_cap(*n, b)) return IMIE_EARG;
   const size_t esz = n->kv32 ? 4 : 8;
-  std::vector<char> kb((size_t)(n->mp * n->Hkv * n->P * n->hd) * esz), vb(kb.size());
-  int bad = 0;
+  std::vector<char> kb((size_t)(n->npg[(size_t)b] * n->Hkv * n->P * n->hd) * esz), vb(kb.size());
+  std::vector<uint64_t> mk((size_t)(n->nl * n->Hkv), 0), mv(mk.size(), 0);
+  for (int64_t l = 0; l < n->nl && n->kv32; ++l)   // transactional: check every value before writing any
+    for (int64_t kv = 0; kv < n->Hkv; ++kv)
+      for (int64_t j = 0; j < Lb; ++j)
+        for (int64_t c = 0; c < n->hd; ++c) {
+          const int64_t src = ((l * n->Hkv + kv) * Lb + j) * n->hd + c;
+          if (!imie_kv8::fits(k[src]) || !imie_kv8::fits(v[src])) return IMIE_EOVF;
+          const uint64_t ak = k[src] < 0 ? (uint64_t)0 - (uint64_t)k[src] : (uint64_t)k[src];
+          const uint64_t av = v[src] < 0 ? (uint64_t)0 - (uint64_t)v[src] : (uint64_t)v[src];
+          uint64_t& a1 = mk[(size_t)(l * n->Hkv + kv)];
+          uint64_t& a2 = mv[(size_t)(l * n->Hkv + kv)];
+          a1 = ak > a1 ? ak : a1;
+          a2 = av > a2 ? av : a2;
+        }
   for (int64_t l = 0; l < n->nl; ++l) {
     memset(kb.data(), 0, kb.size());
     memset(vb.data(), 0, vb.size());
@@ -441,20 +540,29 @@ int bonsai_decode_ctx_seed_seq(int64_t ctx, int64_t b, const int64_t* k, const i
       for (int64_t j = 0; j < Lb; ++j)
         for (int64_t c = 0; c < n->hd; ++c) {
           const int64_t src = ((l * n->Hkv + kv) * Lb + j) * n->hd + c;
-          const int64_t dst = (j / n->P) * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + (j % n->P) * n->hd + c;
+          const int64_t pgl = j / n->P, slot = j % n->P;     // page within sequence b (identity page table)
           if (n->kv32) {
-            if (k[src] != (int64_t)(int32_t)k[src] || v[src] != (int64_t)(int32_t)v[src]) bad = 1;
-            ((int32_t*)kb.data())[dst] = (int32_t)k[src];
-            ((int32_t*)vb.data())[dst] = (int32_t)v[src];
+            const int64_t base = imie_kv8::block_base(pgl, kv, n->Hkv, n->hd, n->P);
+            const uint32_t wk = imie_kv8::encode(k[src]), wv = imie_kv8::encode(v[src]);
+            for (int db = 0; db < 4; ++db) {
+              kb[(size_t)(base + imie_kv8::k_off(slot, db, c, n->hd))] = (char)(wk >> (8 * db));
+              vb[(size_t)(base + imie_kv8::v_off(slot, db, c, n->hd, n->P))] = (char)(wv >> (8 * db));
+            }
           } else {
+            const int64_t dst = pgl * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + slot * n->hd + c;
             ((int64_t*)kb.data())[dst] = k[src];
             ((int64_t*)vb.data())[dst] = v[src];
           }
         }
-    if (bad) return IMIE_EOVF;                      // transactional: nothing of sequence b was written
-    const size_t off = (size_t)(b * n->mp * n->Hkv * n->P * n->hd) * esz;
+    const size_t off = (size_t)(n->pg0[(size_t)b] * n->Hkv * n->P * n->hd) * esz;
     IMIE_HIP(hipMemcpy((char*)n->kpool[(size_t)l] + off, kb.data(), kb.size(), hipMemcpyHostToDevice));
     IMIE_HIP(hipMemcpy((char*)n->vpool[(size_t)l] + off, vb.data(), vb.size(), hipMemcpyHostToDevice));
+    if (n->kv32) {
+      IMIE_HIP(hipMemcpy(run_k(*n, l) + b * n->Hkv, &mk[(size_t)(l * n->Hkv)], (size_t)n->Hkv * 8,
+                         hipMemcpyHostToDevice));
+      IMIE_HIP(hipMemcpy(run_v(*n, l) + b * n->Hkv, &mv[(size_t)(l * n->Hkv)], (size_t)n->Hkv * 8,
+                         hipMemcpyHostToDevice));
+    }
   }
   n->len[(size_t)b] = Lb;
   return IMIE_OK;
@@ -527,7 +635,7 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
   if (!n || !ebits || !escale || !ids_dev || !logits_dev || steps <= 0 || n->out_head < 0) return IMIE_EARG;
   const int64_t cap = n->mp * n->P;
   for (int64_t b = 0; b < n->B; ++b)
-    if (n->len[(size_t)b] + steps > cap) return IMIE_EARG;
+    if (n->len[(size_t)b] + steps > seq_cap(*n, b)) return IMIE_EARG;
   hipStream_t st = (hipStream_t)stream;
   if (net_ensure(*n, 1, cap) || n->amx.ensure(imie_argmax_scratch_bytes(n->B)) || n->stepc.ensure(64) ||
       n->lastx.ensure((size_t)(n->B * n->d) * 8))
@@ -581,6 +689,64 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
   return IMIE_OK;
 }
 
+// Ragged page allocation (no reference counterpart): sequence b gets room for caps[b] positions. Replaces the
+// cache (its contents are discarded and every sequence length restarts at 0).
+int imie_net_set_caps(int64_t ctx, const int64_t* caps) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !caps) return IMIE_EARG;
+  for (int64_t b = 0; b < n->B; ++b)
+    if (caps[b] <= 0) return IMIE_EARG;
+  IMIE_HIP(hipDeviceSynchronize());
+  if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
+  net_free_kv(*n);
+  return net_alloc_kv(*n, std::vector<int64_t>(caps, caps + n->B), n->P, n->kv32);
+}
+
+// Fill every layer's cache with seeded synthetic K / V for lens[b] positions per sequence, on the device (no
+// reference counterpart; the workload generator of the benchmark and the large-context tests). Values are
+// uniform in [lo, hi); see kv_fill_kernel for the stream; seq_ids[b] (0..511, nullptr: b) keys sequence b's
+// draw, so one sequence can be regenerated alone in another context. Sets the sequence lengths.
+int imie_net_fill_kv(int64_t ctx, uint64_t seed, const int64_t* lens, const int64_t* seq_ids, int64_t lo,
+                     int64_t hi) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !lens || hi <= lo || (n->P & (n->P - 1)) != 0) return IMIE_EARG;
+  if (n->kv32 && (!imie_kv8::fits(lo) || !imie_kv8::fits(hi - 1))) return IMIE_EOVF;
+  int64_t lmax = 0;
+  for (int64_t b = 0; b < n->B; ++b) {
+    if (lens[b] < 0 || lens[b] > seq_cap(*n, b)) return IMIE_EARG;
+    lmax = lens[b] > lmax ? lens[b] : lmax;
+  }
+  hipStream_t st = imie_stream();
+  std::vector<int64_t> ls((size_t)(2 * n->B));
+  for (int64_t b = 0; b < n->B; ++b) {
+    ls[(size_t)b] = lens[b];
+    ls[(size_t)(n->B + b)] = seq_ids ? seq_ids[b] : b;
+    if (ls[(size_t)(n->B + b)] < 0 || ls[(size_t)(n->B + b)] >= 512) return IMIE_EARG;
+  }
+  DevBuf dl;
+  if (dl.ensure((size_t)n->B * 16)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpy(dl.p, ls.data(), (size_t)n->B * 16, hipMemcpyHostToDevice));
+  int pshift = 0;
+  while (((int64_t)1 << pshift) < n->P) ++pshift;
+  const unsigned gx = (unsigned)std::min<int64_t>(1024, (lmax * n->hd + 255) / 256 + 1);
+  for (int64_t l = 0; l < n->nl; ++l)
+    for (int kind = 0; kind < 2; ++kind) {
+      uint64_t* run = n->kv32 ? (kind == 0 ? run_k(*n, l) : run_v(*n, l)) : nullptr;
+      hipLaunchKernelGGL(kv_fill_kernel, dim3(gx, (unsigned)n->Hkv, (unsigned)n->B), dim3(256), 0, st,
+                         kind == 0 ? n->kpool[(size_t)l] : n->vpool[(size_t)l], (const int64_t*)n->pt, n->mp, n->P,
+                         pshift, n->Hkv, n->hd, (const int64_t*)dl.p, (const int64_t*)dl.p + n->B, seed, l, kind, lo,
+                         (uint64_t)(hi - lo),
+                         n->kv32, run);
+      IMIE_HIP(hipGetLastError());
+    }
+  IMIE_HIP(hipStreamSynchronize(st));
+  dl.release();
+  for (int64_t b = 0; b < n->B; ++b) n->len[(size_t)b] = lens[b];
+  return IMIE_OK;
+}
+
 // Clear (0) or read the context status word: 0 ok, bit 2 attention / RoPE / int32-KV envelope, bit 4 RMSNorm.
 int imie_net_status(int64_t ctx, int clear, void* stream) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
@@ -598,23 +764,35 @@ int imie_net_export_kv(int64_t ctx, int64_t layer, int64_t b, int64_t count, int
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   Net* n = net_get(ctx);
   if (!n || !k_out || !v_out || layer < 0 || layer >= n->nl || b < 0 || b >= n->B || count < 0 ||
-      count > n->mp * n->P)
+      count > seq_cap(*n, b))
     return IMIE_EARG;
   IMIE_HIP(hipStreamSynchronize(imie_stream()));
   IMIE_HIP(hipDeviceSynchronize());
   const size_t esz = n->kv32 ? 4 : 8;
-  const size_t seq = (size_t)(n->mp * n->Hkv * n->P * n->hd);
+  const size_t seq = (size_t)(n->npg[(size_t)b] * n->Hkv * n->P * n->hd);
   std::vector<char> kb(seq * esz), vb(seq * esz);
-  const size_t off = (size_t)b * seq * esz;
+  const size_t off = (size_t)n->pg0[(size_t)b] * n->Hkv * n->P * n->hd * esz;
   IMIE_HIP(hipMemcpy(kb.data(), (char*)n->kpool[(size_t)layer] + off, kb.size(), hipMemcpyDeviceToHost));
   IMIE_HIP(hipMemcpy(vb.data(), (char*)n->vpool[(size_t)layer] + off, vb.size(), hipMemcpyDeviceToHost));
   for (int64_t kv = 0; kv < n->Hkv; ++kv)
     for (int64_t j = 0; j < count; ++j)
       for (int64_t c = 0; c < n->hd; ++c) {
-        const size_t src = (size_t)((j / n->P) * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + (j % n->P) * n->hd + c);
+        const int64_t pgl = j / n->P, slot = j % n->P;
         const size_t dst = (size_t)((kv * count + j) * n->hd + c);
-        k_out[dst] = n->kv32 ? (int64_t)((int32_t*)kb.data())[src] : ((int64_t*)kb.data())[src];
-        v_out[dst] = n->kv32 ? (int64_t)((int32_t*)vb.data())[src] : ((int64_t*)vb.data())[src];
+        if (n->kv32) {
+          const int64_t base = imie_kv8::block_base(pgl, kv, n->Hkv, n->hd, n->P);
+          int8_t kd[4], vd[4];
+          for (int db = 0; db < 4; ++db) {
+            kd[db] = (int8_t)kb[(size_t)(base + imie_kv8::k_off(slot, db, c, n->hd))];
+            vd[db] = (int8_t)vb[(size_t)(base + imie_kv8::v_off(slot, db, c, n->hd, n->P))];
+          }
+          k_out[dst] = imie_kv8::decode4(kd[0], kd[1], kd[2], kd[3]);
+          v_out[dst] = imie_kv8::decode4(vd[0], vd[1], vd[2], vd[3]);
+        } else {
+          const size_t src = (size_t)(pgl * (n->Hkv * n->P * n->hd) + kv * n->P * n->hd + slot * n->hd + c);
+          k_out[dst] = ((int64_t*)kb.data())[src];
+          v_out[dst] = ((int64_t*)vb.data())[src];
+        }
       }
   return IMIE_OK;
 }

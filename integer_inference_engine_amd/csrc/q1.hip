@@ -20,6 +20,7 @@
 #include "imie_kernels.h"
 #include "imie_q1prep.h"
 #include <string.h>
+#include <type_traits>
 #include <stdlib.h>
 
 namespace {
@@ -286,6 +287,406 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
   out[idx] = (int64_t)tot;
 }
 
+
+// ------------------------------------------------------------------------------------------------------
+// GEMM path (T >= kGemmMinT tokens; prefill): int8 MFMA with TOKENS in the MFMA M dimension.
+//   * K step = 64 positions of one block: the 4 MFMA K-groups are the shifts s = 4h + g (h = half of the
+//     block), 16 positions each. B lane (output n, group g) = (block bits dword d >> s) & 0x01010101: bytes
+//     {0, 1} for positions 32d + 8c + s, the order the digit table uses for A (token m, group g).
+//   * Per block and limb l: D = sum over the block of bit * digit_l (2 MFMAs); pos = sum_l D_l << 8l; then the
+//     exact per-(token, output, block) epilogue S = 2 pos - total, += (S * scale) >> frac (wrapping int64).
+//   * Workgroup tile 64 tokens x 128 outputs, 2 x 2 waves of 32 x 64 (2 x 4 MFMA tiles). Workgroups of one token
+//     tile are mapped to one XCD (blockIdx % 8) so that XCD's L2 keeps the tile's digits.
+//   * Two kernels split the blocks by the workgroup's limb count on the block's slab (max over its 64 tokens):
+//     "narrow" (<= 3 limbs, |x| <= 2^23: pos and S exact in int32; digits staged through double-buffered LDS,
+//     next block's loads in flight during the MFMAs) and "wide" (> 3 limbs: int64 pos / S, per-token limb
+//     masking), which adds its blocks into the narrow kernel's output. Every block is taken by exactly one.
+// Digit table layout for the GEMM: xg[l][block][Tp][s] (uint4), totals tg[block][Tp], limbs lt[t][slab]; the
+// prep writes zero digits for limbs L_t <= l < 3 so narrow tiles need no per-token masking.
+// ------------------------------------------------------------------------------------------------------
+constexpr int kNarrowLimbs = 3;
+constexpr int kGemmMaxSlabs = 64;  // K <= 32768
+
+__global__ __launch_bounds__(64) void q1_prep_gemm_kernel(const int64_t* __restrict__ x, int64_t K, int64_t nb,
+                                                           int64_t nbp, int64_t nslabs, int64_t Tp,
+                                                           uint4* __restrict__ xg, int64_t* __restrict__ tg,
+                                                           int* __restrict__ lt) {
+  const int lane = threadIdx.x;
+  const int64_t sl = blockIdx.x, t = blockIdx.y;
+  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
+  const int64_t blk = sl * kSlabBlocks + g;
+  int64_t v[8];
+  uint64_t mx = 0;
+  int64_t part = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int64_t pos = prep_pos(lane, sl, q);
+    v[q] = (pos < nb * 128) ? x[t * K + pos] : 0;
+    const uint64_t a = imie_absu64(v[q]);
+    mx = a > mx ? a : mx;
+    part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
+  }
+  mx = imie_wave_max_u64(mx);
+  const int L = imie_limbs_needed(mx);
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
+  if ((lane & 15) == 0) tg[blk * Tp + t] = part;
+  if (lane == 0) lt[t * nslabs + sl] = L;
+  const int Lw = L > kNarrowLimbs ? L : kNarrowLimbs;
+  for (int l = 0; l < Lw; ++l) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t dig = ((v[q] + 128) & 255) - 128;
+      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;
+      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
+      if (q < 4) w0 |= byte; else w1 |= byte;
+    }
+    uint32_t* dst = (uint32_t*)(xg + ((l * nbp + blk) * Tp + t) * 8 + s);
+    dst[2 * dh] = w0;
+    dst[2 * dh + 1] = w1;
+  }
+}
+
+struct GemmArgs {
+  const uint4* bitsT;
+  const void* scaleT;
+  const uint4* xg;
+  const int64_t* tg;
+  const int* lt;
+  int64_t T, Tp, N, nb, nbp, nslabs, ntt, nto;
+  int frac, accumulate;
+  int64_t* out;
+};
+
+// block bits of this lane's NT outputs (every K-group reads the same 16 bytes) and their scales
+template <bool S64, int NT>
+__device__ inline void gemm_load_b(const GemmArgs& a, int64_t o0, int m, int64_t b, uint4 w[NT], int64_t sc[NT]) {
+  const int64_t sl = b >> 2;
+#pragma unroll
+  for (int jj = 0; jj < NT; ++jj) {
+    const int64_t o = o0 + 16 * jj + m;
+    w[jj] = uint4{0, 0, 0, 0};
+    sc[jj] = 0;
+    if (o < a.N) {
+      const int64_t idx = ((o >> 4) * a.nslabs + sl) * 64 + 16 * (b & 3) + m;
+      const v4i wv = *((const v4i*)a.bitsT + idx);
+      w[jj] = uint4{(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
+      sc[jj] = S64 ? ((const int64_t*)a.scaleT)[idx] : (int64_t)((const int32_t*)a.scaleT)[idx];
+    }
+  }
+}
+
+__device__ inline v4i expand_bits(const uint4 w, int sh) {
+  return v4i{(int)((w.x >> sh) & 0x01010101u), (int)((w.y >> sh) & 0x01010101u), (int)((w.z >> sh) & 0x01010101u),
+             (int)((w.w >> sh) & 0x01010101u)};
+}
+
+__device__ inline void gemm_tile(const GemmArgs& a, int wave, int64_t& t0w, int64_t& o0w, int64_t& t0g, bool& live) {
+  const int64_t wg = blockIdx.x, xcd = wg & 7, j = wg >> 3;
+  const int64_t tpx = (a.ntt + 7) / 8;
+  const int64_t tt = xcd + 8 * (j / a.nto), ot = j % a.nto;
+  live = tt < a.ntt && (j / a.nto) < tpx;
+  t0g = tt * 64;
+  t0w = t0g + (wave >> 1) * 32;
+  o0w = ot * 128 + (wave & 1) * 64;
+}
+
+// per-slab limb maximum over the workgroup's 64 tokens into s_lw
+__device__ inline void gemm_slab_limbs(const GemmArgs& a, int64_t t0g, int* s_lw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t = t0g + lane;
+  for (int64_t sl = wave; sl < a.nslabs; sl += 4) {
+    int L = t < a.T ? a.lt[t * a.nslabs + sl] : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int w2 = __shfl_xor(L, o, 64); L = w2 > L ? w2 : L; }
+    if (lane == 0) s_lw[sl] = L;
+  }
+  __syncthreads();
+}
+
+template <bool S64>
+__global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
+  constexpr int MT = 2, NT = 4;
+  __shared__ int s_lw[kGemmMaxSlabs];
+  // [buffer][limb][token][shift], tokens padded to 9 x 16 B: the 16 lanes of a quarter-wave read tokens
+  // m = 0..15 at a 144 B stride, which covers all 64 LDS banks once (a 128 B stride would hit 2 of them)
+  __shared__ v4i sA[2][kNarrowLimbs][64][9];
+  __shared__ uint4 sB[2][128];                        // block bits of the 128 outputs
+  typedef typename std::conditional<S64, int64_t, int32_t>::type ST;
+  __shared__ ST sS[2][128];                           // their scales (int32 unless the weight keeps int64)
+  __shared__ int64_t sT[2][64];                       // block totals of the 64 tokens
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int64_t t0, o0, t0g;
+  bool live;
+  gemm_tile(a, wave, t0, o0, t0g, live);
+  if (!live) return;
+  gemm_slab_limbs(a, t0g, s_lw);
+  const int m = lane & 15, g = lane >> 4;
+  const int tb = (wave >> 1) * 32;                    // this wave's first token within the workgroup tile
+  const int ob = (wave & 1) * 64;                     // this wave's first output within the workgroup tile
+  const int64_t o0g = o0 - ob;
+  // cooperative stage: thread -> token tid >> 2, shifts 2 (tid & 3) + {0, 1} of every limb; threads < 128 also
+  // one output's bits + scale, threads < 64 one token's total
+  const int st_tok = tid >> 2, st_s = 2 * (tid & 3);
+  v4i pa[kNarrowLimbs][2];
+  uint4 pb = uint4{0, 0, 0, 0};
+  ST ps = 0;
+  int64_t pt = 0;
+  auto stage_load = [&](int64_t b) {
+    const int lwb = s_lw[b >> 2];
+#pragma unroll
+    for (int l = 0; l < kNarrowLimbs; ++l)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        pa[l][u] = (lwb <= kNarrowLimbs && l < lwb)
+                       ? *((const v4i*)a.xg + (uint32_t)((((uint32_t)l * (uint32_t)a.nbp + (uint32_t)b) *
+                                                             (uint32_t)a.Tp + (uint32_t)(t0g + st_tok)) * 8u +
+                                                            (uint32_t)(st_s + u)))
+                       : v4i{0, 0, 0, 0};
+    if (tid < 128) {
+      const int64_t o = o0g + tid;
+      pb = uint4{0, 0, 0, 0};
+      ps = 0;
+      if (o < a.N) {
+        const int64_t idx = ((o >> 4) * a.nslabs + (b >> 2)) * 64 + 16 * (b & 3) + (o & 15);
+        const v4i wv = *((const v4i*)a.bitsT + idx);
+        pb = uint4{(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
+        ps = ((const ST*)a.scaleT)[idx];
+      }
+    }
+    if (tid < 64) pt = t0g + tid < a.T ? a.tg[b * a.Tp + t0g + tid] : 0;
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int l = 0; l < kNarrowLimbs; ++l)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) sA[buf][l][st_tok][st_s + u] = pa[l][u];
+    if (tid < 128) { sB[buf][tid] = pb; sS[buf][tid] = ps; }
+    if (tid < 64) sT[buf][tid] = pt;
+  };
+  int64_t acc[MT][NT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][jj][r] = 0;
+  stage_load(0);
+  stage_store(0);
+  __syncthreads();
+  for (int64_t b = 0; b < a.nb; ++b) {
+    const int buf = (int)(b & 1);
+    const bool more = b + 1 < a.nb;
+    if (more) stage_load(b + 1);                      // next block's operands in flight during this block
+    const int lw = s_lw[b >> 2];
+    if (lw <= kNarrowLimbs) {
+      v4i bx[NT][2];
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) {
+        const uint4 w = sB[buf][ob + 16 * jj + m];
+        bx[jj][0] = expand_bits(w, g);
+        bx[jj][1] = expand_bits(w, 4 + g);
+      }
+      // pos = sum_l D_l 256^l by Horner from the top limb: acc = (acc << 8) + MFMA(limb l); one shift per
+      // element per limb, exact in int32 (every partial is bounded by |pos| <= 2^30)
+      v4i D[MT][NT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int jj = 0; jj < NT; ++jj) D[i][jj] = v4i{0, 0, 0, 0};
+      for (int l = lw - 1; l >= 0; --l) {
+        v4i av[MT][2];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) av[i][h] = sA[buf][l][tb + 16 * i + m][4 * h + g];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj) {
+            v4i c = D[i][jj];
+            c = v4i{(int)((uint32_t)c[0] << 8), (int)((uint32_t)c[1] << 8), (int)((uint32_t)c[2] << 8),
+                    (int)((uint32_t)c[3] << 8)};
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], c, 0, 0, 0);
+            D[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], c, 0, 0, 0);
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t tot = (uint32_t)sT[buf][tb + 16 * i + 4 * g + r];
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj) {
+            const int32_t S = (int32_t)(((uint32_t)D[i][jj][r] << 1) - tot);
+            const ST sc = sS[buf][ob + 16 * jj + m];
+            const int64_t prod = S64 ? (int64_t)((uint64_t)(int64_t)S * (uint64_t)(int64_t)sc)
+                                     : (int64_t)S * (int64_t)(int32_t)sc;   // one v_mad_i64_i32
+            acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)imie_floor_shift(prod, a.frac));
+          }
+        }
+    }
+    if (more) stage_store(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      const int64_t o = o0 + 16 * jj + m;
+      if (o >= a.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 16 * i + 4 * g + r;
+        if (t >= a.T) continue;
+        int64_t* dst = a.out + t * a.N + o;
+        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]) : acc[i][jj][r];
+      }
+    }
+}
+
+// blocks whose slab needs more than kNarrowLimbs limbs on the workgroup's tokens; adds into out
+template <bool S64>
+__global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
+  constexpr int MT = 2, NT = 4;
+  __shared__ int s_lw[kGemmMaxSlabs];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int64_t t0, o0, t0g;
+  bool live;
+  gemm_tile(a, wave, t0, o0, t0g, live);
+  if (!live) return;
+  gemm_slab_limbs(a, t0g, s_lw);
+  bool any = false;
+  for (int64_t sl = 0; sl < a.nslabs; ++sl) any = any || s_lw[sl] > kNarrowLimbs;
+  if (!any) return;
+  const int m = lane & 15, g = lane >> 4;
+  int64_t ta[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) ta[i] = t0 + 16 * i + m;
+  int64_t acc[MT][NT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][jj][r] = 0;
+  for (int64_t b = 0; b < a.nb; ++b) {
+    const int lwg = s_lw[b >> 2];
+    if (lwg <= kNarrowLimbs) continue;
+    const int64_t sl = b >> 2;
+    int la[MT];
+    int lw = 0;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      la[i] = ta[i] < a.T ? a.lt[ta[i] * a.nslabs + sl] : 0;
+      lw = la[i] > lw ? la[i] : lw;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int w2 = __shfl_xor(lw, o, 64); lw = w2 > lw ? w2 : lw; }
+    lw = __builtin_amdgcn_readfirstlane(lw);
+    uint4 w[NT];
+    int64_t sc[NT];
+    gemm_load_b<S64, NT>(a, o0, m, b, w, sc);
+    v4i bx[NT][2];
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      bx[jj][0] = expand_bits(w[jj], g);
+      bx[jj][1] = expand_bits(w[jj], 4 + g);
+    }
+    uint64_t pos[MT][NT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pos[i][jj][r] = 0;
+    for (int l = 0; l < lw; ++l) {
+      v4i av[MT][2];
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          av[i][h] = (l < la[i]) ? *((const v4i*)a.xg + ((l * a.nbp + b) * a.Tp + ta[i]) * 8 + 4 * h + g)
+                                 : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int jj = 0; jj < NT; ++jj) {
+          v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], d, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pos[i][jj][r] += (uint64_t)(int64_t)d[r] << (8 * l);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 16 * i + 4 * g + r;
+        const uint64_t tot = t < a.T ? (uint64_t)a.tg[b * a.Tp + t] : 0;
+#pragma unroll
+        for (int jj = 0; jj < NT; ++jj) {
+          const uint64_t S = 2u * pos[i][jj][r] - tot;
+          const int64_t prod = (int64_t)(S * (uint64_t)sc[jj]);
+          acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)imie_floor_shift(prod, a.frac));
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      const int64_t o = o0 + 16 * jj + m;
+      if (o >= a.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 16 * i + 4 * g + r;
+        if (t >= a.T) continue;
+        int64_t* dst = a.out + t * a.N + o;
+        *dst = (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]);
+      }
+    }
+}
+
+static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
+                         int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
+  const Q1Weight& w0 = *ws[0];
+  const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks, Tp = (T + 63) / 64 * 64;
+  if (nslabs > kGemmMaxSlabs) return IMIE_EARG;
+  if (wk.xq.ensure((size_t)kMaxLimbs * nbp * Tp * 128) || wk.totals.ensure((size_t)nbp * Tp * 8) ||
+      wk.lslab.ensure((size_t)T * nslabs * 4))
+    return IMIE_EARG;
+  const int64_t K = w0.nb * 128;
+  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
+  hipLaunchKernelGGL(q1_prep_gemm_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w0.nb, nbp,
+                     nslabs, Tp, (uint4*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p);
+  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
+  IMIE_HIP(hipGetLastError());
+  imie_prof_mark(IMIE_K_Q1_GEMM, st, true);
+  for (int i = 0; i < cnt; ++i) {
+    const Q1Weight& w = *ws[i];
+    GemmArgs ga;
+    ga.bitsT = w.bits; ga.scaleT = w.scale; ga.xg = (const uint4*)wk.xq.p; ga.tg = (const int64_t*)wk.totals.p;
+    ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
+    ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128;
+    ga.frac = (int)(frac > 63 ? 63 : frac); ga.accumulate = accumulate; ga.out = outs[i];
+    const dim3 grid((unsigned)(8 * ((ga.ntt + 7) / 8) * ga.nto));
+    if (w.scale64) {
+      hipLaunchKernelGGL(q1_gemm_narrow_kernel<true>, grid, dim3(256), 0, st, ga);
+      hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
+    } else {
+      hipLaunchKernelGGL(q1_gemm_narrow_kernel<false>, grid, dim3(256), 0, st, ga);
+      hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+    }
+    IMIE_HIP(hipGetLastError());
+  }
+  imie_prof_mark(IMIE_K_Q1_GEMM, st, false);
+  return IMIE_OK;
+}
+
 // ------------------------------------------------------------------------------------------------------
 // Launch helpers
 // ------------------------------------------------------------------------------------------------------
@@ -300,6 +701,10 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   const Q1Weight& w0 = *ws[0];
   for (int i = 1; i < cnt; ++i)
     if (ws[i]->nb != w0.nb || ws[i]->scale64 != w0.scale64) return IMIE_EARG;
+  if (T >= kGemmMinT) {
+    if (prepped) return IMIE_EARG;                    // fused producers write the matvec table (T < kGemmMinT)
+    return q1_gemm_multi(ws, cnt, x_dev, T, frac, outs, accumulate, wk, st);
+  }
   const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks;
   if (wk.xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || wk.totals.ensure((size_t)T * nbp * 8) ||
       wk.lslab.ensure((size_t)T * nslabs * 4))

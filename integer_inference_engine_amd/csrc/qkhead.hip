@@ -1,7 +1,7 @@
 // Fused per-head stage of the Bonsai layer, between the q/k/v projections and the attention:
 //   q, k <- head RMSNorm (gain qng / kng)              reference_bonsai.py:286-297 (_head_rmsnorm)
 //   q, k <- NeoX RoPE at the row's position            rope_v2.py:92-117, guard rope.py:26-39
-//   cache <- (k, v) at that position (int32 storage guarded)
+//   cache <- (k, v) at that position (int64 rows, or the kv8 digit planes with their envelope guard)
 // One 64-lane workgroup per (row, head); lane j owns the rotation pair (j, j + hd/2). The per-head RMSNorm
 // follows the whole-row kernel's exact arithmetic (shared helpers); the RoPE envelope
 // 2 * max|x| * max|cos, sin| <= INT64_MAX is evaluated over the whole q (and k) tensor through atomic maxima in
@@ -9,6 +9,7 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_fixed.h"
+#include "imie_kvfmt.h"
 
 namespace {
 
@@ -16,7 +17,7 @@ using namespace imie_fx;
 
 __device__ inline void amax_u64(uint64_t* p, uint64_t v) { atomicMax((unsigned long long*)p, (unsigned long long)v); }
 
-template <typename KT>
+template <bool KV8>
 __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   const int64_t r = blockIdx.x, h = blockIdx.y;
   const bool isq = h < a.H;
@@ -86,32 +87,84 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   }
   const int64_t kvh = h - a.H, b = r / a.M;
   const uint32_t pq = (uint32_t)p / (uint32_t)a.P;              // positions are below 2^31
-  const int64_t off = a.pt[b * a.mp + pq] * (a.Hkv * a.P * a.hd) + kvh * a.P * a.hd + ((uint32_t)p - pq * (uint32_t)a.P) * a.hd;
+  const int64_t pg = a.pt[b * a.mp + pq], slot = (uint32_t)p - pq * (uint32_t)a.P;
   const int64_t* vr = a.v + (r * a.Hkv + kvh) * a.hd;
   const int64_t v0 = act ? vr[j] : 0, v1 = act ? vr[j + half] : 0;
-  if (!act) return;
-  if (sizeof(KT) == 4) {
-    if (o0 != (int64_t)(int32_t)o0 || o1 != (int64_t)(int32_t)o1 || v0 != (int64_t)(int32_t)v0 ||
-        v1 != (int64_t)(int32_t)v1)
-      atomicOr(a.status, IMIE_EOVF);
+  if (KV8) {
+    uint64_t mk = imie_absu64(o0) > imie_absu64(o1) ? imie_absu64(o0) : imie_absu64(o1);
+    uint64_t mv = imie_absu64(v0) > imie_absu64(v1) ? imie_absu64(v0) : imie_absu64(v1);
+    mk = imie_wave_max_u64(mk);
+    mv = imie_wave_max_u64(mv);
+    if (j == 0) {
+      if (mk > (uint64_t)imie_kv8::kCap || mv > (uint64_t)imie_kv8::kCap) atomicOr(a.status, IMIE_EOVF);
+      if (a.M == 1) {
+        amax_u64(&a.run_k[b * a.Hkv + kvh], mk);
+        amax_u64(&a.run_v[b * a.Hkv + kvh], mv);
+      } else {
+        a.rowk[r * a.Hkv + kvh] = mk;
+        a.rowv[r * a.Hkv + kvh] = mv;
+      }
+    }
+    if (!act) return;
+    int8_t* blk = (int8_t*)a.kpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
+    int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
+    const uint32_t wk0 = imie_kv8::encode(o0), wk1 = imie_kv8::encode(o1);
+    const uint32_t wv0 = imie_kv8::encode(v0), wv1 = imie_kv8::encode(v1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      blk[imie_kv8::k_off(slot, db, j, a.hd)] = (int8_t)(wk0 >> (8 * db));
+      blk[imie_kv8::k_off(slot, db, j + half, a.hd)] = (int8_t)(wk1 >> (8 * db));
+      vblk[imie_kv8::v_off(slot, db, j, a.hd, a.P)] = (int8_t)(wv0 >> (8 * db));
+      vblk[imie_kv8::v_off(slot, db, j + half, a.hd, a.P)] = (int8_t)(wv1 >> (8 * db));
+    }
+    return;
   }
-  KT* kp = (KT*)a.kpool + off;
-  KT* vp = (KT*)a.vpool + off;
-  kp[j] = (KT)o0;
-  kp[j + half] = (KT)o1;
-  vp[j] = (KT)v0;
-  vp[j + half] = (KT)v1;
+  if (!act) return;
+  const int64_t off = pg * (a.Hkv * a.P * a.hd) + kvh * a.P * a.hd + slot * a.hd;
+  int64_t* kp = (int64_t*)a.kpool + off;
+  int64_t* vp = (int64_t*)a.vpool + off;
+  kp[j] = o0;
+  kp[j + half] = o1;
+  vp[j] = v0;
+  vp[j + half] = v1;
+}
+
+__global__ __launch_bounds__(64) void kv_runmax_kernel(const uint64_t* __restrict__ rowk,
+                                                       const uint64_t* __restrict__ rowv, int64_t M, int64_t Hkv,
+                                                       uint64_t* __restrict__ run_k, uint64_t* __restrict__ run_v) {
+  const int64_t bkv = blockIdx.x, b = bkv / Hkv, kv = bkv % Hkv;
+  uint64_t mk = 0, mv = 0;
+  for (int64_t m = threadIdx.x; m < M; m += 64) {
+    const uint64_t a = rowk[(b * M + m) * Hkv + kv], c = rowv[(b * M + m) * Hkv + kv];
+    mk = a > mk ? a : mk;
+    mv = c > mv ? c : mv;
+  }
+  mk = imie_wave_max_u64(mk);
+  mv = imie_wave_max_u64(mv);
+  if (threadIdx.x == 0) {
+    run_k[bkv] = mk > run_k[bkv] ? mk : run_k[bkv];
+    run_v[bkv] = mv > run_v[bkv] ? mv : run_v[bkv];
+  }
 }
 
 }  // namespace
 
-int imie_qk_head_launch(const QkHeadArgs& a, int kv32, hipStream_t st) {
+int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st) {
   const int64_t rows = a.rows;
   if (rows <= 0) return IMIE_OK;
   if (a.hd > 128 || (a.hd & 1) || a.hd <= 0) return IMIE_EARG;
+  if (kv8 && (!a.run_k || !a.run_v || (a.M > 1 && (!a.rowk || !a.rowv)))) return IMIE_EARG;
   const dim3 grid((unsigned)rows, (unsigned)(a.H + a.Hkv));
-  if (kv32) hipLaunchKernelGGL(qk_head_kernel<int32_t>, grid, dim3(64), 0, st, a);
-  else hipLaunchKernelGGL(qk_head_kernel<int64_t>, grid, dim3(64), 0, st, a);
+  if (kv8) hipLaunchKernelGGL(qk_head_kernel<true>, grid, dim3(64), 0, st, a);
+  else hipLaunchKernelGGL(qk_head_kernel<false>, grid, dim3(64), 0, st, a);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
+                          uint64_t* run_k, uint64_t* run_v, hipStream_t st) {
+  if (B <= 0 || M <= 1) return IMIE_OK;
+  hipLaunchKernelGGL(kv_runmax_kernel, dim3((unsigned)(B * Hkv)), dim3(64), 0, st, rowk, rowv, M, Hkv, run_k, run_v);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

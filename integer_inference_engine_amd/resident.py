@@ -43,6 +43,25 @@ class ResidentNet:
     def _sp(self):
         return ctypes.c_void_p(self.stream.cuda_stream)
 
+    def set_caps(self, caps) -> None:
+        """Ragged cache: room for caps[b] positions in sequence b; replaces the cache (lengths restart at 0)."""
+        c = np.ascontiguousarray(np.asarray(caps, dtype=np.int64))
+        if c.shape != (self.B,):
+            raise ValueError(f"caps must have {self.B} entries")
+        rc = self.lib.imie_net_set_caps(self.h, c.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"set_caps rc={rc}: {_lib.last_error()}")
+
+    def fill_kv(self, seed: int, lens, lo: int = -(1 << 20), hi: int = 1 << 20, seq_ids=None) -> None:
+        """Seeded synthetic K/V (device-generated) for lens[b] positions of every layer; sets the lengths.
+        seq_ids[b] keys sequence b's draw (default b)."""
+        ln = np.ascontiguousarray(np.asarray(lens, dtype=np.int64))
+        sid = None if seq_ids is None else np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
+        rc = self.lib.imie_net_fill_kv(self.h, int(seed), ln.ctypes.data, None if sid is None else sid.ctypes.data,
+                                       int(lo), int(hi))
+        if rc != 0:
+            raise RuntimeError(f"fill_kv rc={rc}: {_lib.last_error()}")
+
     def seed(self, b: int, k: np.ndarray, v: np.ndarray) -> None:
         """k/v (n_layers, Hkv, Lb, hd) int64."""
         k = np.ascontiguousarray(k, dtype=np.int64)

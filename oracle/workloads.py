@@ -57,3 +57,10 @@ def kv_fill(seed: int, tid: int, Hkv: int, L: int, hd: int, mag: int = 1 << 20):
     k = prng.uniform_int(seed, tid, (Hkv, L, hd), -mag, mag)
     v = prng.uniform_int(seed, tid + 1, (Hkv, L, hd), -mag, mag)
     return k, v
+
+
+def kv_fill_seq(seed: int, layer: int, kind: int, sid: int, Hkv: int, L: int, hd: int, lo: int = -(1 << 20),
+                hi: int = 1 << 20):
+    """The device cache generator's draw (kv_fill_kernel): (Hkv, L, hd) for one layer, kind (0 K, 1 V), sequence
+    id."""
+    return prng.uniform_int(seed, 100000 + 1024 * layer + 512 * kind + sid, (Hkv, L, hd), lo, hi)

@@ -1,0 +1,82 @@
+"""Q1_0 GEMM path (T >= 8 tokens: int8 MFMA with tokens in the M dimension) vs the oracle, byte for byte."""
+import numpy as np
+import pytest
+
+from oracle import c_oracle, prng
+from oracle.q1 import q1_linear, q1_linear_bigint
+
+pytestmark = pytest.mark.gpu
+I64_MIN, I64_MAX = -(1 << 63), (1 << 63) - 1
+
+
+@pytest.mark.parametrize("N,nb,T", [(16, 1, 8), (37, 3, 9), (200, 5, 64), (1000, 8, 100), (129, 32, 300),
+                                    (4096, 32, 64)])
+def test_gemm_shapes(gpu, N, nb, T):
+    seed = N * 7 + nb * 3 + T
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << 11), 1 << 11)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -(1 << 20), 1 << 20)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, c_oracle.q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("xmag,smag", [(7, 11), (23, 11), (24, 40), (30, 12), (45, 20), (62, 62)])
+def test_gemm_limb_paths_and_int64_scales(gpu, xmag, smag):
+    """int32 epilogue (<= 3 limbs) and the int64 one (more limbs / 64-bit scales)."""
+    N, nb, T = 80, 6, 33
+    seed = xmag * 100 + smag
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << smag), 1 << smag)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -(1 << xmag), 1 << xmag)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+def test_gemm_mixed_token_magnitudes(gpu):
+    """Tokens of one MFMA tile needing different limb counts (per-token limb masking)."""
+    N, nb, T = 64, 4, 48
+    bits = prng.uniform_bytes(21, 1, (N, nb, 16))
+    scale = prng.uniform_int(21, 2, (N, nb), -(1 << 15), 1 << 15)
+    x = prng.uniform_int(21, 3, (T, nb * 128), -(1 << 6), 1 << 6)
+    big = prng.uniform_int(21, 4, (T, nb * 128), -(1 << 40), 1 << 40)
+    x[::5] = big[::5]
+    x[7, 130] = (1 << 62)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("frac", [0, 1, 31, 63, 64])
+def test_gemm_extrema_and_frac(gpu, frac):
+    rng = np.random.default_rng(100 + frac)
+    N, nb, T = 24, 2, 16
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    scale = rng.integers(I64_MIN, I64_MAX, size=(N, nb), dtype=np.int64)
+    x = rng.integers(I64_MIN, I64_MAX, size=(T, nb * 128), dtype=np.int64)
+    x[0, :4] = [I64_MIN, I64_MAX, 0, -1]
+    got = gpu.q1_apply_gpu(x, bits, scale, frac)
+    assert got is not None and np.array_equal(got, q1_linear_bigint(x, bits, scale, frac))
+
+
+def test_gemm_resident_matches_matvec_rows(gpu):
+    """The same resident weight through the GEMM (T = 40) and the matvec (T = 1 per row) paths."""
+    N, nb = 300, 12
+    bits = prng.uniform_bytes(6, 1, (N, nb, 16))
+    scale = prng.uniform_int(6, 2, (N, nb), -(1 << 20), 1 << 20)
+    x = prng.uniform_int(6, 3, (40, nb * 128), -(1 << 18), 1 << 18)
+    h = gpu.q1_register_weight(bits, scale)
+    full = gpu.q1_apply_resident(h, x, N, nb, 16)
+    rows = np.concatenate([gpu.q1_apply_resident(h, x[t:t + 1], N, nb, 16) for t in range(0, 40, 7)])
+    assert np.array_equal(full[::7], rows)
+    assert np.array_equal(full, q1_linear(x, bits, scale, 16))
+    gpu.q1_free_weights()
+
+
+def test_gemm_config3_shape(gpu):
+    """Config 3 projection shape: M = 2048 tokens x 4096 -> 4096 (normed-activation magnitudes)."""
+    N = K = 4096
+    T = 2048
+    bits = prng.uniform_bytes(31, 1, (N, K // 128, 16))
+    scale = prng.uniform_int(31, 2, (N, K // 128), 1, 1 << 12)
+    x = prng.uniform_int(31, 3, (T, K), -(1 << 19), 1 << 19)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, c_oracle.q1_linear(x, bits, scale, 16))
