@@ -74,7 +74,8 @@ def cpu_worker(npz: str, seconds: float) -> None:
     print(json.dumps({"value": gbs, "unit": "GB/s", "kind": kind, "calls": n, "seconds": el, "match": match}))
 
 
-def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, vocab: int = 151936) -> dict:
+def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, vocab: int = 151936,
+               c5_tokens: int = 0) -> dict:
     """Bonsai-8B-shape greedy decode at batch 1: embed -> 36 layers over a paged int32 KV cache holding ``ctx``
     positions -> final RMSNorm + Q1_0 LM head (151936x4096) -> lowest-index argmax -> next embed, all on device.
 
@@ -144,6 +145,7 @@ def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, voca
     status = int(so.imie_net_status(net.h, 0, sp))
     last = int(ids.item())
     net.close()
+    c5 = c5_leg(so, torch, w, g, ebits, escale, c5_tokens) if c5_tokens > 0 else None
     wbytes = sum(o * (i // 128) * (16 + 4) for o, i in shapes.values()) * n_layers + vocab * (d // 128) * 20
     kvbytes = n_layers * 2 * Hkv * ctx * hd * 4
     return {"tok_s": round(tokens / (ms / 1e3), 2), "ms_per_token": round(ms / tokens, 3),
@@ -152,7 +154,50 @@ def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, voca
             "context": ctx,
             "layers": n_layers, "vocab": vocab, "kv": "int32 paged (64-token pages)", "status": status,
             "last_token": last, "weight_plus_kv_GB_per_token": round((wbytes + kvbytes) / 1e9, 3),
-            "effective_GB_s": round((wbytes + kvbytes) / (ms / tokens / 1e3) / 1e9, 1), **prof}
+            "effective_GB_s": round((wbytes + kvbytes) / (ms / tokens / 1e3) / 1e9, 1), **prof, "_c5": c5}
+
+
+def c5_leg(so, torch, w, g, ebits, escale, tokens: int, B: int = 32, n_layers: int = 36) -> dict:
+    """Config 5: the 36-layer 8B-shape stack (same resident weights as the b=1 leg) decoding a ragged batch of B
+    sequences with contexts drawn uniformly from [512, 32768] over a paged kv8 cache (device-generated seeded
+    contents, ~153 GB), `tokens` greedy tokens each, as one device call replaying a HIP graph per step."""
+    from integer_inference_engine_amd.resident import ResidentNet
+    from integer_inference_engine_amd.rope_tables import bonsai8b_tables
+    d, H, Hkv, hd, dff = 4096, 32, 8, 128, 12288
+    rng = np.random.default_rng(55)
+    lens = rng.integers(512, 32769, size=B).astype(np.int64)
+    extra = tokens + 8
+    cap = int(lens.max()) + extra
+    cos, sin = bonsai8b_tables(cap)
+    from integer_inference_engine_amd import gpu_native as gn
+    g = dict(g)
+    g["cos_h"], g["sin_h"] = gn.buf_upload_i64(cos), gn.buf_upload_i64(sin)
+    net = ResidentNet(B=B, n_layers=n_layers, H=H, Hkv=Hkv, hd=hd, d=d, dff=dff, cap=64, w=w, g=g, page=64,
+                      kv32=True)
+    t0 = time.perf_counter()
+    net.set_caps(lens + extra)
+    net.fill_kv(55, lens)
+    setup_s = time.perf_counter() - t0
+    ids = torch.tensor(rng.integers(0, ebits.shape[0], size=B), dtype=torch.int64, device="cuda")
+    logits = torch.empty((B, ebits.shape[0]), dtype=torch.int64, device="cuda")
+    hist = torch.empty((tokens, B), dtype=torch.int64, device="cuda")
+    net.clear_status()
+    net.decode(ebits, escale, ids, 2, graph=True, hist=hist[:2], logits=logits)      # warm-up + graph capture
+    net.stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(net.stream)
+    net.decode(ebits, escale, ids, tokens, graph=True, hist=hist, logits=logits)
+    e1.record(net.stream)
+    net.stream.synchronize()
+    ms = e0.elapsed_time(e1)
+    status = net.status()
+    net.close()
+    kv_bytes = int((lens + 2).sum()) * n_layers * 2 * Hkv * hd * 4
+    return {"sequences": B, "tokens_per_sequence": tokens, "layers": n_layers,
+            "context_min": int(lens.min()), "context_max": int(lens.max()), "context_mean": round(float(lens.mean()), 1),
+            "tok_s": round(B * tokens / (ms / 1e3), 1), "ms_per_step": round(ms / tokens, 3), "status": status,
+            "kv_GB": round(kv_bytes / 1e9, 1), "kv_read_GB_s": round(kv_bytes / (ms / tokens / 1e3) / 1e9, 1),
+            "setup_s": round(setup_s, 2), "kv": "kv8 digit planes (int8 x 4 per element), 64-slot pages"}
 
 
 def prefill_leg(so, torch, T: int = 2048) -> dict:
@@ -220,6 +265,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=32, help="8B-shape b=1 decode leg (0 = skip)")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="config-3 layer prefill leg (0 = skip)")
+    ap.add_argument("--c5-tokens", type=int, default=64, help="config-5 ragged batch decode leg (0 = skip)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
@@ -327,7 +373,7 @@ def main() -> int:
         del bits, scale
         so.bonsai_q1_free_weights()
         print("[bench] 8B-shape decode leg", file=sys.stderr, flush=True)
-        dec = decode_leg(so, torch, args.decode_tokens)
+        dec = decode_leg(so, torch, args.decode_tokens, c5_tokens=args.c5_tokens)
 
     pre = None
     if args.prefill_tokens > 0:
@@ -349,7 +395,8 @@ def main() -> int:
                      "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,
-        "decode_8b_b1": dec,
+        "decode_8b_b1": {k: v for k, v in dec.items() if k != "_c5"} if dec else None,
+        "decode_c5_batch32": dec.get("_c5") if dec else None,
         "prefill_8b_layer": pre,
     }
     print(json.dumps(line))

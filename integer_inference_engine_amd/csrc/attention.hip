@@ -805,10 +805,10 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   for (int hb = 0; hb < RBH; ++hb) smax[hb] = INT64_MIN;
   const int64_t jend = min(j0 + d.chunk, L);
   const int8_t* Kb = (const int8_t*)d.K;
-  for (int64_t t = j0 + 16 * wave; t < jend; t += 64) {
+  // 16-key tiles t = j0 + 16 wave + 64 i; the next tile's K slices are loaded before this tile's MFMAs
+  auto load_tile = [&](int64_t t, v4i (&bk)[4][2]) {
     const int64_t j = t + m;
     const bool valid = j < jend;
-    v4i bk[4][2];
     int64_t base = 0, slot = 0;
     if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
 #pragma unroll
@@ -818,6 +818,10 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
         bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
                         ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
                         : v4i{0, 0, 0, 0};
+  };
+  auto score_tile = [&](int64_t t, const v4i (&bk)[4][2]) {
+    const int64_t j = t + m;
+    const bool valid = j < jend;
 #pragma unroll
     for (int hb = 0; hb < RBH; ++hb) {
       uint64_t S = 0;
@@ -837,6 +841,19 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
         smax[hb] = sc > smax[hb] ? sc : smax[hb];
       }
     }
+  };
+  v4i bkA[4][2], bkB[4][2];
+  int64_t t = j0 + 16 * wave;
+  if (t < jend) load_tile(t, bkA);
+  while (t < jend) {
+    const int64_t t2 = t + 64;
+    if (t2 < jend) load_tile(t2, bkB);
+    score_tile(t, bkA);
+    if (t2 >= jend) break;
+    const int64_t t3 = t2 + 64;
+    if (t3 < jend) load_tile(t3, bkA);
+    score_tile(t2, bkB);
+    t = t3;
   }
 #pragma unroll
   for (int hb = 0; hb < RBH; ++hb) {
@@ -897,6 +914,19 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   const int8_t* Vb = (const int8_t*)d.V;
   for (int64_t t0 = j0; t0 < jend; t0 += 64) {
     const int64_t tn = min((int64_t)64, jend - t0);
+    // this step's V slices first: their latency overlaps the p / digit work below
+    int64_t pi, slot0;
+    page_split(d, t0, pi, slot0);
+    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+    v4i bv[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tile = wave + 4 * tt;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        bv[tt][db] = tile < DT ? *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, 16 * tile + m, d.hd, d.P))
+                               : v4i{0, 0, 0, 0};
+    }
     __syncthreads();                                  // previous step's digits consumed
     {
       const int kk = tid & 63;
@@ -925,9 +955,6 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
       }
     }
     __syncthreads();
-    int64_t pi, slot0;
-    page_split(d, t0, pi, slot0);
-    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
     v4i av[RBH];
 #pragma unroll
     for (int hb = 0; hb < RBH; ++hb) av[hb] = *(const v4i*)&sPd[hb][m][16 * g];
@@ -935,13 +962,10 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
     for (int tt = 0; tt < 2; ++tt) {
       const int tile = wave + 4 * tt;
       if (tile >= DT) continue;
-      const int64_t c = 16 * tile + m;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const v4i bv = *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, c, d.hd, d.P));
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int hb = 0; hb < RBH; ++hb) acc[hb][db][tt] = mfma8(av[hb], bv, acc[hb][db][tt]);
-      }
+        for (int hb = 0; hb < RBH; ++hb) acc[hb][db][tt] = mfma8(av[hb], bv[tt][db], acc[hb][db][tt]);
     }
   }
 #pragma unroll

@@ -67,8 +67,11 @@ __global__ __launch_bounds__(256) void kv_fill_kernel(void* pool, const int64_t*
   const uint64_t key = sm_mix(seed * 0x100000001B3ull + tid * 0x9E3779B1ull + 0x632BE59BD9B4E019ull);
   uint64_t mx = 0;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
-    const int64_t j = e / hd, c = e - j * hd;
-    const uint64_t i = (uint64_t)(kv * len * hd + e);
+    // K walks dims fastest and V slots fastest, so consecutive threads store consecutive bytes of a plane
+    int64_t j, c;
+    if (kind == 0 || !kv8) { j = e / hd; c = e - j * hd; }
+    else { c = e / len; j = e - c * len; }
+    const uint64_t i = (uint64_t)(kv * len * hd + j * hd + c);
     const int64_t v = (int64_t)(sm_mix(key + (i + 1) * 0x9E3779B97F4A7C15ull) % span) + lo;
     const uint64_t a = imie_absu64(v);
     mx = a > mx ? a : mx;

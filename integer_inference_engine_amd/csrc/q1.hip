@@ -383,10 +383,20 @@ __device__ inline v4i expand_bits(const uint4 w, int sh) {
 }
 
 __device__ inline void gemm_tile(const GemmArgs& a, int wave, int64_t& t0w, int64_t& o0w, int64_t& t0g, bool& live) {
-  const int64_t wg = blockIdx.x, xcd = wg & 7, j = wg >> 3;
-  const int64_t tpx = (a.ntt + 7) / 8;
-  const int64_t tt = xcd + 8 * (j / a.nto), ot = j % a.nto;
-  live = tt < a.ntt && (j / a.nto) < tpx;
+  const int64_t wg = blockIdx.x;
+  int64_t tt, ot;
+  if (a.ntt >= 8) {
+    // >= 8 token tiles: each XCD (blockIdx % 8) walks whole token tiles, so its L2 keeps those tiles' digits
+    const int64_t xcd = wg & 7, j = wg >> 3, tpx = (a.ntt + 7) / 8;
+    tt = xcd + 8 * (j / a.nto);
+    ot = j % a.nto;
+    live = tt < a.ntt && (j / a.nto) < tpx;
+  } else {
+    // few token tiles (batched decode): spread the output tiles over every XCD
+    tt = wg / a.nto;
+    ot = wg % a.nto;
+    live = tt < a.ntt;
+  }
   t0g = tt * 64;
   t0w = t0g + (wave >> 1) * 32;
   o0w = ot * 128 + (wave & 1) * 64;
@@ -673,7 +683,7 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
     ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128;
     ga.frac = (int)(frac > 63 ? 63 : frac); ga.accumulate = accumulate; ga.out = outs[i];
-    const dim3 grid((unsigned)(8 * ((ga.ntt + 7) / 8) * ga.nto));
+    const dim3 grid((unsigned)(ga.ntt >= 8 ? 8 * ((ga.ntt + 7) / 8) * ga.nto : ga.ntt * ga.nto));
     if (w.scale64) {
       hipLaunchKernelGGL(q1_gemm_narrow_kernel<true>, grid, dim3(256), 0, st, ga);
       hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
