@@ -152,7 +152,7 @@ def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, voca
             "host_enqueue_ms_per_token": round(t_host * 1e3 / tokens, 3), "eager_ms_per_token": round(ms_eager, 3),
             "mode": "HIP graph of one greedy step (embed, 36 layers, head, argmax), replayed", "tokens": tokens,
             "context": ctx,
-            "layers": n_layers, "vocab": vocab, "kv": "int32 paged (64-token pages)", "status": status,
+            "layers": n_layers, "vocab": vocab, "kv": "kv8 digit planes (int8 x 4 per element), 64-slot pages", "status": status,
             "last_token": last, "weight_plus_kv_GB_per_token": round((wbytes + kvbytes) / 1e9, 3),
             "effective_GB_s": round((wbytes + kvbytes) / (ms / tokens / 1e3) / 1e9, 1), **prof, "_c5": c5}
 
@@ -250,6 +250,63 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
             "q1_gemm_frac_of_int8_peak": round(ops / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None, **prof}
 
 
+def moe_leg(so, torch, E: int = 128, k: int = 8, d: int = 2048, e_ffn: int = 768, T: int = 64) -> dict:
+    """Config 4: north-mini-code MoE FFN block, hidden 2048, 128 experts top-8, expert FFN 768; gate/up Q4_K and
+    down Q6_K raw GGML blocks (seeded random quants, finite fp16 scales), 64 tokens routed by seeded integer
+    logits (ragged per-expert groups). Timed on one stream with HIP events; bytes = the distinct experts' blocks."""
+    from integer_inference_engine_amd import qk_gpu
+    rng = np.random.default_rng(4)
+
+    def blocks(out_f, nb, qtype):
+        bs = 144 if qtype == 0 else 210
+        raw = rng.integers(0, 256, size=(out_f * nb, bs), dtype=np.uint8)
+        dv = rng.uniform(0.002, 0.01, size=out_f * nb).astype(np.float16).view(np.uint16)
+        if qtype == 0:
+            mv = rng.uniform(0.0, 0.005, size=out_f * nb).astype(np.float16).view(np.uint16)
+            raw[:, 0], raw[:, 1], raw[:, 2], raw[:, 3] = dv & 0xFF, dv >> 8, mv & 0xFF, mv >> 8
+        else:
+            raw[:, 208], raw[:, 209] = dv & 0xFF, dv >> 8
+        return raw.reshape(-1)
+
+    hs = []
+    for _ in range(E):
+        hs.append((qk_gpu.register_weight(blocks(e_ffn, d // 256, 0), e_ffn, d // 256, 0),
+                   qk_gpu.register_weight(blocks(e_ffn, d // 256, 0), e_ffn, d // 256, 0),
+                   qk_gpu.register_weight(blocks(d, e_ffn // 256, 1), d, e_ffn // 256, 1)))
+    logits = rng.integers(-(1 << 20), 1 << 20, size=(T, E))
+    sel = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    gates = rng.integers(1, 1 << 16, size=(T, k)).astype(np.int64)
+    flat = sel.reshape(-1)
+    arr = lambda i: (ctypes.c_int64 * (T * k))(*[hs[e][i] for e in flat])
+    ga, ua, da = arr(0), arr(1), arr(2)
+    h = torch.from_numpy(rng.integers(-(1 << 16), 1 << 16, size=(T, d), dtype=np.int64)).cuda()
+    gd = torch.from_numpy(np.ascontiguousarray(gates.reshape(-1))).cuda()
+    out = torch.empty((T, d), dtype=torch.int64, device="cuda")
+    st = torch.cuda.Stream()
+    sp = ctypes.c_void_p(st.cuda_stream)
+    call = lambda: so.imie_moe_ffn_batched_dev(ga, ua, da, T, k, ctypes.c_void_p(h.data_ptr()),
+                                               ctypes.c_void_p(gd.data_ptr()), d, e_ffn, 16, 24,
+                                               ctypes.c_void_p(out.data_ptr()), sp)
+    so.imie_moe_status(1, sp)
+    assert call() == 0
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    e0.record(st)
+    for _ in range(reps):
+        call()
+    e1.record(st)
+    st.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    status = so.imie_moe_status(0, sp)
+    qk_gpu.free_all()
+    used = len(set(flat.tolist()))
+    nbytes = used * (2 * e_ffn * (d // 256) * 144 + d * (e_ffn // 256) * 210)
+    return {"tokens": T, "experts": E, "top_k": k, "experts_used": used, "ms": round(ms, 3),
+            "tok_s": round(T / (ms / 1e3), 1), "expert_GB": round(nbytes / 1e9, 3),
+            "expert_GB_s": round(nbytes / (ms / 1e3) / 1e9, 1), "status": int(status)}
+
+
 def _lib_err():
     from integer_inference_engine_amd import _lib
     return _lib.last_error()
@@ -266,6 +323,7 @@ def main() -> int:
     ap.add_argument("--decode-tokens", type=int, default=32, help="8B-shape b=1 decode leg (0 = skip)")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="config-3 layer prefill leg (0 = skip)")
     ap.add_argument("--c5-tokens", type=int, default=64, help="config-5 ragged batch decode leg (0 = skip)")
+    ap.add_argument("--moe-tokens", type=int, default=64, help="config-4 MoE block leg (0 = skip)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
@@ -380,6 +438,11 @@ def main() -> int:
         print("[bench] config-3 prefill leg", file=sys.stderr, flush=True)
         pre = prefill_leg(so, torch, args.prefill_tokens)
 
+    moe = None
+    if args.moe_tokens > 0:
+        print("[bench] config-4 MoE leg", file=sys.stderr, flush=True)
+        moe = moe_leg(so, torch, T=args.moe_tokens)
+
     line = {
         "metric": "Q1 matvec HBM GB/s (% of peak); 8B-shape decode tok/s b=1; byte-exact",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -398,6 +461,7 @@ def main() -> int:
         "decode_8b_b1": {k: v for k, v in dec.items() if k != "_c5"} if dec else None,
         "decode_c5_batch32": dec.get("_c5") if dec else None,
         "prefill_8b_layer": pre,
+        "moe_c4": moe,
     }
     print(json.dumps(line))
     return 0

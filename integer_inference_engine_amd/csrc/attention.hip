@@ -761,45 +761,63 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
   const int64_t* qg = d.q + b * d.qsb + kv * REP * d.qsh;
-  uint64_t mq = 0;
-  for (int i = tid; i < REP * d.hd; i += 256) {
-    const uint64_t a = imie_absu64(qg[imie_udiv32(i, d.hd) * d.qsh + imie_umod32(i, d.hd)]);
-    mq = a > mq ? a : mq;
-  }
-  mq = imie_wave_max_u64(mq);
-  if (lane == 0) s_mq[wave] = mq;
-  if (blockIdx.y == 0 && tid < REP) {
-    uint64_t mr = 0;
-    for (int c = 0; c < d.hd; ++c) { const uint64_t a = imie_absu64(qg[tid * d.qsh + c]); mr = a > mr ? a : mr; }
-    d.maxq[b * d.H + kv * REP + tid] = mr;
-  }
-  __syncthreads();
-  uint64_t mqa = s_mq[0];
-  for (int w = 1; w < 4; ++w) mqa = s_mq[w] > mqa ? s_mq[w] : mqa;
-  const int Lq = imie_limbs_needed(mqa), LB = (Lq + 3) / 4;
-  const int KS = (int)((d.hd + 63) / 64);
-  // digits of every q element once (thread per element) into LDS rows [head block][4 (r % 4) + lq % 4][limb
-  // block][dim]; each lane then reads its 16-byte A operands directly
-  for (int i = tid; i < RBH * 2 * 16 * 128; i += 256) (&sQd[0][0][0][0])[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < REP * d.hd; i += 256) {
-    const int r = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
-    int64_t x = qg[r * d.qsh + c];
-    for (int lq = 0; lq < Lq; ++lq) {
-      const int64_t dg = ((x + 128) & 255) - 128;
-      x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
-      sQd[r >> 2][lq >> 2][4 * (r & 3) + (lq & 3)][c] = (int8_t)dg;
-    }
-  }
-  __syncthreads();
   v4i av[RBH][2][2];
+  int Lq = 0;
+  if (d.qd) {
+    // digits prepared by the head stage: A operands straight from memory, no staging
+    for (int r = 0; r < REP; ++r) { const int lr = d.qlimbs[b * d.H + kv * REP + r]; Lq = lr > Lq ? lr : Lq; }
 #pragma unroll
-  for (int hb = 0; hb < RBH; ++hb)
+    for (int hb = 0; hb < RBH; ++hb)
 #pragma unroll
-    for (int lb = 0; lb < 2; ++lb)
+      for (int lb = 0; lb < 2; ++lb)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
+        for (int h = 0; h < 2; ++h) {
+          const int r = 4 * hb + (m >> 2), lq = 4 * lb + (m & 3);
+          av[hb][lb][h] = (r < REP && lq < Lq && 64 * h + 16 * g < d.hd)
+                              ? *(const v4i*)(d.qd + ((b * d.H + kv * REP + r) * 8 + lq) * d.hd + 64 * h + 16 * g)
+                              : v4i{0, 0, 0, 0};
+        }
+  } else {
+    uint64_t mq = 0;
+    for (int i = tid; i < REP * d.hd; i += 256) {
+      const uint64_t a = imie_absu64(qg[imie_udiv32(i, d.hd) * d.qsh + imie_umod32(i, d.hd)]);
+      mq = a > mq ? a : mq;
+    }
+    mq = imie_wave_max_u64(mq);
+    if (lane == 0) s_mq[wave] = mq;
+    if (blockIdx.y == 0 && tid < REP) {
+      uint64_t mr = 0;
+      for (int c = 0; c < d.hd; ++c) { const uint64_t a = imie_absu64(qg[tid * d.qsh + c]); mr = a > mr ? a : mr; }
+      d.maxq[b * d.H + kv * REP + tid] = mr;
+    }
+    __syncthreads();
+    uint64_t mqa = s_mq[0];
+    for (int w = 1; w < 4; ++w) mqa = s_mq[w] > mqa ? s_mq[w] : mqa;
+    Lq = imie_limbs_needed(mqa);
+    // digits of every q element once (thread per element) into LDS rows [head block][4 (r % 4) + lq % 4][limb
+    // block][dim]; each lane then reads its 16-byte A operands directly
+    for (int i = tid; i < RBH * 2 * 16 * 128; i += 256) (&sQd[0][0][0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < REP * d.hd; i += 256) {
+      const int r = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
+      int64_t x = qg[r * d.qsh + c];
+      for (int lq = 0; lq < Lq; ++lq) {
+        const int64_t dg = ((x + 128) & 255) - 128;
+        x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+        sQd[r >> 2][lq >> 2][4 * (r & 3) + (lq & 3)][c] = (int8_t)dg;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
+  }
+  const int LB = (Lq + 3) / 4;
+  const int KS = (int)((d.hd + 63) / 64);
   int64_t smax[RBH];
 #pragma unroll
   for (int hb = 0; hb < RBH; ++hb) smax[hb] = INT64_MIN;
@@ -1312,7 +1330,8 @@ size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int
   const int64_t rows = B * H * M;
   int64_t chunk = 0, nch = 0;
   dec_geometry(B, Hkv, Lmax, &chunk, &nch);
-  const int64_t part = M == 1 ? nch * (rows * hd + 3 * rows + 2 * B * Hkv) : 0;
+  // decode: per-chunk partials + q digit planes (8 * hd bytes per row) and limb counts from the head stage
+  const int64_t part = M == 1 ? nch * (rows * hd + 3 * rows + 2 * B * Hkv) + rows * hd + rows + 2 : 0;
   // prefill kv8: per-256-key row maxima + 4 digit planes of p (bytes)
   const int64_t pdL = (Lmax + 15) / 16 * 16;
   const int64_t pf = M > 1 ? ((Lmax + kPfKeys - 1) / kPfKeys) * rows + (4 * rows * pdL + 7) / 8 + 2 : 0;
@@ -1344,6 +1363,15 @@ void imie_attn_bind_scratch(AttnDesc& d, void* scratch) {
     d.pd = (int8_t*)(((uintptr_t)p + 15) & ~(uintptr_t)15);
     d.pdL = (d.Lmax + 15) / 16 * 16;
   }
+}
+
+void imie_attn_qdigit_scratch(const AttnDesc& d, int8_t** qd, int** qlimbs) {
+  int64_t chunk = 0, nch = 0;
+  dec_geometry(d.B, d.Hkv, d.Lmax, &chunk, &nch);
+  const int64_t rows = d.B * d.H * d.M;
+  int64_t* p = (int64_t*)d.cvm + nch * d.B * d.Hkv;
+  *qd = (int8_t*)(((uintptr_t)p + 15) & ~(uintptr_t)15);
+  *qlimbs = (int*)(*qd + rows * 8 * d.hd);
 }
 
 int imie_attention_launch(AttnDesc d, hipStream_t st) {

@@ -10,6 +10,8 @@ struct AttnDesc {
   const void* V;
   int kv32;                        // 1: kv8 digit-plane cache (imie_kvfmt.h), 0: int64 elements
   const uint64_t *run_k, *run_v;   // kv8: running max|K|, max|V| per (sequence, kv head) [B*Hkv]
+  const int8_t* qd;                // kv8 decode (optional): q digit planes [B*H][8][hd] from the head stage
+  const int* qlimbs;               //   and their limb counts [B*H] (maxq then points at the head stage's max|q|)
   const int64_t* pt;               // page table [B][mp]
   int64_t P, mp;                   // tokens per page, pages per sequence
   int pshift;                      // log2(P) when P is a power of two, else -1 (set by the launcher)
@@ -37,5 +39,8 @@ struct AttnDesc {
 };
 
 size_t imie_attn_scratch_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t M, int64_t hd, int64_t Lmax);
+// Decode (M == 1) only: the q digit-plane buffer and limb counts inside bound scratch, for a head stage that
+// prepares them (then set d.qd, d.qlimbs and point d.maxq at the head stage's max|q|)
+void imie_attn_qdigit_scratch(const AttnDesc& d, int8_t** qd, int** qlimbs);
 void imie_attn_bind_scratch(AttnDesc& d, void* scratch);
 int imie_attention_launch(AttnDesc d, hipStream_t st);

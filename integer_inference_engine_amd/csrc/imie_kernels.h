@@ -75,6 +75,11 @@ struct QkHeadArgs {
   // kv8 cache only: max|k|, max|v| of the appended rows per (row, kv head) [rows][Hkv] (M > 1), or folded
   // straight into the running per-(sequence, kv head) maxima run_k / run_v [B][Hkv] (M == 1)
   uint64_t *rowk, *rowv, *run_k, *run_v;
+  // kv8 decode (optional): rotated q as 8 balanced digit planes qd[row * H + h][8][hd], max|q| and limb count per
+  // (row, head), consumed directly as MFMA A operands by the decode attention
+  int8_t* qd;
+  uint64_t* qmax;
+  int* qlimbs;
 };
 // kv8 = 1: the digit-plane cache of imie_kvfmt.h; 0: int64 rows
 int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st);

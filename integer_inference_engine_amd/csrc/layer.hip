@@ -261,6 +261,17 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       int64_t* outs[3] = {q, k, v};
       CK(norm_into_matvec(n, x, rows, L.n1g, xn, L.w, 3, outs, st));
     }
+    AttnDesc d = {};
+    d.B = n.B; d.H = n.H; d.Hkv = n.Hkv; d.hd = n.hd; d.M = M;
+    d.qsb = M * qd; d.qsh = n.hd; d.qsm = qd;
+    d.q = qn; d.K = n.kpool[(size_t)l]; d.V = n.vpool[(size_t)l]; d.kv32 = n.kv32;
+    d.pt = n.pt; d.P = n.P; d.mp = n.mp;
+    d.starts = (const int64_t*)n.starts.p; d.lengths = nullptr;
+    d.Lmax = lmax; d.frac = (int)n.frac; d.inv_sqrt = n.inv_sqrt;
+    d.out = att; d.status = status; d.rope_guard = guard + 4 * l;
+    if (n.kv32) { d.run_k = run_k(n, l); d.run_v = run_v(n, l); }
+    imie_attn_bind_scratch(d, n.attn.p);
+    if (n.kv32 && M == 1) imie_attn_qdigit_scratch(d, (int8_t**)&d.qd, (int**)&d.qlimbs);
     {
       QkHeadArgs a = {};
       a.q = q; a.k = k; a.v = v; a.qo = qn;
@@ -272,19 +283,10 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
         a.rowk = (uint64_t*)n.kvrow.p; a.rowv = (uint64_t*)n.kvrow.p + rows * n.Hkv;
         a.run_k = run_k(n, l); a.run_v = run_v(n, l);
       }
+      if (d.qd) { a.qd = (int8_t*)d.qd; a.qlimbs = (int*)d.qlimbs; a.qmax = d.maxq; }
       CK(imie_qk_head_launch(a, n.kv32, st));
       if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));
     }
-    AttnDesc d = {};
-    d.B = n.B; d.H = n.H; d.Hkv = n.Hkv; d.hd = n.hd; d.M = M;
-    d.qsb = M * qd; d.qsh = n.hd; d.qsm = qd;
-    d.q = qn; d.K = n.kpool[(size_t)l]; d.V = n.vpool[(size_t)l]; d.kv32 = n.kv32;
-    d.pt = n.pt; d.P = n.P; d.mp = n.mp;
-    d.starts = (const int64_t*)n.starts.p; d.lengths = nullptr;
-    d.Lmax = lmax; d.frac = (int)n.frac; d.inv_sqrt = n.inv_sqrt;
-    d.out = att; d.status = status; d.rope_guard = guard + 4 * l;
-    if (n.kv32) { d.run_k = run_k(n, l); d.run_v = run_v(n, l); }
-    imie_attn_bind_scratch(d, n.attn.p);
     CK(imie_attention_launch(d, st));
     CK(imie_q1_launch_multi(&L.w[3], 1, att, rows, n.frac, &x, 1, &n.q1w, st));
     {

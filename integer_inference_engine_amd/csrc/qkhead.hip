@@ -83,6 +83,23 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
       a.qo[(r * a.H + h) * a.hd + j] = o0;
       a.qo[(r * a.H + h) * a.hd + j + half] = o1;
     }
+    if (a.qd) {                                       // kv8 decode: q digits (8 limbs), max|q| and limb count
+      uint64_t mq = imie_absu64(o0) > imie_absu64(o1) ? imie_absu64(o0) : imie_absu64(o1);
+      mq = imie_wave_max_u64(mq);
+      const int64_t qrow = r * a.H + h;
+      if (j == 0) { a.qmax[qrow] = mq; a.qlimbs[qrow] = imie_limbs_needed(mq); }
+      if (act) {
+        int8_t* dst = a.qd + qrow * 8 * a.hd;
+        int64_t x0 = o0, x1 = o1;
+        for (int lq = 0; lq < 8; ++lq) {
+          const int64_t d0 = ((x0 + 128) & 255) - 128, d1 = ((x1 + 128) & 255) - 128;
+          x0 = (int64_t)((uint64_t)x0 - (uint64_t)d0) >> 8;
+          x1 = (int64_t)((uint64_t)x1 - (uint64_t)d1) >> 8;
+          dst[lq * a.hd + j] = (int8_t)d0;
+          dst[lq * a.hd + j + half] = (int8_t)d1;
+        }
+      }
+    }
     return;
   }
   const int64_t kvh = h - a.H, b = r / a.M;
