@@ -63,6 +63,11 @@ int imie_q1_linear_simple_dev(const int64_t *x_dev, const uint8_t *bits_dev, con
 /* bonsai_q1_gpu.cu:625-670 `bonsai_rmsnorm_gpu` (gpu_native.py:129-138, 390-415): rc 4 on the 128-bit / gain envelope. */
 int bonsai_rmsnorm_gpu(const int64_t *x, int64_t rows, int64_t cols, int64_t frac, int64_t eps, const int64_t *gain,
                        int64_t *out);
+/* The fused RMSNorm producer of the resident decode (it also writes the next Q1 matvec's digit table, kept in
+ * a workspace here) with the host contract of bonsai_rmsnorm_gpu; cols a multiple of 128, at most 4096. No
+ * reference counterpart: it exposes the fused kernel to the parity tests. */
+int imie_rmsnorm_fused_gpu(const int64_t *x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                           const int64_t *gain, int64_t *out);
 int imie_rmsnorm_dev(const int64_t *x, int64_t rows, int64_t cols, int64_t frac, int64_t eps, const int64_t *gain,
                      int64_t *out, int *status, void *stream);
 /* bonsai_q1_kernel.c:1729-1767 `bonsai_silu_i64` (q1_native.py:1895 `silu_native`) on the GPU: (x*sigmoid(x))>>frac. */

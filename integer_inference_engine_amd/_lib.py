@@ -40,6 +40,7 @@ SIGNATURES = {
                                           c_void_p, c_void_p]),
     # RMSNorm / element-wise
     "bonsai_rmsnorm_gpu": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_rmsnorm_fused_gpu": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_rmsnorm_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                  c_void_p]),
     "bonsai_silu_gpu": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),

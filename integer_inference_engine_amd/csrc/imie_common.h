@@ -78,6 +78,63 @@ __device__ __forceinline__ int64_t imie_wave_sum_i64(int64_t v) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Whole-wave reductions over DPP lane moves (VALU only, no LDS crossbar): xor 1 and xor 2 (quad_perm), the
+// half-row and row mirrors reduce each 16-lane row, row_bcast15 / row_bcast31 fold the four rows into lane
+// 63, which readlane broadcasts as a wave-uniform value. Every lane of the wave must be active, and 0 must be
+// the identity of the operation for the values reduced (sums, unsigned maxima, signed maxima / minima of sets
+// that contain 0): lanes outside a row-masked step contribute 0.
+// ---------------------------------------------------------------------------------------------------------
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint64_t imie_dpp64(uint64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROWS, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROWS, 0xF, false);
+  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ uint64_t imie_readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t imie_readlane63(uint64_t v) { return imie_readlane_u64(v, 63); }
+
+template <typename Op>
+__device__ __forceinline__ uint64_t imie_wave_reduce_full(uint64_t v, Op op) {
+  v = op(v, imie_dpp64<0xB1>(v));        // quad_perm [1,0,3,2]
+  v = op(v, imie_dpp64<0x4E>(v));        // quad_perm [2,3,0,1]
+  v = op(v, imie_dpp64<0x141>(v));       // row_half_mirror
+  v = op(v, imie_dpp64<0x140>(v));       // row_mirror: every lane holds its row's result
+  v = op(v, imie_dpp64<0x142, 0xA>(v));  // row_bcast15 into rows 1 and 3
+  v = op(v, imie_dpp64<0x143, 0xC>(v));  // row_bcast31 into rows 2 and 3: lane 63 holds the wave's result
+  return imie_readlane63(v);
+}
+
+// sum over each 16-lane row (every lane of the row receives it); every lane of the wave must be active
+__device__ __forceinline__ uint64_t imie_row_sum_u64_full(uint64_t v) {
+  v += imie_dpp64<0xB1>(v);
+  v += imie_dpp64<0x4E>(v);
+  v += imie_dpp64<0x141>(v);
+  v += imie_dpp64<0x140>(v);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t imie_wave_max_u64_full(uint64_t v) {
+  return imie_wave_reduce_full(v, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint64_t imie_wave_sum_u64_full(uint64_t v) {
+  return imie_wave_reduce_full(v, [](uint64_t a, uint64_t b) { return a + b; });
+}
+// signed maximum / minimum of sets that contain 0
+__device__ __forceinline__ int64_t imie_wave_max0_i64_full(int64_t v) {
+  return (int64_t)imie_wave_reduce_full((uint64_t)v, [](uint64_t a, uint64_t b) {
+    return (int64_t)a > (int64_t)b ? a : b; });
+}
+__device__ __forceinline__ int64_t imie_wave_min0_i64_full(int64_t v) {
+  return (int64_t)imie_wave_reduce_full((uint64_t)v, [](uint64_t a, uint64_t b) {
+    return (int64_t)a < (int64_t)b ? a : b; });
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Per-kernel HIP-event timing (enabled by imie_profile_begin; used by the benchmark to time the dominant
 // kernel on the stream it runs on). Kernel ids below.
 // ---------------------------------------------------------------------------------------------------------

@@ -104,4 +104,28 @@ __device__ inline void wave_sum_u128(uint64_t& hi, uint64_t& lo, int& bad) {
   }
 }
 
+// 128-bit sums as four 32-bit limb sums: per lane (hi, lo) splits into limbs a[0..3] (a lane-level overflow
+// adds 2^33 to a[3], which survives into the fold as an overflow); limb sums over up to 2^31 lanes stay below
+// 2^64, so lanes combine without carries. fold carries the limbs back into (hi, lo) and flags sums >= 2^128.
+__device__ inline void u128_limbs(uint64_t hi, uint64_t lo, int bad, uint64_t a[4]) {
+  a[0] = lo & 0xFFFFFFFFull;
+  a[1] = lo >> 32;
+  a[2] = hi & 0xFFFFFFFFull;
+  a[3] = (hi >> 32) + (bad ? (1ull << 33) : 0);
+}
+__device__ inline void u128_fold(const uint64_t a[4], uint64_t& hi, uint64_t& lo, int& bad) {
+  const uint64_t c0 = a[0], c1 = a[1] + (c0 >> 32), c2 = a[2] + (c1 >> 32), c3 = a[3] + (c2 >> 32);
+  lo = (c0 & 0xFFFFFFFFull) | (c1 << 32);
+  hi = (c2 & 0xFFFFFFFFull) | (c3 << 32);
+  bad = (c3 >> 32) != 0 ? 1 : 0;
+}
+// wave_sum_u128 over DPP moves; every lane of the wave must be active. Result is wave-uniform.
+__device__ inline void wave_sum_u128_full(uint64_t& hi, uint64_t& lo, int& bad) {
+  uint64_t a[4];
+  u128_limbs(hi, lo, bad, a);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = imie_wave_sum_u64_full(a[i]);
+  u128_fold(a, hi, lo, bad);
+}
+
 }  // namespace imie_fx

@@ -48,11 +48,10 @@ __device__ inline void prep_slab(int64_t v[8], const Q1PrepOut& po, int64_t t, i
     mx = a > mx ? a : mx;
     part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
   }
-  mx = imie_wave_max_u64(mx);
+  mx = imie_wave_max_u64_full(mx);
   const int L = imie_limbs_needed(mx);
-  // block total: sum over the 16 lanes of group g (xor 1,2,4,8 stays inside the group)
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
+  // block total: sum over the 16 lanes of group g (one DPP row)
+  part = (int64_t)imie_row_sum_u64_full((uint64_t)part);
   if ((lane & 15) == 0) po.totals[t * po.nbp + blk] = part;
   if (lane == 0) po.lslab[t * po.nslabs + sl] = L;
   for (int l = 0; l < L; ++l) {
@@ -65,8 +64,7 @@ __device__ inline void prep_slab(int64_t v[8], const Q1PrepOut& po, int64_t t, i
       if (q < 4) w0 |= byte; else w1 |= byte;
     }
     uint32_t* dst = po.xq + ((((t * kMaxLimbs + l) * po.nbp + blk) * 8 + s) * 4);
-    dst[2 * dh] = w0;
-    dst[2 * dh + 1] = w1;
+    *(uint2*)(dst + 2 * dh) = uint2{w0, w1};
   }
 }
 

@@ -169,6 +169,117 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
   }
 }
 
+
+constexpr int kZeroWgs = 8;
+
+// Single-row RMSNorm that writes the Q1 digit table of the next matvec (gain given, cols = nb * 128 <= 4096):
+// eight waves, wave w holding slab w's 512 columns at the table's positions (prep_pos), so each wave turns its
+// own registers into table entries (no LDS staging). One barrier combines the 128-bit sum of squares with the
+// row's largest and smallest x and largest |gain|: n = floor((x << f) / rms) is non-decreasing in x, so max|n|
+// (and whether every n fits int64) follows from the two extremes; the result equals the per-element check.
+// kZeroWgs further workgroups clear the next matvec's K-split outputs in parallel with the row work.
+__global__ __launch_bounds__(512) void rmsnorm_prep_slab_kernel(const int64_t* __restrict__ x, int64_t cols, int frac,
+                                                                int64_t eps, const int64_t* __restrict__ gain,
+                                                                int64_t* __restrict__ out, int* __restrict__ status,
+                                                                imie_q1::Q1PrepOut po, imie_q1::Q1Zero zero) {
+  __shared__ uint64_t s_lm[8][4], s_mg[8];
+  __shared__ int64_t s_xmax[8], s_xmin[8];
+  const int64_t rows = (int64_t)gridDim.x - kZeroWgs;
+  if ((int64_t)blockIdx.x >= rows) {                  // the extra workgroups clear the next matvec's outputs
+    imie_q1::zero_share(zero, (int64_t)blockIdx.x - rows, kZeroWgs, threadIdx.x, 512);
+    return;
+  }
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t* xr = x + row * cols;
+  int64_t xv[8], gv[8];
+  int64_t pos[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    pos[q] = imie_q1::prep_pos(lane, wave, q);
+    xv[q] = pos[q] < cols ? xr[pos[q]] : 0;
+    gv[q] = pos[q] < cols ? gain[pos[q]] : 0;
+  }
+  uint64_t hi = 0, lo = 0, mg = 0;
+  int64_t xmax = 0, xmin = 0;                          // padding zeros are harmless: n(0) = 0 fits
+  int bad = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint64_t a = imie_absu64(xv[q]);
+    const u128 sq = (u128)a * a;
+    const uint64_t sl = (uint64_t)sq, sh = (uint64_t)(sq >> 64);
+    const uint64_t nl = lo + sl;
+    const uint64_t cy = nl < lo ? 1 : 0;
+    const uint64_t nh = hi + sh;
+    bad |= (nh < hi ? 1 : 0) | (nh + cy < nh ? 1 : 0);
+    hi = nh + cy;
+    lo = nl;
+    xmax = xv[q] > xmax ? xv[q] : xmax;
+    xmin = xv[q] < xmin ? xv[q] : xmin;
+    const uint64_t ag = imie_absu64(gv[q]);
+    mg = ag > mg ? ag : mg;
+  }
+  // wave level: DPP reductions (limb sums need no carries); block level: every lane folds the eight
+  // wave results read from LDS (broadcast reads)
+  uint64_t lm[4];
+  u128_limbs(hi, lo, bad, lm);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lm[i] = imie_wave_sum_u64_full(lm[i]);
+  mg = imie_wave_max_u64_full(mg);
+  xmax = imie_wave_max0_i64_full(xmax);
+  xmin = imie_wave_min0_i64_full(xmin);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_lm[wave][i] = lm[i];
+    s_mg[wave] = mg; s_xmax[wave] = xmax; s_xmin[wave] = xmin;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lm[i] = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lm[i] += s_lm[w][i];
+    mg = s_mg[w] > mg ? s_mg[w] : mg;
+    xmax = s_xmax[w] > xmax ? s_xmax[w] : xmax;
+    xmin = s_xmin[w] < xmin ? s_xmin[w] : xmin;
+  }
+  u128_fold(lm, hi, lo, bad);
+  uint64_t rms = 0;
+  if (!bad) {
+    const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)cols);
+    if (mean <= ~(u128)0 - (u128)(uint64_t)eps) rms = isqrt_u128(mean + (u128)(uint64_t)eps);
+  }
+  if (rms == 0) {
+    if (tid == 0) atomicOr(status, IMIE_ERMS);
+    return;
+  }
+  const uint64_t rinv = recip_u64(rms);
+  // the eight own elements and, alongside, one extreme per lane (even lanes the largest x, odd the smallest)
+  int64_t nv[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    bool f;
+    nv[q] = norm_elem(xv[q], frac, rms, rinv, &f);
+  }
+  bool fe = true;
+  const uint64_t ne = imie_absu64(norm_elem((lane & 1) ? xmin : xmax, frac, rms, rinv, &fe));
+  const uint64_t na = imie_readlane_u64(ne, 0), nb = imie_readlane_u64(ne, 1);
+  const int fa = __builtin_amdgcn_readlane(fe ? 1 : 0, 0), fb = __builtin_amdgcn_readlane(fe ? 1 : 0, 1);
+  const uint64_t mxn = na > nb ? na : nb;
+  if (!fa || !fb || (mxn != 0 && mg > (uint64_t)INT64_MAX / mxn)) {
+    if (tid == 0) atomicOr(status, IMIE_ERMS);
+    return;
+  }
+  int64_t y[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    y[q] = imie_floor_shift((int64_t)((uint64_t)nv[q] * (uint64_t)gv[q]), frac);
+    if (pos[q] < cols) out[row * cols + pos[q]] = y[q];
+  }
+  if (wave < po.nslabs) imie_q1::prep_slab(y, po, row, wave);
+}
+
 }  // namespace
 
 int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
@@ -201,7 +312,10 @@ int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64
                              const imie_q1::Q1Zero& zero, hipStream_t st) {
   if (rows <= 0) return IMIE_OK;
   if (cols != po.nb * 128 || cols > kPrepCols) return IMIE_EARG;
-  if (cols <= 1024)
+  if (gain && po.nslabs <= 8)
+    hipLaunchKernelGGL(rmsnorm_prep_slab_kernel, dim3((unsigned)(rows + kZeroWgs)), dim3(512), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, zero);
+  else if (cols <= 1024)
     hipLaunchKernelGGL((rmsnorm_kernel<true, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, zero);
   else
@@ -214,6 +328,7 @@ int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64
 namespace {
 struct NormWs {
   DevBuf x, out, gain, status;
+  Q1Ws q1;                        // digit-table target of the fused entry point
 } g_nws;
 }  // namespace
 
@@ -247,6 +362,38 @@ int bonsai_rmsnorm_gpu(const int64_t* x, int64_t rows, int64_t cols, int64_t fra
 
 // Host evaluation of the RMSNorm kernels' exact helpers (CPU test hooks, no reference counterpart):
 // floor(sqrt(hi * 2^64 + lo)), floor((2^64 - 1) / d) and floor((hi * 2^64 + lo) / d) (low 64 bits).
+// The fused producer (RMSNorm that also writes the next Q1 matvec's digit table, used by the resident decode
+// for rows < 8) with bonsai_rmsnorm_gpu's host contract: same outputs and rc, the table goes to a workspace.
+// cols must be a multiple of 128 and at most 4096.
+int imie_rmsnorm_fused_gpu(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                           const int64_t* gain, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!x || !out || rows < 0 || cols <= 0 || cols % 128 || cols > 4096 || frac < 0 || frac > 62 || eps < 0)
+    return IMIE_EARG;
+  if (rows == 0) return IMIE_OK;
+  if (imie_device_ready() != 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  const size_t xb = (size_t)(rows * cols) * 8;
+  if (g_nws.x.ensure(xb) || g_nws.out.ensure(xb) || g_nws.gain.ensure((size_t)cols * 8) || g_nws.status.ensure(64))
+    return IMIE_EARG;
+  imie_q1::Q1PrepOut po;
+  int rc = imie_q1_prep_target(&g_nws.q1, cols / 128, rows, &po);
+  if (rc) return rc;
+  IMIE_HIP(hipMemcpyAsync(g_nws.x.p, x, xb, hipMemcpyHostToDevice, st));
+  if (gain) IMIE_HIP(hipMemcpyAsync(g_nws.gain.p, gain, (size_t)cols * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemsetAsync(g_nws.status.p, 0, 4, st));
+  const imie_q1::Q1Zero z = {};
+  rc = imie_rmsnorm_prep_launch((const int64_t*)g_nws.x.p, rows, cols, frac, eps,
+                                gain ? (const int64_t*)g_nws.gain.p : nullptr, (int64_t*)g_nws.out.p,
+                                (int*)g_nws.status.p, po, z, st);
+  if (rc) return rc;
+  int stat = 0;
+  IMIE_HIP(hipMemcpyAsync(&stat, g_nws.status.p, 4, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipMemcpyAsync(out, g_nws.out.p, xb, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return stat ? IMIE_ERMS : IMIE_OK;
+}
+
 uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo) { return imie_fx::isqrt_u128(((imie_fx::u128)hi << 64) | lo); }
 uint64_t imie_fx_recip_u64(uint64_t d) { return imie_fx::recip_u64(d); }
 uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d) {

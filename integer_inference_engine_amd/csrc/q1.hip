@@ -130,21 +130,10 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   const int64_t s1 = min(nslabs, s0 + spk);
   const int64_t nsl = s1 - s0;
 
-  // stage the digit operands of this slab range (the same x for every wave of the workgroup)
-  for (int t = 0; t < T; ++t)
-    for (int64_t j = 0; j < nsl; ++j) {
-      const int L = min(lslab[t * nslabs + s0 + j], Lcap);
-      uint4* dst = stage + ((t * spk + j) * Lcap) * 32;
-      for (int i = threadIdx.x; i < L * 32; i += blockDim.x) {
-        const int l = i >> 5, e = i & 31;
-        dst[i] = xq[(((int64_t)t * kMaxLimbs + l) * nbp + (s0 + j) * kSlabBlocks) * 8 + e];
-      }
-    }
-  __syncthreads();
-
   // this wave's tile group -> (segment, first tile)
-  const int64_t gi = (int64_t)blockIdx.x * 4 + wave;
-  if (gi >= sg.gbegin[sg.cnt]) return;
+  const int64_t gi_raw = (int64_t)blockIdx.x * 4 + wave;
+  const bool live = gi_raw < sg.gbegin[sg.cnt];
+  const int64_t gi = live ? gi_raw : sg.gbegin[sg.cnt] - 1;
   int seg = 0;
 #pragma unroll
   for (int z = 1; z < kMaxSegs; ++z)
@@ -169,7 +158,10 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     for (int r = 0; r < R; ++r) acc[t][r] = 0;
 
   uint4 wb[2][R];
-  int64_t sc[2][R];
+  using ScT = typename std::conditional<S64, int64_t, int32_t>::type;   // widened at use: no wait at the load
+  ScT sc[2][R];
+  int Lv[2][TT];
+  int64_t tv[2][TT];
   auto load = [&](int buf, int64_t sl) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -177,16 +169,22 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
       const int64_t idx = (tl * nslabs + sl) * 64 + lane;
       const v4i wv = __builtin_nontemporal_load(&((const v4i*)bitsT)[idx]);
       wb[buf][r] = uint4{(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
-      if (S64) sc[buf][r] = __builtin_nontemporal_load(&((const int64_t*)scaleT)[idx]);
-      else sc[buf][r] = __builtin_nontemporal_load(&((const int32_t*)scaleT)[idx]);
+      sc[buf][r] = __builtin_nontemporal_load(&((const ScT*)scaleT)[idx]);
     }
+    // the slab's digit count and block total travel with its weights (one prefetch, one wait)
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+      if (t < T) {
+        Lv[buf][t] = lslab[t * nslabs + sl];
+        tv[buf][t] = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
+      }
   };
   auto compute = [&](int buf, int64_t sl) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       if (t >= T) break;
-      const int L = lslab[t * nslabs + sl];
-      const int64_t total = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
+      const int L = Lv[buf][t];
+      const int64_t total = tv[buf][t];
       const uint4* st = stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8;
       const uint4* gx = xq + ((int64_t)t * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8;
       uint64_t pos[R];
@@ -225,14 +223,29 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t S = 2u * pos[r] - (uint64_t)total;
-        const int64_t prod = (int64_t)(S * (uint64_t)sc[buf][r]);
+        const int64_t prod = (int64_t)(S * (uint64_t)(int64_t)sc[buf][r]);
         acc[t][r] += (uint64_t)imie_floor_shift(prod, frac);
       }
     }
   };
 
+  // this wave's first weight slab is requested before the shared digit staging, so both latencies overlap
+  if (live) load(0, s0);
+  // stage the digit operands of this slab range (the same x for every wave of the workgroup)
+  for (int t = 0; t < T; ++t)
+    for (int64_t j = 0; j < nsl; ++j) {
+      const int L = Lcap;                         // limbs beyond the slab's count are staged but never read
+      uint4* dst = stage + ((t * spk + j) * Lcap) * 32;
+      for (int i = threadIdx.x; i < L * 32; i += blockDim.x) {
+        const int l = i >> 5, e = i & 31;
+        dst[i] = xq[(((int64_t)t * kMaxLimbs + l) * nbp + (s0 + j) * kSlabBlocks) * 8 + e];
+      }
+    }
+  __syncthreads();
+
+  if (!live) return;
+
   // software pipeline over the slab range: prefetch slab j+1 while computing slab j
-  load(0, s0);
   int64_t sl = s0;
   for (; sl + 1 < s1; sl += 2) {
     load(1, sl + 1);

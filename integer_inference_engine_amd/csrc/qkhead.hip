@@ -37,7 +37,7 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     lo = (uint64_t)sq;
   }
   int bad = 0;
-  wave_sum_u128(hi, lo, bad);
+  wave_sum_u128_full(hi, lo, bad);   // every reduction here runs on the full wave
   uint64_t rms = 0;
   if (!bad) {
     const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)a.hd);
@@ -51,13 +51,11 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   bool f0 = true, f1 = true;
   const int64_t n0 = act ? norm_elem(x0, a.frac, rms, rinv, &f0) : 0;
   const int64_t n1 = act ? norm_elem(x1, a.frac, rms, rinv, &f1) : 0;
-  int ok = (f0 && f1) ? 1 : 0;
+  const bool ok = imie_wave_max_u64_full((f0 && f1) ? 0 : 1) == 0;
   uint64_t mxn = imie_absu64(n0) > imie_absu64(n1) ? imie_absu64(n0) : imie_absu64(n1);
   uint64_t mxg = imie_absu64(g0) > imie_absu64(g1) ? imie_absu64(g0) : imie_absu64(g1);
-  mxn = imie_wave_max_u64(mxn);
-  mxg = imie_wave_max_u64(mxg);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ok &= __shfl_xor(ok, o, 64);
+  mxn = imie_wave_max_u64_full(mxn);
+  mxg = imie_wave_max_u64_full(mxg);
   if (!ok || (mxn != 0 && mxg > (uint64_t)INT64_MAX / mxn)) {
     if (j == 0) atomicOr(a.status, IMIE_ERMS);
     return;
@@ -71,8 +69,8 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   {
     uint64_t mx = imie_absu64(y0) > imie_absu64(y1) ? imie_absu64(y0) : imie_absu64(y1);
     uint64_t mc = imie_absu64(c) > imie_absu64(s) ? imie_absu64(c) : imie_absu64(s);
-    mx = imie_wave_max_u64(mx);
-    mc = imie_wave_max_u64(mc);
+    mx = imie_wave_max_u64_full(mx);
+    mc = imie_wave_max_u64_full(mc);
     if (j == 0) {
       amax_u64(&a.guard[isq ? 0 : 2], mx);
       amax_u64(&a.guard[isq ? 1 : 3], mc);
@@ -85,7 +83,7 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     }
     if (a.qd) {                                       // kv8 decode: q digits (8 limbs), max|q| and limb count
       uint64_t mq = imie_absu64(o0) > imie_absu64(o1) ? imie_absu64(o0) : imie_absu64(o1);
-      mq = imie_wave_max_u64(mq);
+      mq = imie_wave_max_u64_full(mq);
       const int64_t qrow = r * a.H + h;
       if (j == 0) { a.qmax[qrow] = mq; a.qlimbs[qrow] = imie_limbs_needed(mq); }
       if (act) {
@@ -110,8 +108,8 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   if (KV8) {
     uint64_t mk = imie_absu64(o0) > imie_absu64(o1) ? imie_absu64(o0) : imie_absu64(o1);
     uint64_t mv = imie_absu64(v0) > imie_absu64(v1) ? imie_absu64(v0) : imie_absu64(v1);
-    mk = imie_wave_max_u64(mk);
-    mv = imie_wave_max_u64(mv);
+    mk = imie_wave_max_u64_full(mk);
+    mv = imie_wave_max_u64_full(mv);
     if (j == 0) {
       if (mk > (uint64_t)imie_kv8::kCap || mv > (uint64_t)imie_kv8::kCap) atomicOr(a.status, IMIE_EOVF);
       if (a.M == 1) {

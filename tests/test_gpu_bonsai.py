@@ -49,6 +49,55 @@ def test_rmsnorm_refuses_where_oracle_raises(gpu):
     assert gpu.rmsnorm_gpu(big, 16, 1, None) is None
 
 
+def _fused_rmsnorm(x, frac, eps, g):
+    import ctypes
+    from integer_inference_engine_amd import _lib
+    x = np.ascontiguousarray(x, dtype=np.int64)
+    out = np.empty_like(x)
+    gg = None if g is None else np.ascontiguousarray(g, dtype=np.int64)
+    rc = _lib.lib().imie_rmsnorm_fused_gpu(x.ctypes.data, x.shape[0], x.shape[1], frac, eps,
+                                           None if gg is None else gg.ctypes.data, out.ctypes.data)
+    return None if rc != 0 else out
+
+
+@pytest.mark.parametrize("rows,cols,mag", [(1, 4096, 25), (7, 4096, 40), (3, 2560, 30), (2, 128, 50), (1, 640, 61)])
+def test_fused_rmsnorm_prep_matches_oracle(gpu, rows, cols, mag):
+    # the decode's RMSNorm + digit-table producer: per-row extremes decide max|n| (all-negative and
+    # all-positive rows included)
+    x = prng.uniform_int(mag, 3, (rows, cols), -(1 << mag), 1 << mag)
+    x[0] = np.abs(x[0])
+    if rows > 1:
+        x[1] = -np.abs(x[1]) - 1
+    g = prng.uniform_int(mag, 4, (cols,), -(1 << 17), 1 << 17)
+    ssq_over = any(sum(int(v) * int(v) for v in row) >= 1 << 128 for row in x)   # producer refuses (rc 4)
+    for gain in (g, None):
+        try:
+            want = None if ssq_over else fx.rmsnorm(x, 16, 1, gain)
+        except OverflowError:
+            want = None
+        got = _fused_rmsnorm(x, 16, 1, gain)
+        if want is None:
+            assert got is None
+        else:
+            assert_same(got, want, f"fused gain={gain is not None}")
+
+
+def test_fused_rmsnorm_refusals(gpu):
+    # gain envelope decided by the negative extreme alone; ssq beyond 128 bits; one huge element
+    x = np.zeros((1, 128), dtype=np.int64)
+    x[0, :4] = [3, -(1 << 20), 5, 7]
+    g = np.ones(128, dtype=np.int64)
+    g[5] = 1 << 50
+    with pytest.raises(OverflowError):
+        fx.rmsnorm(x, 16, 1, g)
+    assert _fused_rmsnorm(x, 16, 1, g) is None
+    g[5] = 1 << 20
+    assert_same(_fused_rmsnorm(x, 16, 1, g), fx.rmsnorm(x, 16, 1, g), "just inside the envelope")
+    big = np.full((1, 128), I64_MIN, dtype=np.int64)
+    assert _fused_rmsnorm(big, 16, 1, g) is None
+    assert _fused_rmsnorm(big, 16, 1, None) is None
+
+
 def test_silu_matches_oracle_including_int64_extremes(gpu):
     x = np.concatenate([prng.uniform_int(3, 1, (5000,), -(1 << 40), 1 << 40),
                         [I64_MIN, I64_MAX, I64_MIN + 1, 0, 1, -1, 1 << 62, -(1 << 62)]]).astype(np.int64)
