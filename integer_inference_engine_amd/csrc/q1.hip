@@ -6,16 +6,18 @@
 // Reference semantics: bonsai/src/trinote/infer_int/reference_bonsai.py:149-219 (q1_linear_ref) and the C
 // producer bonsai/tools/bonsai_q1_kernel.c:85-106. Bit i of byte j of a block is weight 8j+i.
 //
-// Matvec design (T small): int8 MFMA v_mfma_i32_16x16x64_i8 with
-//   * B operand = weight bits of 16 output rows, expanded with ONE v_and per 4 weights:
-//       B_s dword d = word_d & (0x01010101 << s)   -> bytes in {0, 2^s}  (s = 0..7, 0x80 reads as -128)
-//   * A operand = balanced base-256 digits ("limbs") of x, arranged so the 16 MFMA rows are
-//       (block g in the 4-block slab, shift s & 3); one accumulator for s < 4 and one for s >= 4.
-//     After the MFMAs lane (grp, n) holds the per-(block, shift) partials of output row n; a shift-and-add
-//     plus a 2-step cross-lane reduce-scatter leaves lane (g, n) with pos(block g, row n) for that limb.
-//   * The per-(row, block) epilogue (limb recombination, 2*pos - total, * scale, floor shift, add) runs with
-//     all 64 lanes busy, in int32 when max|x| <= 2^23 and in wrapping int64 otherwise.
-// MFMA int32 accumulation is exact: each D entry is at most 128 * 128 * 2^7 in magnitude.
+// Matvec design (T < 8): int8 MFMA v_mfma_i32_16x16x64_i8 over 16-row tiles and 512-column slabs:
+//   * B operand = one bit position s of the weight bytes of 16 output rows as 0/1 bytes
+//       B_s dword = (word >> s) & 0x01010101                            (2 VALU per 4 dwords of weights)
+//   * A operand = balanced base-256 digits ("limbs") of x from the prepared digit table, rows = (block g of the
+//     slab, limb r of a group of four); the 8 bit positions accumulate into one tile, so up to four limbs
+//     cost 8 MFMAs per slab and tile.
+//   * Slabs whose digits fit one limb (|x| <= 127, e.g. int8 activations) use rows = (block g, bit position
+//     mod 4) instead, with mask-only B bytes (0 or 2^s; 0x80 reads as -128): 8 MFMAs, no shifts.
+//   * Epilogue per (row, block): pos = sum_r D[r] << 8r, 2*pos - total, * scale, floor shift, add (wrapping
+//     int64, as the reference's C producer).
+// MFMA int32 accumulation is exact: each D entry is at most 8 * 16 * 128 = 2^14 in magnitude.
+// Prefill (T >= 8) uses the tiled GEMM further down.
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_q1prep.h"
@@ -100,10 +102,12 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 
 // ------------------------------------------------------------------------------------------------------
 // MFMA matvec / small-T linear.
-//   * MFMA rows m = 4*blk + (s & 3): lane (g, n) of the accumulator holds, for block g of the slab and output
-//     row n, the four partials of shifts 0..3 (d0) and 4..7 (d1). 128*pos = sum d0[r] << (7-r) +
-//     sum_{r<3} d1[r] << (3-r) - d1[3]  (8 v_lshl_add, no cross-lane traffic); the A operand is non-zero in
-//     lane (m, g) iff m >> 2 == g and the MFMA's shift matches m & 3.
+//   * MFMA rows m = 4*blk + limb (limbs in groups of four): A lane (m, g) holds the balanced digits of limb
+//     4*lg + (m & 3) of block g for one bit position s (non-zero iff m >> 2 == g), B lane (n, g) the bit s of
+//     block g's 16 weight bytes of output row n as 0/1 bytes ((w >> s) & 0x01010101). The 8 MFMAs of one slab
+//     (s = 0..7) accumulate into one tile: lane (g, n) then holds D[r] = sum over block g's 128 weights of
+//     digit_r(x) * bit for output row n, and pos = sum_r D[r] << 8 (4 lg + r) (|D| <= 2^14, no cross-lane
+//     traffic). Up to four limbs share the same 8 MFMAs.
 //   * Each wave streams its own R tiles over a slab range with double-buffered 16 B/lane loads; the digit
 //     table of the slab range (up to Lcap limbs) is staged once per workgroup in LDS.
 //   * grid.y splits K: with ksplit > 1 the waves add their int64 partials into a zeroed output with 64-bit
@@ -118,7 +122,7 @@ struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) app
   int cnt;
 };
 
-template <bool S64, int R, int TT>
+template <bool S64, int R, int TT, int PF = 0>
 __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
     int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out) {
@@ -145,11 +149,7 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   const int64_t tile0 = (gi - sg.gbegin[seg]) * R;
   const int g = lane >> 4;       // block within the slab
   const int n = lane & 15;       // output row within the tile
-  const bool aact = (n >> 2) == g;
-  const int as = n & 3;          // this lane feeds A for shifts as and as + 4
-  v4i areg[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) areg[s] = v4i{0, 0, 0, 0};
+  const bool aact = (n >> 2) == g;   // A row n (block n / 4) meets this lane's K group g
 
   uint64_t acc[TT][R];
 #pragma unroll
@@ -157,11 +157,14 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[t][r] = 0;
 
-  uint4 wb[2][R];
+  // PF > 0: the wave's whole slab range (at most PF slabs) is requested at once, before the digit staging
+  // (decode-sized matvecs: every weight byte in flight in one round); PF == 0: two-slab software pipeline
+  constexpr int NB = PF > 2 ? PF : 2;
+  uint4 wb[NB][R];
   using ScT = typename std::conditional<S64, int64_t, int32_t>::type;   // widened at use: no wait at the load
-  ScT sc[2][R];
-  int Lv[2][TT];
-  int64_t tv[2][TT];
+  ScT sc[NB][R];
+  int Lv[NB][TT];
+  int64_t tv[NB][TT];
   auto load = [&](int buf, int64_t sl) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -179,81 +182,149 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
         tv[buf][t] = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
       }
   };
+  // A operands of (token t, limb group lg): the 8 bit positions' digit rows, loaded once and shared by the R
+  // tiles; from LDS (staged limbs), the global table (limbs beyond Lcap), or the 8-entry zero slot for lanes
+  // whose row is not their block or whose limb is beyond the slab's count
+  const uint4* zslot = stage + (int64_t)TT * spk * Lcap * 32;
+  const int arow_l = n & 3;
   auto compute = [&](int buf, int64_t sl) {
+    uint64_t pos[TT][R];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int r = 0; r < R; ++r) pos[t][r] = 0;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       if (t >= T) break;
       const int L = Lv[buf][t];
-      const int64_t total = tv[buf][t];
-      const uint4* st = stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8;
-      const uint4* gx = xq + ((int64_t)t * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8;
-      uint64_t pos[R];
+      if (L == 1) {
+        // one limb (e.g. int8 activations): rows = (block, bit position mod 4) with mask-only B operands
+        // (bytes 0 / 2^s, 0x80 reading as -128); 128 * pos = sum d0[q] << (7 - q) + sum d1[q] << (3 - q)
+        const int as = n & 3;
+        uint4 a0, a1;
+        if (Lcap >= 4) {
+          const uint4* src = aact ? stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8 + as : zslot;
+          a0 = src[0];
+          a1 = src[aact ? 4 : 0];
+        } else {
+          const uint4* src = xq + ((int64_t)t * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8 + as;
+          a0 = aact ? src[0] : uint4{0, 0, 0, 0};
+          a1 = aact ? src[4] : uint4{0, 0, 0, 0};
+        }
+        v4i areg[8];
 #pragma unroll
-      for (int r = 0; r < R; ++r) pos[r] = 0;
-      for (int l = 0; l < L; ++l) {
-        // masked loads: only the lanes active for shift s write areg[s]; the others keep zeros
-        if (aact) {
-          const uint4 a0 = l < Lcap ? st[l * 32 + as] : gx[(int64_t)l * nbp * 8 + as];
-          const uint4 a1 = l < Lcap ? st[l * 32 + as + 4] : gx[(int64_t)l * nbp * 8 + as + 4];
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (as == s) {
-              areg[s] = v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
-              areg[s + 4] = v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-            }
+        for (int sh = 0; sh < 4; ++sh) {
+          areg[sh] = as == sh ? v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w} : v4i{0, 0, 0, 0};
+          areg[sh + 4] = as == sh ? v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w} : v4i{0, 0, 0, 0};
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
+          const uint4 w = wb[buf][r];
           v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            uint32_t m = 0x01010101u << s;
+          for (int sh = 0; sh < 8; ++sh) {
+            uint32_t m = 0x01010101u << sh;
             asm volatile("" : "+s"(m));   // keep each B expansion next to its MFMA (no hoisting across tiles)
-            const uint4 w = wb[buf][r];
             const v4i b = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
-            if (s < 4) d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], b, d0, 0, 0, 0);
-            else d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[s], b, d1, 0, 0, 0);
+            if (sh < 4) d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[sh], b, d0, 0, 0, 0);
+            else d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[sh], b, d1, 0, 0, 0);
           }
-          // 128 * pos for (block g, row n); shift 7 bytes read as -128
           const int p128 = (d0[0] << 7) + (d0[1] << 6) + (d0[2] << 5) + (d0[3] << 4) + (d1[0] << 3) +
                            (d1[1] << 2) + (d1[2] << 1) - d1[3];
-          pos[r] += (uint64_t)(int64_t)(p128 >> 7) << (8 * l);
+          pos[t][r] += (uint64_t)(int64_t)(p128 >> 7);
         }
+        continue;
       }
 #pragma unroll
+      for (int lg = 0; lg < 2; ++lg) {
+        if (4 * lg >= L) break;                       // wave-uniform
+        const int l = 4 * lg + arow_l;
+        const bool on = aact && l < L;
+        v4i A[8];
+        if (4 * lg + 4 <= Lcap) {
+          const uint4* src = on ? stage + ((t * spk + (sl - s0)) * Lcap + l) * 32 + g * 8 : zslot;
+#pragma unroll
+          for (int sh = 0; sh < 8; ++sh) {
+            const uint4 a = src[sh];
+            A[sh] = v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+          }
+        } else {
+          const uint4* src = xq + ((int64_t)t * kMaxLimbs * nbp + (int64_t)l * nbp + sl * kSlabBlocks + g) * 8;
+#pragma unroll
+          for (int sh = 0; sh < 8; ++sh) {
+            const uint4 a = src[sh];
+            A[sh] = on ? v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w} : v4i{0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint4 w = wb[buf][r];
+          v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};   // even / odd bit positions: two independent chains
+#pragma unroll
+          for (int sh = 0; sh < 8; ++sh) {
+            uint32_t k = sh;
+            asm volatile("" : "+s"(k));   // keep each bit-plane expansion next to its MFMA (no hoisting)
+            const v4i b = v4i{(int)((w.x >> k) & 0x01010101u), (int)((w.y >> k) & 0x01010101u),
+                              (int)((w.z >> k) & 0x01010101u), (int)((w.w >> k) & 0x01010101u)};
+            if (sh & 1) D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sh], b, D1, 0, 0, 0);
+            else D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sh], b, D0, 0, 0, 0);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pos[t][r] += (uint64_t)(int64_t)(D0[q] + D1[q]) << (8 * (4 * lg + q));
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t >= T) break;
+#pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint64_t S = 2u * pos[r] - (uint64_t)total;
+        const uint64_t S = 2u * pos[t][r] - (uint64_t)tv[buf][t];
         const int64_t prod = (int64_t)(S * (uint64_t)(int64_t)sc[buf][r]);
         acc[t][r] += (uint64_t)imie_floor_shift(prod, frac);
       }
     }
   };
 
-  // this wave's first weight slab is requested before the shared digit staging, so both latencies overlap
-  if (live) load(0, s0);
+  // this wave's first weight slab (PF: all of its slabs) is requested before the shared digit staging, so the
+  // latencies overlap
+  if (PF > 0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (live && j < nsl) load(j, s0 + j);
+  } else if (live) {
+    load(0, s0);
+  }
   // stage the digit operands of this slab range (the same x for every wave of the workgroup)
   for (int t = 0; t < T; ++t)
     for (int64_t j = 0; j < nsl; ++j) {
-      const int L = Lcap;                         // limbs beyond the slab's count are staged but never read
+      const int L = min(lslab[t * nslabs + s0 + j], Lcap);
       uint4* dst = stage + ((t * spk + j) * Lcap) * 32;
       for (int i = threadIdx.x; i < L * 32; i += blockDim.x) {
         const int l = i >> 5, e = i & 31;
         dst[i] = xq[(((int64_t)t * kMaxLimbs + l) * nbp + (s0 + j) * kSlabBlocks) * 8 + e];
       }
     }
+  if (threadIdx.x < 8) stage[(int64_t)TT * spk * Lcap * 32 + threadIdx.x] = uint4{0, 0, 0, 0};
   __syncthreads();
 
   if (!live) return;
 
-  // software pipeline over the slab range: prefetch slab j+1 while computing slab j
-  int64_t sl = s0;
-  for (; sl + 1 < s1; sl += 2) {
-    load(1, sl + 1);
-    compute(0, sl);
-    if (sl + 2 < s1) load(0, sl + 2);
-    compute(1, sl + 1);
+  if (PF > 0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (j < nsl) compute(j, s0 + j);
+  } else {
+    // software pipeline over the slab range: prefetch slab j+1 while computing slab j
+    int64_t sl = s0;
+    for (; sl + 1 < s1; sl += 2) {
+      load(1, sl + 1);
+      compute(0, sl);
+      if (sl + 2 < s1) load(0, sl + 2);
+      compute(1, sl + 1);
+    }
+    if (sl < s1) compute(0, sl);
   }
-  if (sl < s1) compute(0, sl);
 
   // sum the 4 blocks of each row (lane groups g) and write / accumulate row totals
 #pragma unroll
@@ -736,7 +807,8 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   // to keep ~8 waves per CU busy (decode-sized matvecs).
   int64_t ntiles_all = 0;
   for (int i = 0; i < cnt; ++i) ntiles_all += ws[i]->ntiles;
-  const int R = ntiles_all >= 4 * 16384 ? 4 : (ntiles_all >= 2 * 8192 ? 2 : 1);
+  // R = 4 only for single-token launches (four tokens x four tiles would exceed the register budget)
+  const int R = (ntiles_all >= 4 * 16384 && T == 1) ? 4 : (ntiles_all >= 2 * 8192 ? 2 : 1);
   Q1Segs sg = {};
   sg.cnt = cnt;
   int64_t groups = 0;
@@ -749,11 +821,24 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
     groups += (ws[i]->ntiles + R - 1) / R;
   }
   sg.gbegin[cnt] = groups;
-  int64_t ksplit = 1;
-  while (groups * ksplit < 8 * 1024 && ksplit * 2 <= nslabs && ksplit < 8) ksplit *= 2;
-  const int64_t spk = (nslabs + ksplit - 1) / ksplit;
-  ksplit = (nslabs + spk - 1) / spk;
+  int64_t ksplit = 1, spk = nslabs;
+  int pf = 0;
+  if (T == 1 && R == 1 && groups * nslabs <= 64 * 1024) {
+    // decode-sized: the largest slab range of 4 / 2 / 1 that still gives >= 2048 waves; each wave requests
+    // its whole range at once, so one round of resident waves covers the matrix
+    pf = 1;
+    for (int c = 4; c >= 2; c >>= 1)
+      if (groups * ((nslabs + c - 1) / c) >= 2048) { pf = c; break; }
+    spk = pf < nslabs ? pf : nslabs;
+    ksplit = (nslabs + spk - 1) / spk;
+    if (pf == 1) pf = 0;                              // one slab per wave: the pipelined kernel is the same
+  } else {
+    while (groups * ksplit < 8 * 1024 && ksplit * 2 <= nslabs && ksplit < 8) ksplit *= 2;
+    spk = (nslabs + ksplit - 1) / ksplit;
+    ksplit = (nslabs + spk - 1) / spk;
+  }
   const int TT = T <= 1 ? 1 : (T <= 2 ? 2 : 4);
+  if (TT == 4 && R == 4) return IMIE_EARG;            // not instantiated: R is 4 only for T == 1
   const int Tc = TT;
   // the prep kernel clears the outputs when the matvec adds into them (K-split) and no residual is kept
   Q1Zero zero = {};
@@ -770,9 +855,10 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   imie_prof_mark(IMIE_K_Q1_PREP, st, false);
   IMIE_HIP(hipGetLastError());
   const size_t budget = 48 * 1024;
+  // staged limbs come in whole groups of four (a limb group reads either LDS or the global table)
   int Lcap = (int)(budget / ((size_t)Tc * spk * 512));
-  Lcap = Lcap < 1 ? 1 : (Lcap > kMaxLimbs ? kMaxLimbs : Lcap);
-  const size_t lds = (size_t)Tc * spk * Lcap * 512;
+  Lcap = Lcap >= 8 ? 8 : (Lcap >= 4 ? 4 : 0);
+  const size_t lds = (size_t)Tc * spk * Lcap * 512 + 128;   // + the zero slot (8 x 16 B)
   const int fr = (int)(frac > 63 ? 63 : frac);
   const dim3 grid((unsigned)((groups + 3) / 4), (unsigned)ksplit);
   const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
@@ -790,8 +876,15 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
 #define IMIE_Q1_LAUNCH_R(S64_, TT_)                                                                          \
   if (R == 4) IMIE_Q1_LAUNCH(S64_, 4, TT_); else if (R == 2) IMIE_Q1_LAUNCH(S64_, 2, TT_); else IMIE_Q1_LAUNCH(S64_, 1, TT_)
 #define IMIE_Q1_LAUNCH_T(S64_)                                                                               \
-  if (TT == 1) { IMIE_Q1_LAUNCH_R(S64_, 1); } else if (TT == 2) { IMIE_Q1_LAUNCH_R(S64_, 2); } else { IMIE_Q1_LAUNCH_R(S64_, 4); }
-    if (w0.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
+  if (TT == 1) { IMIE_Q1_LAUNCH_R(S64_, 1); } else if (TT == 2) { IMIE_Q1_LAUNCH_R(S64_, 2); }                 \
+  else if (R == 2) { IMIE_Q1_LAUNCH(S64_, 2, 4); } else { IMIE_Q1_LAUNCH(S64_, 1, 4); }
+#define IMIE_Q1_LAUNCH_PF(S64_, PF_)                                                                         \
+  hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, 1, 1, PF_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs, \
+                     nbp, tn, fr, spk, Lcap, mode)
+    if (pf == 4) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 4); else IMIE_Q1_LAUNCH_PF(false, 4); }
+    else if (pf == 2) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 2); else IMIE_Q1_LAUNCH_PF(false, 2); }
+    else if (w0.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
+#undef IMIE_Q1_LAUNCH_PF
 #undef IMIE_Q1_LAUNCH_T
 #undef IMIE_Q1_LAUNCH_R
 #undef IMIE_Q1_LAUNCH

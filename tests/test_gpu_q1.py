@@ -37,7 +37,10 @@ def test_mfma_operand_and_accumulator_layout(gpu):
             assert d[l, r] == full[4 * (l // 16) + r, l % 16]
 
 
-@pytest.mark.parametrize("N,nb,T", [(16, 4, 1), (37, 3, 1), (256, 32, 1), (1024, 96, 1), (100, 5, 3), (64, 8, 7)])
+@pytest.mark.parametrize("N,nb,T", [(16, 4, 1), (37, 3, 1), (256, 32, 1), (1024, 96, 1), (100, 5, 3), (64, 8, 7),
+                                    # decode-sized launches whose waves request 4 / 2 slabs at once, with a short
+                                    # last slab range (10 = 4 + 4 + 2 slabs, 25 = 12 * 2 + 1)
+                                    (24576, 40, 1), (24576, 32, 1), (4096, 100, 1)])
 def test_q1_apply_matches_oracle_shapes(gpu, N, nb, T):
     seed = N * 1000 + nb * 10 + T
     bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
@@ -46,6 +49,37 @@ def test_q1_apply_matches_oracle_shapes(gpu, N, nb, T):
     got = gpu.q1_apply_gpu(x, bits, scale, 16)
     assert got is not None
     assert np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("N,nb,T,xmag", [
+    (64, 200, 3, 45),      # 50 slabs over 8 K-splits x 3 tokens: no staged limbs, every limb group from memory
+    (64, 128, 4, 45),      # 16 staged slab-tokens: limbs 0-3 from LDS, limbs 4-7 from memory
+    (64, 128, 4, 62),
+    (24576, 40, 1, 45),    # decode launch, 4 slabs requested at once, two limb groups
+    (4096, 100, 1, 62),    # decode launch, 2 slabs at once, eight limbs
+])
+def test_q1_limb_groups_from_lds_and_memory(gpu, N, nb, T, xmag):
+    seed = N + nb + T + xmag
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << 12), 1 << 12)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -(1 << xmag), 1 << xmag)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("N,nb,T", [(4096, 32, 1), (24576, 40, 1), (64, 128, 4), (96, 24, 2)])
+def test_q1_mixed_single_and_multi_limb_slabs(gpu, N, nb, T):
+    # slabs alternate between |x| <= 127 (one limb: the bit-position row layout) and wide values (limb groups)
+    seed = 7 * N + nb + T
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << 20), 1 << 20)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -127, 128)
+    wide = prng.uniform_int(seed, 4, (T, nb * 128), -(1 << 40), 1 << 40)
+    for sl in range(1, (nb + 3) // 4, 2):
+        x[:, sl * 512:(sl + 1) * 512] = wide[:, sl * 512:(sl + 1) * 512]
+    x[:, -1] = -128                                   # the one value that needs a second limb
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
 
 
 @pytest.mark.parametrize("xmag,smag", [(7, 11), (20, 40), (30, 12), (45, 20), (62, 62)])
