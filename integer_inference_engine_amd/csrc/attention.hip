@@ -748,7 +748,9 @@ __device__ inline int64_t kv8_row_base(const AttnDesc& d, int64_t b, int64_t kv,
 
 // Decode scores (M == 1). Workgroup = (b, kv, chunk); wave w takes 16-key tiles w, w + 4, ... MFMA rows are
 // (head r, limb lq): row 4 (r % 4) + (lq % 4) of row block (r / 4, lq / 4); a D lane (g, n) then holds the 4
-// limbs of head 4 * hb + g for key n and recombines them in place.
+// limbs of head 4 * hb + g for key n and recombines them in place. With d.qd set, the head stage has already
+// written q's digit planes, limb counts and max|q|, and the A operands are read from memory directly;
+// otherwise the first wave-pass digitizes q into LDS.
 template <int REP>
 __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   constexpr int RBH = (REP + 3) / 4;
