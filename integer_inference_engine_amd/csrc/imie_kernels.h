@@ -80,9 +80,15 @@ struct QkHeadArgs {
   int8_t* qd;
   uint64_t* qmax;
   int* qlimbs;
+  // many rows (M > 1): per-workgroup RoPE envelope maxima gpart[(row * (H + Hkv) + head) * 2 + {0, 1}] instead of
+  // same-address atomics (reduced into guard by imie_qk_head_finish_launch), and the kv8 V planes appended by
+  // that launch's coalesced kernel instead of per-element byte scatters
+  uint64_t* gpart;
 };
 // kv8 = 1: the digit-plane cache of imie_kvfmt.h; 0: int64 rows
 int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
+// after imie_qk_head_launch with gpart set: guard <- max over gpart; kv8: the V digit planes of the new rows
+int imie_qk_head_finish_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
 // kv8 cache: fold the appended rows' maxima (rowk / rowv, M rows per sequence) into run_k / run_v
 int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
                           uint64_t* run_k, uint64_t* run_v, hipStream_t st);

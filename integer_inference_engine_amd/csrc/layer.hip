@@ -113,6 +113,7 @@ struct Net {
   DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx, amx, stepc;
   DevBuf kvrun;                       // kv8: running max|K|, max|V| per (layer, sequence, kv head): [nl][2][B*Hkv]
   DevBuf kvrow;                       // kv8: appended rows' maxima [2][rows*Hkv]
+  DevBuf gpart;                       // many-row head stage: per-(row, head) RoPE envelope maxima [rows][H+Hkv][2]
   Q1Ws q1w;                           // this net's Q1 workspace (graph-stable addresses)
   // captured greedy decode step (imie_net_decode_dev): valid for the pointer key it was captured with
   hipGraphExec_t gexec = nullptr;
@@ -147,7 +148,7 @@ void net_free(Net* n) {
   if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
                   &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx, &n->amx,
-                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow};
+                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow, &n->gpart};
   for (auto b : bs) b->release();
   n->live = false;
 }
@@ -210,7 +211,8 @@ int net_ensure(Net& n, int64_t M, int64_t lmax) {
       n.up.ensure((size_t)(rows * n.dff) * 8) || n.h.ensure((size_t)(rows * n.dff) * 8) ||
       n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure((size_t)n.nl * 32) ||
       n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)) ||
-      n.kvrow.ensure((size_t)(2 * rows * n.Hkv) * 8))
+      n.kvrow.ensure((size_t)(2 * rows * n.Hkv) * 8) ||
+      (M > 1 && n.gpart.ensure((size_t)(rows * (n.H + n.Hkv) * 2) * 8)))
     return IMIE_EARG;
   return IMIE_OK;
 }
@@ -284,7 +286,9 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
         a.run_k = run_k(n, l); a.run_v = run_v(n, l);
       }
       if (d.qd) { a.qd = (int8_t*)d.qd; a.qlimbs = (int*)d.qlimbs; a.qmax = d.maxq; }
+      if (M > 1) a.gpart = (uint64_t*)n.gpart.p;
       CK(imie_qk_head_launch(a, n.kv32, st));
+      CK(imie_qk_head_finish_launch(a, n.kv32, st));
       if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));
     }
     CK(imie_attention_launch(d, st));

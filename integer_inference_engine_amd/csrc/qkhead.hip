@@ -45,6 +45,7 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   }
   if (rms == 0) {
     if (j == 0) atomicOr(a.status, IMIE_ERMS);
+    if (j == 0 && a.gpart) { a.gpart[(r * (a.H + a.Hkv) + h) * 2] = 0; a.gpart[(r * (a.H + a.Hkv) + h) * 2 + 1] = 0; }
     return;
   }
   const uint64_t rinv = recip_u64(rms);
@@ -58,6 +59,7 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   mxg = imie_wave_max_u64_full(mxg);
   if (!ok || (mxn != 0 && mxg > (uint64_t)INT64_MAX / mxn)) {
     if (j == 0) atomicOr(a.status, IMIE_ERMS);
+    if (j == 0 && a.gpart) { a.gpart[(r * (a.H + a.Hkv) + h) * 2] = 0; a.gpart[(r * (a.H + a.Hkv) + h) * 2 + 1] = 0; }
     return;
   }
   const int64_t y0 = imie_floor_shift((int64_t)((uint64_t)n0 * (uint64_t)g0), a.frac);
@@ -72,8 +74,14 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     mx = imie_wave_max_u64_full(mx);
     mc = imie_wave_max_u64_full(mc);
     if (j == 0) {
-      amax_u64(&a.guard[isq ? 0 : 2], mx);
-      amax_u64(&a.guard[isq ? 1 : 3], mc);
+      if (a.gpart) {
+        uint64_t* gp = a.gpart + (r * (a.H + a.Hkv) + h) * 2;
+        gp[0] = mx;
+        gp[1] = mc;
+      } else {
+        amax_u64(&a.guard[isq ? 0 : 2], mx);
+        amax_u64(&a.guard[isq ? 1 : 3], mc);
+      }
     }
   }
   if (isq) {
@@ -122,13 +130,17 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     }
     if (!act) return;
     int8_t* blk = (int8_t*)a.kpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
-    int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
     const uint32_t wk0 = imie_kv8::encode(o0), wk1 = imie_kv8::encode(o1);
-    const uint32_t wv0 = imie_kv8::encode(v0), wv1 = imie_kv8::encode(v1);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       blk[imie_kv8::k_off(slot, db, j, a.hd)] = (int8_t)(wk0 >> (8 * db));
       blk[imie_kv8::k_off(slot, db, j + half, a.hd)] = (int8_t)(wk1 >> (8 * db));
+    }
+    if (a.gpart) return;                              // V planes: kv8_v_append_kernel (coalesced over slots)
+    int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
+    const uint32_t wv0 = imie_kv8::encode(v0), wv1 = imie_kv8::encode(v1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
       vblk[imie_kv8::v_off(slot, db, j, a.hd, a.P)] = (int8_t)(wv0 >> (8 * db));
       vblk[imie_kv8::v_off(slot, db, j + half, a.hd, a.P)] = (int8_t)(wv1 >> (8 * db));
     }
@@ -162,6 +174,55 @@ __global__ __launch_bounds__(64) void kv_runmax_kernel(const uint64_t* __restric
   }
 }
 
+
+// RoPE envelope maxima of a many-row head stage: grid-stride max over the per-workgroup partials, one atomic
+// per wave and quantity
+__global__ __launch_bounds__(256) void guard_reduce_kernel(const uint64_t* __restrict__ gpart, int64_t n, int64_t H,
+                                                           int64_t heads, uint64_t* __restrict__ guard) {
+  uint64_t m[4] = {0, 0, 0, 0};
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int k = (e % heads) < H ? 0 : 2;
+    const uint64_t a = gpart[2 * e], c = gpart[2 * e + 1];
+    if (k == 0) { m[0] = a > m[0] ? a : m[0]; m[1] = c > m[1] ? c : m[1]; }
+    else { m[2] = a > m[2] ? a : m[2]; m[3] = c > m[3] ? c : m[3]; }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint64_t v = imie_wave_max_u64_full(m[i]);
+    if ((threadIdx.x & 63) == 0 && v != 0) amax_u64(&guard[i], v);
+  }
+}
+
+// kv8 V append of many rows: workgroup = (64 consecutive new positions of sequence b, kv head). The rows'
+// digits are transposed through LDS to the cache's [digit][dim][slot] order, so each store instruction writes
+// 64 consecutive slots.
+__global__ __launch_bounds__(256) void kv8_v_append_kernel(QkHeadArgs a) {
+  __shared__ int8_t sv[4][128][64];
+  const int64_t bkv = blockIdx.y, b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  const int64_t m0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  for (int64_t i = tid; i < 64 * a.hd; i += 256) {
+    const int64_t ml = i / a.hd, c = i % a.hd, m = m0 + ml;
+    const int64_t v = m < a.M ? a.v[((b * a.M + m) * a.Hkv + kvh) * a.hd + c] : 0;
+    const uint32_t w = imie_kv8::encode(imie_kv8::fits(v) ? v : 0);   // out-of-range rows are flagged upstream
+#pragma unroll
+    for (int db = 0; db < 4; ++db) sv[db][c][ml] = (int8_t)(w >> (8 * db));
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int64_t m = m0 + lane;
+  if (m >= a.M) return;
+  const int64_t p = a.pos[b * a.M + m];
+  const uint32_t pq = (uint32_t)p / (uint32_t)a.P;
+  const int64_t pg = a.pt[b * a.mp + pq], slot = (uint32_t)p - pq * (uint32_t)a.P;
+  int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
+  for (int64_t e = wave; e < 4 * a.hd; e += 4) {
+    const int db = (int)(e / a.hd);
+    const int64_t c = e % a.hd;
+    vblk[imie_kv8::v_off(slot, db, c, a.hd, a.P)] = sv[db][c][lane];
+  }
+}
+
 }  // namespace
 
 int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st) {
@@ -181,5 +242,20 @@ int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B,
   if (B <= 0 || M <= 1) return IMIE_OK;
   hipLaunchKernelGGL(kv_runmax_kernel, dim3((unsigned)(B * Hkv)), dim3(64), 0, st, rowk, rowv, M, Hkv, run_k, run_v);
   IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_qk_head_finish_launch(const QkHeadArgs& a, int kv8, hipStream_t st) {
+  if (!a.gpart || a.rows <= 0) return IMIE_OK;
+  const int64_t heads = a.H + a.Hkv, n = a.rows * heads;
+  const unsigned g = (unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64);
+  hipLaunchKernelGGL(guard_reduce_kernel, dim3(g), dim3(256), 0, st, a.gpart, n, a.H, heads, a.guard);
+  IMIE_HIP(hipGetLastError());
+  if (kv8) {
+    if (a.hd > 128) return IMIE_EARG;
+    const dim3 grid((unsigned)((a.M + 63) / 64), (unsigned)(a.rows / a.M * a.Hkv));
+    hipLaunchKernelGGL(kv8_v_append_kernel, grid, dim3(256), 0, st, a);
+    IMIE_HIP(hipGetLastError());
+  }
   return IMIE_OK;
 }
