@@ -851,7 +851,10 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
           v4i D = mfma8(av[hb][lb][0], bk[db][0], v4i{0, 0, 0, 0});
           if (KS > 1) D = mfma8(av[hb][lb][1], bk[db][1], D);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S += (uint64_t)(int64_t)D[i] << (8 * (4 * lb + i + db));
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lb + i + db;              // 256^e = 0 mod 2^64 for e >= 8
+            if (e < 8) S += (uint64_t)(int64_t)D[i] << (8 * e);
+          }
         }
       const int r = 4 * hb + g;
       if (valid && r < REP) {
@@ -1094,25 +1097,30 @@ __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
         bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
                         ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
                         : v4i{0, 0, 0, 0};
-    v4i T[11];
+    v4i T[8];
 #pragma unroll
-    for (int e = 0; e < 11; ++e) T[e] = v4i{0, 0, 0, 0};
-    for (int lq = 0; lq < Lq; ++lq) {
-      v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
-      v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
-      if (16 * g >= d.hd) a0 = v4i{0, 0, 0, 0};
-      if (64 + 16 * g >= d.hd) a1 = v4i{0, 0, 0, 0};
+    for (int e = 0; e < 8; ++e) T[e] = v4i{0, 0, 0, 0};
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        v4i x = mfma8(a0, bk[db][0], T[lq + db]);
-        if (KS > 1) x = mfma8(a1, bk[db][1], x);
-        T[lq + db] = x;
+    for (int lq = 0; lq < 8; ++lq) {                  // compile-time limb index: T stays in registers
+      if (lq < Lq) {
+        v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
+        v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
+        if (16 * g >= d.hd) a0 = v4i{0, 0, 0, 0};
+        if (64 + 16 * g >= d.hd) a1 = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          if (lq + db >= 8) continue;                 // 256^(lq+db) = 0 mod 2^64
+          v4i x = mfma8(a0, bk[db][0], T[lq + db]);
+          if (KS > 1) x = mfma8(a1, bk[db][1], x);
+          T[lq + db] = x;
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint64_t S = 0;
-      for (int e = 0; e < Lq + 3; ++e) S += (uint64_t)(int64_t)T[e][i] << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) S += (uint64_t)(int64_t)T[e][i] << (8 * e);   // 256^e = 0 mod 2^64, e >= 8
       if (rr[i] >= 0 && j < lvr[i]) {
         int64_t sc = (int64_t)S >> d.frac;
         sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
@@ -1265,7 +1273,9 @@ __global__ __launch_bounds__(256) void pf_pv8_kernel(AttnDesc d) {
     page_split(d, t0, pi, slot0);
     const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
     const int nv = (int)max((int64_t)0, min((int64_t)16, alv - (t0 + 16 * g)));
-    for (int lp = 0; lp < Lp; ++lp) {
+#pragma unroll
+    for (int lp = 0; lp < 4; ++lp) {                  // Lp <= 4 (frac <= 29): T stays in registers
+      if (lp >= Lp) break;
       v4i a = nv > 0 ? *(const v4i*)(d.pd + ((int64_t)lp * rows + ar) * d.pdL + t0 + 16 * g) : v4i{0, 0, 0, 0};
       a = keep_bytes(a, nv);
 #pragma unroll

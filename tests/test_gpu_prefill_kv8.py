@@ -104,3 +104,33 @@ def test_8b_layer_prefill_kv8(gpu):
         assert np.array_equal(k, nk[0]) and np.array_equal(v, nv[0])
     finally:
         net.close()
+
+
+def test_kv8_attention_with_wide_queries(gpu):
+    """q-norm gains scaled by 2^23 and k-norm gains by 2^-12: q needs 6 limbs, the scores' digit products reach
+    exponents >= 8 (which vanish mod 2^64). Prefill of 24 rows, then 3 single-row decode steps over the cache."""
+    import torch
+    model = workloads.small_bonsai(seed=91, ctx=256)
+    for layer in model["layers"]:
+        layer["qng"] = (layer["qng"].astype(np.int64) << 23).astype(np.int64)
+        layer["kng"] = np.maximum(layer["kng"].astype(np.int64) >> 12, 1)
+    cfg = model["cfg"]
+    c = {"H": cfg["H"], "Hkv": cfg["Hkv"], "hd": cfg["hd"]}
+    T = 24
+    ids = prng.uniform_int(91, 5, (T + 3,), 0, cfg["vocab"])
+    x0 = q1_rows(*model["embed"], ids)
+    net = _net(gpu, model, 1, 64)
+    try:
+        x = torch.from_numpy(x0[:T].copy()).cuda()
+        assert net.forward(x, [0], T) == 0
+        want, kc, vc = _oracle_layers(model, x0[:T], c, None, None, 0)
+        assert np.array_equal(x.cpu().numpy(), want), "prefill"
+        for s in range(3):
+            xs = torch.from_numpy(x0[T + s:T + s + 1].copy()).cuda()
+            assert net.forward(xs, [T + s], 1) == 0
+            w1, nk, nv = _oracle_layers(model, x0[T + s:T + s + 1], c, kc, vc, T + s)
+            assert np.array_equal(xs.cpu().numpy(), w1), f"decode step {s}"
+            kc = [np.concatenate([a, b], axis=1) for a, b in zip(kc, nk)]
+            vc = [np.concatenate([a, b], axis=1) for a, b in zip(vc, nv)]
+    finally:
+        net.close()
