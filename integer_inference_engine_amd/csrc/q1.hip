@@ -41,6 +41,7 @@ struct Q1Weight {
   uint4* bits = nullptr;
   void* scale = nullptr;
   int scale64 = 0;
+  int64_t maxsc = 0;               // max |scale| (host-side bounds for the GEMM epilogue)
   size_t bytes = 0;
   bool live = false;
 };
@@ -440,6 +441,7 @@ struct GemmArgs {
   const int* lt;
   int64_t T, Tp, N, nb, nbp, nslabs, ntt, nto;
   int frac, accumulate;
+  int kfold;                       // > 0: high-dword epilogue (narrow kernel), folded every kfold blocks
   int64_t* out;
 };
 
@@ -499,17 +501,23 @@ __device__ inline void gemm_slab_limbs(const GemmArgs& a, int64_t t0g, int* s_lw
   __syncthreads();
 }
 
-template <bool S64>
+// NBUF = 2: double-buffered LDS operands, one barrier per block (62 KB of LDS: 2 workgroups per CU); NBUF = 1:
+// one buffer and two barriers per block (31 KB: more workgroups per CU to overlap one another's waits)
+// FE (int32 scales with |scale| < 2^(frac-1), frac <= 31): per element and block, p = S * (scale << (32 - frac))
+// + H with H = A * 2^32, so the high dword of p is A + floor(S * scale / 2^frac) exactly; clearing p's low dword
+// gives the next H (one v_mad_i64_i32 and one clear). A is folded into the int64 sum every kfold blocks, chosen
+// on the host so |A| + max|q| stays below 2^31 (|S| < 2^30 on <= 3 limbs).
+template <bool S64, int NBUF, bool FE>
 __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
   constexpr int MT = 2, NT = 4;
   __shared__ int s_lw[kGemmMaxSlabs];
   // [buffer][limb][token][shift], tokens padded to 9 x 16 B: the 16 lanes of a quarter-wave read tokens
   // m = 0..15 at a 144 B stride, which covers all 64 LDS banks once (a 128 B stride would hit 2 of them)
-  __shared__ v4i sA[2][kNarrowLimbs][64][9];
-  __shared__ uint4 sB[2][128];                        // block bits of the 128 outputs
+  __shared__ v4i sA[NBUF][kNarrowLimbs][64][9];
+  __shared__ uint4 sB[NBUF][128];                     // block bits of the 128 outputs
   typedef typename std::conditional<S64, int64_t, int32_t>::type ST;
-  __shared__ ST sS[2][128];                           // their scales (int32 unless the weight keeps int64)
-  __shared__ int64_t sT[2][64];                       // block totals of the 64 tokens
+  __shared__ ST sS[NBUF][128];                        // their scales (int32 unless the weight keeps int64)
+  __shared__ int64_t sT[NBUF][64];                    // block totals of the 64 tokens
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int64_t t0, o0, t0g;
@@ -558,20 +566,36 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) sA[buf][l][st_tok][st_s + u] = pa[l][u];
     if (tid < 128) { sB[buf][tid] = pb; sS[buf][tid] = ps; }
-    if (tid < 64) sT[buf][tid] = pt;
+    if (tid < 64) sT[buf][tid] = 0 - pt;             // negated block totals: S = (D << 1) + sT, one v_lshl_add
   };
   int64_t acc[MT][NT][4];
+  int64_t accH[FE ? MT : 1][FE ? NT : 1][4];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int jj = 0; jj < NT; ++jj)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[i][jj][r] = 0;
+      for (int r = 0; r < 4; ++r) {
+        acc[i][jj][r] = 0;
+        if (FE) accH[FE ? i : 0][FE ? jj : 0][r] = 0;
+      }
+  int fcount = 0;
+  auto fold = [&]() {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)(accH[FE ? i : 0][FE ? jj : 0][r] >> 32));
+          accH[FE ? i : 0][FE ? jj : 0][r] = 0;
+        }
+  };
   stage_load(0);
   stage_store(0);
   __syncthreads();
   for (int64_t b = 0; b < a.nb; ++b) {
-    const int buf = (int)(b & 1);
+    const int buf = NBUF == 2 ? (int)(b & 1) : 0;
     const bool more = b + 1 < a.nb;
     if (more) stage_load(b + 1);                      // next block's operands in flight during this block
     const int lw = s_lw[b >> 2];
@@ -586,11 +610,23 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
       // pos = sum_l D_l 256^l by Horner from the top limb: acc = (acc << 8) + MFMA(limb l); one shift per
       // element per limb, exact in int32 (every partial is bounded by |pos| <= 2^30)
       v4i D[MT][NT];
+      {
+        // top limb from a zero accumulator (no shift), then Horner down to limb 0
+        const int l = lw - 1;
+        v4i av[MT][2];
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int jj = 0; jj < NT; ++jj) D[i][jj] = v4i{0, 0, 0, 0};
-      for (int l = lw - 1; l >= 0; --l) {
+          for (int h = 0; h < 2; ++h) av[i][h] = sA[buf][l][tb + 16 * i + m][4 * h + g];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj) {
+            const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            D[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], c, 0, 0, 0);
+          }
+      }
+      for (int l = lw - 2; l >= 0; --l) {
         v4i av[MT][2];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
@@ -607,24 +643,50 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
             D[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], c, 0, 0, 0);
           }
       }
+      if (FE) {
+        int32_t scp[NT];
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
+        for (int jj = 0; jj < NT; ++jj) scp[jj] = (int32_t)((uint32_t)sS[buf][ob + 16 * jj + m] << (32 - a.frac));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t tot = (uint32_t)sT[buf][tb + 16 * i + 4 * g + r];
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int jj = 0; jj < NT; ++jj) {
-            const int32_t S = (int32_t)(((uint32_t)D[i][jj][r] << 1) - tot);
-            const ST sc = sS[buf][ob + 16 * jj + m];
-            const int64_t prod = S64 ? (int64_t)((uint64_t)(int64_t)S * (uint64_t)(int64_t)sc)
-                                     : (int64_t)S * (int64_t)(int32_t)sc;   // one v_mad_i64_i32
-            acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)imie_floor_shift(prod, a.frac));
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t ntot = (uint32_t)sT[buf][tb + 16 * i + 4 * g + r];
+#pragma unroll
+            for (int jj = 0; jj < NT; ++jj) {
+              const int32_t S = (int32_t)(((uint32_t)D[i][jj][r] << 1) + ntot);
+              const int64_t p = (int64_t)S * (int64_t)scp[jj] + accH[FE ? i : 0][FE ? jj : 0][r];
+              accH[FE ? i : 0][FE ? jj : 0][r] = p & (int64_t)0xFFFFFFFF00000000ll;
+            }
           }
-        }
+        if (++fcount == a.kfold) { fold(); fcount = 0; }
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t ntot = (uint32_t)sT[buf][tb + 16 * i + 4 * g + r];
+#pragma unroll
+            for (int jj = 0; jj < NT; ++jj) {
+              const int32_t S = (int32_t)(((uint32_t)D[i][jj][r] << 1) + ntot);
+              const ST sc = sS[buf][ob + 16 * jj + m];
+              const int64_t prod = S64 ? (int64_t)((uint64_t)(int64_t)S * (uint64_t)(int64_t)sc)
+                                       : (int64_t)S * (int64_t)(int32_t)sc;   // one v_mad_i64_i32
+              acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)imie_floor_shift(prod, a.frac));
+            }
+          }
+      }
     }
-    if (more) stage_store(buf ^ 1);
-    __syncthreads();
+    if (NBUF == 2) {
+      if (more) stage_store(buf ^ 1);
+      __syncthreads();
+    } else {
+      __syncthreads();                                // every wave is done with this block's operands
+      if (more) stage_store(0);
+      __syncthreads();
+    }
   }
+  if (FE) fold();
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -745,6 +807,22 @@ __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
     }
 }
 
+// narrow GEMM LDS buffering (IMIE_GEMM_NBUF = 1 or 2 overrides; tuning)
+static int gemm_nbuf() {
+  static const int v = [] {
+    const char* e = getenv("IMIE_GEMM_NBUF");
+    const int n = e ? atoi(e) : 0;
+    return n == 1 || n == 2 ? n : 1;
+  }();
+  return v;
+}
+
+// high-dword GEMM epilogue where the scales allow it (IMIE_GEMM_FASTEPI=0 disables; tuning and tests)
+static bool gemm_fast_epi() {
+  static const bool v = [] { const char* e = getenv("IMIE_GEMM_FASTEPI"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
 static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
                          int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
   const Q1Weight& w0 = *ws[0];
@@ -768,11 +846,27 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128;
     ga.frac = (int)(frac > 63 ? 63 : frac); ga.accumulate = accumulate; ga.out = outs[i];
     const dim3 grid((unsigned)(ga.ntt >= 8 ? 8 * ((ga.ntt + 7) / 8) * ga.nto : ga.ntt * ga.nto));
+    const int nbuf = gemm_nbuf();
+    // high-dword epilogue: int32 scales below 2^(frac-1); |q| = |floor(S * scale / 2^frac)| <= max_q with
+    // |S| < 2^30 (narrow blocks); fold before |A| + max_q could reach 2^31
+    ga.kfold = 0;
+    if (!w.scale64 && ga.frac >= 1 && ga.frac <= 31 && w.maxsc < ((int64_t)1 << (ga.frac - 1)) && gemm_fast_epi()) {
+      const int64_t max_q = (((int64_t)w.maxsc << 30) >> ga.frac) + 2;
+      const int64_t k = (((int64_t)1 << 31) - 1) / max_q - 1;
+      ga.kfold = (int)(k < 1 ? 1 : (k > (1 << 20) ? (1 << 20) : k));
+    }
     if (w.scale64) {
-      hipLaunchKernelGGL(q1_gemm_narrow_kernel<true>, grid, dim3(256), 0, st, ga);
+      if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), grid, dim3(256), 0, st, ga);
+      else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), grid, dim3(256), 0, st, ga);
       hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
     } else {
-      hipLaunchKernelGGL(q1_gemm_narrow_kernel<false>, grid, dim3(256), 0, st, ga);
+      if (ga.kfold > 0) {
+        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, true>), grid, dim3(256), 0, st, ga);
+        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, true>), grid, dim3(256), 0, st, ga);
+      } else {
+        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, false>), grid, dim3(256), 0, st, ga);
+        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, false>), grid, dim3(256), 0, st, ga);
+      }
       hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
     }
     IMIE_HIP(hipGetLastError());
@@ -905,11 +999,14 @@ static int64_t q1_register(const uint8_t* bits, const void* scale, int64_t N, in
   if (!bits || !scale || N <= 0 || nb <= 0 || imie_device_ready() != 0) return -1;
   // narrow the scales to int32 when every value fits (lossless); keep int64 otherwise
   int scale64 = 0;
+  uint64_t maxsc = 0;
   std::vector<int64_t> s64((size_t)(N * nb));
   for (int64_t i = 0; i < N * nb; ++i) {
     const int64_t v = src32 ? (int64_t)((const int32_t*)scale)[i] : ((const int64_t*)scale)[i];
     s64[(size_t)i] = v;
     if (v < INT32_MIN || v > INT32_MAX) scale64 = 1;
+    const uint64_t av = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+    maxsc = av > maxsc ? av : maxsc;
   }
   Q1Weight w;
   w.N = N;
@@ -927,6 +1024,7 @@ static int64_t q1_register(const uint8_t* bits, const void* scale, int64_t N, in
     (void)hipFree(w.bits); (void)hipFree(w.scale); return -1;
   }
   w.scale64 = scale64;
+  w.maxsc = maxsc > (uint64_t)INT64_MAX ? INT64_MAX : (int64_t)maxsc;
   w.bytes = hb.size() + hs.size();
   w.live = true;
   g_resident_bytes += w.bytes;

@@ -80,3 +80,24 @@ def test_gemm_config3_shape(gpu):
     x = prng.uniform_int(31, 3, (T, K), -(1 << 19), 1 << 19)
     got = gpu.q1_apply_gpu(x, bits, scale, 16)
     assert got is not None and np.array_equal(got, c_oracle.q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("frac", [16, 24, 31])
+def test_gemm_high_dword_epilogue_extremes(gpu, frac):
+    """Scales at +-(2^(frac-1) - 1), the largest the high-dword epilogue takes, with activations at the 3-limb
+    cap and all-one / all-zero bit rows: |S| ~ 2^30 per block, so the 32-bit partial is folded every 2 blocks."""
+    cap3 = 127 * (1 + 256 + 65536)
+    N, nb, T = 48, 32, 72
+    rng = np.random.default_rng(frac)
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    bits[:8] = 0xFF
+    bits[8:16] = 0
+    smax = (1 << (frac - 1)) - 1
+    scale = rng.choice(np.array([smax, -smax, smax - 1, 1], dtype=np.int64), size=(N, nb))
+    scale[:4] = smax
+    scale[8:12] = -smax
+    x = rng.choice(np.array([cap3, -cap3, cap3 - 1, 0], dtype=np.int64), size=(T, nb * 128))
+    x[:16] = cap3
+    x[16:24] = -cap3
+    got = gpu.q1_apply_gpu(x, bits, scale, frac)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, frac))
