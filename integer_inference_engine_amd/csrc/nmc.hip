@@ -15,6 +15,7 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include <string.h>
+#include <stdlib.h>
 #include <algorithm>
 #include <map>
 
@@ -77,12 +78,14 @@ struct Item {               // one weight applied to `count` x rows
 };
 
 // y[yi[p]][o] = floor(W[o] . x[xi[p]] / 2^fw) for the pairs of one item.
+// run_gate (nullable): the launch runs only when *run_gate != 0 (the MFMA path found activations it cannot take)
 __global__ __launch_bounds__(256) void qk_group_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
                                                        const int* __restrict__ yi, const int64_t* __restrict__ X,
                                                        int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
-                                                       int* __restrict__ status) {
+                                                       int* __restrict__ status, const int* __restrict__ run_gate) {
   __shared__ int64_t sx[kXRows][257];
   __shared__ int s_wide;
+  if (run_gate && *run_gate == 0) return;
   const Item it = items[blockIdx.y];
   const int64_t o = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 2);
   if ((int64_t)blockIdx.x * kRows >= it.out_f) return;
@@ -245,12 +248,372 @@ __global__ void qk_combine_kernel(const int64_t* __restrict__ dd, int m, int k, 
   out[idx] = (int64_t)acc;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// int8-MFMA path (v_mfma_i32_16x16x32_i8, tokens in M, weight rows in N, one sub-block per K = 32 step):
+//   prep  : the activation rows' balanced base-256 digit planes xd[l][row][K] (l < kQkLimbs), the sums of every
+//           16 consecutive activations xs16[row][K / 16], and a flag when a row needs more than kQkLimbs limbs
+//   Q4_K  : qdot_j = sum_l 256^l D_l with D_l = MFMA(digits_l(x), q) over sub-block j (32 positions, q in 0..15),
+//           S1 = sum_j sc_j qdot_j, S2 = sum_j m_j xsum_j (int64: |x| <= 127 (256^5 - 1) / 255 keeps
+//           |qdot| < 2^48, |S1| < 2^57, |S2| < 2^53), then acc += dq S1 - dmq S2 (int128) per 256-block
+//   Q6_K  : the same with q6 - 32 as int8, sub-blocks of 16 (two MFMAs per 32 positions, each with the other
+//           sub-block's K groups zeroed in A), no min term (|S1| < 2^59)
+//   y = acc >> fw, refused (status bit 2) outside int64, as the VALU path.
+// MFMA operands: A lane l = token l % 16, K group l / 16 (8 bytes); B lane l = weight row l % 16, K group l / 16;
+// D lane l holds tokens 4 (l / 16) + r of row l % 16.
+// ---------------------------------------------------------------------------------------------------------
+constexpr int kQkLimbs = 5;
+
+__global__ __launch_bounds__(256) void qk_prep_kernel(const int64_t* __restrict__ X, int64_t rows, int64_t K,
+                                                      int8_t* __restrict__ xd, int64_t* __restrict__ xs16,
+                                                      int* __restrict__ Lrow, int* __restrict__ wide) {
+  __shared__ uint64_t s_mx[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t mx = 0;
+  for (int64_t c = tid; c < K; c += 256) {
+    int64_t v = X[r * K + c];
+    const uint64_t a = imie_absu64(v);
+    mx = a > mx ? a : mx;
+#pragma unroll
+    for (int l = 0; l < kQkLimbs; ++l) {
+      const int64_t dg = ((v + 128) & 255) - 128;
+      v = (int64_t)((uint64_t)v - (uint64_t)dg) >> 8;
+      xd[((int64_t)l * rows + r) * K + c] = (int8_t)dg;
+    }
+  }
+  // sums of 16 consecutive activations (thread per group)
+  for (int64_t gq = tid; gq < K / 16; gq += 256) {
+    int64_t sm = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sm = (int64_t)((uint64_t)sm + (uint64_t)X[r * K + 16 * gq + e]);
+    xs16[r * (K / 16) + gq] = sm;
+  }
+  mx = imie_wave_max_u64_full(mx);
+  if (lane == 0) s_mx[wave] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t m = s_mx[0];
+    for (int w = 1; w < 4; ++w) m = s_mx[w] > m ? s_mx[w] : m;
+    const bool fits = m <= imie_balanced_cap(kQkLimbs);
+    Lrow[r] = fits ? imie_limbs_needed(m) : kQkLimbs;
+    if (!fits) atomicOr(wide, 1);
+  }
+}
+
+__global__ void qk_flag_reset_kernel(int* f) { *f = 0; }
+
+__device__ inline v4i mfma32(int64_t a, int64_t b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, c, 0, 0, 0);
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void qk_mfma_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
+                                                      const int* __restrict__ yi, const int8_t* __restrict__ xd,
+                                                      const int64_t* __restrict__ xs16, const int* __restrict__ Lrow,
+                                                      int64_t rows, int64_t K, int64_t* __restrict__ Y, int64_t ldy,
+                                                      int fw, int* __restrict__ status, const int* __restrict__ wide,
+                                                      int dot4_max) {
+  if (*wide) return;                                  // the VALU kernel takes this call
+  const Item it = items[blockIdx.y];
+  if (it.qtype != QT || it.count <= dot4_max) return; // small items: qk_dot4_kernel
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, kg = lane >> 4;
+  const int64_t o = (int64_t)blockIdx.x * 64 + wave * 16 + n;
+  if ((int64_t)blockIdx.x * 64 + wave * 16 >= it.out_f) return;
+  const bool orow = o < it.out_f;
+  constexpr int BS = QT == 0 ? 144 : 210;
+  const uint8_t* wrow = it.w + (orow ? o : 0) * it.nb * BS;
+  const int64_t K16 = K / 16;
+  for (int c0 = 0; c0 < it.count; c0 += 16) {
+    // A rows: token c0 + n of the item (zero past the item's count)
+    const bool arow = c0 + n < it.count;
+    const int64_t xr = arow ? xi[it.first + c0 + n] : 0;
+    int La = arow ? Lrow[xr] : 1;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) { const int t = __shfl_xor(La, off, 64); La = t > La ? t : La; }
+    const int L = La;                                 // limbs of this token tile (wave-uniform)
+    // D rows: tokens c0 + 4 kg + q
+    int64_t drow[4];
+    bool dlive[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dlive[q] = c0 + 4 * kg + q < it.count;
+      drow[q] = dlive[q] ? xi[it.first + c0 + 4 * kg + q] : 0;
+    }
+    i128 acc[4] = {0, 0, 0, 0};
+    for (int64_t b = 0; b < it.nb; ++b) {
+      const uint8_t* blk = wrow + b * BS;
+      int64_t S1[4] = {0, 0, 0, 0}, S2[4] = {0, 0, 0, 0};
+      if (QT == 0) {
+        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const uint8_t* scb = blk + 4;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 qv = *(const uint2*)(blk + 16 + 32 * g + 8 * kg);
+#pragma unroll
+          for (int hi = 0; hi < 2; ++hi) {
+            const int j = 2 * g + hi;
+            const uint32_t b0 = hi ? (qv.x >> 4) & 0x0F0F0F0Fu : qv.x & 0x0F0F0F0Fu;
+            const uint32_t b1 = hi ? (qv.y >> 4) & 0x0F0F0F0Fu : qv.y & 0x0F0F0F0Fu;
+            const int64_t bq = (int64_t)(((uint64_t)b1 << 32) | b0);
+            const int64_t pos = b * 256 + 32 * j + 8 * kg;
+            int64_t qdot[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int l = 0; l < kQkLimbs; ++l) {
+              if (l >= L) break;
+              const int64_t av = arow ? *(const int64_t*)(xd + ((int64_t)l * rows + xr) * K + pos) : 0;
+              const v4i d = mfma32(av, bq, v4i{0, 0, 0, 0});
+#pragma unroll
+              for (int q = 0; q < 4; ++q) qdot[q] += (int64_t)d[q] << (8 * l);
+            }
+            int sc, mn;
+            if (j < 4) { sc = scb[j] & 63; mn = scb[j + 4] & 63; }
+            else { sc = (scb[j + 4] & 0xF) | ((scb[j - 4] >> 6) << 4); mn = (scb[j + 4] >> 4) | ((scb[j] >> 6) << 4); }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int64_t xs = xs16[drow[q] * K16 + (b * 256 + 32 * j) / 16] + xs16[drow[q] * K16 + (b * 256 + 32 * j) / 16 + 1];
+              S1[q] += (int64_t)sc * qdot[q];
+              S2[q] += (int64_t)mn * xs;
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] += (i128)dq * S1[q] - (i128)dmq * S2[q];
+      } else {
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* scs = (const int8_t*)(blk + 192);
+        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            // 32 positions 128 half + 32 qq + (0..31): lane K group kg takes 8 kg .. 8 kg + 7 (sub-block is = kg / 2)
+            const uint2 lv = *(const uint2*)(ql + 64 * half + ((qq & 1) ? 32 : 0) + 8 * kg);
+            const uint2 hv = *(const uint2*)(qh + 32 * half + 8 * kg);
+            const int sl = qq >= 2 ? 4 : 0, sh = 2 * qq;
+            uint32_t v0 = ((lv.x >> sl) & 0x0F0F0F0Fu) | (((hv.x >> sh) & 0x03030303u) << 4);
+            uint32_t v1 = ((lv.y >> sl) & 0x0F0F0F0Fu) | (((hv.y >> sh) & 0x03030303u) << 4);
+            v0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise q6 - 32 as int8
+            v1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            const int64_t bq = (int64_t)(((uint64_t)v1 << 32) | v0);
+            const int64_t pos = b * 256 + 128 * half + 32 * qq + 8 * kg;
+            int64_t qd0[4] = {0, 0, 0, 0}, qd1[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int l = 0; l < kQkLimbs; ++l) {
+              if (l >= L) break;
+              const int64_t av = arow ? *(const int64_t*)(xd + ((int64_t)l * rows + xr) * K + pos) : 0;
+              const v4i d0 = mfma32(kg < 2 ? av : 0, bq, v4i{0, 0, 0, 0});
+              const v4i d1 = mfma32(kg < 2 ? 0 : av, bq, v4i{0, 0, 0, 0});
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                qd0[q] += (int64_t)d0[q] << (8 * l);
+                qd1[q] += (int64_t)d1[q] << (8 * l);
+              }
+            }
+            const int s0 = scs[8 * half + 2 * qq], s1 = scs[8 * half + 2 * qq + 1];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) S1[q] += (int64_t)s0 * qd0[q] + (int64_t)s1 * qd1[q];
+          }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] += (i128)dq * S1[q];
+      }
+    }
+    if (orow) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!dlive[q]) continue;
+        const i128 y = acc[q] >> fw;
+        if (y > (i128)INT64_MAX || y < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+        Y[(int64_t)yi[it.first + c0 + 4 * kg + q] * ldy + o] = (int64_t)y;
+      }
+    }
+  }
+}
+
+// v_dot4_i32_i8 path for items with few tokens (the MoE experts: ~4 tokens each), every token of the item once
+// (no 16-row MFMA padding). Workgroup = (item, 64 weight rows); thread = (row, quarter q of each 256-block):
+//   Q4_K: q covers qs bytes 32 q .. 32 q + 31, i.e. sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles)
+//   Q6_K: q = (half, pair of quarters qq): sub-blocks 8 half + 2 qq + is for qq in {2 (q & 1), 2 (q & 1) + 1}
+// The weights are expanded to int8 once per block; per token and limb, 16 dot4s give the sub-block dot products.
+// The 256-block's digits of up to 8 tokens are staged in LDS. Partial int128 sums of the 4 quarter-threads of a
+// row are added by shuffles at the end (integer addition: order-free).
+constexpr int kDotTok = 8;
+
+__device__ inline i128 shfl_xor_i128(i128 v, int m) {
+  const uint64_t lo = (uint64_t)v, hi = (uint64_t)((unsigned __int128)v >> 64);
+  const uint64_t lo2 = (uint64_t)__shfl_xor((long long)lo, m, 64), hi2 = (uint64_t)__shfl_xor((long long)hi, m, 64);
+  return (i128)(((unsigned __int128)hi2 << 64) | lo2);
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
+                                                      const int* __restrict__ yi, const int8_t* __restrict__ xd,
+                                                      const int64_t* __restrict__ xs16, const int* __restrict__ Lrow,
+                                                      int64_t rows, int64_t K, int64_t* __restrict__ Y, int64_t ldy,
+                                                      int fw, int* __restrict__ status, const int* __restrict__ wide,
+                                                      int maxcount) {
+  __shared__ __align__(16) int8_t sx[kQkLimbs][kDotTok][256];
+  __shared__ int64_t sxs[kDotTok][16];
+  __shared__ int s_L;
+  if (*wide) return;
+  const Item it = items[blockIdx.y];
+  if (it.qtype != QT || it.count > maxcount) return;
+  const int tid = threadIdx.x, q = tid & 3;
+  const int64_t o = (int64_t)blockIdx.x * 64 + (tid >> 2);
+  if ((int64_t)blockIdx.x * 64 >= it.out_f) return;
+  const bool orow = o < it.out_f;
+  constexpr int BS = QT == 0 ? 144 : 210;
+  const uint8_t* wrow = it.w + (orow ? o : 0) * it.nb * BS;
+  const int64_t K16 = K / 16;
+  for (int t0 = 0; t0 < it.count; t0 += kDotTok) {
+    const int tn = min(kDotTok, it.count - t0);
+    if (tid == 0) {
+      int L = 1;
+      for (int t = 0; t < tn; ++t) { const int lr = Lrow[xi[it.first + t0 + t]]; L = lr > L ? lr : L; }
+      s_L = L;
+    }
+    __syncthreads();
+    const int L = s_L;
+    i128 acc[kDotTok];
+#pragma unroll
+    for (int t = 0; t < kDotTok; ++t) acc[t] = 0;
+    for (int64_t b = 0; b < it.nb; ++b) {
+      // stage the block's digits (L limbs x tn tokens x 256 bytes, 16 B per thread-step) and 16-sums
+      for (int i = tid; i < L * tn * 16; i += 256) {
+        const int l = i / (tn * 16), rem = i % (tn * 16), t = rem >> 4, c = rem & 15;
+        const int64_t xr = xi[it.first + t0 + t];
+        *(uint4*)&sx[l][t][16 * c] = *(const uint4*)(xd + ((int64_t)l * rows + xr) * K + b * 256 + 16 * c);
+      }
+      if (tid < tn * 16) {
+        const int t = tid >> 4, c = tid & 15;
+        sxs[t][c] = xs16[(int64_t)xi[it.first + t0 + t] * K16 + b * 16 + c];
+      }
+      __syncthreads();
+      const uint8_t* blk = wrow + b * BS;
+      if (QT == 0) {
+        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const uint8_t* scb = blk + 4;
+        const uint4 qa = *(const uint4*)(blk + 16 + 32 * q), qb = *(const uint4*)(blk + 32 + 32 * q);
+        const uint32_t qd[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        int wl[8], wh[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) { wl[d] = (int)(qd[d] & 0x0F0F0F0Fu); wh[d] = (int)((qd[d] >> 4) & 0x0F0F0F0Fu); }
+        int sc[2], mn[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int j = 2 * q + h;
+          if (j < 4) { sc[h] = scb[j] & 63; mn[h] = scb[j + 4] & 63; }
+          else { sc[h] = (scb[j + 4] & 0xF) | ((scb[j - 4] >> 6) << 4); mn[h] = (scb[j + 4] >> 4) | ((scb[j] >> 6) << 4); }
+        }
+#pragma unroll
+        for (int t = 0; t < kDotTok; ++t) {
+          if (t >= tn) break;
+          int64_t qlo = 0, qhi = 0;
+          for (int l = 0; l < L; ++l) {
+            const int* xl = (const int*)&sx[l][t][64 * q];
+            const int* xh = (const int*)&sx[l][t][64 * q + 32];
+            int al = 0, ah = 0;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+              al = __builtin_amdgcn_sdot4(xl[d], wl[d], al, false);
+              ah = __builtin_amdgcn_sdot4(xh[d], wh[d], ah, false);
+            }
+            qlo += (int64_t)al << (8 * l);
+            qhi += (int64_t)ah << (8 * l);
+          }
+          const int64_t S1 = (int64_t)sc[0] * qlo + (int64_t)sc[1] * qhi;
+          const int64_t S2 = (int64_t)mn[0] * (sxs[t][4 * q] + sxs[t][4 * q + 1]) +
+                             (int64_t)mn[1] * (sxs[t][4 * q + 2] + sxs[t][4 * q + 3]);
+          acc[t] += (i128)dq * S1 - (i128)dmq * S2;
+        }
+      } else {
+        const int half = q >> 1, qq0 = 2 * (q & 1);
+        const uint8_t* ql = blk + 64 * half;
+        const uint8_t* qh = blk + 128 + 32 * half;
+        const int8_t* scs = (const int8_t*)(blk + 192);
+        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+        const uint4 l0 = *(const uint4*)ql, l1 = *(const uint4*)(ql + 16), l2 = *(const uint4*)(ql + 32),
+                    l3 = *(const uint4*)(ql + 48);
+        const uint4 h0 = *(const uint4*)qh, h1 = *(const uint4*)(qh + 16);
+        const uint32_t lq[16] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w, l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w};
+        const uint32_t hq[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const int sl = (q & 1) ? 4 : 0;
+        int w[2][8];                                  // [qq - qq0][dword of the 32 positions]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int qq = qq0 + u;
+#pragma unroll
+          for (int d = 0; d < 8; ++d) {
+            uint32_t v = ((lq[((qq & 1) ? 8 : 0) + d] >> sl) & 0x0F0F0F0Fu) | (((hq[d] >> (2 * qq)) & 0x03030303u) << 4);
+            v = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise q6 - 32 as int8
+            w[u][d] = (int)v;
+          }
+        }
+        int sc[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int is = 0; is < 2; ++is) sc[u][is] = scs[8 * half + 2 * (qq0 + u) + is];
+#pragma unroll
+        for (int t = 0; t < kDotTok; ++t) {
+          if (t >= tn) break;
+          int64_t qs4[2][2] = {{0, 0}, {0, 0}};
+          for (int l = 0; l < L; ++l) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int* xp = (const int*)&sx[l][t][128 * half + 32 * (qq0 + u)];
+              int a0 = 0, a1 = 0;
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                a0 = __builtin_amdgcn_sdot4(xp[d], w[u][d], a0, false);
+                a1 = __builtin_amdgcn_sdot4(xp[4 + d], w[u][4 + d], a1, false);
+              }
+              qs4[u][0] += (int64_t)a0 << (8 * l);
+              qs4[u][1] += (int64_t)a1 << (8 * l);
+            }
+          }
+          const int64_t S1 = (int64_t)sc[0][0] * qs4[0][0] + (int64_t)sc[0][1] * qs4[0][1] +
+                             (int64_t)sc[1][0] * qs4[1][0] + (int64_t)sc[1][1] * qs4[1][1];
+          acc[t] += (i128)dq * S1;
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int t = 0; t < kDotTok; ++t) {
+      if (t >= tn) break;
+      i128 v = acc[t];
+      v += shfl_xor_i128(v, 1);
+      v += shfl_xor_i128(v, 2);
+      if (q == 0 && orow) {
+        const i128 y = v >> fw;
+        if (y > (i128)INT64_MAX || y < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
+        Y[(int64_t)yi[it.first + t0 + t] * ldy + o] = (int64_t)y;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// int8-MFMA path on/off (IMIE_QK_MFMA=0 forces the VALU kernel; tests compare both)
+bool qk_mfma_enabled() {
+  static const bool v = [] { const char* e = getenv("IMIE_QK_MFMA"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
 const QKWeight* qk_get(int64_t h) {
   if (h < 0 || h >= (int64_t)g_qk.size() || !g_qk[(size_t)h].p) return nullptr;
   return &g_qk[(size_t)h];
 }
 
-// Enqueue a set of items over device X (rows x K) into device Y (rows x ldy). pairs: host arrays.
+// Enqueue a set of items over device X (rows x K) into device Y (rows x ldy). pairs: host arrays. The int8-MFMA
+// kernels run unless an activation row needs more than kQkLimbs limbs (or K is not a multiple of 256); then the
+// exact VALU kernel does (both are enqueued, a device flag selects).
+struct QkPrepWs {
+  DevBuf xd, xs, lr, flag;
+} g_qprep;
+
 int run_items(const std::vector<Item>& items, const std::vector<int>& xi, const std::vector<int>& yi,
               const int64_t* X, int64_t K, int64_t* Y, int64_t ldy, int fw, int* status, hipStream_t st,
               DevBuf& ibuf, DevBuf& pbuf) {
@@ -262,10 +625,41 @@ int run_items(const std::vector<Item>& items, const std::vector<int>& xi, const 
   IMIE_HIP(hipMemcpyAsync((int*)pbuf.p + np, yi.data(), np * 4, hipMemcpyHostToDevice, st));
   int64_t maxo = 0;
   for (auto& it : items) maxo = it.out_f > maxo ? it.out_f : maxo;
+  int64_t rows = 0;
+  for (int r : xi) rows = r + 1 > rows ? r + 1 : rows;
+  const bool mfma_ok = K % 256 == 0 && qk_mfma_enabled();
+  const int* gate = nullptr;
   imie_prof_mark(IMIE_K_QK, st, true);
+  if (mfma_ok) {
+    if (g_qprep.xd.ensure((size_t)(kQkLimbs * rows * K)) || g_qprep.xs.ensure((size_t)(rows * (K / 16)) * 8) ||
+        g_qprep.lr.ensure((size_t)rows * 4) || g_qprep.flag.ensure(64))
+      return IMIE_EARG;
+    int* flag = (int*)g_qprep.flag.p;
+    hipLaunchKernelGGL(qk_flag_reset_kernel, dim3(1), dim3(1), 0, st, flag);
+    hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)rows), dim3(256), 0, st, X, rows, K, (int8_t*)g_qprep.xd.p,
+                       (int64_t*)g_qprep.xs.p, (int*)g_qprep.lr.p, flag);
+    const dim3 grid((unsigned)((maxo + 63) / 64), (unsigned)items.size());
+    constexpr int kDot4Max = 32;                      // items with at most this many tokens take the dot4 kernel
+    bool q4s = false, q6s = false, q4b = false, q6b = false;
+    for (auto& it : items) {
+      const bool small = it.count <= kDot4Max;
+      q4s = q4s || (it.qtype == 0 && small); q6s = q6s || (it.qtype == 1 && small);
+      q4b = q4b || (it.qtype == 0 && !small); q6b = q6b || (it.qtype == 1 && !small);
+    }
+    const Item* ip = (const Item*)ibuf.p;
+    const int *xip = (const int*)pbuf.p, *yip = (const int*)pbuf.p + np;
+    const int8_t* xdp = (const int8_t*)g_qprep.xd.p;
+    const int64_t* xsp = (const int64_t*)g_qprep.xs.p;
+    const int* lrp = (const int*)g_qprep.lr.p;
+    if (q4s) hipLaunchKernelGGL(qk_dot4_kernel<0>, grid, dim3(256), 0, st, ip, xip, yip, xdp, xsp, lrp, rows, K, Y, ldy, fw, status, flag, kDot4Max);
+    if (q6s) hipLaunchKernelGGL(qk_dot4_kernel<1>, grid, dim3(256), 0, st, ip, xip, yip, xdp, xsp, lrp, rows, K, Y, ldy, fw, status, flag, kDot4Max);
+    if (q4b) hipLaunchKernelGGL(qk_mfma_kernel<0>, grid, dim3(256), 0, st, ip, xip, yip, xdp, xsp, lrp, rows, K, Y, ldy, fw, status, flag, kDot4Max);
+    if (q6b) hipLaunchKernelGGL(qk_mfma_kernel<1>, grid, dim3(256), 0, st, ip, xip, yip, xdp, xsp, lrp, rows, K, Y, ldy, fw, status, flag, kDot4Max);
+    gate = flag;
+  }
   hipLaunchKernelGGL(qk_group_kernel, dim3((unsigned)((maxo + kRows - 1) / kRows), (unsigned)items.size()),
                      dim3(256), 0, st, (const Item*)ibuf.p, (const int*)pbuf.p, (const int*)pbuf.p + np, X, K, Y,
-                     ldy, fw, status);
+                     ldy, fw, status, gate);
   imie_prof_mark(IMIE_K_QK, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;

@@ -16,7 +16,11 @@ def qkg():
 
 
 @pytest.mark.parametrize("qtype,out_f,nb,T,xmag", [(0, 33, 2, 1, 16), (1, 70, 3, 5, 16), (0, 128, 8, 17, 30),
-                                                   (1, 64, 1, 3, 55), (0, 5, 1, 2, 62)])
+                                                   (1, 64, 1, 3, 55), (0, 5, 1, 2, 62),
+                                                   # int8-MFMA path: token tiles of 16 with ragged tails, 1..5
+                                                   # limbs, and 2^39 (beyond 5 limbs: the VALU kernel takes over)
+                                                   (0, 96, 4, 40, 30), (1, 80, 2, 33, 36), (0, 16, 1, 16, 38),
+                                                   (1, 48, 2, 7, 39), (0, 200, 3, 1, 6), (1, 130, 1, 18, 20)])
 def test_qk_linear_matches_oracle(qkg, qtype, out_f, nb, T, xmag):
     raw = qk.random_blocks(out_f, qtype, out_f, nb, qtype)
     x = prng.uniform_int(xmag, T, (T, nb * 256), -(1 << xmag), 1 << xmag)
