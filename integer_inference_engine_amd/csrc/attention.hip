@@ -1221,6 +1221,76 @@ __global__ __launch_bounds__(256) void pf_softmax8_kernel(AttnDesc d) {
   }
 }
 
+// The same softmax with one wave per row (4 rows per workgroup) for rows of at most 64 * kSmPer keys: e_j stay in
+// registers between the Z sum and the p pass, every reduction is a whole-wave DPP one (no barriers, no LDS).
+constexpr int kSmPer = 32;
+__global__ __launch_bounds__(256) void pf_softmax8_wave_kernel(AttnDesc d) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t rows = d.B * d.H * d.M;
+  if (r >= rows) return;                              // whole wave
+  const RowInfo ri = row_info(d, r);
+  const int64_t bkv = ri.b * d.Hkv + ri.kv;
+  if (lane == 0) {
+    const u128 qk = (u128)d.maxq[r] * d.run_k[bkv];
+    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+  }
+  const int64_t nkt = (ri.lv + kPfKeys - 1) / kPfKeys;
+  // row max over the score kernel's per-256-key maxima (a set that may not contain 0: offset by INT64_MIN so the
+  // unsigned maximum of the shifted values is the signed maximum)
+  uint64_t mo = 0;
+  for (int64_t kt = lane; kt < nkt; kt += 64) {
+    const uint64_t v = (uint64_t)d.pmax[kt * rows + r] ^ 0x8000000000000000ull;
+    mo = v > mo ? v : mo;
+  }
+  const int64_t m = (int64_t)(imie_wave_max_u64_full(mo) ^ 0x8000000000000000ull);
+  const int64_t* s = d.scores + r * d.Lmax;
+  int64_t e[kSmPer];
+  uint64_t z = 0;
+#pragma unroll
+  for (int i = 0; i < kSmPer; ++i) {
+    const int64_t j = lane + 64 * i;
+    e[i] = 0;
+    if (j < ri.lv) {
+      int64_t dd = (int64_t)((uint64_t)m - (uint64_t)s[j]);
+      if (dd > d.dclip) dd = d.dclip;
+      e[i] = exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+      z += (uint64_t)e[i];
+    }
+  }
+  const uint64_t Z = imie_wave_sum_u64_full(z);
+  const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
+  const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
+  uint64_t mp = 0;
+#pragma unroll
+  for (int i = 0; i < kSmPer; ++i) {
+    const int64_t j = lane + 64 * i;
+    if (j >= ri.lv) continue;
+    int64_t p = 0;
+    if (Z != 0) {
+      const uint64_t num = (uint64_t)e[i] << d.frac;
+      if (Z == 1) p = (int64_t)num;
+      else {
+        uint64_t qq = __umul64hi(num, rz);
+        uint64_t rem = num - qq * Z;
+        while (rem >= Z) { ++qq; rem -= Z; }
+        p = (int64_t)qq;
+      }
+    }
+    mp = (uint64_t)p > mp ? (uint64_t)p : mp;
+    int64_t x = p;
+#pragma unroll
+    for (int lp = 0; lp < 4; ++lp) {                  // Lp <= 4 (frac <= 29)
+      if (lp >= Lp) break;
+      const int64_t dg = ((x + 128) & 255) - 128;
+      x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+      d.pd[((int64_t)lp * rows + r) * d.pdL + j] = (int8_t)dg;
+    }
+  }
+  mp = imie_wave_max_u64_full(mp);
+  if (lane == 0) d.maxp[r] = mp;
+}
+
 // Prefill PV (kv8) + final: workgroup = (b, kv, 16 group rows); wave w owns dim tiles w and w + 4. Per 64-key
 // step: A = p digit plane lp of the 16 rows (keys past a row's causal limit masked to 0), B = V digit plane b;
 // T_e (e = lp + b) in int32, folded into int64 every 4096 keys (|T_e| < 2^27 before a fold).
@@ -1443,7 +1513,10 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
     const int64_t nrt16 = (grows + 15) / 16, nkt8 = (d.Lmax + kPfKeys - 1) / kPfKeys;
     hipLaunchKernelGGL(pf_scores8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16), (unsigned)nkt8), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(pf_softmax8_kernel, dim3((unsigned)rows), dim3(256), 0, st, d);
+    if (d.Lmax <= 64 * kSmPer)
+      hipLaunchKernelGGL(pf_softmax8_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, d);
+    else
+      hipLaunchKernelGGL(pf_softmax8_kernel, dim3((unsigned)rows), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
     hipLaunchKernelGGL(pf_pv8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16)), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
