@@ -1382,6 +1382,120 @@ __global__ __launch_bounds__(256) void pf_pv8_kernel(AttnDesc d) {
   }
 }
 
+// Prefill PV (kv8), 64 group rows per workgroup: 8 waves, wave w owns dim tile w (16 dims). The p digits of the
+// 64 rows x 64 keys of a step are staged once in LDS (keys past a row's causal limit zeroed); each wave's V
+// loads (4 digit planes of its 16 dims) serve all 4 row tiles and all Lp limbs. T_e (e = lp + b) in int32 per row
+// tile, folded into int64 every 64 steps (|T_e| < 2^28 before a fold).
+constexpr int kPvRows = 64;
+__global__ __launch_bounds__(512) void pf_pv8w_kernel(AttnDesc d) {
+  __shared__ __align__(16) int8_t sA[4][kPvRows][64];
+  __shared__ int64_t s_vis;
+  const int64_t rep = d.H / d.Hkv, grows = rep * d.M;
+  const int64_t nrt = (grows + kPvRows - 1) / kPvRows;
+  const int64_t bkv = imie_udiv32(blockIdx.x, nrt), rt = imie_umod32(blockIdx.x, nrt);
+  const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
+  const int64_t rows = d.B * d.H * d.M;
+  const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  if (blockIdx.x == 0 && tid == 0) check_rope_guard(d);
+  // staging role: thread -> (row sr, 8-key chunk sc)
+  const int sr = tid >> 3, sc = tid & 7;
+  const int64_t sgr = rt * kPvRows + sr;
+  const bool srow = sgr < grows;
+  const int64_t sar = srow ? group_row(d, b, kv, sgr) : 0;
+  const int64_t salv = srow ? (d.starts ? d.starts[b] + imie_umod32(sgr, d.M) + 1 : len) : 0;
+  if (tid == 0) s_vis = 0;
+  __syncthreads();
+  if (sc == 0 && salv > 0) atomicMax((unsigned long long*)&s_vis, (unsigned long long)salv);
+  __syncthreads();
+  const int64_t vismax = s_vis;
+  const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
+  const int DT = (int)(d.hd / 16);
+  const bool wt = wave < DT;
+  v4i T[4][7];
+  uint64_t O[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int e = 0; e < 7; ++e) T[i][e] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) O[i][r] = 0;
+  }
+  auto fold = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 7; ++e) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[i][r] += (uint64_t)(int64_t)T[i][e][r] << (8 * e);
+        T[i][e] = v4i{0, 0, 0, 0};
+      }
+  };
+  const int8_t* Vb = (const int8_t*)d.V;
+  int steps = 0;
+  for (int64_t t0 = 0; t0 < vismax; t0 += 64) {
+    // stage the p digits (masked past each row's visible length)
+    {
+      const int nvis = (int)max((int64_t)0, min((int64_t)8, salv - (t0 + 8 * sc)));
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp) {
+        if (lp >= Lp) break;
+        uint2 v = uint2{0, 0};
+        if (nvis > 0) v = *(const uint2*)(d.pd + ((int64_t)lp * rows + sar) * d.pdL + t0 + 8 * sc);
+        const uint32_t m0 = nvis >= 4 ? 0xFFFFFFFFu : ((1u << (8 * nvis)) - 1u);
+        const uint32_t m1 = nvis >= 8 ? 0xFFFFFFFFu : (nvis <= 4 ? 0u : ((1u << (8 * (nvis - 4))) - 1u));
+        v.x &= m0;
+        v.y &= m1;
+        *(uint2*)&sA[lp][sr][8 * sc] = v;
+      }
+    }
+    __syncthreads();
+    if (wt) {
+      int64_t pi, slot0;
+      page_split(d, t0, pi, slot0);
+      const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+      const int64_t c = 16 * wave + m;
+      v4i bv[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) bv[db] = *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, c, d.hd, d.P));
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp) {
+        if (lp >= Lp) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v4i a = *(const v4i*)&sA[lp][16 * i + m][16 * g];
+#pragma unroll
+          for (int db = 0; db < 4; ++db) T[i][lp + db] = mfma8(a, bv[db], T[i][lp + db]);
+        }
+      }
+    }
+    if (++steps == 64) { fold(); steps = 0; }
+    __syncthreads();                                  // the stage is consumed
+  }
+  if (!wt) return;
+  fold();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t gr = rt * kPvRows + 16 * i + 4 * g + r;
+      if (gr >= grows) continue;
+      const int64_t row = group_row(d, b, kv, gr);
+      d.out[qoff(d, row) + 16 * wave + m] = (int64_t)O[i][r] >> d.frac;
+      if (wave == 0 && m == 0) {
+        const int64_t lv = d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len;
+        const u128 pv = (u128)d.maxp[row] * d.run_v[bkv];
+        if (pv > (u128)(INT64_MAX / lv)) atomicOr(d.status, IMIE_EOVF);
+      }
+    }
+}
+
+// prefill PV with 64-row workgroups (IMIE_PV_WIDE=0 selects the 16-row kernel; tuning and tests)
+bool pv_wide() {
+  static const bool v = [] { const char* e = getenv("IMIE_PV_WIDE"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
 // decode chunking: ~2048 workgroups over the (b, kv) groups, chunks of >= 64 keys (multiple of 64)
 void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t* nch) {
   static const int64_t target = [] {               // workgroups to aim for (IMIE_DEC_WGS overrides, tuning)
@@ -1518,7 +1632,11 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
     else
       hipLaunchKernelGGL(pf_softmax8_kernel, dim3((unsigned)rows), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(pf_pv8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16)), dim3(256), 0, st, d);
+    if (d.hd <= 128 && pv_wide())
+      hipLaunchKernelGGL(pf_pv8w_kernel, dim3((unsigned)(d.B * d.Hkv * ((grows + kPvRows - 1) / kPvRows))), dim3(512), 0,
+                         st, d);
+    else
+      hipLaunchKernelGGL(pf_pv8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16)), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
     imie_prof_mark(IMIE_K_ATTN, st, false);
     return IMIE_OK;
