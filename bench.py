@@ -204,7 +204,8 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
     """Config 3: one Bonsai-8B-shape decoder layer in prefill over a T-token prompt (causal attention over all T
     positions, int32 paged KV). Seeded random Q1_0 weights and activations; timed on one stream with HIP events.
     The Q1 projections run as int8-MFMA GEMMs (tokens in M); `q1_gemm_alg_TOPS` counts 2*T*N*K ops of the
-    projections over the GEMM kernels' time (each +-1 weight times an int64 activation counted as one MAC)."""
+    projections over the GEMM kernels' time (each +-1 weight times an int64 activation counted as one MAC);
+    `q1_gemm_mfma_util` counts the int8 MFMA ops the kernels executed (one MAC per limb)."""
     from integer_inference_engine_amd import gpu_native as gn
     from integer_inference_engine_amd.resident import ResidentNet
     from integer_inference_engine_amd.rope_tables import bonsai8b_tables
@@ -229,12 +230,15 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     x.copy_(x0)
     net.stream.synchronize()
+    gops = ctypes.c_ulonglong()
+    so.imie_profile_gemm_ops(ctypes.byref(gops), 1)
     so.imie_profile_begin()
     e0.record(net.stream)
     st = net.forward(x, [0], T)
     e1.record(net.stream)
     net.stream.synchronize()
     ms = e0.elapsed_time(e1)
+    so.imie_profile_gemm_ops(ctypes.byref(gops), 1)
     prof = {}
     for kid, name in ((0, "q1_prep"), (2, "q1_gemm"), (3, "attention")):
         kms, kcnt = ctypes.c_double(), ctypes.c_int64()
@@ -247,7 +251,11 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
     gemm_ms = prof["q1_gemm_ms"]
     return {"tokens": T, "layer_ms": round(ms, 3), "tok_s": round(T / (ms / 1e3), 1), "status": int(st),
             "q1_gemm_alg_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1) if gemm_ms > 0 else None,
-            "q1_gemm_frac_of_int8_peak": round(ops / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None, **prof}
+            "q1_gemm_frac_of_int8_peak": round(ops / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None,
+            # executed int8 MFMA ops (2*M*N*K per limb the kernels ran, counted on the device from the limb
+            # tables, padding tiles included) over the GEMM kernels' time: utilisation of the 5.0 POPS peak
+            "q1_gemm_mfma_ops": int(gops.value), "q1_gemm_mean_limbs": round(gops.value / ops, 3) if ops else None,
+            "q1_gemm_mfma_util": round(gops.value / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None, **prof}
 
 
 def moe_leg(so, torch, E: int = 128, k: int = 8, d: int = 2048, e_ffn: int = 768, T: int = 64) -> dict:

@@ -28,6 +28,9 @@ int imie_synchronize(void);
  * 2 q1 GEMM, 3 attention, 4 Q4_K/Q6_K linear); read synchronizes. */
 void imie_profile_begin(void);
 int imie_profile_read(int kernel, double *total_ms, int64_t *count);
+/* Executed int8 MFMA ops of the Q1 GEMM launches (prefill) recorded while profiling is on, counted on the device
+ * from the limb tables (synchronizes); reset != 0 clears the counter. No reference counterpart (measurement). */
+int imie_profile_gemm_ops(unsigned long long *ops, int reset);
 void imie_profile_end(void);
 /* one int8 MFMA over per-lane operands (A, B: 64x16 int8, D: 64x4 int32); pins the lane mapping in tests. */
 int imie_probe_mfma(const int8_t *a, const int8_t *b, int32_t *d);

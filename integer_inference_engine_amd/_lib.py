@@ -24,6 +24,7 @@ SIGNATURES = {
     "imie_synchronize": (c_int, []),
     "imie_probe_mfma": (c_int, [c_void_p, c_void_p, c_void_p]),
     "imie_profile_begin": (None, []),
+    "imie_profile_gemm_ops": (c_int, [c_void_p, c_int]),
     "imie_profile_read": (c_int, [c_int, c_void_p, c_void_p]),
     "imie_profile_end": (None, []),
     # Q1_0 linear

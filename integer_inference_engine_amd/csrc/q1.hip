@@ -60,6 +60,19 @@ struct Workspace {
 }  // namespace
 
 // Host repack: natural (N, nb, 16) bits + (N, nb) scales -> tiled layout. Exposed for CPU tests.
+static DevBuf g_gemm_ops;   // executed GEMM int8 MFMA ops while profiling (gemm_opcount_kernel)
+
+// Executed int8 MFMA ops of the GEMM launches recorded while profiling (synchronizes); reset != 0 clears.
+extern "C" int imie_profile_gemm_ops(unsigned long long* ops, int reset) {
+  if (!ops) return IMIE_EARG;
+  *ops = 0;
+  if (g_gemm_ops.ensure(64)) return IMIE_EARG;
+  IMIE_HIP(hipDeviceSynchronize());
+  IMIE_HIP(hipMemcpy(ops, g_gemm_ops.p, 8, hipMemcpyDeviceToHost));
+  if (reset) IMIE_HIP(hipMemset(g_gemm_ops.p, 0, 8));
+  return IMIE_OK;
+}
+
 extern "C" int imie_q1_repack_host(const uint8_t* bits, const int64_t* scale, int64_t N, int64_t nb,
                                    int scale64, uint8_t* bitsT, void* scaleT) {
   if (!bits || !scale || !bitsT || !scaleT || N <= 0 || nb <= 0) return IMIE_EARG;
@@ -807,6 +820,20 @@ __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
     }
 }
 
+// Executed int8 MFMA ops of one GEMM launch pair (profiling only): per (token tile, slab) the limb count the
+// kernels use (max over the tile's tokens) x the slab's blocks x the output tiles x 64 MFMAs of 2*16*16*64 ops.
+__global__ void gemm_opcount_kernel(const int* __restrict__ lt, int64_t T, int64_t nslabs, int64_t nb, int64_t nto,
+                                    unsigned long long* __restrict__ ops) {
+  const int64_t tt = blockIdx.x;
+  unsigned long long sum = 0;
+  for (int64_t sl = threadIdx.x; sl < nslabs; sl += blockDim.x) {
+    int lw = 0;
+    for (int64_t t = tt * 64; t < min(T, tt * 64 + 64); ++t) lw = lt[t * nslabs + sl] > lw ? lt[t * nslabs + sl] : lw;
+    const int64_t blocks = min((int64_t)kSlabBlocks, nb - sl * kSlabBlocks);
+    sum += (unsigned long long)(nto * blocks * lw) * 64ull * 32768ull;
+  }
+  if (sum) atomicAdd(ops, sum);
+}
 // narrow GEMM LDS buffering (IMIE_GEMM_NBUF = 1 or 2 overrides; tuning)
 static int gemm_nbuf() {
   static const int v = [] {
@@ -872,6 +899,15 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     IMIE_HIP(hipGetLastError());
   }
   imie_prof_mark(IMIE_K_Q1_GEMM, st, false);
+  if (imie_prof_on() && !imie_prof_suspend(true)) {   // count outside the timed window
+    imie_prof_suspend(false);
+    if (!g_gemm_ops.ensure(64)) {
+      for (int i = 0; i < cnt; ++i)
+        hipLaunchKernelGGL(gemm_opcount_kernel, dim3((unsigned)((T + 63) / 64)), dim3(64), 0, st, (const int*)wk.lslab.p,
+                           T, nslabs, w0.nb, (ws[i]->N + 127) / 128, (unsigned long long*)g_gemm_ops.p);
+      IMIE_HIP(hipGetLastError());
+    }
+  }
   return IMIE_OK;
 }
 
