@@ -249,13 +249,19 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
     so.bonsai_q1_free_weights()
     ops = 2 * T * sum(o * i for o, i in shapes.values())
     gemm_ms = prof["q1_gemm_ms"]
+    peak = ctypes.c_double()                          # measured sustained int8 MFMA ops/s of this device
+    mpeak = peak.value if so.imie_mfma_peak(ctypes.byref(peak)) == 0 and peak.value > 0 else None
     return {"tokens": T, "layer_ms": round(ms, 3), "tok_s": round(T / (ms / 1e3), 1), "status": int(st),
             "q1_gemm_alg_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1) if gemm_ms > 0 else None,
             "q1_gemm_frac_of_int8_peak": round(ops / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None,
             # executed int8 MFMA ops (2*M*N*K per limb the kernels ran, counted on the device from the limb
             # tables, padding tiles included) over the GEMM kernels' time: utilisation of the 5.0 POPS peak
             "q1_gemm_mfma_ops": int(gops.value), "q1_gemm_mean_limbs": round(gops.value / ops, 3) if ops else None,
-            "q1_gemm_mfma_util": round(gops.value / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None, **prof}
+            "q1_gemm_mfma_util": round(gops.value / (gemm_ms / 1e3) / 5.0e15, 4) if gemm_ms > 0 else None,
+            # the same against the measured sustained MFMA throughput (imie_mfma_peak), when that is lower
+            "int8_mfma_measured_peak_POPS": round(mpeak / 1e15, 3) if mpeak else None,
+            "q1_gemm_mfma_util_measured_peak": (round(gops.value / (gemm_ms / 1e3) / mpeak, 4)
+                                                if mpeak and gemm_ms > 0 else None), **prof}
 
 
 def moe_leg(so, torch, E: int = 128, k: int = 8, d: int = 2048, e_ffn: int = 768, T: int = 64) -> dict:

@@ -34,6 +34,9 @@ int imie_profile_gemm_ops(unsigned long long *ops, int reset);
 void imie_profile_end(void);
 /* one int8 MFMA over per-lane operands (A, B: 64x16 int8, D: 64x4 int32); pins the lane mapping in tests. */
 int imie_probe_mfma(const int8_t *a, const int8_t *b, int32_t *d);
+/* Sustained int8 MFMA throughput of the device in ops/s (8 independent 16x16x64 chains per wave, 4 waves per
+ * SIMD, HIP events). No reference counterpart (measurement: the measured peak the prefill GEMM is quoted against). */
+int imie_mfma_peak(double *ops_per_s);
 
 /* ---- packed Q1_0 linear: out[t,o] = sum_b ((sum_i sign*x) * scale[o,b]) >> frac, mod 2^64 ----------- */
 /* bonsai_q1_gpu.cu:2200-2241 `bonsai_q1_linear_gpu` (bound at gpu_native.py:44-52, called :212-217). */

@@ -23,6 +23,7 @@ SIGNATURES = {
     "imie_default_stream": (c_void_p, []),
     "imie_synchronize": (c_int, []),
     "imie_probe_mfma": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "imie_mfma_peak": (c_int, [c_void_p]),
     "imie_profile_begin": (None, []),
     "imie_profile_gemm_ops": (c_int, [c_void_p, c_int]),
     "imie_profile_read": (c_int, [c_int, c_void_p, c_void_p]),

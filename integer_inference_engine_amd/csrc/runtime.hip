@@ -110,6 +110,49 @@ extern "C" int imie_probe_mfma(const int8_t* a_host, const int8_t* b_host, int32
   return IMIE_OK;
 }
 
+// Sustained int8 MFMA throughput of this device: every SIMD runs waves of 8 independent
+// v_mfma_i32_16x16x64_i8 accumulator chains (no memory traffic in the loop), timed with HIP events. The bench
+// quotes the prefill GEMM's MFMA utilisation against this as well as against the published dense peak.
+__global__ __launch_bounds__(256) void imie_mfma_peak_kernel(int iters, int seed, int32_t* sink) {
+  const v4i a = {seed, seed + 1, seed + 2, (int)threadIdx.x}, b = {seed + 3, seed, (int)threadIdx.x, 7};
+  v4i c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = v4i{i, 0, 0, 0};
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[i], 0, 0, 0);
+  int32_t v = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v ^= c[i][0] ^ c[i][3];
+  if (v == 0x7F3A5C11) sink[threadIdx.x] = v;        // keeps the chains live; practically never taken
+}
+
+extern "C" int imie_mfma_peak(double* ops_per_s) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  if (!ops_per_s || imie_device_ready() != 0) return IMIE_EARG;
+  int dev = 0, cus = 0;
+  IMIE_HIP(hipGetDevice(&dev));
+  IMIE_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  void* sink = nullptr;
+  IMIE_HIP(hipMalloc(&sink, 1024));
+  hipEvent_t e0, e1;
+  IMIE_HIP(hipEventCreate(&e0));
+  IMIE_HIP(hipEventCreate(&e1));
+  const int wgs = cus * 4, iters = 2000;               // 4 workgroups of 4 waves per CU: 4 waves per SIMD
+  float ms = 0.f;
+  for (int rep = 0; rep < 2; ++rep) {                 // the first launch warms up clocks and code
+    IMIE_HIP(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL(imie_mfma_peak_kernel, dim3((unsigned)wgs), dim3(256), 0, 0, iters, 1, (int32_t*)sink);
+    IMIE_HIP(hipEventRecord(e1, 0));
+    IMIE_HIP(hipEventSynchronize(e1));
+    IMIE_HIP(hipEventElapsedTime(&ms, e0, e1));
+  }
+  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); (void)hipFree(sink);
+  const double mfmas = (double)wgs * 4 * iters * 8;   // waves x iterations x chains
+  *ops_per_s = mfmas * (2.0 * 16 * 16 * 64) / (ms * 1e-3);
+  return IMIE_OK;
+}
+
 // ---- per-kernel event profiler ---------------------------------------------------------------------------
 namespace {
 struct ProfSlot {

@@ -37,6 +37,16 @@ def test_mfma_operand_and_accumulator_layout(gpu):
             assert d[l, r] == full[4 * (l // 16) + r, l % 16]
 
 
+def test_mfma_peak_calibration_is_plausible(gpu):
+    """The measured sustained int8 MFMA rate the bench quotes utilisation against: between 1 POPS and the published
+    dense 5.0 POPS (plus clock headroom)."""
+    from integer_inference_engine_amd import _lib
+    so = _lib.lib()
+    v = ctypes.c_double()
+    assert so.imie_mfma_peak(ctypes.byref(v)) == 0
+    assert 1.0e15 < v.value < 5.6e15
+
+
 @pytest.mark.parametrize("N,nb,T", [(16, 4, 1), (37, 3, 1), (256, 32, 1), (1024, 96, 1), (100, 5, 3), (64, 8, 7),
                                     # decode-sized launches whose waves request 4 / 2 slabs at once, with a short
                                     # last slab range (10 = 4 + 4 + 2 slabs, 25 = 12 * 2 + 1)
