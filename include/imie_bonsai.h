@@ -161,6 +161,30 @@ uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d);
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);
 
+/* ---- integer samplers (bonsai/src/trinote/infer_int/sampler.py) ------------------------------------------ */
+/* Committed fixed-point sampler settings. mode 0 greedy, 1 temp, 2 top_k, 3 top_p, 4 min_p; inv_temp =
+ * round(2^frac / T), top_p / min_p in 2^frac units (sampler.py:214-258); the field order and mode numbering follow
+ * the reference sampler ABI struct `Bonsai35SamplerConfig` (bonsai/tools/bonsai_q1_gpu.cu:905-910) plus the seed. */
+typedef struct ImieSamplerConfig {
+  int64_t mode, frac, inv_temp, top_k, top_p, min_p, rep_penalty, no_repeat_ngram, seed;
+} ImieSamplerConfig;
+/* sample_token (sampler.py:403-437) for one host logits row: replaces the host sampler call at
+ * reference_bonsai.py:1110-1146 / :1260-1310 and the device pair bonsai35_sample_prepare / bonsai35_sample_select
+ * (bonsai_q1_gpu.cu:3342-3418; the SHA-256 Lemire draw runs on the device here). rc 0, 1 bad arguments or a
+ * history token outside the vocabulary, 2 temperature overflow (the reference raises OverflowError). */
+int imie_sample_token(const int64_t *logits, int64_t vocab, const ImieSamplerConfig *cfg, const int64_t *history,
+                      int64_t history_n, int64_t position, int64_t *token);
+/* Device rows (no reference counterpart: the sampled decode step without a logits row on the host): token_dev[r]
+ * for logits_dev[r * ld ...], history hist_dev[r * hist_ld + i] (i < hist_len_dev[r]), draw key pos_dev[r].
+ * Asynchronous on `stream`; *status_dev |= 2 on the temperature guard, |= 1 on a bad history token. The first
+ * call for a shape sizes the workspace (synchronous); later calls only launch kernels. */
+int imie_sample_dev(const int64_t *logits_dev, int64_t rows, int64_t vocab, int64_t ld, const ImieSamplerConfig *cfg,
+                    const int64_t *hist_dev, int64_t hist_ld, const int64_t *hist_len_dev, const int64_t *pos_dev,
+                    int64_t *token_dev, int *status_dev, void *stream);
+/* Test hook (no reference counterpart): the device SHA-256 counter word 0 and the Lemire value for
+ * (total, seed, position) (sampler.py:283-315). */
+int imie_sample_draw_probe(int64_t total, int64_t seed, int64_t position, uint64_t *word0, int64_t *target);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,3 +92,13 @@ int imie_qk_head_finish_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
 // kv8 cache: fold the appended rows' maxima (rowk / rowv, M rows per sequence) into run_k / run_v
 int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
                           uint64_t* run_k, uint64_t* run_v, hipStream_t st);
+
+// Integer sampler config (committed fixed-point settings; layout shared with include/imie_bonsai.h).
+// mode: 0 greedy, 1 temp, 2 top_k, 3 top_p, 4 min_p (the reference ABI's numbering, bonsai_q1_gpu.cu:905-910)
+struct ImieSamplerConfig {
+  int64_t mode, frac, inv_temp, top_k, top_p, min_p, rep_penalty, no_repeat_ngram, seed;
+};
+// tokens of `rows` logits rows (stride ld) into token[r]; per-row history / positions on the device
+int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t ld, const ImieSamplerConfig& c,
+                       const int64_t* hist, int64_t hld, const int64_t* hlen, const int64_t* pos, int64_t* token,
+                       int* status, hipStream_t st);
