@@ -181,6 +181,14 @@ int imie_sample_token(const int64_t *logits, int64_t vocab, const ImieSamplerCon
 int imie_sample_dev(const int64_t *logits_dev, int64_t rows, int64_t vocab, int64_t ld, const ImieSamplerConfig *cfg,
                     const int64_t *hist_dev, int64_t hist_ld, const int64_t *hist_len_dev, const int64_t *pos_dev,
                     int64_t *token_dev, int *status_dev, void *stream);
+/* Sampled decode on the device (no reference counterpart for the fused loop): per step embed -> layers -> head
+ * -> sampler over the B rows, each token equal to sample_token(row, cfg, len(ids), frac, ids) (sampler.py:403-437)
+ * as the reference generate loops call it (reference_bonsai.py:1110-1146, :1260-1310). hist_dev (B, hist_ld)
+ * row-major holds every sequence's tokens so far (hist_len_dev[b] of them; the draw key), the drawn token is
+ * appended. ids_dev holds the step's input tokens and receives the drawn ones. One step is captured as a graph. */
+int imie_net_decode_sampled_dev(int64_t ctx, const uint8_t *ebits, const int64_t *escale, int64_t *ids_dev,
+                                int64_t *logits_dev, const ImieSamplerConfig *cfg, int64_t *hist_dev,
+                                int64_t hist_ld, int64_t *hist_len_dev, int64_t steps, int use_graph, void *stream);
 /* Test hook (no reference counterpart): the device SHA-256 counter word 0 and the Lemire value for
  * (total, seed, position) (sampler.py:283-315). */
 int imie_sample_draw_probe(int64_t total, int64_t seed, int64_t position, uint64_t *word0, int64_t *target);

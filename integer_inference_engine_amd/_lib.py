@@ -28,6 +28,8 @@ SIGNATURES = {
     "imie_sample_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p]),
     "imie_sample_draw_probe": (c_int, [c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_net_decode_sampled_dev": (c_int, [c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_int64, c_void_p, c_int64, c_int, c_void_p]),
     "imie_profile_begin": (None, []),
     "imie_profile_gemm_ops": (c_int, [c_void_p, c_int]),
     "imie_profile_read": (c_int, [c_int, c_void_p, c_void_p]),

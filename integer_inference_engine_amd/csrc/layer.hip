@@ -346,6 +346,21 @@ __global__ void decode_advance_kernel(const int64_t* __restrict__ ids, int64_t* 
   if (threadIdx.x == 0) *stepc = s + 1;
 }
 
+// After a sampled step: the token joins its sequence's history row (hist[b * hld + len]), len++ (the next draw
+// key), and every sequence advances one position.
+__global__ void decode_advance_sampled_kernel(const int64_t* __restrict__ ids, int64_t* __restrict__ hist, int64_t hld,
+                                              int64_t* __restrict__ hlen, int64_t* __restrict__ starts,
+                                              int64_t* __restrict__ pos, int64_t B) {
+  for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
+    const int64_t L = hlen[b];
+    if (L >= 0 && L < hld) hist[b * hld + L] = ids[b];
+    hlen[b] = L + 1;
+    const int64_t p = starts[b] + 1;
+    starts[b] = p;
+    pos[b] = p;
+  }
+}
+
 // final norm of selected rows + output head (+ argmax). rows_idx: host list of row indices into x.
 int net_head(Net& n, const int64_t* x, const std::vector<int64_t>& rows_idx, int64_t* logits, int64_t* ids,
              hipStream_t st) {
@@ -692,6 +707,77 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
         memcpy(n->gkey, key, sizeof(key));
       }
       for (int64_t s = 1; s < steps; ++s) IMIE_HIP(hipGraphLaunch(n->gexec, st));
+    }
+  }
+  for (int64_t b = 0; b < n->B; ++b) n->len[(size_t)b] += steps;
+  return IMIE_OK;
+}
+
+// Sampled decode on the device (no reference counterpart for the fused loop; each token equals
+// sample_token(logits_row, cfg, len(ids), frac, ids), sampler.py:403-437, as the reference generate loops call it,
+// reference_bonsai.py:1110-1146 / :1260-1310): per step embed -> layers -> head -> imie_sample_launch over the B
+// logits rows with history rows hist_dev[b * hist_ld + i] (i < hist_len_dev[b]: prompt + generated tokens) and
+// draw key hist_len_dev[b]; the token is appended and hist_len_dev[b] advances. One step is captured as a graph.
+int imie_net_decode_sampled_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale, int64_t* ids_dev,
+                                int64_t* logits_dev, const ImieSamplerConfig* cfg, int64_t* hist_dev, int64_t hist_ld,
+                                int64_t* hist_len_dev, int64_t steps, int use_graph, void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n || !ebits || !escale || !ids_dev || !logits_dev || !cfg || !hist_dev || !hist_len_dev || hist_ld <= 0 ||
+      steps <= 0 || n->out_head < 0 || cfg->frac != n->frac)
+    return IMIE_EARG;
+  const int64_t cap = n->mp * n->P;
+  for (int64_t b = 0; b < n->B; ++b)
+    if (n->len[(size_t)b] + steps > seq_cap(*n, b)) return IMIE_EARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (net_ensure(*n, 1, cap) || n->stepc.ensure(64) || n->lastx.ensure((size_t)(n->B * n->d) * 8)) return IMIE_EARG;
+  std::vector<int64_t> hl((size_t)n->B);
+  IMIE_HIP(hipMemcpyAsync(hl.data(), hist_len_dev, (size_t)n->B * 8, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipMemcpyAsync(n->starts.p, n->len.data(), (size_t)n->B * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipMemcpyAsync(n->pos.p, n->len.data(), (size_t)n->B * 8, hipMemcpyHostToDevice, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  for (int64_t b = 0; b < n->B; ++b)                  // every drawn token must fit its history row
+    if (hl[(size_t)b] < 0 || hl[(size_t)b] + steps > hist_ld) return IMIE_EARG;
+  std::vector<int64_t> rows((size_t)n->B);
+  for (int64_t b = 0; b < n->B; ++b) rows[(size_t)b] = b;
+  const ImieSamplerConfig c = *cfg;
+  auto step = [&]() -> int {
+    int rc = imie_embed_launch(ebits, escale, n->d / 128, ids_dev, n->B, (int64_t*)n->x.p, st);
+    if (rc) return rc;
+    if ((rc = net_run_core(*n, (int64_t*)n->x.p, 1, cap, st))) return rc;
+    if ((rc = net_head(*n, (const int64_t*)n->x.p, rows, logits_dev, nullptr, st))) return rc;
+    if ((rc = imie_sample_launch(logits_dev, n->B, n->vocab, n->vocab, c, hist_dev, hist_ld, hist_len_dev,
+                                 hist_len_dev, ids_dev, (int*)n->status.p, st)))
+      return rc;
+    hipLaunchKernelGGL(decode_advance_sampled_kernel, dim3(1), dim3(256), 0, st, ids_dev, hist_dev, hist_ld,
+                       hist_len_dev, (int64_t*)n->starts.p, (int64_t*)n->pos.p, n->B);
+    IMIE_HIP(hipGetLastError());
+    return IMIE_OK;
+  };
+  if (n->x.ensure((size_t)(n->B * n->d) * 8)) return IMIE_EARG;
+  int rc = step();                                    // eager: also sizes every workspace the graph will use
+  if (rc) return rc;
+  if (steps > 1) {
+    if (!use_graph) {
+      for (int64_t s = 1; s < steps && !rc; ++s) rc = step();
+      if (rc) return rc;
+    } else {
+      const bool prof = imie_prof_suspend(true);
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      IMIE_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      rc = step();
+      const hipError_t ec = hipStreamEndCapture(st, &g);
+      imie_prof_suspend(prof);
+      if (rc || ec != hipSuccess || !g) { if (g) (void)hipGraphDestroy(g); return rc ? rc : IMIE_EARG; }
+      const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (ei != hipSuccess) return IMIE_EARG;
+      for (int64_t s = 1; s < steps && !rc; ++s)
+        if (hipGraphLaunch(ge, st) != hipSuccess) rc = IMIE_EARG;
+      (void)hipStreamSynchronize(st);
+      (void)hipGraphExecDestroy(ge);
+      if (rc) return rc;
     }
   }
   for (int64_t b = 0; b < n->B; ++b) n->len[(size_t)b] += steps;

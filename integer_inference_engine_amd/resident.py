@@ -108,6 +108,27 @@ class ResidentNet:
             raise RuntimeError(f"decode rc={rc}: {_lib.last_error()}")
         return logits, hist
 
+    def decode_sampled(self, embed_bits, embed_scale, ids, steps: int, cfg, frac: int, hist, hist_len, *,
+                       graph: bool = True, logits=None):
+        """Sampled decode of ``steps`` tokens on the device (imie_net_decode_sampled_dev). cfg: a SamplerConfig
+        (duck-typed, see sampler_gpu); hist (B, hist_ld) int64 device tensor of every sequence's tokens so far,
+        hist_len (B,) their counts (both advanced in place); ids (B,) the step's input tokens, overwritten with
+        the last drawn token. Returns the last step's logits (B, vocab)."""
+        from .sampler_gpu import config_c
+        t = self.torch
+        if logits is None:
+            logits = t.empty((self.B, self.vocab), dtype=t.int64, device="cuda")
+        c = config_c(cfg, frac)
+        rc = self.lib.imie_net_decode_sampled_dev(self.h, ctypes.c_void_p(embed_bits.data_ptr()),
+                                                  ctypes.c_void_p(embed_scale.data_ptr()),
+                                                  ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(logits.data_ptr()),
+                                                  ctypes.byref(c), ctypes.c_void_p(hist.data_ptr()), hist.shape[1],
+                                                  ctypes.c_void_p(hist_len.data_ptr()), int(steps), 1 if graph else 0,
+                                                  self._sp())
+        if rc != 0:
+            raise RuntimeError(f"sampled decode rc={rc}: {_lib.last_error()}")
+        return logits
+
     def status(self) -> int:
         return int(self.lib.imie_net_status(self.h, 0, self._sp()))
 

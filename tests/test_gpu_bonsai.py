@@ -279,3 +279,77 @@ def test_device_greedy_decode_matches_oracle(gpu, graph):
             assert so.imie_net_export_kv(ctx, li, b, T0[b] + steps, k.ctypes.data, v.ctypes.data) == 0
             assert np.array_equal(k, caches[b][0][li][:, :T0[b] + steps]) and np.array_equal(v, caches[b][1][li][:, :T0[b] + steps])
     gpu.decode_ctx_free(ctx)
+
+
+@pytest.mark.parametrize("graph", [0, 1])
+def test_device_sampled_decode_matches_oracle(gpu, graph):
+    """imie_net_decode_sampled_dev: each token equals the oracle's sample_token(logits, cfg, len(ids), 16, ids) over
+    the oracle model's logits (top-p with top-k, temperature, repetition penalty and a 2-gram ban)."""
+    import ctypes
+    from types import SimpleNamespace
+    import torch
+    from integer_inference_engine_amd import _lib
+    from integer_inference_engine_amd.sampler_gpu import config_c
+    from oracle import sampler as osm
+    model = workloads.small_bonsai(seed=44)
+    cfg = model["cfg"]
+    w, g = register_model(gpu, model)
+    B, T0, steps, hld = 3, [5, 9, 2], 6, 32
+    scfg = SimpleNamespace(mode="top_p", temperature=0.5, top_k=12, top_p=0.9, min_p=0.0, seed=11,
+                           rep_penalty=13107, no_repeat_ngram=2)
+    c = config_c(scfg, 16)
+    draw = lambda row, ids: osm.sample_token(row, "top_p", 16, inv_temp=c.inv_temp, top_k=c.top_k, top_p_fp=c.top_p,
+                                             seed=scfg.seed, position=len(ids), hist=ids, rep_penalty=c.rep_penalty,
+                                             no_repeat_ngram=c.no_repeat_ngram)
+    prompts = [prng.uniform_int(44, 400 + b, (T0[b],), 0, cfg["vocab"]) for b in range(B)]
+    lc = {"H": cfg["H"], "Hkv": cfg["Hkv"], "hd": cfg["hd"]}
+    ctx = gpu.decode_ctx_create((B, cfg["n_layers"], cfg["H"], cfg["Hkv"], cfg["hd"], cfg["d"], cfg["dff"],
+                                 cfg["vocab"]), w, g, 16, 1, fx.inv_sqrt_fp(cfg["hd"], 16), 64)
+    assert ctx is not None
+    caches, ids = [], []
+    for b in range(B):
+        x, ks, vs = _oracle_prefill(model, prompts[b])
+        assert gpu.decode_ctx_seed_seq(ctx, b, ks, vs)
+        caches.append(([ks[li] for li in range(len(ks))], [vs[li] for li in range(len(vs))]))
+        toks = [int(t) for t in prompts[b]]
+        toks.append(draw(obm.head_logits(model, x[-1:], 16)[0], toks))
+        ids.append(toks)
+    first = [t[-1] for t in ids]
+    hist0 = np.full((B, hld), -1, dtype=np.int64)
+    for b in range(B):
+        hist0[b, :len(ids[b])] = ids[b]
+    len0 = [len(t) for t in ids]
+    pos = list(T0)
+    for _ in range(steps):
+        x_in = q1_rows(*model["embed"], [t[-1] for t in ids])
+        for b in range(B):
+            xb = x_in[b:b + 1]
+            kc, vc = caches[b]
+            for li, layer in enumerate(model["layers"]):
+                xb, kn, vn = obm.layer_forward(xb, layer, lc, model["cos"], model["sin"], 16, kc[li], vc[li], pos[b])
+                kc[li] = np.concatenate([kc[li], kn], axis=1)
+                vc[li] = np.concatenate([vc[li], vn], axis=1)
+            ids[b].append(draw(obm.head_logits(model, xb, 16)[0], ids[b]))
+        pos = [p + 1 for p in pos]
+    so = _lib.lib()
+    eb = torch.from_numpy(np.ascontiguousarray(model["embed"][0])).cuda()
+    es = torch.from_numpy(np.ascontiguousarray(model["embed"][1])).cuda()
+    dids = torch.tensor(first, dtype=torch.int64, device="cuda")
+    lg = torch.empty((B, cfg["vocab"]), dtype=torch.int64, device="cuda")
+    hist = torch.from_numpy(hist0).cuda()
+    hlen = torch.tensor(len0, dtype=torch.int64, device="cuda")
+    s = torch.cuda.Stream()
+    sp = ctypes.c_void_p(s.cuda_stream)
+    so.imie_net_status(ctx, 1, sp)
+    rc = so.imie_net_decode_sampled_dev(ctx, ctypes.c_void_p(eb.data_ptr()), ctypes.c_void_p(es.data_ptr()),
+                                        ctypes.c_void_p(dids.data_ptr()), ctypes.c_void_p(lg.data_ptr()),
+                                        ctypes.byref(c), ctypes.c_void_p(hist.data_ptr()), hld,
+                                        ctypes.c_void_p(hlen.data_ptr()), steps, graph, sp)
+    assert rc == 0, _lib.last_error()
+    assert so.imie_net_status(ctx, 0, sp) == 0
+    s.synchronize()
+    got = hist.cpu().numpy()
+    assert hlen.cpu().numpy().tolist() == [len(t) for t in ids]
+    for b in range(B):
+        assert got[b, :len(ids[b])].tolist() == ids[b], b
+    gpu.decode_ctx_free(ctx)
