@@ -166,7 +166,7 @@ def c5_leg(so, torch, w, g, ebits, escale, tokens: int, B: int = 32, n_layers: i
     d, H, Hkv, hd, dff = 4096, 32, 8, 128, 12288
     rng = np.random.default_rng(55)
     lens = rng.integers(512, 32769, size=B).astype(np.int64)
-    extra = tokens + 8
+    extra = 2 * tokens + 8                             # greedy warm-up + timed run, then the sampled run
     cap = int(lens.max()) + extra
     cos, sin = bonsai8b_tables(cap)
     from integer_inference_engine_amd import gpu_native as gn
@@ -191,13 +191,33 @@ def c5_leg(so, torch, w, g, ebits, escale, tokens: int, B: int = 32, n_layers: i
     net.stream.synchronize()
     ms = e0.elapsed_time(e1)
     status = net.status()
+    # the same step with the device sampler instead of argmax (qwen3-rec preset: T 0.6, top-k 20, top-p 0.95),
+    # histories = the greedy tokens so far; tokens - 2 timed steps after one eager + one captured step
+    from types import SimpleNamespace
+    scfg = SimpleNamespace(mode="top_p", temperature=0.6, top_k=20, top_p=0.95, min_p=0.0, seed=0, rep_penalty=0,
+                           no_repeat_ngram=0)
+    hld = 2 * tokens + 8
+    shist = torch.full((B, hld), -1, dtype=torch.int64, device="cuda")
+    shist[:, :tokens] = hist.t()
+    slen = torch.full((B,), tokens, dtype=torch.int64, device="cuda")
+    net.decode_sampled(ebits, escale, ids, 2, scfg, 16, shist, slen, graph=True, logits=logits)
+    net.stream.synchronize()
+    ns = max(tokens - 2, 1)
+    e0.record(net.stream)
+    net.decode_sampled(ebits, escale, ids, ns, scfg, 16, shist, slen, graph=True, logits=logits)
+    e1.record(net.stream)
+    net.stream.synchronize()
+    ms_s = e0.elapsed_time(e1)
+    status |= net.status()
     net.close()
     kv_bytes = int((lens + 2).sum()) * n_layers * 2 * Hkv * hd * 4
     return {"sequences": B, "tokens_per_sequence": tokens, "layers": n_layers,
             "context_min": int(lens.min()), "context_max": int(lens.max()), "context_mean": round(float(lens.mean()), 1),
             "tok_s": round(B * tokens / (ms / 1e3), 1), "ms_per_step": round(ms / tokens, 3), "status": status,
             "kv_GB": round(kv_bytes / 1e9, 1), "kv_read_GB_s": round(kv_bytes / (ms / tokens / 1e3) / 1e9, 1),
-            "setup_s": round(setup_s, 2), "kv": "kv8 digit planes (int8 x 4 per element), 64-slot pages"}
+            "setup_s": round(setup_s, 2), "kv": "kv8 digit planes (int8 x 4 per element), 64-slot pages",
+            "sampled_tok_s": round(B * ns / (ms_s / 1e3), 1), "sampled_ms_per_step": round(ms_s / ns, 3),
+            "sampled_mode": "top_p, qwen3-rec (T 0.6, top-k 20, top-p 0.95), device SHA-256 draws"}
 
 
 def prefill_leg(so, torch, T: int = 2048) -> dict:

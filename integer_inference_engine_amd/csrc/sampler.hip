@@ -382,25 +382,74 @@ __global__ void smp_minp_final_kernel(const int64_t* __restrict__ part, SmpRow* 
   st[r].total = (int64_t)sum;
 }
 
-// keys for the descending order: (p << 32) | token id; unique, so the sorted order has the reference's ties
-__global__ __launch_bounds__(256) void smp_keys_kernel(int64_t V, int64_t rows, const SmpRow* __restrict__ st,
-                                                       const int64_t* __restrict__ pr, uint64_t* __restrict__ keys) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= rows * V) return;
-  const int64_t r = i / V, k = i - r * V;
-  keys[i] = st[r].done ? (uint64_t)k : ((uint64_t)pr[i] << 32) | (uint64_t)k;
+// keys for the descending order: (p << 32) | token id, unique, so any sort reproduces the reference's ties. Only
+// nonzero probabilities are keyed (compacted per row): a zero-probability token adds nothing to the kept total
+// or to the draw whether it is kept or not, and the all-zero fallback (the highest id) is handled directly.
+__global__ __launch_bounds__(256) void smp_count_kernel(int64_t V, const SmpRow* __restrict__ st,
+                                                        const int64_t* __restrict__ pr, int64_t* __restrict__ part) {
+  const int64_t r = blockIdx.y, per = (V + kSmpParts - 1) / kSmpParts;
+  const int64_t c0 = (int64_t)blockIdx.x * per, c1 = min(V, c0 + per);
+  uint64_t n = 0;
+  if (!st[r].done)
+    for (int64_t k = c0 + threadIdx.x; k < c1; k += 256) n += pr[r * V + k] != 0;
+  n = smp_block_u64<false>(n);
+  if (threadIdx.x == 0) part[(r * kSmpParts + blockIdx.x) * 4 + 3] = (int64_t)n;
+}
+
+// per-row exclusive offsets of the parts' nonzero counts (part[.. + 3] <- offset) and the sort segment ends
+__global__ void smp_offsets_kernel(int64_t V, int64_t* __restrict__ part, int* __restrict__ seg_end) {
+  const int64_t r = blockIdx.x;
+  if (threadIdx.x) return;
+  int64_t run = 0;
+  for (int k = 0; k < kSmpParts; ++k) {
+    int64_t* p = part + (r * kSmpParts + k) * 4 + 3;
+    const int64_t n = *p;
+    *p = run;
+    run += n;
+  }
+  seg_end[r] = (int)(r * V + run);
+}
+
+__global__ __launch_bounds__(256) void smp_scatter_kernel(int64_t V, const SmpRow* __restrict__ st,
+                                                          const int64_t* __restrict__ pr,
+                                                          const int64_t* __restrict__ part, uint64_t* __restrict__ keys) {
+  __shared__ int s_base;
+  __shared__ int s_w[4];
+  const int64_t r = blockIdx.y, per = (V + kSmpParts - 1) / kSmpParts;
+  if (st[r].done) return;
+  const int64_t c0 = (int64_t)blockIdx.x * per, c1 = min(V, c0 + per);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_base = (int)part[(r * kSmpParts + blockIdx.x) * 4 + 3];
+  __syncthreads();
+  for (int64_t k0 = c0; k0 < c1; k0 += 256) {       // order-preserving compaction, 256 ids per step
+    const int64_t k = k0 + threadIdx.x;
+    const int64_t p = k < c1 ? pr[r * V + k] : 0;
+    const uint64_t m = __ballot(p != 0);
+    const int before = __popcll(m & ((1ull << lane) - 1));
+    if (lane == 0) s_w[w] = __popcll(m);
+    __syncthreads();
+    int wb = 0, tot = 0;
+    for (int i = 0; i < 4; ++i) { if (i < w) wb += s_w[i]; tot += s_w[i]; }
+    if (p != 0) keys[r * V + s_base + wb + before] = ((uint64_t)p << 32) | (uint64_t)k;
+    __syncthreads();
+    if (threadIdx.x == 0) s_base += tot;
+    __syncthreads();
+  }
 }
 
 // top-k / nucleus over the sorted keys (one workgroup per row): keep the first `keep` ranks, where the nucleus
 // ends at the first rank whose running sum reaches top_p (that rank included); zero the rest; total of the kept
 __global__ __launch_bounds__(kSmpScan) void smp_trunc_kernel(ImieSamplerConfig c, int64_t V,
                                                              const uint64_t* __restrict__ sorted,
+                                                             const int* __restrict__ seg_end,
                                                              SmpRow* __restrict__ st, int64_t* __restrict__ pr) {
   __shared__ int64_t s_nuc;
   const int64_t r = blockIdx.x;
   if (st[r].done) return;
   const uint64_t* sk = sorted + r * V;
+  const int64_t nnz = (int64_t)seg_end[r] - r * V;    // ranks past nnz hold zero probabilities
   int64_t keep = c.top_k > 0 ? (c.top_k < V ? c.top_k : V) : V;
+  if (keep > nnz) keep = nnz;
   const int t = threadIdx.x;
   if (t == 0) s_nuc = INT64_MAX;
   __syncthreads();
@@ -420,11 +469,10 @@ __global__ __launch_bounds__(kSmpScan) void smp_trunc_kernel(ImieSamplerConfig c
     }
     __syncthreads();
     if (s_nuc != INT64_MAX && s_nuc + 1 < keep) keep = s_nuc + 1;
-    if (keep < 1) keep = 1;
   }
-  // zero the dropped ranks and sum the kept probabilities
+  // zero the dropped nonzero ranks and sum the kept probabilities
   uint64_t kept = 0;
-  for (int64_t k = t; k < V; k += kSmpScan) {
+  for (int64_t k = t; k < nnz; k += kSmpScan) {
     const int64_t id = (int64_t)(sk[k] & 0xFFFFFFFFu);
     if (k < keep) kept += sk[k] >> 32;
     else pr[r * V + id] = 0;
@@ -433,7 +481,7 @@ __global__ __launch_bounds__(kSmpScan) void smp_trunc_kernel(ImieSamplerConfig c
   uint64_t total;
   (void)smp_block_excl(kept, &total);
   if (t == 0) {
-    if (total == 0) { pr[r * V + (int64_t)(sk[0] & 0xFFFFFFFFu)] = 1; total = 1; }
+    if (total == 0) { pr[r * V + V - 1] = 1; total = 1; }   // all zero: the first rank is the highest id
     st[r].total = (int64_t)total;
   }
 }
@@ -545,32 +593,34 @@ int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t l
       hipLaunchKernelGGL(smp_minp_final_kernel, dim3((unsigned)rows), dim3(64), 0, st, part, srow, pr, V);
     }
     if (sorted) {
-      if (g_smp.keys.ensure(rv * 8) || g_smp.sorted.ensure(rv * 8) || g_smp.offs.ensure((size_t)(rows + 1) * 4))
+      if (g_smp.keys.ensure(rv * 8) || g_smp.sorted.ensure(rv * 8) || g_smp.offs.ensure((size_t)(2 * rows + 1) * 4))
         return IMIE_EARG;
-      // segment offsets r * V (host-computed once per shape)
+      if (rv >= ((size_t)1 << 31)) return IMIE_EARG;
+      // segment begins r * V (host-computed once per shape); ends r * V + nonzero count (device)
       static int64_t offs_rows = -1, offs_v = -1;
       if (offs_rows != rows || offs_v != V) {
-        std::vector<int> h((size_t)rows + 1);
-        for (int64_t i = 0; i <= rows; ++i) h[(size_t)i] = (int)(i * V);
+        std::vector<int> h((size_t)rows);
+        for (int64_t i = 0; i < rows; ++i) h[(size_t)i] = (int)(i * V);
         IMIE_HIP(hipMemcpy(g_smp.offs.p, h.data(), h.size() * 4, hipMemcpyHostToDevice));
         offs_rows = rows; offs_v = V;
       }
-      if (rv >= ((size_t)1 << 31)) return IMIE_EARG;
-      hipLaunchKernelGGL(smp_keys_kernel, dim3((unsigned)((rv + 255) / 256)), dim3(256), 0, st, V, rows, srow, pr,
-                         (uint64_t*)g_smp.keys.p);
-      const int* offs = (const int*)g_smp.offs.p;
+      const int* begs = (const int*)g_smp.offs.p;
+      int* ends = (int*)g_smp.offs.p + rows;
+      hipLaunchKernelGGL(smp_count_kernel, gv, dim3(256), 0, st, V, srow, pr, part);
+      hipLaunchKernelGGL(smp_offsets_kernel, dim3((unsigned)rows), dim3(64), 0, st, V, part, ends);
+      hipLaunchKernelGGL(smp_scatter_kernel, gv, dim3(256), 0, st, V, srow, pr, part, (uint64_t*)g_smp.keys.p);
       const int end_bit = 33 + (int)c.frac;           // p <= 2^frac
       size_t tmp_bytes = 0;
       IMIE_HIP(hipcub::DeviceSegmentedRadixSort::SortKeysDescending(nullptr, tmp_bytes, (const uint64_t*)g_smp.keys.p,
                                                                      (uint64_t*)g_smp.sorted.p, (int)rv, (int)rows,
-                                                                     offs, offs + 1, 0, end_bit, st));
+                                                                     begs, (const int*)ends, 0, end_bit, st));
       if (g_smp.tmp.ensure(tmp_bytes)) return IMIE_EARG;
       IMIE_HIP(hipcub::DeviceSegmentedRadixSort::SortKeysDescending(g_smp.tmp.p, tmp_bytes,
                                                                      (const uint64_t*)g_smp.keys.p,
                                                                      (uint64_t*)g_smp.sorted.p, (int)rv, (int)rows,
-                                                                     offs, offs + 1, 0, end_bit, st));
+                                                                     begs, (const int*)ends, 0, end_bit, st));
       hipLaunchKernelGGL(smp_trunc_kernel, dim3((unsigned)rows), dim3(kSmpScan), 0, st, c, V,
-                         (const uint64_t*)g_smp.sorted.p, srow, pr);
+                         (const uint64_t*)g_smp.sorted.p, (const int*)ends, srow, pr);
     }
     hipLaunchKernelGGL(smp_select_kernel, dim3((unsigned)rows), dim3(kSmpScan), 0, st, c, V, pos, srow, pr, token);
   }
