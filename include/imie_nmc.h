@@ -62,6 +62,36 @@ void qk_profile_reset(void);
 void qk_profile_set_enabled(int enabled);
 int qk_profile_snapshot(unsigned long long *out, int capacity);
 
+/* ---- resident preprocessing and attention bank (the steps either side of the MoE block) ------------------ */
+/* nmc_qk_cuda.cu:1068 `qk_register_i64` (qk_cuda.py:285-303): dense int64 [rows, cols] (gains, router). */
+long long qk_register_i64(const int64_t *W, long long rows, long long cols);
+/* nmc_qk_cuda.cu:1116 `qk_rmsnorm_router` (qk_cuda.py:331-372): RMSNorm + router + lowest-index top-k + sigmoid
+ * gates; rc 3 = exact envelope rejection. */
+int qk_rmsnorm_router(long long gain_h, long long router_h, const int64_t *x, long long rows, int fa, int fw,
+                      unsigned long long eps, int used, long long h_capacity, long long route_capacity,
+                      int64_t *h_out, int *ids_out, int64_t *gates_out);
+/* nmc_qk_cuda.cu:877-933, :1363-1780 attention bank (qk_cuda.py:476-715 `ResidentAttentionCache`). */
+long long qk_attention_bank_create(int n_layers, long long max_length, long long d_model, int heads, int n_kv,
+                                   int head_dim, int fa, const int64_t *cos, const int64_t *sin);
+int qk_attention_bank_import(long long h, int layer, const int64_t *k, const int64_t *v, long long length);
+int qk_attention_bank_apply(long long h, int layer, long long qh, long long kh, long long vh, long long oh,
+                            const int64_t *x, int fw, int window, int rope, int64_t inv_sqrt,
+                            long long output_capacity, int64_t *out);
+int qk_attention_bank_moe_configure(long long h, int layer, int experts, int used, long long d_model,
+                                    long long expert_ffn);
+int qk_attention_bank_moe_bind(long long h, int layer, int expert, long long gate_h, long long up_h,
+                               long long down_h);
+int qk_attention_bank_moe_begin(long long h, int layer, long long gain_h, long long router_h, long long qh,
+                                long long kh, long long vh, long long oh, const int64_t *x, int use_retained, int fw,
+                                unsigned long long eps, int window, int rope, int64_t inv_sqrt, int cold_capacity,
+                                int *cold_count_out, int *cold_ids_out);
+int qk_attention_bank_moe_continue(long long h, int layer, int fw, int publish, long long output_capacity,
+                                   int64_t *out);
+int qk_attention_bank_moe_export(long long h, long long output_capacity, int64_t *out);
+unsigned long long qk_attention_bank_workspace_bytes(long long h);
+int qk_attention_bank_reset(long long h);
+void qk_attention_bank_destroy(long long h);
+
 #ifdef __cplusplus
 }
 #endif

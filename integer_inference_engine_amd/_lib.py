@@ -101,6 +101,23 @@ SIGNATURES = {
     "imie_moe_ffn_batched_dev": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int,
                                                             c_int, c_void_p, c_void_p]),
     "imie_moe_status": (c_int, [c_int, c_void_p]),
+    "qk_register_i64": (c_int64, [c_void_p, c_int64, c_int64]),
+    "qk_rmsnorm_router": (c_int, [c_int64, c_int64, c_void_p, c_int64, c_int, c_int, c_uint64, c_int, c_int64, c_int64,
+                                  c_void_p, c_void_p, c_void_p]),
+    "qk_attention_bank_create": (c_int64, [c_int, c_int64, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "qk_attention_bank_import": (c_int, [c_int64, c_int, c_void_p, c_void_p, c_int64]),
+    "qk_attention_bank_apply": (c_int, [c_int64, c_int, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int, c_int,
+                                        c_int, c_int64, c_int64, c_void_p]),
+    "qk_attention_bank_moe_configure": (c_int, [c_int64, c_int, c_int, c_int, c_int64, c_int64]),
+    "qk_attention_bank_moe_bind": (c_int, [c_int64, c_int, c_int, c_int64, c_int64, c_int64]),
+    "qk_attention_bank_moe_begin": (c_int, [c_int64, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                            c_void_p, c_int, c_int, c_uint64, c_int, c_int, c_int64, c_int, c_void_p,
+                                            c_void_p]),
+    "qk_attention_bank_moe_continue": (c_int, [c_int64, c_int, c_int, c_int, c_int64, c_void_p]),
+    "qk_attention_bank_moe_export": (c_int, [c_int64, c_int64, c_void_p]),
+    "qk_attention_bank_workspace_bytes": (c_uint64, [c_int64]),
+    "qk_attention_bank_reset": (c_int, [c_int64]),
+    "qk_attention_bank_destroy": (None, [c_int64]),
     "qk_free_all": (None, []),
     "qk_resident_count": (c_int64, []),
     "qk_resident_capacity": (c_int64, []),

@@ -602,8 +602,9 @@ bool qk_mfma_enabled() {
   return v;
 }
 
+// a Q4_K / Q6_K handle (int64 matrices registered by qk_register_i64 are qtype 2 and not accepted here)
 const QKWeight* qk_get(int64_t h) {
-  if (h < 0 || h >= (int64_t)g_qk.size() || !g_qk[(size_t)h].p) return nullptr;
+  if (h < 0 || h >= (int64_t)g_qk.size() || !g_qk[(size_t)h].p || g_qk[(size_t)h].qtype > 1) return nullptr;
   return &g_qk[(size_t)h];
 }
 
@@ -778,6 +779,59 @@ int64_t qk_register(const uint8_t* W, int64_t out_f, int64_t nb, int qtype) {
 }
 
 }  // namespace
+
+// ---- internal API for the resident attention bank (csrc/nmcbank.hip) --------------------------------------------
+int imie_qk_info(int64_t h, int64_t* out_f, int64_t* nb, int* qtype, const uint8_t** p) {
+  if (h < 0 || h >= (int64_t)g_qk.size() || !g_qk[(size_t)h].p) return IMIE_EARG;
+  const QKWeight& w = g_qk[(size_t)h];
+  if (out_f) *out_f = w.out_f;
+  if (nb) *nb = w.nb;
+  if (qtype) *qtype = w.qtype;
+  if (p) *p = w.p;
+  return IMIE_OK;
+}
+
+// int64 matrix [rows, cols] registered as qtype 2 (nb holds cols)
+int64_t imie_qk_register_i64(const int64_t* W, int64_t rows, int64_t cols) {
+  if (!W || rows <= 0 || cols <= 0 || imie_device_ready() != 0) return -1;
+  QKWeight w;
+  w.out_f = rows; w.nb = cols; w.qtype = 2;
+  w.bytes = (size_t)(rows * cols) * 8;
+  if (hipMalloc((void**)&w.p, w.bytes) != hipSuccess) return -1;
+  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(w.p); return -1; }
+  g_qk.push_back(w);
+  ++g_qk_live;
+  prof(PM_REG_CALLS); prof(PM_ALLOC_CALLS); prof(PM_ALLOC_BYTES, w.bytes);
+  return (int64_t)g_qk.size() - 1;
+}
+
+// y[t, :] = (W . x[t, :]) >> fw for T device rows into device out (T x out_f); status gets IMIE_EOVF where the
+// oracle's int64 conversion would raise
+int imie_qk_linear_dev(int64_t h, const int64_t* x, int64_t T, int fw, int64_t* out, int* status, hipStream_t st) {
+  const QKWeight* w = qk_get(h);
+  if (!w || !x || !out || !status || T <= 0) return IMIE_EARG;
+  std::vector<Item> items{Item{w->p, w->out_f, w->nb, w->qtype, 0, (int)T}};
+  std::vector<int> xi((size_t)T), yi((size_t)T);
+  for (int64_t t = 0; t < T; ++t) { xi[(size_t)t] = (int)t; yi[(size_t)t] = (int)t; }
+  static DevBuf ib[4], pb[4];
+  static int slot = 0;
+  slot = (slot + 1) & 3;                              // distinct item buffers for back-to-back launches
+  return run_items(items, xi, yi, x, w->nb * 256, out, w->out_f, fw, status, st, ib[slot], pb[slot]);
+}
+
+// one token's MoE over k selected experts (host handle arrays), gates on the device; synchronous; 0, or IMIE_EOVF
+// where the oracle's int64 conversions would raise
+int imie_qk_moe_dev(const long long* gate_h, const long long* up_h, const long long* down_h, int k,
+                    const int64_t* h_dev, const int64_t* gates_dev, int64_t d_model, int64_t e_ffn, int fa, int fw,
+                    int64_t* out_dev, hipStream_t st) {
+  if (g_mws.status.ensure(64)) return IMIE_EARG;
+  IMIE_HIP(hipMemsetAsync(g_mws.status.p, 0, 4, st));
+  int rc = moe_batched(gate_h, up_h, down_h, 1, k, h_dev, gates_dev, d_model, e_ffn, fa, fw, out_dev, st);
+  if (rc) return rc;
+  int stat = 0;
+  if (read_status_and(st, &stat)) return IMIE_EARG;
+  return stat ? IMIE_EOVF : IMIE_OK;
+}
 
 extern "C" {
 

@@ -239,3 +239,280 @@ def release_moe_workspace() -> bool:
         return False
     lib.qk_moe_workspace_release()
     return True
+
+
+# ---- resident preprocessing and attention bank (qk_cuda.py:285-715) -----------------------------------------
+class CudaContextError(RuntimeError):
+    """A resident request context failed validation, allocation, or an exact envelope guard (qk_cuda.py:79-80)."""
+
+
+def register_i64(weight_int, rows: int = None, cols: int = None) -> int:
+    """Upload a dense int64 matrix (norm gain [1, d] or router [experts, d]); handle or CudaRegistrationError."""
+    lib = _dev()
+    if lib is None:
+        raise CudaRegistrationError("gfx950 device unavailable")
+    w = np.ascontiguousarray(np.atleast_2d(np.asarray(weight_int, dtype=np.int64)))
+    r, c = w.shape if rows is None else (int(rows), int(cols))
+    if w.size != r * c or r <= 0 or c <= 0:
+        raise ValueError("int64 registration shape does not match the data")
+    with _LOCK:
+        h = int(lib.qk_register_i64(w.ctypes.data, r, c))
+    if h < 0:
+        raise CudaRegistrationError(f"resident int64 registration failed for shape [{r}, {c}]")
+    return h
+
+
+def _rms_envelope_ok(x: np.ndarray) -> bool:
+    """Every row's sum of squares fits signed 128 bits (the producer's exact RMSNorm envelope)."""
+    lim = (1 << 127) - 1
+    for row in x:
+        m = max(abs(int(row.min())), abs(int(row.max())))
+        if m * m * x.shape[1] <= lim:
+            continue
+        if sum(int(v) * int(v) for v in row) > lim:
+            return False
+    return True
+
+
+def rmsnorm_router(gain_handle: int, router_handle: int, x_int, n_used: int, fa: int, fw: int, eps: int = 1):
+    """(normalized h [T, D], selected ids [T, K] int32, gates [T, K]) or None outside the envelope (the caller's
+    host path then runs); shape or runtime failures raise (qk_cuda.py:331-372)."""
+    lib = _dev()
+    if lib is None:
+        return None
+    x = np.asarray(x_int, dtype=np.int64)
+    x = x.reshape(1, -1) if x.ndim == 1 else x
+    if x.ndim != 2 or x.shape[0] <= 0 or x.shape[1] <= 0:
+        raise ValueError("resident RMSNorm/router requires a non-empty vector or 2-D activation")
+    n_used, fa, fw, eps = int(n_used), int(fa), int(fw), int(eps)
+    if not 0 < n_used <= np.iinfo(np.int32).max or not 1 <= fa <= 29 or not 0 <= fw <= 62 or \
+            not 0 <= eps < (1 << 64):
+        raise ValueError("resident RMSNorm/router parameters are outside the native envelope")
+    x = np.ascontiguousarray(x)
+    if not _rms_envelope_ok(x):
+        return None
+    rows = x.shape[0]
+    h = np.empty_like(x)
+    ids = np.empty((rows, n_used), dtype=np.int32)
+    gates = np.empty((rows, n_used), dtype=np.int64)
+    with _LOCK:
+        rc = int(lib.qk_rmsnorm_router(int(gain_handle), int(router_handle), x.ctypes.data, rows, fa, fw, eps, n_used,
+                                       h.size, ids.size, h.ctypes.data, ids.ctypes.data, gates.ctypes.data))
+    if rc == 3:
+        return None
+    if rc != 0:
+        raise CudaContextError(f"resident RMSNorm/router failed with native status {rc}")
+    return h, ids, gates
+
+
+def resident_attention_available() -> bool:
+    return _dev() is not None
+
+
+def resident_layer_available() -> bool:
+    return _dev() is not None
+
+
+class ResidentLayerHidden:
+    """Marker for the M=1 residual a bank retains between MoE layers (no host activation)."""
+
+    __slots__ = ("_cache", "_generation", "shape")
+
+    def __init__(self, cache, generation: int):
+        self._cache, self._generation = cache, int(generation)
+        self.shape = (1, cache.d_model)
+
+
+class ResidentAttentionCache:
+    """Request-scoped device K/V bank with the exact M=1 attention sublayer and the MoE layer begin / continue
+    chain (qk_cuda.py:476-715). A failed native call poisons the layer and raises CudaContextError."""
+
+    def __init__(self, n_layers: int, max_length: int, d_model: int, n_heads: int, n_kv: int, head_dim: int,
+                 fa: int, cos, sin):
+        lib = _dev()
+        if lib is None:
+            raise CudaContextError("resident attention context API is unavailable")
+        n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa = (
+            int(v) for v in (n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa))
+        if min(n_layers, max_length, d_model, n_heads, n_kv, head_dim) <= 0 or n_heads % n_kv or head_dim % 2 or \
+                not 1 <= fa <= 29 or d_model % 256 or (n_heads * head_dim) % 256:
+            raise ValueError("invalid resident attention dimensions")
+        c = np.ascontiguousarray(np.asarray(cos, dtype=np.int64))
+        s = np.ascontiguousarray(np.asarray(sin, dtype=np.int64))
+        if c.shape != (max_length, head_dim // 2) or s.shape != c.shape:
+            raise ValueError(f"resident attention RoPE tables must both have shape {(max_length, head_dim // 2)}")
+        with _LOCK:
+            self.handle = int(lib.qk_attention_bank_create(n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa,
+                                                           c.ctypes.data, s.ctypes.data))
+        if self.handle < 0:
+            raise CudaContextError("resident attention context creation failed")
+        self.n_layers, self.max_length, self.d_model = n_layers, max_length, d_model
+        self.n_heads, self.n_kv, self.head_dim, self.fa = n_heads, n_kv, head_dim, fa
+        self.q_width = n_heads * head_dim
+        self._lengths = [0] * n_layers
+        self._moe = {}
+        self._generation = 0
+        self._pending = None
+        self._closed = False
+
+    def _lib(self):
+        if self._closed:
+            raise CudaContextError("resident attention context is closed")
+        return _lib.lib()
+
+    def _inv_sqrt(self) -> int:
+        import math
+        return int(round((1.0 / math.sqrt(self.head_dim)) * (1 << self.fa)))
+
+    def length(self, layer=0):
+        return self._lengths[layer]
+
+    def import_layer(self, layer: int, k, v) -> None:
+        lib = self._lib()
+        kk = np.ascontiguousarray(np.asarray(k, dtype=np.int64))
+        vv = np.ascontiguousarray(np.asarray(v, dtype=np.int64))
+        if kk.shape != vv.shape or kk.ndim != 3 or kk.shape[0] != self.n_kv or kk.shape[2] != self.head_dim:
+            raise ValueError("resident attention import expects matching [n_kv, length, head_dim] K/V")
+        if not 0 <= int(layer) < self.n_layers or kk.shape[1] > self.max_length:
+            raise ValueError("resident attention import exceeds layer or context bounds")
+        with _LOCK:
+            rc = lib.qk_attention_bank_import(self.handle, int(layer), kk.ctypes.data, vv.ctypes.data, kk.shape[1])
+        if rc != 0:
+            raise CudaContextError(f"resident attention K/V import failed for layer {layer}")
+        self._lengths[int(layer)] = int(kk.shape[1])
+
+    def apply(self, layer: int, q_handle: int, k_handle: int, v_handle: int, o_handle: int, hidden, fw: int,
+              window, rope: bool):
+        lib = self._lib()
+        layer = int(layer)
+        if not 0 <= layer < self.n_layers or self._lengths[layer] >= self.max_length:
+            raise ValueError("resident attention decode exceeds layer or context bounds")
+        x = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
+        if x.shape != (1, self.d_model):
+            raise ValueError(f"resident attention apply expects hidden shape (1, {self.d_model})")
+        out = np.empty((1, self.d_model), dtype=np.int64)
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_apply(self.handle, layer, int(q_handle), int(k_handle), int(v_handle),
+                                                 int(o_handle), x.ctypes.data, int(fw), -1 if window is None else int(window),
+                                                 int(bool(rope)), self._inv_sqrt(), out.size, out.ctypes.data))
+        if rc != 0:
+            why = "exact overflow guard fired" if rc == 3 else f"native status {rc}"
+            raise CudaContextError(f"resident attention apply failed for layer {layer}: {why}")
+        self._lengths[layer] += 1
+        return out
+
+    def configure_moe_layer(self, layer: int, n_experts: int, n_used: int, d_model: int, expert_ffn: int) -> None:
+        lib = self._lib()
+        cfg = tuple(int(v) for v in (n_experts, n_used, d_model, expert_ffn))
+        layer = int(layer)
+        if not 0 <= layer < self.n_layers or cfg[0] <= 0 or not 0 < cfg[1] <= cfg[0] or cfg[2] != self.d_model or \
+                cfg[3] <= 0 or cfg[2] % 256 or cfg[3] % 256:
+            raise ValueError("invalid resident MoE layer dimensions")
+        if layer in self._moe and self._moe[layer] != cfg:
+            raise ValueError("resident MoE layer cannot be reconfigured with different dimensions")
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_moe_configure(self.handle, layer, *cfg))
+        if rc != 0:
+            raise CudaContextError(f"resident MoE layer configuration failed for layer {layer}")
+        self._moe[layer] = cfg
+
+    def bind_moe_expert(self, layer: int, expert: int, gate_handle: int, up_handle: int, down_handle: int) -> None:
+        lib = self._lib()
+        layer, expert = int(layer), int(expert)
+        if layer not in self._moe or not 0 <= expert < self._moe[layer][0]:
+            raise ValueError("resident MoE expert binding is outside the configured layer")
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_moe_bind(self.handle, layer, expert, int(gate_handle), int(up_handle),
+                                                    int(down_handle)))
+        if rc != 0:
+            raise CudaContextError(f"resident MoE expert binding failed for layer {layer}, expert {expert}")
+
+    def begin_moe_layer(self, layer: int, gain_handle: int, router_handle: int, q_handle: int, k_handle: int,
+                        v_handle: int, o_handle: int, hidden, fw: int, eps: int, window, rope: bool) -> tuple:
+        lib = self._lib()
+        layer = int(layer)
+        if layer not in self._moe or self._pending is not None or self._lengths[layer] >= self.max_length:
+            raise ValueError("resident MoE layer begin violates configuration, pending, or context bounds")
+        retained = isinstance(hidden, ResidentLayerHidden)
+        if retained:
+            if hidden._cache is not self or hidden._generation != self._generation:
+                raise ValueError("resident hidden marker is stale or belongs to another request")
+            xp = None
+        else:
+            x = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
+            if x.shape != (1, self.d_model):
+                raise ValueError(f"resident MoE layer begin expects hidden shape (1, {self.d_model})")
+            xp = x.ctypes.data
+        used = self._moe[layer][1]
+        cold = np.empty(used, dtype=np.int32)
+        count = ctypes.c_int(0)
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_moe_begin(
+                self.handle, layer, int(gain_handle), int(router_handle), int(q_handle), int(k_handle),
+                int(v_handle), int(o_handle), xp, int(retained), int(fw), int(eps),
+                -1 if window is None else int(window), int(bool(rope)), self._inv_sqrt(), cold.size,
+                ctypes.byref(count), cold.ctypes.data))
+        if rc != 0:
+            why = "exact overflow guard fired" if rc == 3 else f"native status {rc}"
+            raise CudaContextError(f"resident MoE layer begin failed for layer {layer}: {why}")
+        n = int(count.value)
+        if not 0 <= n <= used:
+            raise CudaContextError("resident MoE layer returned an invalid cold-route count")
+        self._lengths[layer] += 1
+        self._pending = layer
+        return tuple(int(e) for e in cold[:n])
+
+    def continue_moe_layer(self, layer: int, fw: int, *, publish: bool = False):
+        lib = self._lib()
+        layer = int(layer)
+        if self._pending != layer:
+            raise ValueError("resident MoE continuation has no matching prepared layer")
+        out = np.empty((1, self.d_model), dtype=np.int64) if publish else None
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_moe_continue(self.handle, layer, int(fw), int(bool(publish)),
+                                                        0 if out is None else out.size,
+                                                        None if out is None else out.ctypes.data))
+        if rc != 0:
+            why = ("selected cold experts remain unbound" if rc == 4 else
+                   "exact overflow guard fired" if rc == 3 else f"native status {rc}")
+            raise CudaContextError(f"resident MoE continuation failed for layer {layer}: {why}")
+        self._pending = None
+        self._generation += 1
+        return out if publish else ResidentLayerHidden(self, self._generation)
+
+    def export_moe_hidden(self) -> np.ndarray:
+        lib = self._lib()
+        if self._pending is not None:
+            raise CudaContextError("resident MoE hidden cannot be exported from this context state")
+        out = np.empty((1, self.d_model), dtype=np.int64)
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_moe_export(self.handle, out.size, out.ctypes.data))
+        if rc != 0:
+            raise CudaContextError("resident MoE hidden export failed")
+        return out
+
+    def workspace_bytes(self) -> int:
+        lib = self._lib()
+        with _LOCK:
+            v = int(lib.qk_attention_bank_workspace_bytes(self.handle))
+        if v == (1 << 64) - 1:
+            raise CudaContextError("resident attention workspace accounting failed")
+        return v
+
+    def reset(self) -> None:
+        lib = self._lib()
+        with _LOCK:
+            rc = int(lib.qk_attention_bank_reset(self.handle))
+        if rc != 0:
+            raise CudaContextError("resident attention context reset failed")
+        self._lengths = [0] * self.n_layers
+        self._generation += 1
+        self._pending = None
+
+    def close(self) -> None:
+        if not self._closed:
+            with _LOCK:
+                _lib.lib().qk_attention_bank_destroy(self.handle)
+            self._closed = True
+            self._pending = None
+            self._generation += 1

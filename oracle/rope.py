@@ -104,3 +104,18 @@ def apply_neox_rows(x: np.ndarray, cos_rows: np.ndarray, sin_rows: np.ndarray, f
     out[..., :half] = (x[..., :half] * c - x[..., half:] * s) >> np.int64(frac)
     out[..., half:] = (x[..., :half] * s + x[..., half:] * c) >> np.int64(frac)
     return out
+
+
+def apply_interleaved(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, frac: int) -> np.ndarray:
+    """Pairwise (x[2i], x[2i+1]) rotation of x (..., seq, hd) with rows cos[:seq] (the cohere2 / north-mini-code
+    convention, north-mini-code/src/nmc/_bonsai/rope.py:79-100); raises on the int64 envelope (rope.py:26-39)."""
+    x = np.asarray(x, dtype=np.int64)
+    seq = x.shape[-2]
+    c, s = cos[:seq], sin[:seq]
+    if x.size and c.size and 2 * _absmax(x) * max(_absmax(c), _absmax(s)) > INT64_MAX:
+        raise OverflowError("RoPE apply overflows int64")
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    out = np.empty_like(x)
+    out[..., 0::2] = (x0 * c - x1 * s) >> np.int64(frac)
+    out[..., 1::2] = (x0 * s + x1 * c) >> np.int64(frac)
+    return out

@@ -71,3 +71,20 @@ def test_exact_norm_helpers_host():
         for v in vals[:40]:
             v &= (1 << 128) - 1
             assert so.imie_fx_div_u128(v >> 64, v & ((1 << 64) - 1), d) == (v // d) & ((1 << 64) - 1), (v, d)
+
+
+def test_exports_every_symbol_the_reference_nmc_loader_requires():
+    """north-mini-code/src/nmc/qk_cuda.py:39-72 (_REQUIRED_CUDA_SYMBOLS) and the ABI version it checks (:22, 83-92):
+    the reference bridge binds this library unchanged."""
+    names = """qk_cuda_abi_version qk_linear_cuda qk_cuda_available qk_register_weight qk_register_i64
+    qk_resident_reserve qk_apply_resident qk_apply_resident_grouped qk_rmsnorm_router qk_attention_bank_create
+    qk_attention_bank_import qk_attention_bank_apply qk_attention_bank_moe_configure qk_attention_bank_moe_bind
+    qk_attention_bank_moe_begin qk_attention_bank_moe_continue qk_attention_bank_moe_export
+    qk_attention_bank_workspace_bytes qk_attention_bank_reset qk_attention_bank_destroy qk_free_all
+    qk_resident_count qk_resident_capacity qk_moe_workspace_allocations qk_moe_workspace_bytes
+    qk_moe_workspace_release qk_moe_ffn qk_moe_ffn_batched qk_moe_ffn_batched_dp4a qk_profile_reset
+    qk_profile_set_enabled qk_profile_snapshot""".split()
+    assert len(names) == 32
+    so = _lib.lib()
+    assert [n for n in names if not hasattr(so, n)] == []
+    assert so.qk_cuda_abi_version() == 5

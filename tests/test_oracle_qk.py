@@ -117,3 +117,25 @@ def test_moe_composition_tracks_float_math():
             want[t] += gate * (W["down"] @ a)
     rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
     assert rel < 5e-3, rel
+
+
+def test_interleaved_rope_is_neox_on_a_permuted_head():
+    """Pairwise (2i, 2i+1) rotation == the NeoX (i, i + hd/2) rotation after the even/odd -> halves permutation."""
+    from oracle.rope import apply_interleaved, apply_neox, build_rope_tables
+    rng = np.random.default_rng(12)
+    hd, seq = 16, 5
+    cos, sin = build_rope_tables(seq, hd, base=50000, frac=16)
+    x = rng.integers(-(1 << 30), 1 << 30, size=(3, seq, hd), dtype=np.int64)
+    perm = np.concatenate([np.arange(0, hd, 2), np.arange(1, hd, 2)])
+    got = apply_interleaved(x, cos, sin, 16)
+    want = np.empty_like(x)
+    want[..., perm] = apply_neox(x[..., perm], cos, sin, 16)
+    assert np.array_equal(got, want)
+
+
+def test_router_logits_guard():
+    from oracle.nmc_block import router_logits
+    h = np.array([[1 << 40, 1 << 40]], dtype=np.int64)
+    assert router_logits(h, np.array([[3, -2]], dtype=np.int64), 4).tolist() == [[(1 << 40) >> 4]]
+    with pytest.raises(OverflowError):
+        router_logits(h, np.array([[1 << 30, 1 << 30]], dtype=np.int64), 4)
