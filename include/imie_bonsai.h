@@ -147,6 +147,9 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t *ebits, const int64_t *escale
 /* Ragged paged cache: sequence b gets room for caps[b] positions; the cache is replaced (lengths restart at 0).
  * No reference counterpart (the reference decode context is dense). */
 int imie_net_set_caps(int64_t ctx, const int64_t *caps);
+/* Every sequence back to length 0 with the pools kept (no reference counterpart: the receipt verifier's repeated
+   prefills). Synchronous. */
+int imie_net_reset(int64_t ctx);
 /* Seeded synthetic K/V for lens[b] positions per sequence, generated on the device (benchmark / large-context
  * test workloads; no reference counterpart). Values uniform in [lo, hi); seq_ids (nullable) keys each
  * sequence's draw. */
@@ -176,7 +179,7 @@ int imie_sample_token(const int64_t *logits, int64_t vocab, const ImieSamplerCon
                       int64_t history_n, int64_t position, int64_t *token);
 /* Device rows (no reference counterpart: the sampled decode step without a logits row on the host): token_dev[r]
  * for logits_dev[r * ld ...], history hist_dev[r * hist_ld + i] (i < hist_len_dev[r]), draw key pos_dev[r].
- * Asynchronous on `stream`; *status_dev |= 2 on the temperature guard, |= 1 on a bad history token. The first
+ * Asynchronous on `stream` (null: the default stream); *status_dev |= 2 on the temperature guard, |= 1 on a bad history token. The first
  * call for a shape sizes the workspace (synchronous); later calls only launch kernels. */
 int imie_sample_dev(const int64_t *logits_dev, int64_t rows, int64_t vocab, int64_t ld, const ImieSamplerConfig *cfg,
                     const int64_t *hist_dev, int64_t hist_ld, const int64_t *hist_len_dev, const int64_t *pos_dev,
@@ -192,6 +195,11 @@ int imie_net_decode_sampled_dev(int64_t ctx, const uint8_t *ebits, const int64_t
 /* Test hook (no reference counterpart): the device SHA-256 counter word 0 and the Lemire value for
  * (total, seed, position) (sampler.py:283-315). */
 int imie_sample_draw_probe(int64_t total, int64_t seed, int64_t position, uint64_t *word0, int64_t *target);
+/* logits_digest (sampler.py:421-425) on the device: digest_dev (rows, 32) = SHA-256 of each row's little-endian
+   int64 bytes (row stride ld). Used by the receipt re-execution (verify.py:156-235) to commit every row without a
+   device-to-host copy of the logits. Asynchronous on `stream` (null: the default stream). */
+int imie_logits_digest_dev(const int64_t *logits_dev, int64_t rows, int64_t vocab, int64_t ld, uint8_t *digest_dev,
+                           void *stream);
 
 #ifdef __cplusplus
 }

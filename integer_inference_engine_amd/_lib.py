@@ -28,6 +28,7 @@ SIGNATURES = {
     "imie_sample_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p]),
     "imie_sample_draw_probe": (c_int, [c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_logits_digest_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_net_decode_sampled_dev": (c_int, [c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_int64, c_void_p, c_int64, c_int, c_void_p]),
     "imie_profile_begin": (None, []),
@@ -70,6 +71,7 @@ SIGNATURES = {
     "bonsai_decode_ctx_seed_seq": (c_int, [c_int64, c_int64, c_void_p, c_void_p, c_int64]),
     "bonsai_decode_step": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
     "bonsai_decode_ctx_free": (None, [c_int64]),
+    "imie_net_reset": (c_int, [c_int64]),
     "imie_net_forward_dev": (c_int, [c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
     "imie_net_head_dev": (c_int, [c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),

@@ -798,6 +798,18 @@ int imie_net_set_caps(int64_t ctx, const int64_t* caps) {
   return net_alloc_kv(*n, std::vector<int64_t>(caps, caps + n->B), n->P, n->kv32);
 }
 
+// Restart every sequence at length 0, keeping the allocated pools and page tables (no reference counterpart; the
+// receipt verifier's repeated prefills of one context). Clears the kv8 running maxima. Synchronous.
+int imie_net_reset(int64_t ctx) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  Net* n = net_get(ctx);
+  if (!n) return IMIE_EARG;
+  IMIE_HIP(hipDeviceSynchronize());
+  n->len.assign((size_t)n->B, 0);
+  if (n->kv32 && n->kvrun.p) IMIE_HIP(hipMemset(n->kvrun.p, 0, (size_t)(n->nl * 2 * n->B * n->Hkv) * 8));
+  return IMIE_OK;
+}
+
 // Fill every layer's cache with seeded synthetic K / V for lens[b] positions per sequence, on the device (no
 // reference counterpart; the workload generator of the benchmark and the large-context tests). Values are
 // uniform in [lo, hi); see kv_fill_kernel for the stream; seq_ids[b] (0..511, nullptr: b) keys sequence b's

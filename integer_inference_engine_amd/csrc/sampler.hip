@@ -155,6 +155,73 @@ __device__ inline uint64_t smp_sha256_first8(const uint32_t m[16]) {
   return ((uint64_t)(0x6a09e667u + a) << 32) | (uint64_t)(0xbb67ae85u + b);
 }
 
+// One SHA-256 compression of a 64-byte block (w[0..15] big-endian message words) into the running state
+__device__ inline void smp_sha256_compress(uint32_t st[8], uint32_t w[16]) {
+  uint32_t a = st[0], b = st[1], c = st[2], d = st[3], e = st[4], f = st[5], g = st[6], h = st[7];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    uint32_t wi;
+    if (i < 16) {
+      wi = w[i];
+    } else {                                          // rolling 16-word schedule
+      const uint32_t w15 = w[(i - 15) & 15], w2 = w[(i - 2) & 15];
+      const uint32_t s0 = smp_rotr(w15, 7) ^ smp_rotr(w15, 18) ^ (w15 >> 3);
+      const uint32_t s1 = smp_rotr(w2, 17) ^ smp_rotr(w2, 19) ^ (w2 >> 10);
+      wi = w[i & 15] + s0 + w[(i - 7) & 15] + s1;
+      w[i & 15] = wi;
+    }
+    const uint32_t S1 = smp_rotr(e, 6) ^ smp_rotr(e, 11) ^ smp_rotr(e, 25);
+    const uint32_t ch = (e & f) ^ (~e & g);
+    const uint32_t t1 = h + S1 + ch + kSha256K[i] + wi;
+    const uint32_t S0 = smp_rotr(a, 2) ^ smp_rotr(a, 13) ^ smp_rotr(a, 22);
+    const uint32_t mj = (a & b) ^ (a & c) ^ (b & c);
+    h = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + S0 + mj;
+  }
+  st[0] += a; st[1] += b; st[2] += c; st[3] += d; st[4] += e; st[5] += f; st[6] += g; st[7] += h;
+}
+
+// logits_digest (sampler.py:421-425): SHA-256 of a row's little-endian int64 bytes, one lane per row. The
+// message is vocab * 8 bytes, so whole 8-byte values fill the blocks and the tail holds 0..7 values.
+__global__ __launch_bounds__(64) void smp_digest_kernel(const int64_t* __restrict__ x, int64_t rows, int64_t vocab,
+                                                        int64_t ld, uint32_t* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (r >= rows) return;
+  const uint64_t* p = reinterpret_cast<const uint64_t*>(x + r * ld);
+  uint32_t st[8] = {0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au,
+                    0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u};
+  uint32_t w[16];
+  const int64_t full = vocab / 8;                     // 8 values = one 64-byte block
+  for (int64_t blk = 0; blk < full; ++blk) {
+    uint64_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(p + blk * 8 + j);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      w[2 * j] = __builtin_bswap32((uint32_t)v[j]);
+      w[2 * j + 1] = __builtin_bswap32((uint32_t)(v[j] >> 32));
+    }
+    smp_sha256_compress(st, w);
+  }
+  const int tail = (int)(vocab - full * 8);           // 0..7 values left
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {                       // static indices keep w in registers
+    const uint64_t v = j < tail ? p[full * 8 + j] : 0;
+    w[2 * j] = j < tail ? __builtin_bswap32((uint32_t)v) : (j == tail ? 0x80000000u : 0u);   // 0x80 pad byte
+    w[2 * j + 1] = j < tail ? __builtin_bswap32((uint32_t)(v >> 32)) : 0u;
+  }
+  const uint64_t bits = (uint64_t)vocab * 64;
+  if (tail >= 7) {                                    // no room for the 8-byte length: one more block
+    smp_sha256_compress(st, w);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = 0;
+  }
+  w[14] = (uint32_t)(bits >> 32);
+  w[15] = (uint32_t)bits;
+  smp_sha256_compress(st, w);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) out[r * 8 + j] = __builtin_bswap32(st[j]);   // digest bytes in order
+}
+
 // "trinote-sampler-draw/v1" || seed || position || counter (8 bytes each, big-endian), SHA-256, first 8 bytes
 __device__ inline uint64_t smp_prng_word(uint64_t seed, uint64_t pos, uint64_t ctr) {
   uint8_t msg[64];
@@ -643,7 +710,7 @@ int imie_sample_dev(const int64_t* logits_dev, int64_t rows, int64_t vocab, int6
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   if (!cfg || imie_device_ready() != 0) return IMIE_EARG;
   return imie_sample_launch(logits_dev, rows, vocab, ld, *cfg, hist_dev, hist_ld, hist_len_dev, pos_dev, token_dev,
-                            status_dev, stream ? (hipStream_t)stream : imie_stream());
+                            status_dev, (hipStream_t)stream);
 }
 
 // Host row: sample_token(logits_row, cfg, position, frac, history_ids) (sampler.py:403-437). rc 0, 1 (bad
@@ -673,6 +740,20 @@ int imie_sample_token(const int64_t* logits, int64_t vocab, const ImieSamplerCon
   if (stat & IMIE_EARG) return IMIE_EARG;
   if (stat & IMIE_EOVF) return IMIE_EOVF;
   *token = out[0];
+  return IMIE_OK;
+}
+
+// logits_digest on the device (sampler.py:421-425): digests (rows, 32) bytes of SHA-256 over each row's
+// little-endian int64 bytes. Asynchronous on `stream`.
+int imie_logits_digest_dev(const int64_t* logits_dev, int64_t rows, int64_t vocab, int64_t ld, uint8_t* digest_dev,
+                           void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!logits_dev || !digest_dev || rows <= 0 || vocab <= 0 || ld < vocab || imie_device_ready() != 0)
+    return IMIE_EARG;
+  if ((reinterpret_cast<uintptr_t>(digest_dev) & 3) != 0) return IMIE_EARG;
+  hipLaunchKernelGGL(smp_digest_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0,
+                     (hipStream_t)stream, logits_dev, rows, vocab, ld, (uint32_t*)digest_dev);
+  IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
 

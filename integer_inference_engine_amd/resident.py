@@ -52,6 +52,12 @@ class ResidentNet:
         if rc != 0:
             raise RuntimeError(f"set_caps rc={rc}: {_lib.last_error()}")
 
+    def reset(self) -> None:
+        """Every sequence back to length 0; the pools stay allocated."""
+        rc = self.lib.imie_net_reset(self.h)
+        if rc != 0:
+            raise RuntimeError(f"reset rc={rc}: {_lib.last_error()}")
+
     def fill_kv(self, seed: int, lens, lo: int = -(1 << 20), hi: int = 1 << 20, seq_ids=None) -> None:
         """Seeded synthetic K/V (device-generated) for lens[b] positions of every layer; sets the lengths.
         seq_ids[b] keys sequence b's draw (default b)."""
