@@ -115,6 +115,12 @@ def test_sampled_audit_uses_the_reference_selection(verifier):
     assert res["ok"] and res["checked"] == 4 and res["of"] == 9 and res["strategy"] == "greedy-sampled"
     assert [p["position"] - 3 for p in res["positions"]] == chosen
     assert [p["logitsDigest"] for p in res["positions"]] == [_digest(rows[i]) for i in chosen]
+    v.DIGEST_DEVICE_MIN_ROWS = 1                                 # the device digest path on the same rows
+    try:
+        again = V.verify_sampled(v, inp, out, k=4, seed=7)
+    finally:
+        v.DIGEST_DEVICE_MIN_ROWS = 64
+    assert again == res
 
 
 def test_penalized_greedy_and_sliding_window(verifier):
@@ -157,6 +163,11 @@ def test_cached_replay_strategies(verifier):
     pen_out, _ = _produce(model, inp, 6, pen, v.eff)
     samp = _cfg("top_k", temperature=0.8, top_k=9, seed=5)
     samp_out, _ = _produce(model, inp, 6, samp, v.eff)
+    assert v.receipt_verify_cached_threshold is None                     # "auto" never replays on the device
+    assert V.verify_greedy(v, inp, greedy_out * 6)["strategy"] == "greedy-full"
+    v.receipt_verify_strategy = "cached-replay"                            # explicit replay, no threshold
+    assert V.verify_greedy(v, inp, greedy_out)["strategy"] == "greedy-cached-replay"
+    v.receipt_verify_strategy = "auto"
     v.receipt_verify_cached_threshold = 1
     try:
         res = V.verify_greedy(v, inp, greedy_out)
@@ -173,5 +184,5 @@ def test_cached_replay_strategies(verifier):
         with pytest.raises(ValueError, match="exceeds the exact context window"):
             V.verify_greedy(v, list(range(v.eff)), greedy_out)
     finally:
-        v.receipt_verify_cached_threshold = 64
+        v.receipt_verify_cached_threshold = None
         v.receipt_verify_strategy = "auto"
