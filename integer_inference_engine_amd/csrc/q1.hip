@@ -40,6 +40,7 @@ struct Q1Weight {
   int64_t N = 0, nb = 0, ntiles = 0, nslabs = 0;
   uint4* bits = nullptr;
   void* scale = nullptr;
+  uint4* signs = nullptr;          // prefill copy: +-1 int8 per weight in MFMA operand order (made on first use)
   int scale64 = 0;
   int64_t maxsc = 0;               // max |scale| (host-side bounds for the GEMM epilogue)
   size_t bytes = 0;
@@ -447,12 +448,14 @@ __global__ __launch_bounds__(64) void q1_prep_gemm_kernel(const int64_t* __restr
 }
 
 struct GemmArgs {
+  const uint4* signs;              // q1_gemm_pm_kernel: [o][block][8] uint4 of +-1 bytes
   const uint4* bitsT;
   const void* scaleT;
   const uint4* xg;
   const int64_t* tg;
   const int* lt;
   int64_t T, Tp, N, nb, nbp, nslabs, ntt, nto;
+  int64_t ntiles16;                // 16 * tiles: rows of the tiled scale layout
   int frac, accumulate;
   int kfold;                       // > 0: high-dword epilogue (narrow kernel), folded every kfold blocks
   int64_t* out;
@@ -716,6 +719,275 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------------
+// Prefill GEMM over a +-1 sign copy of the weight (T >= kPmMinT tokens, int32 scales with the high-dword
+// epilogue). With the 288 GB of HBM a second copy of 1 byte per weight is affordable for prefill, and it takes
+// the per-block work off the VALU: no bit expansion, and S = sum(sign * x) comes straight out of the MFMA (no
+// 2 * pos - total correction). Operands are staged with buffer loads at per-thread offsets fixed for the whole
+// loop and a uniform per-block offset, so the loop carries no address arithmetic.
+// Sign layout: signs[(o * nb + b) * 8 + c] (uint4): byte k of chunk c is +1 when bit c of byte k of the block's
+// 16 bit-bytes is set, else -1; chunk c = 4 h + g is the B operand of lane group g in K half h, the same chunk
+// index the digit table uses for the A operand, so both sides of the MFMA see the same K order.
+// ------------------------------------------------------------------------------------------------------
+constexpr int64_t kPmMinT = 256;
+
+__global__ __launch_bounds__(256) void q1_signs_kernel(const uint4* __restrict__ bitsT, int64_t N, int64_t nb,
+                                                       int64_t nslabs, uint4* __restrict__ signs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N * nb) return;
+  const int64_t o = i / nb, b = i - (i / nb) * nb;
+  const uint4 w = bitsT[((o >> 4) * nslabs + (b >> 2)) * 64 + 16 * (b & 3) + (o & 15)];
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    uint32_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = 0xFFFFFFFFu ^ (((ww[q] >> c) & 0x01010101u) * 0xFEu);   // 1 -> 0x01, 0 -> 0xFF
+    signs[i * 8 + c] = uint4{v[0], v[1], v[2], v[3]};
+  }
+}
+
+__device__ inline __amdgpu_buffer_rsrc_t pm_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 B per lane from global straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds; M0 = lds)
+__device__ inline void pm_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Tile 128 tokens x 128 outputs, 8 waves (4 token quarters x 2 output halves, each 32 x 64 as in the narrow
+// kernel). Operands of block b + 1 are copied from global memory straight into the other half of a
+// double-buffered LDS ring while block b computes (no staging registers, one barrier per block). Rows (tokens,
+// outputs) are 8 chunks of 16 B with chunk c stored at slot c ^ ((row >> 1) & 7): the 16 lanes that read one
+// chunk of 16 consecutive rows hit 16 distinct bank groups, and since every wave's rows start at a multiple of
+// 16 the swizzle term depends on the lane only, so each operand read is one ds_read_b128 at a constant offset.
+constexpr int kPmTok = 128;
+
+__global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg_bytes, uint32_t sg_bytes,
+                                                         uint32_t sc_bytes) {
+  constexpr int MT = 2, NT = 4;
+  // per-slab limb maxima of the two 64-token halves: a half whose slab needs more than 3 limbs leaves that slab to
+  // q1_gemm_wide_kernel, which decides on the same 64-token tiles
+  __shared__ int s_lw[2][kGemmMaxSlabs];
+  // the two halves of the ring are separate arrays: reads of one half then carry no wait on copies into the other
+  __shared__ v4i sA0[kNarrowLimbs][kPmTok * 8], sA1[kNarrowLimbs][kPmTok * 8];   // 2 x 48 KB
+  __shared__ v4i sB0[128 * 8], sB1[128 * 8];                                      // 2 x 16 KB
+  __shared__ int32_t sS0[128], sS1[128];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t ntt = (a.T + kPmTok - 1) / kPmTok, wg = blockIdx.x;
+  int64_t tt, ot;
+  bool live;
+  if (ntt >= 8) {                                     // each XCD walks whole token tiles (their digits stay in L2)
+    const int64_t xcd = wg & 7, j = wg >> 3, tpx = (ntt + 7) / 8;
+    tt = xcd + 8 * (j / a.nto);
+    ot = j % a.nto;
+    live = tt < ntt && (j / a.nto) < tpx;
+  } else {
+    tt = wg / a.nto;
+    ot = wg % a.nto;
+    live = tt < ntt;
+  }
+  if (!live) return;
+  const int64_t t0g = tt * kPmTok, o0g = ot * 128;
+  for (int64_t q = wave; q < 2 * a.nslabs; q += 8) {  // (half, slab) limb maxima over 64 tokens each
+    const int hh = (int)(q & 1);
+    const int64_t sl = q >> 1, t = t0g + 64 * hh + lane;
+    int L = t < a.T ? a.lt[t * a.nslabs + sl] : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int w2 = __shfl_xor(L, o, 64); L = w2 > L ? w2 : L; }
+    if (lane == 0) s_lw[hh][sl] = L;
+  }
+  const int m = lane & 15, g = lane >> 4;
+  const int tb = (wave >> 1) * 32, ob = (wave & 1) * 64;
+  const __amdgpu_buffer_rsrc_t rA = pm_rsrc(a.xg, xg_bytes), rB = pm_rsrc(a.signs, sg_bytes),
+                               rS = pm_rsrc(a.scaleT, sc_bytes);
+  // DMA roles: A = 3 limbs x 16 row groups of 8 tokens = 48 copies of 1 KB, 6 per wave; B = 16 row groups of 8
+  // outputs, 2 per wave. Lane L of a copy fills slot L & 7 of row (L >> 3) of the group.
+  const int drow = lane >> 3, dslot = lane & 7;
+  uint32_t voA[6], voB[2];
+#pragma unroll
+  for (int q = 0; q < 6; ++q) {
+    const int rg = (wave * 6 + q) & 15, t = rg * 8 + drow;
+    voA[q] = (uint32_t)(t0g + t) * 128u + (uint32_t)(dslot ^ ((t >> 1) & 7)) * 16u;
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r = (wave * 2 + q) * 8 + drow;
+    const int64_t o = o0g + r < a.N ? o0g + r : a.N - 1;                     // clamp: padding columns unused
+    voB[q] = (uint32_t)o * (uint32_t)a.nb * 128u + (uint32_t)(dslot ^ ((r >> 1) & 7)) * 16u;
+  }
+  const int64_t so_ = o0g + (tid & 127) < a.ntiles16 ? o0g + (tid & 127) : a.ntiles16 - 1;
+  const uint32_t voS = (uint32_t)(((so_ >> 4) * a.nslabs * 64 + (so_ & 15)) * 4);
+  const uint32_t limb_stride = (uint32_t)a.nbp * (uint32_t)a.Tp * 128u, blk_stride = (uint32_t)a.Tp * 128u;
+  auto issue = [&](int64_t b, v4i (*dA)[kPmTok * 8], v4i* dB) {
+    const int l0 = s_lw[0][b >> 2], l1 = s_lw[1][b >> 2];
+    const int a0 = l0 <= kNarrowLimbs ? l0 : 0, a1 = l1 <= kNarrowLimbs ? l1 : 0;
+    const int lwb = a0 > a1 ? a0 : a1;                // limbs needed by the halves this kernel computes
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const int qi = wave * 6 + q, l = qi >> 4, rg = qi & 15;
+      if (l < lwb)
+        pm_dma(rA, &dA[l][rg * 64], voA[q], (uint32_t)l * limb_stride + (uint32_t)b * blk_stride);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) pm_dma(rB, &dB[(wave * 2 + q) * 64], voB[q], (uint32_t)b * 128u);
+  };
+  auto load_scale = [&](int64_t b) -> int32_t {
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rS, (int)voS, (int)((((b >> 2) * 64) + 16 * (b & 3)) * 4), 0);
+  };
+  int64_t acc[MT][NT][4];
+  int32_t part[MT][NT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { acc[i][jj][r] = 0; part[i][jj][r] = 0; }
+  // per-lane physical chunk of K half h (the swizzle term (row >> 1) & 7 is (m >> 1) & 7 for every read row)
+  const int pc0 = (0 + g) ^ ((m >> 1) & 7), pc1 = (4 + g) ^ ((m >> 1) & 7);
+  __syncthreads();                                    // s_lw
+  issue(0, sA0, sB0);
+  if (tid < 128) sS0[tid] = load_scale(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int fcount = 0;
+  // one block from (cA, cB, cS) while block b + 1 is copied into (nA, nB, nS)
+  auto step = [&](int64_t b, const v4i (*cA)[kPmTok * 8], const v4i* cB, const int32_t* cS, v4i (*nA)[kPmTok * 8],
+                  v4i* nB, int32_t* nS) {
+    const bool more = b + 1 < a.nb;
+    int32_t ps = 0;
+    if (more) {
+      issue(b + 1, nA, nB);
+      if (tid < 128) ps = load_scale(b + 1);
+    }
+    const int lw = s_lw[wave >> 2][b >> 2];             // this wave's 64-token half
+    if (lw <= kNarrowLimbs) {
+      v4i bx[NT][2];
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) {
+        const int r = ob + 16 * jj + m;
+        bx[jj][0] = cB[r * 8 + pc0];
+        bx[jj][1] = cB[r * 8 + pc1];
+      }
+      int32_t scp[NT];
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) scp[jj] = (int32_t)((uint32_t)cS[ob + 16 * jj + m] << (32 - a.frac));
+      if (lw == kNarrowLimbs) {
+        // the common case, chain-major: every (token tile, output tile) chain runs its three limbs (and the
+        // shifts between them) on its own, so one chain's VALU work overlaps the other chains' MFMAs
+        v4i av[kNarrowLimbs][MT][2];
+#pragma unroll
+        for (int l = 0; l < kNarrowLimbs; ++l)
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const int r = tb + 16 * i + m;
+            av[l][i][0] = cA[l][r * 8 + pc0];
+            av[l][i][1] = cA[l][r * 8 + pc1];
+          }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj) {
+            v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[2][i][0], bx[jj][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[2][i][1], bx[jj][1], c, 0, 0, 0);
+#pragma unroll
+            for (int l = 1; l >= 0; --l) {
+              c = v4i{(int)((uint32_t)c[0] << 8), (int)((uint32_t)c[1] << 8), (int)((uint32_t)c[2] << 8),
+                      (int)((uint32_t)c[3] << 8)};
+              c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[l][i][0], bx[jj][0], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[l][i][1], bx[jj][1], c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)   // high dword of S * (scale << (32 - frac)) = floor(S * scale / 2^frac)
+              part[i][jj][r] = (int32_t)((uint32_t)part[i][jj][r] + (uint32_t)__mulhi(c[r], scp[jj]));
+          }
+      } else {
+        v4i D[MT][NT];
+        {
+          const int l = lw - 1;
+          v4i av[MT][2];
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const int r = tb + 16 * i + m;
+            av[i][0] = cA[l][r * 8 + pc0];
+            av[i][1] = cA[l][r * 8 + pc1];
+          }
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int jj = 0; jj < NT; ++jj) {
+              const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+              D[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], c, 0, 0, 0);
+            }
+        }
+        for (int l = lw - 2; l >= 0; --l) {
+          v4i av[MT][2];
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const int r = tb + 16 * i + m;
+            av[i][0] = cA[l][r * 8 + pc0];
+            av[i][1] = cA[l][r * 8 + pc1];
+          }
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int jj = 0; jj < NT; ++jj) {
+              v4i c = D[i][jj];
+              c = v4i{(int)((uint32_t)c[0] << 8), (int)((uint32_t)c[1] << 8), (int)((uint32_t)c[2] << 8),
+                      (int)((uint32_t)c[3] << 8)};
+              c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], c, 0, 0, 0);
+              D[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], c, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int jj = 0; jj < NT; ++jj)
+              part[i][jj][r] = (int32_t)((uint32_t)part[i][jj][r] + (uint32_t)__mulhi(D[i][jj][r], scp[jj]));
+      }
+      if (++fcount == a.kfold) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[i][jj][r] = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)(int64_t)part[i][jj][r]);
+              part[i][jj][r] = 0;
+            }
+        fcount = 0;
+      }
+    }
+    if (more && tid < 128) nS[tid] = ps;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of block b + 1 have landed
+    __syncthreads();                                  // ... and every wave's; block b's half is free again
+  };
+  for (int64_t b = 0; b < a.nb; b += 2) {
+    step(b, sA0, sB0, sS0, sA1, sB1, sS1);
+    if (b + 1 < a.nb) step(b + 1, sA1, sB1, sS1, sA0, sB0, sS0);
+  }
+  const int64_t t0 = t0g + tb, o0 = o0g + ob;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      const int64_t o = o0 + 16 * jj + m;
+      if (o >= a.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 16 * i + 4 * g + r;
+        if (t >= a.T) continue;
+        const int64_t v = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)(int64_t)part[i][jj][r]);
+        int64_t* dst = a.out + t * a.N + o;
+        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)v) : v;
+      }
+    }
+}
+
 // blocks whose slab needs more than kNarrowLimbs limbs on the workgroup's tokens; adds into out
 template <bool S64>
 __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
@@ -850,10 +1122,33 @@ static bool gemm_fast_epi() {
   return v;
 }
 
+// +-1 sign GEMM for T >= kPmMinT (IMIE_GEMM_PM=0 disables; tuning and tests)
+static bool gemm_pm() {
+  static const bool v = [] { const char* e = getenv("IMIE_GEMM_PM"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
+// The weight's sign copy, made on first use (1 byte per weight). Not made while `st` is being captured into a
+// graph (allocation is not capturable); the caller then uses the bit kernels.
+static int q1_ensure_signs(Q1Weight& w, hipStream_t st) {
+  if (w.signs) return 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return 1;
+  const size_t bytes = (size_t)w.N * w.nb * 128;
+  if (hipMalloc((void**)&w.signs, bytes) != hipSuccess) { w.signs = nullptr; (void)hipGetLastError(); return 1; }
+  const int64_t n = w.N * w.nb;
+  hipLaunchKernelGGL(q1_signs_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint4*)w.bits, w.N,
+                     w.nb, w.nslabs, w.signs);
+  if (hipGetLastError() != hipSuccess) { (void)hipFree(w.signs); w.signs = nullptr; return 1; }
+  w.bytes += bytes;
+  g_resident_bytes += bytes;
+  return 0;
+}
+
 static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
                          int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
   const Q1Weight& w0 = *ws[0];
-  const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks, Tp = (T + 63) / 64 * 64;
+  const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks, Tp = (T + kPmTok - 1) / kPmTok * kPmTok;
   if (nslabs > kGemmMaxSlabs) return IMIE_EARG;
   if (wk.xq.ensure((size_t)kMaxLimbs * nbp * Tp * 128) || wk.totals.ensure((size_t)nbp * Tp * 8) ||
       wk.lslab.ensure((size_t)T * nslabs * 4))
@@ -868,9 +1163,10 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
   for (int i = 0; i < cnt; ++i) {
     const Q1Weight& w = *ws[i];
     GemmArgs ga;
+    ga.signs = nullptr;
     ga.bitsT = w.bits; ga.scaleT = w.scale; ga.xg = (const uint4*)wk.xq.p; ga.tg = (const int64_t*)wk.totals.p;
     ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
-    ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128;
+    ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128; ga.ntiles16 = w.ntiles * 16;
     ga.frac = (int)(frac > 63 ? 63 : frac); ga.accumulate = accumulate; ga.out = outs[i];
     const dim3 grid((unsigned)(ga.ntt >= 8 ? 8 * ((ga.ntt + 7) / 8) * ga.nto : ga.ntt * ga.nto));
     const int nbuf = gemm_nbuf();
@@ -882,7 +1178,17 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
       const int64_t k = (((int64_t)1 << 31) - 1) / max_q - 1;
       ga.kfold = (int)(k < 1 ? 1 : (k > (1 << 20) ? (1 << 20) : k));
     }
-    if (w.scale64) {
+    const uint64_t xg_bytes = (uint64_t)kNarrowLimbs * nbp * Tp * 128, sg_bytes = (uint64_t)w.N * w.nb * 128,
+                   sc_bytes = (uint64_t)w.ntiles * nslabs * 64 * 4;
+    if (!w.scale64 && ga.kfold > 0 && T >= kPmMinT && gemm_pm() && xg_bytes < (1ull << 32) &&
+        sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32) && q1_ensure_signs(const_cast<Q1Weight&>(w), st) == 0) {
+      ga.signs = w.signs;
+      const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
+      const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * ga.nto : ntt128 * ga.nto));
+      hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
+                         (uint32_t)sc_bytes);
+      hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+    } else if (w.scale64) {
       if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), grid, dim3(256), 0, st, ga);
       else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), grid, dim3(256), 0, st, ga);
       hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
@@ -1140,6 +1446,7 @@ int bonsai_q1_linear_gpu(const int64_t* x, const uint8_t* bits, const int64_t* s
   const int rc = q1_host_apply(registry()[(size_t)h], x, tokens, frac, out);
   Q1Weight& w = registry()[(size_t)h];
   (void)hipFree(w.bits); (void)hipFree(w.scale);
+  if (w.signs) (void)hipFree(w.signs);
   g_resident_bytes -= w.bytes;
   w.live = false;
   if (h == (int64_t)registry().size() - 1) registry().pop_back();
@@ -1172,7 +1479,7 @@ void bonsai_q1_free_weights(void) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   (void)hipStreamSynchronize(imie_stream());
   for (auto& w : registry())
-    if (w.live) { (void)hipFree(w.bits); (void)hipFree(w.scale); }
+    if (w.live) { (void)hipFree(w.bits); (void)hipFree(w.scale); if (w.signs) (void)hipFree(w.signs); }
   registry().clear();
   g_resident_bytes = 0;
 }

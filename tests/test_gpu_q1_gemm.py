@@ -101,3 +101,69 @@ def test_gemm_high_dword_epilogue_extremes(gpu, frac):
     x[16:24] = -cap3
     got = gpu.q1_apply_gpu(x, bits, scale, frac)
     assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, frac))
+
+
+# ---- T >= 256: the +-1 sign-copy kernel (int32 scales under 2^(frac-1)) -----------------------------------------
+@pytest.mark.parametrize("N,nb,T", [(129, 32, 300), (1000, 8, 256), (4096, 32, 512), (72, 3, 1000)])
+def test_gemm_sign_copy_shapes(gpu, N, nb, T):
+    seed = N * 11 + nb * 5 + T
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << 11), 1 << 11)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -(1 << 22), 1 << 22)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, c_oracle.q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("frac", [16, 31])
+def test_gemm_sign_copy_epilogue_extremes(gpu, frac):
+    """As the high-dword extremes above, at T = 320: |S| ~ 2^30 per block, scales at +-(2^(frac-1) - 1)."""
+    cap3 = 127 * (1 + 256 + 65536)
+    N, nb, T = 48, 32, 320
+    rng = np.random.default_rng(50 + frac)
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    bits[:8] = 0xFF
+    bits[8:16] = 0
+    smax = (1 << (frac - 1)) - 1
+    scale = rng.choice(np.array([smax, -smax, smax - 1, 1], dtype=np.int64), size=(N, nb))
+    scale[:4] = smax
+    scale[8:12] = -smax
+    x = rng.choice(np.array([cap3, -cap3, cap3 - 1, 0], dtype=np.int64), size=(T, nb * 128))
+    x[:16] = cap3
+    x[16:24] = -cap3
+    got = gpu.q1_apply_gpu(x, bits, scale, frac)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, frac))
+
+
+def test_gemm_sign_copy_with_wide_slabs(gpu):
+    """Some slabs need more than 3 limbs on some token tiles: those blocks go to the wide kernel, which adds into
+    the same outputs."""
+    N, nb, T = 200, 16, 384
+    bits = prng.uniform_bytes(77, 1, (N, nb, 16))
+    scale = prng.uniform_int(77, 2, (N, nb), -(1 << 12), 1 << 12)
+    x = prng.uniform_int(77, 3, (T, nb * 128), -(1 << 20), 1 << 20)
+    big = prng.uniform_int(77, 4, (T, nb * 128), -(1 << 45), 1 << 45)
+    x[100:140, 512:1024] = big[100:140, 512:1024]           # slab 1 of token tiles 1 and 2
+    x[300, 1900] = (1 << 62)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+def test_gemm_sign_copy_resident_lifecycle(gpu):
+    """The sign copy is made once per resident weight on its first T >= 256 use (N * K bytes), reused, and
+    released with the weight."""
+    N, nb, T = 300, 12, 260
+    bits = prng.uniform_bytes(8, 1, (N, nb, 16))
+    scale = prng.uniform_int(8, 2, (N, nb), -(1 << 12), 1 << 12)
+    x = prng.uniform_int(8, 3, (T, nb * 128), -(1 << 21), 1 << 21)
+    gpu.q1_free_weights()
+    h = gpu.q1_register_weight(bits, scale)
+    base = gpu.gpu_memory_info()["resident_weight_bytes"]
+    small = gpu.q1_apply_resident(h, x[:40], N, nb, 16)
+    assert gpu.gpu_memory_info()["resident_weight_bytes"] == base
+    want = q1_linear(x, bits, scale, 16)
+    assert np.array_equal(small, want[:40])
+    for _ in range(2):
+        assert np.array_equal(gpu.q1_apply_resident(h, x, N, nb, 16), want)
+        assert gpu.gpu_memory_info()["resident_weight_bytes"] == base + N * nb * 128
+    gpu.q1_free_weights()
+    assert gpu.gpu_memory_info()["resident_weight_bytes"] == 0
