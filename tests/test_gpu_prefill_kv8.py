@@ -32,15 +32,16 @@ def _net(gpu, model, B, cap, page=64):
                        dff=cfg["dff"], cap=cap, w=w, g=g, page=page, kv32=True)
 
 
-@pytest.mark.parametrize("T", [2, 17, 64, 100])
+@pytest.mark.parametrize("T", [2, 17, 64, 100, 256])
 def test_small_model_prefill_kv8(gpu, T):
+    """T = 256 runs the projections on the +-1 sign-copy GEMM (wo / w2 accumulating into the residual)."""
     import torch
-    model = workloads.small_bonsai(seed=50 + T, ctx=256)
+    model = workloads.small_bonsai(seed=50 + T, ctx=320)
     cfg = model["cfg"]
     c = {"H": cfg["H"], "Hkv": cfg["Hkv"], "hd": cfg["hd"]}
     ids = prng.uniform_int(T, 5, (T,), 0, cfg["vocab"])
     x0 = q1_rows(*model["embed"], ids)
-    net = _net(gpu, model, 1, 192)
+    net = _net(gpu, model, 1, 320)
     try:
         x = torch.from_numpy(x0.copy()).cuda()
         assert net.forward(x, [0], T) == 0
