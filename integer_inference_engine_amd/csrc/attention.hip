@@ -1022,6 +1022,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
 // as 4 MFMA tiles of 16. MFMA rows are the 16 query rows; each limb lq is a separate A operand and the products
 // are summed per exponent e = lq + b in int32 (|T_e| <= 4 * 2 * 2^20), then S = sum_e T_e << 8e in int64.
 constexpr int kPfKeys = 256;
+constexpr int kPfTilesPerWg = 8;                      // key tiles per workgroup, all sharing one q setup
 __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
   __shared__ __align__(16) int8_t sQ[8][16][128];
   __shared__ uint64_t s_mq[16];
@@ -1031,7 +1032,7 @@ __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
   const int64_t bkv = imie_udiv32(blockIdx.x, nrt), rt = imie_umod32(blockIdx.x, nrt);
   const int64_t b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t rows = d.B * d.H * d.M;
-  const int64_t j0 = (int64_t)blockIdx.y * kPfKeys;
+  const int64_t jw = (int64_t)blockIdx.y * kPfKeys * kPfTilesPerWg;
   const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
   int64_t vismax = 0;
@@ -1042,7 +1043,7 @@ __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
       vismax = lv > vismax ? lv : vismax;
     }
   }
-  if (j0 >= vismax) return;
+  if (jw >= vismax) return;
   // q rows: thread -> row tid / 16, dims 8 * (tid % 16) .. + 7
   const int qi = tid >> 4, qc = 8 * (tid & 15);
   const int64_t qgr = rt * 16 + qi;
@@ -1080,70 +1081,75 @@ __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
     rr[i] = gr < grows ? group_row(d, b, kv, gr) : -1;
     lvr[i] = gr < grows ? (d.starts ? d.starts[b] + imie_umod32(gr, d.M) + 1 : len) : 0;
   }
-  int64_t pm[4] = {INT64_MIN, INT64_MIN, INT64_MIN, INT64_MIN};
   const int8_t* Kb = (const int8_t*)d.K;
-  for (int st = 0; st < 4; ++st) {
-    const int64_t t = j0 + 64 * wave + 16 * st;
-    if (t >= vismax) break;
-    const int64_t j = t + m;
-    const bool valid = j < len;
-    v4i bk[4][2];
-    int64_t base = 0, slot = 0;
-    if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
+  for (int kti = 0; kti < kPfTilesPerWg; ++kti) {
+    const int64_t kt = (int64_t)blockIdx.y * kPfTilesPerWg + kti, j0 = kt * kPfKeys;
+    if (j0 >= vismax) break;                            // uniform: later tiles see no row of this workgroup
+    int64_t pm[4] = {INT64_MIN, INT64_MIN, INT64_MIN, INT64_MIN};
+    for (int st = 0; st < 4; ++st) {
+      const int64_t t = j0 + 64 * wave + 16 * st;
+      if (t >= vismax) break;
+      const int64_t j = t + m;
+      const bool valid = j < len;
+      v4i bk[4][2];
+      int64_t base = 0, slot = 0;
+      if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
-                        ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
-                        : v4i{0, 0, 0, 0};
-    v4i T[8];
+        for (int h = 0; h < 2; ++h)
+          bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
+                          ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
+                          : v4i{0, 0, 0, 0};
+      v4i T[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T[e] = v4i{0, 0, 0, 0};
+      for (int e = 0; e < 8; ++e) T[e] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int lq = 0; lq < 8; ++lq) {                  // compile-time limb index: T stays in registers
-      if (lq < Lq) {
-        v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
-        v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
-        if (16 * g >= d.hd) a0 = v4i{0, 0, 0, 0};
-        if (64 + 16 * g >= d.hd) a1 = v4i{0, 0, 0, 0};
+      for (int lq = 0; lq < 8; ++lq) {                  // compile-time limb index: T stays in registers
+        if (lq < Lq) {
+          v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
+          v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
+          if (16 * g >= d.hd) a0 = v4i{0, 0, 0, 0};
+          if (64 + 16 * g >= d.hd) a1 = v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          if (lq + db >= 8) continue;                 // 256^(lq+db) = 0 mod 2^64
-          v4i x = mfma8(a0, bk[db][0], T[lq + db]);
-          if (KS > 1) x = mfma8(a1, bk[db][1], x);
-          T[lq + db] = x;
+          for (int db = 0; db < 4; ++db) {
+            if (lq + db >= 8) continue;                 // 256^(lq+db) = 0 mod 2^64
+            v4i x = mfma8(a0, bk[db][0], T[lq + db]);
+            if (KS > 1) x = mfma8(a1, bk[db][1], x);
+            T[lq + db] = x;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint64_t S = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) S += (uint64_t)(int64_t)T[e][i] << (8 * e);   // 256^e = 0 mod 2^64, e >= 8
+        if (rr[i] >= 0 && j < lvr[i]) {
+          int64_t sc = (int64_t)S >> d.frac;
+          sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+          d.scores[rr[i] * d.Lmax + j] = sc;
+          pm[i] = sc > pm[i] ? sc : pm[i];
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint64_t S = 0;
+      int64_t mx = pm[i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) S += (uint64_t)(int64_t)T[e][i] << (8 * e);   // 256^e = 0 mod 2^64, e >= 8
-      if (rr[i] >= 0 && j < lvr[i]) {
-        int64_t sc = (int64_t)S >> d.frac;
-        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
-        d.scores[rr[i] * d.Lmax + j] = sc;
-        pm[i] = sc > pm[i] ? sc : pm[i];
+      for (int o = 8; o >= 1; o >>= 1) { const int64_t w2 = __shfl_xor(mx, o, 64); mx = w2 > mx ? w2 : mx; }
+      if (m == 0) s_pm[wave][4 * g + i] = mx;
+    }
+    __syncthreads();
+    if (tid < 16) {
+      const int64_t gr = rt * 16 + tid;
+      if (gr < grows) {
+        int64_t mx = s_pm[0][tid];
+        for (int w = 1; w < 4; ++w) mx = s_pm[w][tid] > mx ? s_pm[w][tid] : mx;
+        d.pmax[kt * rows + group_row(d, b, kv, gr)] = mx;
       }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int64_t mx = pm[i];
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) { const int64_t w2 = __shfl_xor(mx, o, 64); mx = w2 > mx ? w2 : mx; }
-    if (m == 0) s_pm[wave][4 * g + i] = mx;
-  }
-  __syncthreads();
-  if (tid < 16) {
-    const int64_t gr = rt * 16 + tid;
-    if (gr < grows) {
-      int64_t mx = s_pm[0][tid];
-      for (int w = 1; w < 4; ++w) mx = s_pm[w][tid] > mx ? s_pm[w][tid] : mx;
-      d.pmax[blockIdx.y * rows + group_row(d, b, kv, gr)] = mx;
-    }
+    __syncthreads();                                    // s_pm is reused by the next key tile
   }
 }
 
@@ -1625,7 +1631,8 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
   if (d.kv32) {                                      // kv8 prefill: MFMA scores, softmax to p digits, MFMA PV
     if (d.hd % 16 != 0 || !d.run_k || !d.run_v) return IMIE_EARG;
     const int64_t nrt16 = (grows + 15) / 16, nkt8 = (d.Lmax + kPfKeys - 1) / kPfKeys;
-    hipLaunchKernelGGL(pf_scores8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16), (unsigned)nkt8), dim3(256), 0, st, d);
+    const int64_t nkg = (nkt8 + kPfTilesPerWg - 1) / kPfTilesPerWg;
+    hipLaunchKernelGGL(pf_scores8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16), (unsigned)nkg), dim3(256), 0, st, d);
     IMIE_HIP(hipGetLastError());
     if (d.Lmax <= 64 * kSmPer)
       hipLaunchKernelGGL(pf_softmax8_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, d);
