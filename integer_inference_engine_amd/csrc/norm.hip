@@ -294,11 +294,19 @@ int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t fr
   else if (force_nt == 256)
     hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
+  else if (force_nt == 512)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 512, 8>), dim3((unsigned)rows), dim3(512), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, z);
   else if (cols <= 256)
     hipLaunchKernelGGL((rmsnorm_kernel<false, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
                        gain, out, status, po, z);
   else if (cols <= 1024)
     hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+                       eps, gain, out, status, po, z);
+  else if (rows >= 64 && cols <= 4096)
+    // many rows (prefill): 256 threads x 16 cached columns keep more rows in flight per CU than 1024 x 4; measured
+    // 47 us against 71 us for 2048 rows of 4096 on MI355X (a single row is latency-bound and keeps 1024 threads)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   else
     hipLaunchKernelGGL((rmsnorm_kernel<false, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,

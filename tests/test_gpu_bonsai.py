@@ -20,7 +20,8 @@ def assert_same(got, want, what=""):
     assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[0]}: {got.ravel()[bad[0]]} != {want.ravel()[bad[0]]}"
 
 
-@pytest.mark.parametrize("rows,cols,mag", [(1, 4096, 25), (40, 128, 14), (7, 4096, 40), (3, 96, 57), (2, 12288, 20)])
+@pytest.mark.parametrize("rows,cols,mag", [(1, 4096, 25), (40, 128, 14), (7, 4096, 40), (3, 96, 57), (2, 12288, 20),
+                                           (70, 4096, 30), (64, 2560, 20)])
 def test_rmsnorm_matches_oracle(gpu, rows, cols, mag):
     x = prng.uniform_int(mag, 1, (rows, cols), -(1 << mag), 1 << mag)
     g = prng.uniform_int(mag, 2, (cols,), 1 << 15, 1 << 17)
