@@ -59,6 +59,27 @@ __global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t*
   out[i] = up ? (int64_t)((uint64_t)silu * (uint64_t)up[i]) >> frac : silu;
 }
 
+// silu_mul for the GEMM: one wave per (token, 512-slab) computes h at its eight table positions and writes the
+// GEMM digit table directly (the prep of the next projection, without h round-tripping through HBM)
+__global__ __launch_bounds__(64) void silu_mul_gemm_prep_kernel(const int64_t* __restrict__ gate,
+                                                                const int64_t* __restrict__ up, int64_t n, int frac,
+                                                                int64_t log2e, int64_t dclip, imie_q1::GemmPrepOut gp) {
+  const int lane = threadIdx.x;
+  const int64_t sl = blockIdx.x, t = blockIdx.y;
+  int64_t v[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int64_t p = imie_q1::prep_pos(lane, sl, q);
+    v[q] = 0;
+    if (p < n) {
+      const int64_t g = gate[t * n + p];
+      const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
+      v[q] = (int64_t)((uint64_t)silu * (uint64_t)up[t * n + p]) >> frac;
+    }
+  }
+  imie_q1::prep_gemm_slab(v, gp, t, sl);
+}
+
 // silu_mul for one (token, 512-slab): thread per element into LDS, then wave 0 builds the slab's digit table
 __global__ __launch_bounds__(512) void silu_mul_prep_kernel(const int64_t* __restrict__ gate,
                                                             const int64_t* __restrict__ up, int64_t n, int frac,
@@ -224,6 +245,18 @@ int imie_silu_mul_prep_launch(const int64_t* gate, const int64_t* up, int64_t T,
   silu_consts(frac, &log2e, &dclip);
   hipLaunchKernelGGL(silu_mul_prep_kernel, dim3((unsigned)po.nslabs, (unsigned)T), dim3(512), 0, st, gate, up, n,
                      (int)frac, log2e, dclip, out, po);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_silu_mul_gemm_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
+                                   const imie_q1::GemmPrepOut& gp, hipStream_t st) {
+  if (T <= 0) return IMIE_OK;
+  if (n != gp.nb * 128 || frac < 1 || frac > 62) return IMIE_EARG;
+  int64_t log2e, dclip;
+  silu_consts(frac, &log2e, &dclip);
+  hipLaunchKernelGGL(silu_mul_gemm_prep_kernel, dim3((unsigned)gp.nslabs, (unsigned)T), dim3(64), 0, st, gate, up, n,
+                     (int)frac, log2e, dclip, gp);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

@@ -45,6 +45,13 @@ int imie_rope_launch(const int64_t* x, int64_t rows, int64_t nh, int64_t hd, con
 int imie_rope_guard_check(const uint64_t* guard, int* status, hipStream_t st);
 
 // h = ((silu(gate) * up) >> frac) with the bonsai wrap semantics (reference_bonsai.py:245-264, 611-614)
+// The GEMM digit table (T >= kGemmMinT) of wk for weights of nb blocks; a producer that writes it passes
+// prepped = 2 to imie_q1_launch_multi.
+int imie_q1_gemm_target(Q1Ws* wk, int64_t nb, int64_t T, imie_q1::GemmPrepOut* gp);
+// h = silu(gate) * up >> frac for T >= kGemmMinT rows of n = nb * 128 straight into the GEMM digit table gp (h
+// itself is not stored): SiLU * up fused with the prep of the next GEMM.
+int imie_silu_mul_gemm_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
+                                   const imie_q1::GemmPrepOut& gp, hipStream_t st);
 int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int64_t frac, int64_t* out,
                          hipStream_t st);
 int imie_silu_launch(const int64_t* x, int64_t n, int64_t frac, int64_t* out, hipStream_t st);

@@ -23,6 +23,14 @@ struct Q1PrepOut {                 // where a prep writes its table (sized for T
   int64_t nb, nbp, nslabs;
 };
 
+struct GemmPrepOut {               // the GEMM digit table (T >= kGemmMinT): xg[limb][block][Tp][s], tg, lt
+  uint4* xg;
+  int64_t* tg;
+  int* lt;
+  int64_t nb, nbp, nslabs, Tp;
+};
+constexpr int kGemmNarrowLimbs = 3;  // the GEMM's narrow kernels read 3 limbs; the prep zero-fills up to that
+
 struct Q1Zero {                    // outputs a producer clears before a K-split matvec adds into them
   int64_t* p[kMaxSegs];
   int64_t n[kMaxSegs];
@@ -72,6 +80,43 @@ __device__ inline void prep_slab(int64_t v[8], const Q1PrepOut& po, int64_t t, i
 __device__ inline void zero_share(const Q1Zero& z, int64_t wg, int64_t nwg, int tid, int nthreads) {
   for (int i = 0; i < z.cnt; ++i)
     for (int64_t e = wg * nthreads + tid; e < z.n[i]; e += nwg * nthreads) z.p[i][e] = 0;
+}
+
+// GEMM table entries of token t, slab sl from v[q] = x at prep_pos(lane, sl, q) (0 beyond the row): the slab's
+// limb count (its max|x| over the 64 lanes), per-block totals, and balanced base-256 digits for every limb up to
+// max(L, kGemmNarrowLimbs) (zeros above L). One full wave.
+__device__ inline void prep_gemm_slab(int64_t v[8], const GemmPrepOut& gp, int64_t t, int64_t sl) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
+  const int64_t blk = sl * kSlabBlocks + g;
+  uint64_t mx = 0;
+  int64_t part = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint64_t a = imie_absu64(v[q]);
+    mx = a > mx ? a : mx;
+    part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
+  }
+  mx = imie_wave_max_u64(mx);
+  const int L = imie_limbs_needed(mx);
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
+  if ((lane & 15) == 0) gp.tg[blk * gp.Tp + t] = part;
+  if (lane == 0) gp.lt[t * gp.nslabs + sl] = L;
+  const int Lw = L > kGemmNarrowLimbs ? L : kGemmNarrowLimbs;
+  for (int l = 0; l < Lw; ++l) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t dig = ((v[q] + 128) & 255) - 128;
+      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;
+      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
+      if (q < 4) w0 |= byte; else w1 |= byte;
+    }
+    uint32_t* dst = (uint32_t*)(gp.xg + ((l * gp.nbp + blk) * gp.Tp + t) * 8 + s);
+    dst[2 * dh] = w0;
+    dst[2 * dh + 1] = w1;
+  }
 }
 
 }  // namespace imie_q1

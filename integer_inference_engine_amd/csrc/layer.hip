@@ -302,6 +302,11 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       CK(imie_q1_prep_target(&n.q1w, n.dff / 128, rows, &po));
       CK(imie_silu_mul_prep_launch(gate, up, rows, n.dff, n.frac, hh, po, st));
       CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st, 1));
+    } else if (n.dff % 128 == 0) {                 // GEMM: SiLU * up writes the down projection's digit table
+      imie_q1::GemmPrepOut gp;
+      CK(imie_q1_gemm_target(&n.q1w, n.dff / 128, rows, &gp));
+      CK(imie_silu_mul_gemm_prep_launch(gate, up, rows, n.dff, n.frac, gp, st));
+      CK(imie_q1_launch_multi(&L.w[6], 1, nullptr, rows, n.frac, &x, 1, &n.q1w, st, 2));
     } else {
       CK(imie_silu_mul_launch(gate, up, rows * n.dff, n.frac, hh, st));
       CK(imie_q1_launch_multi(&L.w[6], 1, hh, rows, n.frac, &x, 1, &n.q1w, st));

@@ -403,48 +403,19 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
 // Digit table layout for the GEMM: xg[l][block][Tp][s] (uint4), totals tg[block][Tp], limbs lt[t][slab]; the
 // prep writes zero digits for limbs L_t <= l < 3 so narrow tiles need no per-token masking.
 // ------------------------------------------------------------------------------------------------------
-constexpr int kNarrowLimbs = 3;
+constexpr int kNarrowLimbs = kGemmNarrowLimbs;
 constexpr int kGemmMaxSlabs = 64;  // K <= 32768
 
-__global__ __launch_bounds__(64) void q1_prep_gemm_kernel(const int64_t* __restrict__ x, int64_t K, int64_t nb,
-                                                           int64_t nbp, int64_t nslabs, int64_t Tp,
-                                                           uint4* __restrict__ xg, int64_t* __restrict__ tg,
-                                                           int* __restrict__ lt) {
+__global__ __launch_bounds__(64) void q1_prep_gemm_kernel(const int64_t* __restrict__ x, int64_t K, GemmPrepOut gp) {
   const int lane = threadIdx.x;
   const int64_t sl = blockIdx.x, t = blockIdx.y;
-  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
-  const int64_t blk = sl * kSlabBlocks + g;
   int64_t v[8];
-  uint64_t mx = 0;
-  int64_t part = 0;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int64_t pos = prep_pos(lane, sl, q);
-    v[q] = (pos < nb * 128) ? x[t * K + pos] : 0;
-    const uint64_t a = imie_absu64(v[q]);
-    mx = a > mx ? a : mx;
-    part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
+    v[q] = (pos < gp.nb * 128) ? x[t * K + pos] : 0;
   }
-  mx = imie_wave_max_u64(mx);
-  const int L = imie_limbs_needed(mx);
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
-  if ((lane & 15) == 0) tg[blk * Tp + t] = part;
-  if (lane == 0) lt[t * nslabs + sl] = L;
-  const int Lw = L > kNarrowLimbs ? L : kNarrowLimbs;
-  for (int l = 0; l < Lw; ++l) {
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t dig = ((v[q] + 128) & 255) - 128;
-      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;
-      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
-      if (q < 4) w0 |= byte; else w1 |= byte;
-    }
-    uint32_t* dst = (uint32_t*)(xg + ((l * nbp + blk) * Tp + t) * 8 + s);
-    dst[2 * dh] = w0;
-    dst[2 * dh + 1] = w1;
-  }
+  prep_gemm_slab(v, gp, t, sl);
 }
 
 struct GemmArgs {
@@ -1145,20 +1116,32 @@ static int q1_ensure_signs(Q1Weight& w, hipStream_t st) {
   return 0;
 }
 
-static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
-                         int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st) {
-  const Q1Weight& w0 = *ws[0];
-  const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks, Tp = (T + kPmTok - 1) / kPmTok * kPmTok;
+// The GEMM table of T tokens for weights of nb blocks (imie_q1_gemm_target and the prep below agree on it).
+static int gemm_table(Q1Ws& wk, int64_t nb, int64_t T, GemmPrepOut* gp) {
+  const int64_t nslabs = (nb + kSlabBlocks - 1) / kSlabBlocks, nbp = nslabs * kSlabBlocks;
+  const int64_t Tp = (T + kPmTok - 1) / kPmTok * kPmTok;
   if (nslabs > kGemmMaxSlabs) return IMIE_EARG;
   if (wk.xq.ensure((size_t)kMaxLimbs * nbp * Tp * 128) || wk.totals.ensure((size_t)nbp * Tp * 8) ||
       wk.lslab.ensure((size_t)T * nslabs * 4))
     return IMIE_EARG;
-  const int64_t K = w0.nb * 128;
-  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
-  hipLaunchKernelGGL(q1_prep_gemm_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, w0.nb, nbp,
-                     nslabs, Tp, (uint4*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p);
-  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
-  IMIE_HIP(hipGetLastError());
+  *gp = GemmPrepOut{(uint4*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, nb, nbp, nslabs, Tp};
+  return IMIE_OK;
+}
+
+// prepped != 0: the table is already in wk (a fused producer wrote it through imie_q1_gemm_target)
+static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_dev, int64_t T, int64_t frac,
+                         int64_t* const* outs, int accumulate, Q1Ws& wk, hipStream_t st, int prepped = 0) {
+  const Q1Weight& w0 = *ws[0];
+  GemmPrepOut gp;
+  if (gemm_table(wk, w0.nb, T, &gp)) return IMIE_EARG;
+  const int64_t nslabs = gp.nslabs, nbp = gp.nbp, Tp = gp.Tp;
+  if (!prepped) {
+    imie_prof_mark(IMIE_K_Q1_PREP, st, true);
+    hipLaunchKernelGGL(q1_prep_gemm_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, w0.nb * 128,
+                       gp);
+    imie_prof_mark(IMIE_K_Q1_PREP, st, false);
+    IMIE_HIP(hipGetLastError());
+  }
   imie_prof_mark(IMIE_K_Q1_GEMM, st, true);
   for (int i = 0; i < cnt; ++i) {
     const Q1Weight& w = *ws[i];
@@ -1232,8 +1215,8 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   for (int i = 1; i < cnt; ++i)
     if (ws[i]->nb != w0.nb || ws[i]->scale64 != w0.scale64) return IMIE_EARG;
   if (T >= kGemmMinT) {
-    if (prepped) return IMIE_EARG;                    // fused producers write the matvec table (T < kGemmMinT)
-    return q1_gemm_multi(ws, cnt, x_dev, T, frac, outs, accumulate, wk, st);
+    if (prepped == 1) return IMIE_EARG;               // a matvec table (T < kGemmMinT) cannot feed the GEMM
+    return q1_gemm_multi(ws, cnt, x_dev, T, frac, outs, accumulate, wk, st, prepped);
   }
   const int64_t nslabs = w0.nslabs, nbp = nslabs * kSlabBlocks;
   if (wk.xq.ensure((size_t)T * kMaxLimbs * nbp * 8 * 16) || wk.totals.ensure((size_t)T * nbp * 8) ||
@@ -1413,6 +1396,11 @@ int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int6
     if (rc) return rc;
   }
   return IMIE_OK;
+}
+
+int imie_q1_gemm_target(Q1Ws* wk, int64_t nb, int64_t T, GemmPrepOut* gp) {
+  if (!wk || !gp || nb <= 0 || T < kGemmMinT) return IMIE_EARG;
+  return gemm_table(*wk, nb, T, gp);
 }
 
 int imie_q1_prep_target(Q1Ws* wk, int64_t nb, int64_t T, Q1PrepOut* po) {
