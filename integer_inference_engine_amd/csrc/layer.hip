@@ -237,6 +237,13 @@ int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, i
     if ((rc = imie_rmsnorm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, po, z, st))) return rc;
     return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, 1);
   }
+  if (n.d % 128 == 0 && n.d <= 4096) {                // GEMM: the norm writes the projections' digit table
+    imie_q1::GemmPrepOut gp;
+    int rc = imie_q1_gemm_target(&n.q1w, n.d / 128, rows, &gp);
+    if (rc) return rc;
+    if ((rc = imie_rmsnorm_gemm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, gp, st))) return rc;
+    return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, 2);
+  }
   int rc = imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, st);
   if (rc) return rc;
   return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st);

@@ -36,16 +36,34 @@ __device__ inline void prep_row(const int64_t* s_y, int64_t row, const imie_q1::
   imie_q1::zero_share(zero, row, (int64_t)gridDim.x, tid, nt);
 }
 
+// GEMM digit table of a row staged in LDS (T >= kGemmMinT): wave w takes slabs w, w + nw, ...
+__device__ inline void prep_row_gemm(const int64_t* s_y, int64_t row, const imie_q1::GemmPrepOut& gp, int tid, int nt) {
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+  const int64_t cols = gp.nb * 128;
+  for (int64_t sl = wave; sl < gp.nslabs; sl += nw) {
+    int64_t v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t p = imie_q1::prep_pos(lane, sl, q);
+      v[q] = p < cols ? s_y[p] : 0;
+    }
+    imie_q1::prep_gemm_slab(v, gp, row, sl);
+  }
+}
+
 // NT threads with PER cached columns each (the per-thread serial work is what bounds a single-row launch, so
 // wide rows get many threads). PREP: the row (cols = nb * 128 <= NT * PER) is also staged in LDS and turned
 // into the Q1 digit table (one wave per 512-slab), and the workgroups clear the zero list of the next matvec.
 constexpr int kPrepCols = 4096;
 
-template <bool PREP, int NT, int kNormPer>
+// PREP: 0 none, 1 the matvec digit table (po, zero), 2 the GEMM digit table (gp)
+template <int PREP, int NT, int kNormPer>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__ x, int64_t cols, int frac,
                                                       int64_t eps, const int64_t* __restrict__ gain,
                                                       int64_t* __restrict__ out, int* __restrict__ status,
-                                                      imie_q1::Q1PrepOut po, imie_q1::Q1Zero zero) {
+                                                      imie_q1::Q1PrepOut po, imie_q1::Q1Zero zero,
+                                                      imie_q1::GemmPrepOut gp = {}) {
   constexpr int NW = NT / 64;
   __shared__ int64_t s_y[PREP ? kPrepCols : 1];
   __shared__ uint64_t s_hi[NW], s_lo[NW], s_mn[NW], s_mg[NW];
@@ -129,7 +147,8 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
   }
   if (!gain) {
     if (!nfit) atomicOr(status, IMIE_ERMS);
-    if (PREP) prep_row(s_y, row, po, zero, tid, nt);
+    if (PREP == 1) prep_row(s_y, row, po, zero, tid, nt);
+    if (PREP == 2) prep_row_gemm(s_y, row, gp, tid, nt);
     return;
   }
   mxn = imie_wave_max_u64(mxn);
@@ -159,7 +178,8 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
         if (PREP) s_y[c] = y;
       }
     }
-    if (PREP) prep_row(s_y, row, po, zero, tid, nt);
+    if (PREP == 1) prep_row(s_y, row, po, zero, tid, nt);
+    if (PREP == 2) prep_row_gemm(s_y, row, gp, tid, nt);
   } else {
     for (int64_t c = tid; c < cols; c += nt) {
       bool fits;
@@ -289,27 +309,27 @@ int imie_rmsnorm_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t fr
   const imie_q1::Q1Zero z = {};
   static const int force_nt = [] { const char* e = getenv("IMIE_NORM_NT"); return e ? atoi(e) : 0; }();  // tuning
   if (force_nt == 64)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
                        gain, out, status, po, z);
   else if (force_nt == 256)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   else if (force_nt == 512)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 512, 8>), dim3((unsigned)rows), dim3(512), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 512, 8>), dim3((unsigned)rows), dim3(512), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   else if (cols <= 256)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 64, 4>), dim3((unsigned)rows), dim3(64), 0, st, x, cols, (int)frac, eps,
                        gain, out, status, po, z);
   else if (cols <= 1024)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   else if (rows >= 64 && cols <= 4096)
     // many rows (prefill): 256 threads x 16 cached columns keep more rows in flight per CU than 1024 x 4; measured
     // 47 us against 71 us for 2048 rows of 4096 on MI355X (a single row is latency-bound and keeps 1024 threads)
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   else
-    hipLaunchKernelGGL((rmsnorm_kernel<false, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<0, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, z);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
@@ -324,11 +344,24 @@ int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64
     hipLaunchKernelGGL(rmsnorm_prep_slab_kernel, dim3((unsigned)(rows + kZeroWgs)), dim3(512), 0, st, x, cols, (int)frac, eps,
                        gain, out, status, po, zero);
   else if (cols <= 1024)
-    hipLaunchKernelGGL((rmsnorm_kernel<true, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<1, 256, 4>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, zero);
   else
-    hipLaunchKernelGGL((rmsnorm_kernel<true, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
+    hipLaunchKernelGGL((rmsnorm_kernel<1, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac,
                        eps, gain, out, status, po, zero);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+int imie_rmsnorm_gemm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
+                                  const int64_t* gain, int64_t* out, int* status, const imie_q1::GemmPrepOut& gp,
+                                  hipStream_t st) {
+  if (rows <= 0) return IMIE_OK;
+  if (cols != gp.nb * 128 || cols > kPrepCols || rows < imie_q1::kGemmMinT) return IMIE_EARG;
+  const imie_q1::Q1PrepOut po = {};
+  const imie_q1::Q1Zero z = {};
+  hipLaunchKernelGGL((rmsnorm_kernel<2, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac, eps,
+                     gain, out, status, po, z, gp);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
