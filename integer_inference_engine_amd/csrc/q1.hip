@@ -429,6 +429,7 @@ struct GemmArgs {
   int64_t ntiles16;                // 16 * tiles: rows of the tiled scale layout
   int frac, accumulate;
   int kfold;                       // > 0: high-dword epilogue (narrow kernel), folded every kfold blocks
+  int ksplit;                      // narrow kernel: blocks split over gridDim.y ranges, outputs added atomically
   int64_t* out;
 };
 
@@ -578,12 +579,15 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
           accH[FE ? i : 0][FE ? jj : 0][r] = 0;
         }
   };
-  stage_load(0);
-  stage_store(0);
+  // this workgroup's block range (the whole K unless the launch splits it for a small token count)
+  const int64_t b0 = (int64_t)blockIdx.y * a.nb / a.ksplit, b1 = ((int64_t)blockIdx.y + 1) * a.nb / a.ksplit;
+  if (b0 >= b1) return;
+  stage_load(b0);
+  stage_store(NBUF == 2 ? (int)(b0 & 1) : 0);
   __syncthreads();
-  for (int64_t b = 0; b < a.nb; ++b) {
+  for (int64_t b = b0; b < b1; ++b) {
     const int buf = NBUF == 2 ? (int)(b & 1) : 0;
-    const bool more = b + 1 < a.nb;
+    const bool more = b + 1 < b1;
     if (more) stage_load(b + 1);                      // next block's operands in flight during this block
     const int lw = s_lw[b >> 2];
     if (lw <= kNarrowLimbs) {
@@ -685,7 +689,10 @@ __global__ __launch_bounds__(256) void q1_gemm_narrow_kernel(GemmArgs a) {
         const int64_t t = t0 + 16 * i + 4 * g + r;
         if (t >= a.T) continue;
         int64_t* dst = a.out + t * a.N + o;
-        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]) : acc[i][jj][r];
+        if (a.ksplit > 1)                             // sums mod 2^64 commute: the result is order independent
+          atomicAdd((unsigned long long*)dst, (unsigned long long)acc[i][jj][r]);
+        else
+          *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]) : acc[i][jj][r];
       }
     }
 }
@@ -1093,6 +1100,11 @@ static bool gemm_fast_epi() {
   return v;
 }
 
+__global__ void q1_zero_kernel(int64_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 // +-1 sign GEMM for T >= kPmMinT (IMIE_GEMM_PM=0 disables; tuning and tests)
 static bool gemm_pm() {
   static const bool v = [] { const char* e = getenv("IMIE_GEMM_PM"); return !(e && atoi(e) == 0); }();
@@ -1147,6 +1159,7 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     const Q1Weight& w = *ws[i];
     GemmArgs ga;
     ga.signs = nullptr;
+    ga.ksplit = 1;
     ga.bitsT = w.bits; ga.scaleT = w.scale; ga.xg = (const uint4*)wk.xq.p; ga.tg = (const int64_t*)wk.totals.p;
     ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
     ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128; ga.ntiles16 = w.ntiles * 16;
@@ -1171,19 +1184,35 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
       hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
                          (uint32_t)sc_bytes);
       hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
-    } else if (w.scale64) {
-      if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), grid, dim3(256), 0, st, ga);
-      else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), grid, dim3(256), 0, st, ga);
-      hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
     } else {
-      if (ga.kfold > 0) {
-        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, true>), grid, dim3(256), 0, st, ga);
-        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, true>), grid, dim3(256), 0, st, ga);
-      } else {
-        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, false>), grid, dim3(256), 0, st, ga);
-        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, false>), grid, dim3(256), 0, st, ga);
+      // few token tiles (batched decode): split K over grid.y so the launch fills the chip; each split adds its
+      // partial sums with 64-bit atomics (exact: integer sums mod 2^64 in any order)
+      const int64_t tiles = (int64_t)grid.x;
+      ga.ksplit = 1;
+      if (tiles < 256 && w.nb >= 8) {
+        const int64_t want = (512 + tiles - 1) / tiles, cap = w.nb / 4;
+        ga.ksplit = (int)(want < cap ? want : cap);
+        if (ga.ksplit < 1) ga.ksplit = 1;
       }
-      hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+      const dim3 ngrid(grid.x, (unsigned)ga.ksplit);
+      if (ga.ksplit > 1 && !accumulate) {
+        const int64_t n = T * w.N;
+        hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, outs[i], n);
+      }
+      if (w.scale64) {
+        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), ngrid, dim3(256), 0, st, ga);
+        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), ngrid, dim3(256), 0, st, ga);
+        hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
+      } else {
+        if (ga.kfold > 0) {
+          if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, true>), ngrid, dim3(256), 0, st, ga);
+          else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, true>), ngrid, dim3(256), 0, st, ga);
+        } else {
+          if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, false>), ngrid, dim3(256), 0, st, ga);
+          else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, false>), ngrid, dim3(256), 0, st, ga);
+        }
+        hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+      }
     }
     IMIE_HIP(hipGetLastError());
   }
