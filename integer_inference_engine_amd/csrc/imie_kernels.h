@@ -51,9 +51,13 @@ int imie_q1_gemm_target(Q1Ws* wk, int64_t nb, int64_t T, imie_q1::GemmPrepOut* g
 // h = silu(gate) * up >> frac for T >= kGemmMinT rows of n = nb * 128 straight into the GEMM digit table gp (h
 // itself is not stored): SiLU * up fused with the prep of the next GEMM.
 // RMSNorm of rows >= kGemmMinT rows (cols = nb * 128 <= 4096) that also writes the next GEMM's digit table gp
+// and clears the outputs in `zero` (for a K-split GEMM, which then adds into them: prepped = 3)
 int imie_rmsnorm_gemm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
                                   const int64_t* gain, int64_t* out, int* status, const imie_q1::GemmPrepOut& gp,
-                                  hipStream_t st);
+                                  const imie_q1::Q1Zero& zero, hipStream_t st);
+// Whether the GEMM of weight `handle` over T tokens is expected to split K (its outputs are then worth clearing
+// in the producer); a wrong guess costs a redundant clear or a separate one, never a wrong result
+int imie_q1_gemm_splits(int64_t handle, int64_t T);
 int imie_silu_mul_gemm_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
                                    const imie_q1::GemmPrepOut& gp, hipStream_t st);
 int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int64_t frac, int64_t* out,

@@ -241,8 +241,17 @@ int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, i
     imie_q1::GemmPrepOut gp;
     int rc = imie_q1_gemm_target(&n.q1w, n.d / 128, rows, &gp);
     if (rc) return rc;
-    if ((rc = imie_rmsnorm_gemm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, gp, st))) return rc;
-    return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, 2);
+    imie_q1::Q1Zero z = {};
+    for (int i = 0; i < cnt && imie_q1_gemm_splits(hs[i], rows); ++i) {   // K-split GEMMs add into cleared outputs
+      int64_t N = 0, nb = 0;
+      if (imie_q1_dims(hs[i], &N, &nb)) return IMIE_EARG;
+      z.p[i] = outs[i];
+      z.n[i] = rows * N;
+      z.cnt = i + 1;
+    }
+    if (z.cnt != cnt) z.cnt = 0;                      // all or none: the GEMM is told the outputs are clear
+    if ((rc = imie_rmsnorm_gemm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, gp, z, st))) return rc;
+    return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, z.cnt ? 3 : 2);
   }
   int rc = imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, st);
   if (rc) return rc;

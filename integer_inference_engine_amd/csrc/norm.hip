@@ -148,7 +148,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
   if (!gain) {
     if (!nfit) atomicOr(status, IMIE_ERMS);
     if (PREP == 1) prep_row(s_y, row, po, zero, tid, nt);
-    if (PREP == 2) prep_row_gemm(s_y, row, gp, tid, nt);
+    if (PREP == 2) { prep_row_gemm(s_y, row, gp, tid, nt); imie_q1::zero_share(zero, row, (int64_t)gridDim.x, tid, nt); }
     return;
   }
   mxn = imie_wave_max_u64(mxn);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
       }
     }
     if (PREP == 1) prep_row(s_y, row, po, zero, tid, nt);
-    if (PREP == 2) prep_row_gemm(s_y, row, gp, tid, nt);
+    if (PREP == 2) { prep_row_gemm(s_y, row, gp, tid, nt); imie_q1::zero_share(zero, row, (int64_t)gridDim.x, tid, nt); }
   } else {
     for (int64_t c = tid; c < cols; c += nt) {
       bool fits;
@@ -355,13 +355,12 @@ int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64
 
 int imie_rmsnorm_gemm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64_t frac, int64_t eps,
                                   const int64_t* gain, int64_t* out, int* status, const imie_q1::GemmPrepOut& gp,
-                                  hipStream_t st) {
+                                  const imie_q1::Q1Zero& zero, hipStream_t st) {
   if (rows <= 0) return IMIE_OK;
   if (cols != gp.nb * 128 || cols > kPrepCols || rows < imie_q1::kGemmMinT) return IMIE_EARG;
   const imie_q1::Q1PrepOut po = {};
-  const imie_q1::Q1Zero z = {};
   hipLaunchKernelGGL((rmsnorm_kernel<2, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac, eps,
-                     gain, out, status, po, z, gp);
+                     gain, out, status, po, zero, gp);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

@@ -1195,7 +1195,7 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
         if (ga.ksplit < 1) ga.ksplit = 1;
       }
       const dim3 ngrid(grid.x, (unsigned)ga.ksplit);
-      if (ga.ksplit > 1 && !accumulate) {
+      if (ga.ksplit > 1 && !accumulate && prepped != 3) {   // prepped == 3: the producer cleared the outputs
         const int64_t n = T * w.N;
         hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, outs[i], n);
       }
@@ -1425,6 +1425,14 @@ int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int6
     if (rc) return rc;
   }
   return IMIE_OK;
+}
+
+int imie_q1_gemm_splits(int64_t handle, int64_t T) {
+  const Q1Weight* w = q1_get(handle);
+  if (!w || T < kGemmMinT || T >= kPmMinT) return 0;
+  const int64_t ntt = (T + 63) / 64, nto = (w->N + 127) / 128;
+  const int64_t tiles = ntt >= 8 ? 8 * ((ntt + 7) / 8) * nto : ntt * nto;
+  return tiles < 256 && w->nb >= 8 ? 1 : 0;
 }
 
 int imie_q1_gemm_target(Q1Ws* wk, int64_t nb, int64_t T, GemmPrepOut* gp) {
