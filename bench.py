@@ -367,7 +367,8 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures ONE MI355X; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(one GPU's share of a sharded model is what runs here; the sharding itself is not built)",
+              file=sys.stderr)
         return 2
 
     import ctypes
