@@ -150,6 +150,11 @@ int imie_net_set_caps(int64_t ctx, const int64_t *caps);
 /* Every sequence back to length 0 with the pools kept (no reference counterpart: the receipt verifier's repeated
    prefills). Synchronous. */
 int imie_net_reset(int64_t ctx);
+/* gpu_native.py:334-361 / bonsai_q1_gpu.cu:2160-2197 `bonsai_gpu_reservation_create` / `_free`: reserve several
+   exact device allocations as one failure-atomic probe (returns the handle and the bytes taken, or -1 with nothing
+   left allocated); freeing twice is a no-op. */
+int64_t bonsai_gpu_reservation_create(const uint64_t *sizes, int64_t count, uint64_t *allocated);
+void bonsai_gpu_reservation_free(int64_t handle);
 /* Seeded synthetic K/V for lens[b] positions per sequence, generated on the device (benchmark / large-context
  * test workloads; no reference counterpart). Values uniform in [lo, hi); seq_ids (nullable) keys each
  * sequence's draw. */

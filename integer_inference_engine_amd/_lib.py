@@ -72,6 +72,8 @@ SIGNATURES = {
     "bonsai_decode_step": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
     "bonsai_decode_ctx_free": (None, [c_int64]),
     "imie_net_reset": (c_int, [c_int64]),
+    "bonsai_gpu_reservation_create": (c_int64, [c_void_p, c_int64, c_void_p]),
+    "bonsai_gpu_reservation_free": (None, [c_int64]),
     "imie_net_forward_dev": (c_int, [c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
     "imie_net_head_dev": (c_int, [c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "imie_net_status": (c_int, [c_int64, c_int, c_void_p]),

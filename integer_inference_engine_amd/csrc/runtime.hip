@@ -1,5 +1,6 @@
 // Process-global runtime: device probe, default stream, error notes, workspace buffers, memory info.
 #include "imie_common.h"
+#include <vector>
 #include <stdio.h>
 #include <string.h>
 
@@ -219,3 +220,39 @@ void imie_profile_end(void) {
 }
 
 }  // extern "C"
+
+// Failure-atomic device reservations (gpu_native.py:334-361 / bonsai_q1_gpu.cu:2160-2197): a memory-feasibility
+// probe that takes several exact allocations at once; a failed reservation frees what it took and returns -1.
+namespace {
+std::vector<std::vector<void*>>& reservations() {
+  static std::vector<std::vector<void*>> r;
+  return r;
+}
+}  // namespace
+
+extern "C" int64_t bonsai_gpu_reservation_create(const uint64_t* sizes, int64_t count, uint64_t* allocated) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!sizes || count <= 0 || !allocated || imie_device_ready() != 0) return -1;
+  std::vector<void*> taken;
+  uint64_t total = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    void* p = nullptr;
+    if (sizes[i] == 0 || hipMalloc(&p, (size_t)sizes[i]) != hipSuccess) {
+      (void)hipGetLastError();
+      for (void* q : taken) (void)hipFree(q);
+      return -1;
+    }
+    taken.push_back(p);
+    total += sizes[i];
+  }
+  reservations().push_back(std::move(taken));
+  *allocated = total;
+  return (int64_t)reservations().size() - 1;
+}
+
+extern "C" void bonsai_gpu_reservation_free(int64_t handle) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (handle < 0 || handle >= (int64_t)reservations().size()) return;
+  for (void* p : reservations()[(size_t)handle]) (void)hipFree(p);
+  reservations()[(size_t)handle].clear();            // a second free is a no-op
+}

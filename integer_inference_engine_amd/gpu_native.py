@@ -98,6 +98,27 @@ def q1_register_weight(bits: np.ndarray, scale_fp: np.ndarray, *, gpu_coalesced:
     return None if int(h) < 0 else int(h)
 
 
+def gpu_reservation_create(component_bytes) -> "tuple[int, int] | None":
+    """Reserve several exact device allocations as one failure-atomic probe (gpu_native.py:334-355): (handle,
+    allocated_bytes), or None with nothing left allocated."""
+    lib = _dev()
+    if lib is None:
+        return None
+    sizes = np.ascontiguousarray(np.asarray(tuple(component_bytes), dtype=np.uint64))
+    if sizes.ndim != 1 or sizes.size == 0 or np.any(sizes == 0):
+        raise ValueError("GPU reservation components must be a non-empty list of positive byte counts")
+    allocated = ctypes.c_uint64()
+    h = lib.bonsai_gpu_reservation_create(sizes.ctypes.data, int(sizes.size), ctypes.byref(allocated))
+    return None if int(h) < 0 else (int(h), int(allocated.value))
+
+
+def gpu_reservation_free(handle: int) -> None:
+    """Release a reservation; safe to call more than once."""
+    lib = _dev()
+    if lib is not None:
+        lib.bonsai_gpu_reservation_free(int(handle))
+
+
 def q1_apply_resident(handle: int, x_fp: np.ndarray, out_features: int, n_blocks: int,
                       frac: int) -> "np.ndarray | None":
     """Apply a registered weight to host activations (gpu_native.py:364-380)."""

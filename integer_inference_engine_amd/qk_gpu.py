@@ -516,3 +516,90 @@ class ResidentAttentionCache:
             self._closed = True
             self._pending = None
             self._generation += 1
+
+
+# ---- telemetry and capability probes (qk_cuda.py:24-34, 870-910, 1029-1101) ---------------------------------------
+PROFILE_METRICS = (
+    "registration_calls", "registration_ns",
+    "h2d_calls", "h2d_bytes", "h2d_ns",
+    "d2h_calls", "d2h_bytes", "d2h_ns",
+    "allocation_calls", "allocation_bytes", "allocation_ns", "free_calls",
+    "native_calls", "resident_apply_calls", "grouped_apply_calls",
+    "moe_calls", "moe_batched_calls", "moe_batched_dp4a_calls",
+    "q_projection_calls", "q_projection_ns", "k_projection_calls", "k_projection_ns",
+    "v_projection_calls", "v_projection_ns", "o_projection_calls", "o_projection_ns",
+    "other_projection_calls", "other_projection_ns",
+)
+
+
+def resident_preprocess_available() -> bool:
+    """Whether the exact resident RMSNorm / router / top-k boundary is usable (qk_cuda.py:319-322)."""
+    lib = _dev()
+    return lib is not None and hasattr(lib, "qk_register_i64") and hasattr(lib, "qk_rmsnorm_router")
+
+
+def resident_preprocess_bytes(n_layers: int, d_model: int, n_experts: int) -> int:
+    """Device bytes of the per-layer int64 norm gains plus router matrices (expert slices excluded: they are
+    registered lazily by route)."""
+    n_layers, d_model, n_experts = int(n_layers), int(d_model), int(n_experts)
+    if n_layers < 0 or d_model <= 0 or n_experts <= 0:
+        raise ValueError("resident preprocessing memory dimensions must be non-negative layers and positive widths")
+    return n_layers * (n_experts + 1) * d_model * np.dtype(np.int64).itemsize
+
+
+def profile_reset(*, enabled: bool = True) -> bool:
+    """Zero the boundary counters and enable / disable them."""
+    lib = _dev()
+    if lib is None:
+        return False
+    with _LOCK:
+        lib.qk_profile_set_enabled(0)
+        lib.qk_profile_reset()
+        lib.qk_profile_set_enabled(int(bool(enabled)))
+    return True
+
+
+def profile_set_enabled(enabled: bool) -> bool:
+    lib = _dev()
+    if lib is None:
+        return False
+    with _LOCK:
+        lib.qk_profile_set_enabled(int(bool(enabled)))
+    return True
+
+
+def profile_snapshot() -> "dict | None":
+    """Allocation / copy / call counters of the current profile window, by name."""
+    import ctypes
+    lib = _dev()
+    if lib is None:
+        return None
+    values = (ctypes.c_uint64 * len(PROFILE_METRICS))()
+    with _LOCK:
+        required = int(lib.qk_profile_snapshot(values, len(values)))
+    if required != len(PROFILE_METRICS):
+        raise RuntimeError(f"profile metric ABI mismatch: native={required}, python={len(PROFILE_METRICS)}")
+    return {name: int(values[i]) for i, name in enumerate(PROFILE_METRICS)}
+
+
+def moe_workspace_allocations() -> "int | None":
+    """Number of MoE workspace grows since free_all."""
+    lib = _dev()
+    if lib is None:
+        return None
+    with _LOCK:
+        return int(lib.qk_moe_workspace_allocations())
+
+
+def apply_resident_q6k_dp4a(handle: int, x_int: np.ndarray, out_f: int, fw: int, ln: int = None):
+    return apply_resident_dp4a(handle, x_int, out_f, fw, 1, ln)
+
+
+def moe_ffn_dp4a_available() -> bool:
+    lib = _dev()
+    return lib is not None and hasattr(lib, "qk_moe_ffn_dp4a")
+
+
+def moe_ffn_batched_dp4a_available() -> bool:
+    lib = _dev()
+    return lib is not None and hasattr(lib, "qk_moe_ffn_batched_dp4a")
