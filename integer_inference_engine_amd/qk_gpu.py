@@ -603,3 +603,129 @@ def moe_ffn_dp4a_available() -> bool:
 def moe_ffn_batched_dp4a_available() -> bool:
     lib = _dev()
     return lib is not None and hasattr(lib, "qk_moe_ffn_batched_dp4a")
+
+
+# ---- retained MoE token chain (qk_cuda.py:726-868) ------------------------------------------------------------------
+from dataclasses import dataclass
+
+
+@dataclass(frozen=True)
+class ResidentMoeLayerSpec:
+    """Resident dense-handle inputs of one M = 1 MoE layer."""
+    layer: int
+    gain_handle: int
+    router_handle: int
+    q_handle: int
+    k_handle: int
+    v_handle: int
+    o_handle: int
+    window: "int | None"
+    rope: bool
+
+
+class ResidentMoeTokenExecutor:
+    """One token through consecutive MoE layers of a ResidentAttentionCache with the hidden state retained on the
+    device between layers. ``lookup_expert(layer, e)`` returns an already resident (gate, up, down) triplet or None
+    (no side effects); ``load_expert(layer, e)`` is called only for the experts the device reports unbound. Any
+    error poisons the executor: the caller resets or destroys the bank instead of mixing partly advanced K/V with
+    another path."""
+
+    def __init__(self, cache: "ResidentAttentionCache", *, first_layer: int, layer_count: int, n_experts: int,
+                 n_used: int, d_model: int, expert_ffn: int, fw: int, eps: int, lookup_expert, load_expert):
+        if not isinstance(cache, ResidentAttentionCache) or cache._closed:
+            raise ValueError("resident token executor requires an open attention bank")
+        first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps = (
+            int(v) for v in (first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps))
+        if (first_layer < 0 or layer_count <= 0 or first_layer + layer_count > cache.n_layers or n_experts <= 0
+                or not 0 < n_used <= n_experts or d_model != cache.d_model or d_model % 256 or expert_ffn <= 0
+                or expert_ffn % 256 or not 0 <= fw <= 62 or not 0 <= eps <= (1 << 64) - 1):
+            raise ValueError("invalid resident token executor dimensions")
+        if not callable(lookup_expert) or not callable(load_expert):
+            raise TypeError("resident token executor requires expert lookup and lazy-load callables")
+        self.cache = cache
+        self.first_layer, self.layer_count = first_layer, layer_count
+        self.n_experts, self.n_used, self.d_model, self.expert_ffn = n_experts, n_used, d_model, expert_ffn
+        self.fw, self.eps = fw, eps
+        self.lookup_expert, self.load_expert = lookup_expert, load_expert
+        self._configured, self._scanned, self._bound = set(), set(), set()
+        self._poisoned = False
+
+    @property
+    def poisoned(self) -> bool:
+        return self._poisoned
+
+    @staticmethod
+    def _triplet(value, *, allow_none: bool, label: str):
+        if value is None and allow_none:
+            return None
+        try:
+            hs = tuple(int(h) for h in value)
+        except (TypeError, ValueError):
+            hs = ()
+        if len(hs) != 3 or any(h < 0 for h in hs):
+            raise CudaContextError(f"{label} did not return a valid gate/up/down handle triplet")
+        return hs
+
+    def _configure_and_bind_known(self, layer: int) -> None:
+        if layer not in self._configured:
+            self.cache.configure_moe_layer(layer, self.n_experts, self.n_used, self.d_model, self.expert_ffn)
+            self._configured.add(layer)
+        if layer in self._scanned:
+            return
+        for e in range(self.n_experts):
+            hs = self._triplet(self.lookup_expert(layer, e), allow_none=True,
+                               label=f"resident expert lookup for layer {layer}, expert {e}")
+            if hs is not None:
+                self.cache.bind_moe_expert(layer, e, *hs)
+                self._bound.add((layer, e))
+        self._scanned.add(layer)
+
+    def _specs(self, layers):
+        specs = tuple(layers)
+        want = tuple(range(self.first_layer, self.first_layer + self.layer_count))
+        if (len(specs) != self.layer_count or any(not isinstance(s, ResidentMoeLayerSpec) for s in specs)
+                or tuple(int(s.layer) for s in specs) != want):
+            raise ValueError(f"resident token executor requires consecutive layers {want[0]}..{want[-1]}")
+        return specs
+
+    def prepare(self, layers):
+        """Configure every layer and bind the experts already resident, before any K/V changes."""
+        if self._poisoned:
+            raise CudaContextError("resident token executor is poisoned; destroy or reset the request bank")
+        specs = self._specs(layers)
+        try:
+            for s in specs:
+                self._configure_and_bind_known(int(s.layer))
+            return specs
+        except Exception:
+            self._poisoned = True
+            raise
+
+    def run(self, hidden, layers) -> np.ndarray:
+        if self._poisoned:
+            raise CudaContextError("resident token executor is poisoned; destroy or reset the request bank")
+        specs = self.prepare(layers)
+        state = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
+        if state.shape != (1, self.d_model):
+            raise ValueError(f"resident token executor expects hidden shape (1, {self.d_model})")
+        try:
+            for i, s in enumerate(specs):
+                layer = int(s.layer)
+                self._configure_and_bind_known(layer)
+                cold = self.cache.begin_moe_layer(layer, int(s.gain_handle), int(s.router_handle), int(s.q_handle),
+                                                  int(s.k_handle), int(s.v_handle), int(s.o_handle), state, self.fw,
+                                                  self.eps, s.window, bool(s.rope))
+                if len(cold) != len(set(cold)) or any(not 0 <= e < self.n_experts for e in cold):
+                    raise CudaContextError(f"resident layer {layer} returned invalid cold expert IDs")
+                for e in cold:
+                    hs = self._triplet(self.load_expert(layer, e), allow_none=False,
+                                       label=f"lazy expert loader for layer {layer}, expert {e}")
+                    self.cache.bind_moe_expert(layer, e, *hs)
+                    self._bound.add((layer, e))
+                state = self.cache.continue_moe_layer(layer, self.fw, publish=i + 1 == self.layer_count)
+            if not isinstance(state, np.ndarray) or state.shape != (1, self.d_model):
+                raise CudaContextError("resident token executor did not publish its final residual")
+            return state
+        except Exception:
+            self._poisoned = True
+            raise

@@ -157,3 +157,51 @@ def test_bank_guard_poisons_layer(gpu):
         bank.apply(0, hs["wq"], hs["wk"], hs["wv"], hs["wo"], np.zeros((1, D), np.int64), FW, None, False)
     bank.close()
     qk_gpu.free_all()
+
+
+def test_token_executor_chains_layers_like_the_oracle(gpu):
+    """ResidentMoeTokenExecutor (qk_cuda.py:738-868): two consecutive layers with one expert resident up front
+    (lookup) and the rest loaded lazily on the device's cold report; result equals two oracle block steps. A bad
+    loader poisons the executor."""
+    from integer_inference_engine_amd import qk_gpu
+    W, hs, experts, eh = _weights(17)
+    cos, sin = build_rope_tables(CAP, HD, base=50000, frac=FA)
+    bank = qk_gpu.ResidentAttentionCache(2, CAP, D, H, HKV, HD, FA, cos, sin)
+    rng = np.random.default_rng(18)
+    caches = []
+    for layer in range(2):
+        L0 = 4 + layer
+        kc = np.zeros((HKV, CAP, HD), dtype=np.int64)
+        vc = np.zeros_like(kc)
+        kc[:, :L0] = rng.integers(-(1 << 17), 1 << 17, size=(HKV, L0, HD))
+        vc[:, :L0] = rng.integers(-(1 << 17), 1 << 17, size=(HKV, L0, HD))
+        bank.import_layer(layer, kc[:, :L0], vc[:, :L0])
+        caches.append([kc, vc, L0])
+    loaded = []
+    ex = qk_gpu.ResidentMoeTokenExecutor(
+        bank, first_layer=0, layer_count=2, n_experts=E, n_used=USED, d_model=D, expert_ffn=EFF, fw=FW, eps=1,
+        lookup_expert=lambda layer, e: eh[e] if (layer, e) == (1, 0) else None,
+        load_expert=lambda layer, e: loaded.append((layer, e)) or eh[e])
+    specs = [qk_gpu.ResidentMoeLayerSpec(l, hs["gain"], hs["router"], hs["wq"], hs["wk"], hs["wv"], hs["wo"],
+                                         w, r) for l, (w, r) in enumerate([(None, False), (4, True)])]
+    x = rng.integers(-(1 << 20), 1 << 20, size=(1, D), dtype=np.int64)
+    got = ex.run(x, specs)
+    want = x
+    for layer, (window, rope) in enumerate([(None, False), (4, True)]):
+        kc, vc, L0 = caches[layer]
+        want, _, sel, _, k, v = onb.block_step(want, W, kc, vc, L0, window, rope, cos, sin, CFG, experts)
+    assert np.array_equal(got, want)
+    assert (1, 0) not in loaded and loaded                 # the resident one was bound, the others loaded lazily
+    bank.reset()
+    bank2 = qk_gpu.ResidentAttentionCache(1, CAP, D, H, HKV, HD, FA, cos, sin)
+    bad = qk_gpu.ResidentMoeTokenExecutor(
+        bank2, first_layer=0, layer_count=1, n_experts=E, n_used=USED, d_model=D, expert_ffn=EFF, fw=FW, eps=1,
+        lookup_expert=lambda layer, e: None, load_expert=lambda layer, e: (1, 2))
+    with pytest.raises(qk_gpu.CudaContextError):
+        bad.run(x, specs[:1])
+    assert bad.poisoned
+    with pytest.raises(qk_gpu.CudaContextError):
+        bad.run(x, specs[:1])
+    bank2.close()
+    bank.close()
+    qk_gpu.free_all()
