@@ -80,3 +80,29 @@ def test_truncated_file_is_refused(tmp_path):
     p.write_bytes(data[:-40])
     with pytest.raises(ValueError):
         gguf.GGUF(p)
+
+
+@pytest.mark.parametrize("version,ok", [(2, True), (3, True), (1, False), (4, False)])
+def test_header_versions(tmp_path, version, ok):
+    p = tmp_path / "v.gguf"
+    write_gguf(p, [("general.architecture", "str", "qwen3")], [("g", [4], gguf.F32, np.ones(4, "<f4").tobytes())])
+    raw = bytearray(p.read_bytes())
+    raw[4:8] = np.array([version], dtype="<u4").tobytes()
+    p.write_bytes(bytes(raw))
+    if ok:
+        assert gguf.GGUF(p).version == version
+    else:
+        with pytest.raises(ValueError, match="version"):
+            gguf.GGUF(p)
+
+
+def test_unknown_value_type_and_bad_magic(tmp_path):
+    import struct
+    p = tmp_path / "u.gguf"
+    body = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 3) + b"key" + struct.pack("<I", 99)
+    p.write_bytes(body + b"\0" * 64)
+    with pytest.raises(ValueError, match="value type"):
+        gguf.GGUF(p)
+    p.write_bytes(b"GGML" + body[4:])
+    with pytest.raises(ValueError, match="not a GGUF"):
+        gguf.GGUF(p)
