@@ -88,3 +88,21 @@ def test_exports_every_symbol_the_reference_nmc_loader_requires():
     so = _lib.lib()
     assert [n for n in names if not hasattr(so, n)] == []
     assert so.qk_cuda_abi_version() == 5
+
+
+def test_profile_metric_names_match_the_native_enum():
+    """qk_profile_snapshot writes the counters in the order of the PM_* enum of csrc/nmc.hip; the Python names must
+    match it one for one (qk_cuda.py:24-34 order)."""
+    import re
+    from pathlib import Path
+    from integer_inference_engine_amd import qk_gpu
+    src = (Path(__file__).resolve().parents[1] / "integer_inference_engine_amd/csrc/nmc.hip").read_text()
+    body = re.search(r"enum \{ (PM_REG_CALLS.*?)PM_COUNT \};", src, re.S).group(1)
+    native = [n.strip() for n in body.replace("\n", " ").split(",") if n.strip()]
+    assert len(native) == len(qk_gpu.PROFILE_METRICS) == 28
+    short = {"registration": "REG", "allocation": "ALLOC", "resident_apply": "RESIDENT", "grouped_apply": "GROUPED",
+             "q_projection": "Q", "k_projection": "K", "v_projection": "V", "o_projection": "O",
+             "other_projection": "OTHER"}
+    for name, enum in zip(qk_gpu.PROFILE_METRICS, native):
+        stem, _, unit = name.rpartition("_")
+        assert enum == f"PM_{short.get(stem, stem.upper())}_{unit.upper()}", (name, enum)
