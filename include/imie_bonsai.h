@@ -20,6 +20,12 @@ extern "C" {
 int bonsai_gpu_available(void);
 /* bonsai_q1_gpu.cu `bonsai_gpu_mem_info` (gpu_native.py:107-115, 309-331). */
 int bonsai_gpu_mem_info(uint64_t *free_bytes, uint64_t *total_bytes);
+/* bonsai_q1_gpu.cu:1970-1972 `bonsai_gpu_abi_version`: the bonsai_* ABI generation mirrored here (3). */
+int bonsai_gpu_abi_version(void);
+/* bonsai_q1_gpu.cu:1974-1980 `bonsai_gpu_last_error_code` / `bonsai_gpu_last_error` (read by gpu_bonsai35.py:52-58):
+ * the last HIP error any entry point noted (number, text). */
+int bonsai_gpu_last_error_code(void);
+const char *bonsai_gpu_last_error(void);
 int imie_abi_version(void);
 const char *imie_last_error(void);
 void *imie_default_stream(void);
@@ -47,6 +53,20 @@ int64_t bonsai_q1_register_weight(const uint8_t *bits, const int64_t *scale, int
 /* bonsai_q1_gpu.cu `bonsai_q1_register_weight_i32` (gpu_native.py:79-87). */
 int64_t bonsai_q1_register_weight_i32(const uint8_t *bits, const int32_t *scale, int64_t out_features,
                                       int64_t n_blocks);
+/* bonsai_q1_gpu.cu:2350-2366 `bonsai_q1_register_weight_i32_gpu_layout` (gpu_native.py:89-96, 286-306): the
+ * reference's coalesced runtime layout; every registration here is already the gfx950 tile-major layout. */
+int64_t bonsai_q1_register_weight_i32_gpu_layout(const uint8_t *bits, const int32_t *scale, int64_t out_features,
+                                                 int64_t n_blocks);
+/* bonsai_q1_gpu.cu:2368-2385 `bonsai_q1_register_weight_i32_bmma` (gpu_native.py:98-105, 286-306): -1 unless
+ * out_features % 8 == 0, as there; stored in the same tile-major layout. */
+int64_t bonsai_q1_register_weight_i32_bmma(const uint8_t *bits, const int32_t *scale, int64_t out_features,
+                                           int64_t n_blocks);
+/* bonsai_q1_gpu.cu:2245-2300 `bonsai_q1_linear_dp4a_gpu` (bound at gpu_native.py:55-64, called :235-261): the Q1
+ * linear of x taken as L balanced base-256 digits (|L| in 1..8, L < 0 the reference's warp variant, same bytes).
+ * rc 0; 1 bad arguments; 4 when |L| == 4 and some |x| > 2,139,062,143 (nothing computed). x needing more than L
+ * digits is truncated to its low L digits (mod 2^64) as the reference's digit kernel does. */
+int bonsai_q1_linear_dp4a_gpu(const int64_t *x, const uint8_t *bits, const int64_t *scale, int64_t tokens,
+                              int64_t out_features, int64_t n_blocks, int64_t frac, int L, int64_t *out);
 /* bonsai_q1_gpu.cu:2388-2423 `bonsai_q1_apply_resident` (gpu_native.py:75-76, 364-380). */
 int bonsai_q1_apply_resident(int64_t handle, const int64_t *x, int64_t tokens, int64_t frac, int64_t *out);
 /* bonsai_q1_gpu.cu `bonsai_q1_free_weights` (gpu_native.py:77-78, 383-387). */
@@ -185,7 +205,8 @@ int imie_sample_token(const int64_t *logits, int64_t vocab, const ImieSamplerCon
 /* Device rows (no reference counterpart: the sampled decode step without a logits row on the host): token_dev[r]
  * for logits_dev[r * ld ...], history hist_dev[r * hist_ld + i] (i < hist_len_dev[r]), draw key pos_dev[r].
  * Asynchronous on `stream` (null: the default stream); *status_dev |= 2 on the temperature guard, |= 1 on a bad history token. The first
- * call for a shape sizes the workspace (synchronous); later calls only launch kernels. */
+ * call for a shape sizes the workspace (synchronous); later calls only launch kernels.
+ * Single-stream: the sampler's scratch is shared library-wide, so calls overlapping on two streams race. */
 int imie_sample_dev(const int64_t *logits_dev, int64_t rows, int64_t vocab, int64_t ld, const ImieSamplerConfig *cfg,
                     const int64_t *hist_dev, int64_t hist_ld, const int64_t *hist_len_dev, const int64_t *pos_dev,
                     int64_t *token_dev, int *status_dev, void *stream);

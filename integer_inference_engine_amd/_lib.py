@@ -18,6 +18,9 @@ SIGNATURES = {
     # runtime (include/imie_bonsai.h)
     "bonsai_gpu_available": (c_int, []),
     "bonsai_gpu_mem_info": (c_int, [c_void_p, c_void_p]),
+    "bonsai_gpu_abi_version": (c_int, []),
+    "bonsai_gpu_last_error_code": (c_int, []),
+    "bonsai_gpu_last_error": (ctypes.c_char_p, []),
     "imie_abi_version": (c_int, []),
     "imie_last_error": (ctypes.c_char_p, []),
     "imie_default_stream": (c_void_p, []),
@@ -39,6 +42,10 @@ SIGNATURES = {
     "bonsai_q1_linear_gpu": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "bonsai_q1_register_weight": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
     "bonsai_q1_register_weight_i32": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
+    "bonsai_q1_register_weight_i32_gpu_layout": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
+    "bonsai_q1_register_weight_i32_bmma": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),
+    "bonsai_q1_linear_dp4a_gpu": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int,
+                                          c_void_p]),
     "bonsai_q1_apply_resident": (c_int, [c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "bonsai_q1_free_weights": (None, []),
     "bonsai_q1_resident_weight_bytes": (c_uint64, []),

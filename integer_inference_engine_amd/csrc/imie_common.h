@@ -25,6 +25,12 @@ hipStream_t imie_stream();                 // the library's default stream (crea
 std::recursive_mutex& imie_lock();         // the library is single-caller; ABI entry points take this lock
 int imie_device_ready();                   // 0 when a gfx9xx device is usable
 
+// Every device free in the library goes through imie_free, which advances a process-wide allocation generation.
+// A captured HIP graph records raw device addresses; its owner compares the generation it was captured under with
+// the current one and re-captures when any block may have been freed (and its address handed out again).
+void imie_free(void* p);
+uint64_t imie_alloc_gen();
+
 // Grow-only device workspace owned by the library (host-pointer ABI staging buffers).
 struct DevBuf {
   void* p = nullptr;

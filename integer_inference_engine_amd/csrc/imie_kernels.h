@@ -113,7 +113,9 @@ int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B,
 struct ImieSamplerConfig {
   int64_t mode, frac, inv_temp, top_k, top_p, min_p, rep_penalty, no_repeat_ngram, seed;
 };
-// tokens of `rows` logits rows (stride ld) into token[r]; per-row history / positions on the device
+// tokens of `rows` logits rows (stride ld) into token[r]; per-row history / positions on the device.
+// Single-stream: the flag, probability, key and sort scratch is one library-wide set, so two calls in flight on
+// different streams at once race on it (the library lock serialises the enqueues, not the kernels).
 int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t ld, const ImieSamplerConfig& c,
                        const int64_t* hist, int64_t hld, const int64_t* hlen, const int64_t* pos, int64_t* token,
                        int* status, hipStream_t st);

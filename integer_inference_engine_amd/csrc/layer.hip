@@ -102,6 +102,7 @@ struct Net {
   const int64_t* finalg = nullptr;
   int64_t out_head = -1;
   const int64_t *cos = nullptr, *sin = nullptr;
+  int64_t rope_rows = 0;              // positions the uploaded RoPE tables cover (rows of hd/2 entries)
   // KV
   int kv32 = 0;                       // 1: kv8 digit-plane cache (imie_kvfmt.h), 0: int64 rows
   int64_t P = 0, mp = 0, npages = 0;  // page size, page-table row length (max pages of a sequence), pool pages
@@ -118,6 +119,7 @@ struct Net {
   // captured greedy decode step (imie_net_decode_dev): valid for the pointer key it was captured with
   hipGraphExec_t gexec = nullptr;
   const void* gkey[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  uint64_t ggen = 0;                  // allocation generation (imie_alloc_gen) the graph was captured under
   bool live = false;
 };
 
@@ -133,11 +135,11 @@ Net* net_get(int64_t h) {
 }
 
 void net_free_kv(Net& n) {
-  for (auto p : n.kpool) if (p) (void)hipFree(p);
-  for (auto p : n.vpool) if (p) (void)hipFree(p);
+  for (auto p : n.kpool) if (p) imie_free(p);
+  for (auto p : n.vpool) if (p) imie_free(p);
   n.kpool.clear();
   n.vpool.clear();
-  if (n.pt) (void)hipFree(n.pt);
+  if (n.pt) imie_free(n.pt);
   n.pt = nullptr;
 }
 
@@ -196,6 +198,9 @@ int net_alloc_kv(Net& n, const std::vector<int64_t>& caps, int64_t P, int kv32) 
 }
 
 int64_t seq_cap(const Net& n, int64_t b) { return n.npg[(size_t)b] * n.P; }
+// Positions sequence b can hold: its pages, and no further than the RoPE tables reach (page rounding can give a
+// sequence more slots than the tables have rows; a position past them would read beyond the uploaded table).
+int64_t pos_cap(const Net& n, int64_t b) { return std::min(seq_cap(n, b), n.rope_rows); }
 
 uint64_t* run_k(Net& n, int64_t l) { return (uint64_t*)n.kvrun.p + (l * 2) * n.B * n.Hkv; }
 uint64_t* run_v(Net& n, int64_t l) { return (uint64_t*)n.kvrun.p + (l * 2 + 1) * n.B * n.Hkv; }
@@ -338,7 +343,7 @@ int net_run(Net& n, int64_t* x, const int64_t* starts, int64_t M, hipStream_t st
   const int64_t rows = n.B * M;
   int64_t lmax = 0;
   for (int64_t b = 0; b < n.B; ++b) {
-    if (starts[b] < 0 || starts[b] + M > seq_cap(n, b)) return IMIE_EARG;
+    if (starts[b] < 0 || starts[b] + M > pos_cap(n, b)) return IMIE_EARG;
     lmax = starts[b] + M > lmax ? starts[b] + M : lmax;
   }
   if (net_ensure(n, M, lmax)) return IMIE_EARG;
@@ -447,6 +452,7 @@ int64_t net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t 
   n->cos = buf_get(cos_h, cap * (hd / 2));
   n->sin = buf_get(sin_h, cap * (hd / 2));
   if (!n->cos || !n->sin) { delete n; return -1; }
+  n->rope_rows = std::min(bufs()[(size_t)cos_h].n, bufs()[(size_t)sin_h].n) / (hd / 2);
   n->live = true;
   if (net_alloc_kv(*n, std::vector<int64_t>((size_t)B, cap), page, kv32)) { net_free(n); delete n; return -1; }
   nets().push_back(n);
@@ -463,7 +469,7 @@ int64_t bonsai_buf_upload_i64(const int64_t* host, int64_t n) {
   if (!host || n <= 0 || imie_device_ready() != 0) return -1;
   BufEntry e;
   if (hipMalloc((void**)&e.p, (size_t)n * 8) != hipSuccess) return -1;
-  if (hipMemcpy(e.p, host, (size_t)n * 8, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(e.p); return -1; }
+  if (hipMemcpy(e.p, host, (size_t)n * 8, hipMemcpyHostToDevice) != hipSuccess) { imie_free(e.p); return -1; }
   e.n = n;
   bufs().push_back(e);
   return (int64_t)bufs().size() - 1;
@@ -478,7 +484,7 @@ const int64_t* imie_buf_device_ptr(int64_t handle) {
 void imie_buf_free_all(void) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   (void)hipStreamSynchronize(imie_stream());
-  for (auto& e : bufs()) if (e.p) (void)hipFree(e.p);
+  for (auto& e : bufs()) if (e.p) imie_free(e.p);
   bufs().clear();
 }
 
@@ -561,7 +567,7 @@ int64_t imie_net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int
 int bonsai_decode_ctx_seed_seq(int64_t ctx, int64_t b, const int64_t* k, const int64_t* v, int64_t Lb) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   Net* n = net_get(ctx);
-  if (!n || !k || !v || b < 0 || b >= n->B || Lb < 0 || Lb > seq_cap(*n, b)) return IMIE_EARG;
+  if (!n || !k || !v || b < 0 || b >= n->B || Lb < 0 || Lb > pos_cap(*n, b)) return IMIE_EARG;
   const size_t esz = n->kv32 ? 4 : 8;
   std::vector<char> kb((size_t)(n->npg[(size_t)b] * n->Hkv * n->P * n->hd) * esz), vb(kb.size());
   std::vector<uint64_t> mk((size_t)(n->nl * n->Hkv), 0), mv(mk.size(), 0);
@@ -680,7 +686,7 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
   if (!n || !ebits || !escale || !ids_dev || !logits_dev || steps <= 0 || n->out_head < 0) return IMIE_EARG;
   const int64_t cap = n->mp * n->P;
   for (int64_t b = 0; b < n->B; ++b)
-    if (n->len[(size_t)b] + steps > seq_cap(*n, b)) return IMIE_EARG;
+    if (n->len[(size_t)b] + steps > pos_cap(*n, b)) return IMIE_EARG;
   hipStream_t st = (hipStream_t)stream;
   if (net_ensure(*n, 1, cap) || n->amx.ensure(imie_argmax_scratch_bytes(n->B)) || n->stepc.ensure(64) ||
       n->lastx.ensure((size_t)(n->B * n->d) * 8))
@@ -710,7 +716,9 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
       if (rc) return rc;
     } else {
       const void* key[5] = {ebits, escale, ids_dev, logits_dev, hist_dev};
-      if (n->gexec && memcmp(key, n->gkey, sizeof(key)) != 0) {
+      // The graph also holds this net's workspaces, pools and the weights' addresses: any device free since
+      // the capture (a larger prefill regrowing a workspace, a weight freed) invalidates it.
+      if (n->gexec && (memcmp(key, n->gkey, sizeof(key)) != 0 || n->ggen != imie_alloc_gen())) {
         (void)hipGraphExecDestroy(n->gexec);
         n->gexec = nullptr;
       }
@@ -726,6 +734,7 @@ int imie_net_decode_dev(int64_t ctx, const uint8_t* ebits, const int64_t* escale
         (void)hipGraphDestroy(g);
         if (ei != hipSuccess) { n->gexec = nullptr; return IMIE_EARG; }
         memcpy(n->gkey, key, sizeof(key));
+        n->ggen = imie_alloc_gen();
       }
       for (int64_t s = 1; s < steps; ++s) IMIE_HIP(hipGraphLaunch(n->gexec, st));
     }
@@ -749,7 +758,7 @@ int imie_net_decode_sampled_dev(int64_t ctx, const uint8_t* ebits, const int64_t
     return IMIE_EARG;
   const int64_t cap = n->mp * n->P;
   for (int64_t b = 0; b < n->B; ++b)
-    if (n->len[(size_t)b] + steps > seq_cap(*n, b)) return IMIE_EARG;
+    if (n->len[(size_t)b] + steps > pos_cap(*n, b)) return IMIE_EARG;
   hipStream_t st = (hipStream_t)stream;
   if (net_ensure(*n, 1, cap) || n->stepc.ensure(64) || n->lastx.ensure((size_t)(n->B * n->d) * 8)) return IMIE_EARG;
   std::vector<int64_t> hl((size_t)n->B);
@@ -811,8 +820,8 @@ int imie_net_set_caps(int64_t ctx, const int64_t* caps) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   Net* n = net_get(ctx);
   if (!n || !caps) return IMIE_EARG;
-  for (int64_t b = 0; b < n->B; ++b)
-    if (caps[b] <= 0) return IMIE_EARG;
+  for (int64_t b = 0; b < n->B; ++b)                  // no position beyond the RoPE tables is ever usable
+    if (caps[b] <= 0 || caps[b] > n->rope_rows) return IMIE_EARG;
   IMIE_HIP(hipDeviceSynchronize());
   if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   net_free_kv(*n);
@@ -843,7 +852,7 @@ int imie_net_fill_kv(int64_t ctx, uint64_t seed, const int64_t* lens, const int6
   if (n->kv32 && (!imie_kv8::fits(lo) || !imie_kv8::fits(hi - 1))) return IMIE_EOVF;
   int64_t lmax = 0;
   for (int64_t b = 0; b < n->B; ++b) {
-    if (lens[b] < 0 || lens[b] > seq_cap(*n, b)) return IMIE_EARG;
+    if (lens[b] < 0 || lens[b] > pos_cap(*n, b)) return IMIE_EARG;
     lmax = lens[b] > lmax ? lens[b] : lmax;
   }
   hipStream_t st = imie_stream();

@@ -771,7 +771,7 @@ int64_t qk_register(const uint8_t* W, int64_t out_f, int64_t nb, int qtype) {
   w.out_f = out_f; w.nb = nb; w.qtype = qtype;
   w.bytes = (size_t)(out_f * nb) * (qtype == 0 ? 144 : 210);
   if (hipMalloc((void**)&w.p, w.bytes) != hipSuccess) return -1;
-  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(w.p); return -1; }
+  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { imie_free(w.p); return -1; }
   g_qk.push_back(w);
   ++g_qk_live;
   prof(PM_REG_CALLS); prof(PM_ALLOC_CALLS); prof(PM_ALLOC_BYTES, w.bytes);
@@ -798,7 +798,7 @@ int64_t imie_qk_register_i64(const int64_t* W, int64_t rows, int64_t cols) {
   w.out_f = rows; w.nb = cols; w.qtype = 2;
   w.bytes = (size_t)(rows * cols) * 8;
   if (hipMalloc((void**)&w.p, w.bytes) != hipSuccess) return -1;
-  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(w.p); return -1; }
+  if (hipMemcpy(w.p, W, w.bytes, hipMemcpyHostToDevice) != hipSuccess) { imie_free(w.p); return -1; }
   g_qk.push_back(w);
   ++g_qk_live;
   prof(PM_REG_CALLS); prof(PM_ALLOC_CALLS); prof(PM_ALLOC_BYTES, w.bytes);
@@ -854,7 +854,7 @@ int qk_linear_cuda(const uint8_t* W, const int64_t* x, long long T, long long ou
   const int64_t h = qk_register(W, out_f, n_blocks, qtype);
   if (h < 0) return IMIE_EARG;
   const int rc = host_linear({h}, x, T, fw, out);
-  (void)hipFree(g_qk[(size_t)h].p);
+  imie_free(g_qk[(size_t)h].p);
   g_qk[(size_t)h].p = nullptr;
   --g_qk_live;
   if (h == (int64_t)g_qk.size() - 1) g_qk.pop_back();
@@ -996,7 +996,7 @@ int imie_moe_status(int clear, void* stream) {
 void qk_free_all(void) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   (void)hipDeviceSynchronize();
-  for (auto& w : g_qk) if (w.p) { (void)hipFree(w.p); prof(PM_FREE_CALLS); }
+  for (auto& w : g_qk) if (w.p) { imie_free(w.p); prof(PM_FREE_CALLS); }
   g_qk.clear();
   g_qk_live = 0;
 }

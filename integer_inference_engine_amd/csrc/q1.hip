@@ -19,6 +19,7 @@
 // MFMA int32 accumulation is exact: each D entry is at most 8 * 16 * 128 = 2^14 in magnitude.
 // Prefill (T >= 8) uses the tiled GEMM further down.
 #include "imie_common.h"
+#include <vector>
 #include "imie_kernels.h"
 #include "imie_q1prep.h"
 #include <string.h>
@@ -1122,7 +1123,7 @@ static int q1_ensure_signs(Q1Weight& w, hipStream_t st) {
   const int64_t n = w.N * w.nb;
   hipLaunchKernelGGL(q1_signs_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint4*)w.bits, w.N,
                      w.nb, w.nslabs, w.signs);
-  if (hipGetLastError() != hipSuccess) { (void)hipFree(w.signs); w.signs = nullptr; return 1; }
+  if (hipGetLastError() != hipSuccess) { imie_free(w.signs); w.signs = nullptr; return 1; }
   w.bytes += bytes;
   g_resident_bytes += bytes;
   return 0;
@@ -1372,10 +1373,10 @@ static int64_t q1_register(const uint8_t* bits, const void* scale, int64_t N, in
   std::vector<uint8_t> hs(nlanes * (scale64 ? 8 : 4));
   imie_q1_repack_host(bits, s64.data(), N, nb, scale64, hb.data(), hs.data());
   if (hipMalloc((void**)&w.bits, hb.size()) != hipSuccess) return -1;
-  if (hipMalloc(&w.scale, hs.size()) != hipSuccess) { (void)hipFree(w.bits); return -1; }
+  if (hipMalloc(&w.scale, hs.size()) != hipSuccess) { imie_free(w.bits); return -1; }
   if (hipMemcpy(w.bits, hb.data(), hb.size(), hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(w.scale, hs.data(), hs.size(), hipMemcpyHostToDevice) != hipSuccess) {
-    (void)hipFree(w.bits); (void)hipFree(w.scale); return -1;
+    imie_free(w.bits); imie_free(w.scale); return -1;
   }
   w.scale64 = scale64;
   w.maxsc = maxsc > (uint64_t)INT64_MAX ? INT64_MAX : (int64_t)maxsc;
@@ -1470,8 +1471,8 @@ int bonsai_q1_linear_gpu(const int64_t* x, const uint8_t* bits, const int64_t* s
   if (h < 0) return IMIE_EARG;
   const int rc = q1_host_apply(registry()[(size_t)h], x, tokens, frac, out);
   Q1Weight& w = registry()[(size_t)h];
-  (void)hipFree(w.bits); (void)hipFree(w.scale);
-  if (w.signs) (void)hipFree(w.signs);
+  imie_free(w.bits); imie_free(w.scale);
+  if (w.signs) imie_free(w.signs);
   g_resident_bytes -= w.bytes;
   w.live = false;
   if (h == (int64_t)registry().size() - 1) registry().pop_back();
@@ -1491,6 +1492,65 @@ int64_t bonsai_q1_register_weight_i32(const uint8_t* bits, const int32_t* scale,
   return q1_register(bits, scale, out_features, n_blocks, 1);
 }
 
+// bonsai_q1_gpu.cu:2350-2366 `bonsai_q1_register_weight_i32_gpu_layout` (gpu_native.py:89-96, 286-306). The
+// reference keeps a second, coalesced runtime layout for its CUDA kernels; here every registration is already the
+// tile-major layout the gfx950 kernels stream (one wave reads 1 KB contiguous per tile and slab), so this is the
+// int32 registration under the name its callers bind. Same refusals: null pointers or empty shapes give -1.
+int64_t bonsai_q1_register_weight_i32_gpu_layout(const uint8_t* bits, const int32_t* scale, int64_t out_features,
+                                                 int64_t n_blocks) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!bits || !scale || out_features <= 0 || n_blocks <= 0) return -1;
+  return q1_register(bits, scale, out_features, n_blocks, 1);
+}
+
+// bonsai_q1_gpu.cu:2368-2385 `bonsai_q1_register_weight_i32_bmma` (gpu_native.py:98-105, 286-306): the reference's
+// tensor-core layout needs out_features % 8 == 0 and refuses other shapes with -1; that refusal is kept so a
+// caller sees the same handles, and the weight is stored in the same tile-major layout as every registration.
+int64_t bonsai_q1_register_weight_i32_bmma(const uint8_t* bits, const int32_t* scale, int64_t out_features,
+                                           int64_t n_blocks) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!bits || !scale || out_features <= 0 || n_blocks <= 0 || out_features % 8) return -1;
+  return q1_register(bits, scale, out_features, n_blocks, 1);
+}
+
+// bonsai_q1_gpu.cu:2245-2300 `bonsai_q1_linear_dp4a_gpu` (gpu_native.py:55-64, called :235-261): the Q1 linear of
+// x written as L balanced base-256 digits (|L| in 1..8; L < 0 selects the reference's warp variant, which gives
+// the same bytes). Digits are taken from the low end exactly as bonsai_q1_gpu.cu:419-432 does, so for an x that
+// needs more than L digits the result is the Q1 linear of the L-digit truncation (mod 2^64), as there; with
+// L = 8 every int64 is exact. |L| == 4 refuses (rc 4, nothing computed) any |x| > 2,139,062,143, the reference's
+// L=4 guard (:475-481). rc 1 on bad arguments. Here the digits are the kernels' own limb planes: the truncated
+// activations are formed on the host only when some value does not fit L digits.
+int bonsai_q1_linear_dp4a_gpu(const int64_t* x, const uint8_t* bits, const int64_t* scale, int64_t tokens,
+                              int64_t out_features, int64_t n_blocks, int64_t frac, int L, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  const int LL = L < 0 ? -L : L;
+  if (!x || !bits || !scale || !out || tokens <= 0 || out_features <= 0 || n_blocks <= 0 || LL < 1 || LL > 8 ||
+      frac < 0)
+    return IMIE_EARG;
+  const size_t n = (size_t)(tokens * n_blocks * 128);
+  const uint64_t cap = imie_balanced_cap(LL);
+  bool fits = true;
+  for (size_t i = 0; i < n && fits; ++i) {
+    const uint64_t a = x[i] < 0 ? (uint64_t)0 - (uint64_t)x[i] : (uint64_t)x[i];
+    fits = LL == 8 || a <= cap;
+  }
+  if (LL == 4 && !fits) return 4;
+  if (fits) return bonsai_q1_linear_gpu(x, bits, scale, tokens, out_features, n_blocks, frac, out);
+  std::vector<int64_t> xt(n);
+  for (size_t i = 0; i < n; ++i) {
+    uint64_t r = (uint64_t)x[i], acc = 0, w = 1;
+    for (int l = 0; l < LL; ++l) {
+      const int lb = (int)(r & 0xFFu);
+      const int d = lb >= 128 ? lb - 256 : lb;
+      acc += (uint64_t)(int64_t)d * w;
+      w <<= 8;
+      r = (r - (uint64_t)(int64_t)d) >> 8;
+    }
+    xt[i] = (int64_t)acc;
+  }
+  return bonsai_q1_linear_gpu(xt.data(), bits, scale, tokens, out_features, n_blocks, frac, out);
+}
+
 // bonsai_q1_gpu.cu:2388-2423 `bonsai_q1_apply_resident`: host x in, host out, synchronous.
 int bonsai_q1_apply_resident(int64_t handle, const int64_t* x, int64_t tokens, int64_t frac, int64_t* out) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
@@ -1504,7 +1564,7 @@ void bonsai_q1_free_weights(void) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   (void)hipStreamSynchronize(imie_stream());
   for (auto& w : registry())
-    if (w.live) { (void)hipFree(w.bits); (void)hipFree(w.scale); if (w.signs) (void)hipFree(w.signs); }
+    if (w.live) { imie_free(w.bits); imie_free(w.scale); if (w.signs) imie_free(w.signs); }
   registry().clear();
   g_resident_bytes = 0;
 }

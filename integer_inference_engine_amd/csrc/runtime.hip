@@ -7,6 +7,7 @@
 static hipStream_t g_stream = nullptr;
 static int g_ready = -1;
 static char g_last_error[256];
+static int g_last_error_code = 0;
 
 std::recursive_mutex& imie_lock() {
   static std::recursive_mutex m;
@@ -14,6 +15,7 @@ std::recursive_mutex& imie_lock() {
 }
 
 void imie_note_error(hipError_t e, const char* what) {
+  g_last_error_code = (int)e;
   snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(e));
 }
 
@@ -36,9 +38,19 @@ hipStream_t imie_stream() {
   return g_stream;
 }
 
+static uint64_t g_alloc_gen = 1;
+
+void imie_free(void* p) {
+  if (!p) return;
+  (void)hipFree(p);
+  ++g_alloc_gen;
+}
+
+uint64_t imie_alloc_gen() { return g_alloc_gen; }
+
 int DevBuf::ensure(size_t bytes) {
   if (bytes <= cap && p) return 0;
-  if (p) { (void)hipFree(p); p = nullptr; cap = 0; }
+  if (p) { imie_free(p); p = nullptr; cap = 0; }
   size_t want = bytes < 256 ? 256 : bytes;
   if (hipMalloc(&p, want) != hipSuccess) { p = nullptr; return 1; }
   cap = want;
@@ -46,7 +58,7 @@ int DevBuf::ensure(size_t bytes) {
 }
 
 void DevBuf::release() {
-  if (p) (void)hipFree(p);
+  if (p) imie_free(p);
   p = nullptr;
   cap = 0;
 }
@@ -60,6 +72,15 @@ int bonsai_gpu_available(void) {
 }
 
 int imie_abi_version(void) { return 1; }
+
+// bonsai_q1_gpu.cu:1970-1980 `bonsai_gpu_abi_version` / `bonsai_gpu_last_error_code` / `bonsai_gpu_last_error`:
+// the generation of the bonsai_* entry points this library mirrors (3), and the last runtime error noted by any
+// entry point (HIP error number and text; 0 / empty when none).
+int bonsai_gpu_abi_version(void) { return 3; }
+
+int bonsai_gpu_last_error_code(void) { return g_last_error_code; }
+
+const char* bonsai_gpu_last_error(void) { return g_last_error; }
 
 const char* imie_last_error(void) { return g_last_error; }
 
@@ -107,7 +128,7 @@ extern "C" int imie_probe_mfma(const int8_t* a_host, const int8_t* b_host, int32
   hipLaunchKernelGGL(imie_probe_mfma_kernel, dim3(1), dim3(64), 0, 0, (const v4i*)a, (const v4i*)b, (v4i*)d);
   IMIE_HIP(hipGetLastError());
   IMIE_HIP(hipMemcpy(d_host, d, 1024, hipMemcpyDeviceToHost));
-  (void)hipFree(a); (void)hipFree(b); (void)hipFree(d);
+  imie_free(a); imie_free(b); imie_free(d);
   return IMIE_OK;
 }
 
@@ -148,7 +169,7 @@ extern "C" int imie_mfma_peak(double* ops_per_s) {
     IMIE_HIP(hipEventSynchronize(e1));
     IMIE_HIP(hipEventElapsedTime(&ms, e0, e1));
   }
-  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); (void)hipFree(sink);
+  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); imie_free(sink);
   const double mfmas = (double)wgs * 4 * iters * 8;   // waves x iterations x chains
   *ops_per_s = mfmas * (2.0 * 16 * 16 * 64) / (ms * 1e-3);
   return IMIE_OK;
@@ -239,7 +260,7 @@ extern "C" int64_t bonsai_gpu_reservation_create(const uint64_t* sizes, int64_t 
     void* p = nullptr;
     if (sizes[i] == 0 || hipMalloc(&p, (size_t)sizes[i]) != hipSuccess) {
       (void)hipGetLastError();
-      for (void* q : taken) (void)hipFree(q);
+      for (void* q : taken) imie_free(q);
       return -1;
     }
     taken.push_back(p);
@@ -253,6 +274,6 @@ extern "C" int64_t bonsai_gpu_reservation_create(const uint64_t* sizes, int64_t 
 extern "C" void bonsai_gpu_reservation_free(int64_t handle) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());
   if (handle < 0 || handle >= (int64_t)reservations().size()) return;
-  for (void* p : reservations()[(size_t)handle]) (void)hipFree(p);
+  for (void* p : reservations()[(size_t)handle]) imie_free(p);
   reservations()[(size_t)handle].clear();            // a second free is a no-op
 }

@@ -464,9 +464,11 @@ __global__ __launch_bounds__(256) void smp_count_kernel(int64_t V, const SmpRow*
 }
 
 // per-row exclusive offsets of the parts' nonzero counts (part[.. + 3] <- offset) and the sort segment ends
-__global__ void smp_offsets_kernel(int64_t V, int64_t* __restrict__ part, int* __restrict__ seg_end) {
+__global__ void smp_offsets_kernel(int64_t V, int64_t* __restrict__ part, int* __restrict__ seg_beg,
+                                   int* __restrict__ seg_end) {
   const int64_t r = blockIdx.x;
   if (threadIdx.x) return;
+  seg_beg[r] = (int)(r * V);
   int64_t run = 0;
   for (int k = 0; k < kSmpParts; ++k) {
     int64_t* p = part + (r * kSmpParts + k) * 4 + 3;
@@ -610,7 +612,7 @@ int64_t smp_dclip(int frac) {
 bool smp_config_ok(const ImieSamplerConfig& c) {
   if (c.frac < 1 || c.frac > 29 || c.mode < 0 || c.mode > 4) return false;
   const int64_t fp = (int64_t)1 << c.frac;
-  if (c.inv_temp <= 0 || c.top_k < 0 || c.top_p <= 0 || c.top_p > fp || c.min_p < 0 || c.min_p > fp ||
+  if (c.inv_temp <= 0 || c.top_k < 0 || c.min_p < 0 || c.min_p > fp ||
       c.rep_penalty < 0 || c.no_repeat_ngram < 0)
     return false;
   if (c.mode == 2 && c.top_k <= 0) return false;
@@ -620,9 +622,18 @@ bool smp_config_ok(const ImieSamplerConfig& c) {
 
 }  // namespace
 
-int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t ld, const ImieSamplerConfig& c,
+int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t ld, const ImieSamplerConfig& c_in,
                        const int64_t* hist, int64_t hld, const int64_t* hlen, const int64_t* pos, int64_t* token,
                        int* status, hipStream_t st) {
+  // The nucleus threshold only acts in top_k / top_p modes (sampler.py:403-437 passes it to _truncate there only),
+  // so other modes take 2^frac whatever the config carries. Within those modes _truncate (sampler.py:334-363)
+  // keeps the first token for any threshold <= 0 (exactly what threshold 1 keeps, the top probability being >= 1
+  // whenever the total is positive) and truncates nothing for a threshold >= 2^frac: clamp to [1, 2^frac].
+  ImieSamplerConfig c = c_in;
+  if (c.frac >= 1 && c.frac <= 29) {
+    const int64_t fp = (int64_t)1 << c.frac;
+    c.top_p = (c.mode == 2 || c.mode == 3) ? (c.top_p < 1 ? 1 : (c.top_p > fp ? fp : c.top_p)) : fp;
+  }
   if (!logits || rows <= 0 || V <= 0 || V >= ((int64_t)1 << 32) || ld < V || !pos || !token || !status ||
       !smp_config_ok(c))
     return IMIE_EARG;
@@ -663,18 +674,11 @@ int imie_sample_launch(const int64_t* logits, int64_t rows, int64_t V, int64_t l
       if (g_smp.keys.ensure(rv * 8) || g_smp.sorted.ensure(rv * 8) || g_smp.offs.ensure((size_t)(2 * rows + 1) * 4))
         return IMIE_EARG;
       if (rv >= ((size_t)1 << 31)) return IMIE_EARG;
-      // segment begins r * V (host-computed once per shape); ends r * V + nonzero count (device)
-      static int64_t offs_rows = -1, offs_v = -1;
-      if (offs_rows != rows || offs_v != V) {
-        std::vector<int> h((size_t)rows);
-        for (int64_t i = 0; i < rows; ++i) h[(size_t)i] = (int)(i * V);
-        IMIE_HIP(hipMemcpy(g_smp.offs.p, h.data(), h.size() * 4, hipMemcpyHostToDevice));
-        offs_rows = rows; offs_v = V;
-      }
+      // segment r is [r * V, r * V + its nonzero count): both ends written on the device, in stream order
       const int* begs = (const int*)g_smp.offs.p;
       int* ends = (int*)g_smp.offs.p + rows;
       hipLaunchKernelGGL(smp_count_kernel, gv, dim3(256), 0, st, V, srow, pr, part);
-      hipLaunchKernelGGL(smp_offsets_kernel, dim3((unsigned)rows), dim3(64), 0, st, V, part, ends);
+      hipLaunchKernelGGL(smp_offsets_kernel, dim3((unsigned)rows), dim3(64), 0, st, V, part, (int*)g_smp.offs.p, ends);
       hipLaunchKernelGGL(smp_scatter_kernel, gv, dim3(256), 0, st, V, srow, pr, part, (uint64_t*)g_smp.keys.p);
       const int end_bit = 33 + (int)c.frac;           // p <= 2^frac
       size_t tmp_bytes = 0;

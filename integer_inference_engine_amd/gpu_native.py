@@ -59,16 +59,30 @@ def q1_apply_gpu(x_fp: np.ndarray, bits: np.ndarray, scale_fp: np.ndarray, frac:
 
 
 def q1_apply_dp4a_gpu(x_fp, bits, scale_fp, frac: int, L: "int | None" = None) -> "np.ndarray | None":
-    """Limb-decomposed Q1 apply (gpu_native.py:226-261). On gfx950 every Q1 apply already runs over balanced
-    base-256 limbs on int8 MFMA, so this is the same kernel; an explicit L=4 outside the L=4 envelope raises
-    as in the reference."""
+    """Limb-decomposed Q1 apply through ``bonsai_q1_linear_dp4a_gpu`` (gpu_native.py:226-261): L = 4 when the
+    activations fit the balanced base-256 L=4 range, else 8; an explicit L=4 outside it raises; rc != 0 (the
+    library's own L=4 guard included) gives None."""
+    lib = _dev()
+    if lib is None:
+        return None
     x = _as_i64_2d(x_fp)
-    if L is not None and int(L) == 4 and x.size:
+    b = np.ascontiguousarray(np.asarray(bits, dtype=np.uint8))
+    s = np.ascontiguousarray(np.asarray(scale_fp, dtype=np.int64))
+    out_f, n_blocks = s.shape
+    if x.shape[1] != n_blocks * 128:
+        raise ValueError(f"Q1_0 contraction mismatch: x has {x.shape[1]}, weight expects {n_blocks * 128}")
+    if L is None:
+        mn, mx = (int(x.min()), int(x.max())) if x.size else (0, 0)
+        L = 4 if (_L4_LO <= mn and mx <= _L4_HI) else 8
+    elif int(L) == 4 and x.size:
         mn, mx = int(x.min()), int(x.max())
         if not (_L4_LO <= mn and mx <= _L4_HI):
             raise ValueError(f"q1_apply_dp4a_gpu: explicit L=4 requires activations in [{_L4_LO}, {_L4_HI}], "
-                             f"got [{mn}, {mx}]")
-    return q1_apply_gpu(x, bits, scale_fp, frac)
+                             f"got [{mn}, {mx}]; use L=8 (always exact) or L=None")
+    out = np.empty((x.shape[0], out_f), dtype=np.int64)
+    rc = lib.bonsai_q1_linear_dp4a_gpu(x.ctypes.data, b.ctypes.data, s.ctypes.data, x.shape[0], int(out_f),
+                                       int(n_blocks), int(frac), int(L), out.ctypes.data)
+    return None if rc != 0 else out
 
 
 def residency_available() -> bool:
@@ -79,7 +93,8 @@ def q1_register_weight(bits: np.ndarray, scale_fp: np.ndarray, *, gpu_coalesced:
                        gpu_bmma: bool = False) -> "int | None":
     """Upload bits + scale once; return a handle >= 0 or None (gpu_native.py:270-306). The weight is stored in
     the gfx950 tile layout; scales are narrowed to int32 on device when lossless. ``gpu_coalesced`` /
-    ``gpu_bmma`` select CUDA-specific layouts in the reference and are accepted for interface parity."""
+    ``gpu_bmma`` bind the reference's layout-specific entry points (same refusals: int32 scales only, and
+    out_features % 8 == 0 for bmma); on gfx950 all three store the same tile layout."""
     lib = _dev()
     if lib is None:
         return None
@@ -89,9 +104,14 @@ def q1_register_weight(bits: np.ndarray, scale_fp: np.ndarray, *, gpu_coalesced:
     src = np.asarray(scale_fp)
     if not np.issubdtype(src.dtype, np.integer):
         raise TypeError(f"Q1_0 scale must be an integer dtype, got {src.dtype}")
-    if src.dtype.itemsize <= 4:
+    use_i32 = src.dtype.itemsize <= 4
+    if (gpu_coalesced or gpu_bmma) and not use_i32:
+        raise ValueError("GPU-coalesced Q1 registration currently requires committed int32 scales")
+    if use_i32:
         s = np.ascontiguousarray(src, dtype=np.int32)
-        h = lib.bonsai_q1_register_weight_i32(b.ctypes.data, s.ctypes.data, int(s.shape[0]), int(s.shape[1]))
+        fn = (lib.bonsai_q1_register_weight_i32_bmma if gpu_bmma else
+              lib.bonsai_q1_register_weight_i32_gpu_layout if gpu_coalesced else lib.bonsai_q1_register_weight_i32)
+        h = fn(b.ctypes.data, s.ctypes.data, int(s.shape[0]), int(s.shape[1]))
     else:
         s = np.ascontiguousarray(src, dtype=np.int64)
         h = lib.bonsai_q1_register_weight(b.ctypes.data, s.ctypes.data, int(s.shape[0]), int(s.shape[1]))

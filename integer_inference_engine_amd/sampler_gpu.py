@@ -49,7 +49,7 @@ def _validate(cfg) -> None:
     mode = cfg.mode
     if mode not in MODES:
         raise ValueError(f"unsupported sampler mode {mode!r}")
-    if mode != "greedy" and cfg.temperature <= 0 and getattr(cfg, "inv_temp_fp_committed", None) is None:
+    if mode != "greedy" and cfg.temperature <= 0:
         raise ValueError("temperature must be > 0 for sampling modes")
     if mode == "top_k" and cfg.top_k <= 0:
         raise ValueError("top_k must be > 0 for top_k sampling")
@@ -70,7 +70,10 @@ def config_c(cfg, frac_bits: int) -> SamplerConfigC:
         itf = getattr(cfg, "inv_temp_fp_committed", None)
         itf = inv_temp_fp(cfg.temperature, frac_bits) if itf is None else int(itf)
         tpf = getattr(cfg, "top_p_fp_committed", None)
-        tpf = top_p_fp(cfg.top_p, frac_bits) if tpf is None else int(tpf)
+        if cfg.mode in ("top_k", "top_p"):               # _truncate reads it in these modes only (sampler.py:423)
+            tpf = top_p_fp(cfg.top_p, frac_bits) if tpf is None else int(tpf)
+        else:
+            tpf = 1 << frac_bits
         mpf = getattr(cfg, "min_p_fp_committed", None)
         mpf = min_p_fp(cfg.min_p, frac_bits) if mpf is None else int(mpf)
     seed = int(cfg.seed) & ((1 << 64) - 1)              # the draw keys on the low 64 bits (sampler.py:291)

@@ -90,6 +90,38 @@ def test_exports_every_symbol_the_reference_nmc_loader_requires():
     assert so.qk_cuda_abi_version() == 5
 
 
+def test_exports_every_symbol_the_reference_bonsai_loader_binds():
+    """Every bonsai_* name bonsai/src/trinote/infer_int/gpu_native.py binds (:44-172, including the optional
+    dp4a :55-64 and layout registrations :80-105), plus the ABI queries of bonsai_q1_gpu.cu:1970-1980: the
+    reference loader pointed at this library finds all of them, so none of its optional paths falls back."""
+    names = """bonsai_q1_linear_gpu bonsai_q1_linear_dp4a_gpu bonsai_q1_register_weight bonsai_q1_apply_resident
+    bonsai_q1_free_weights bonsai_q1_register_weight_i32 bonsai_q1_register_weight_i32_gpu_layout
+    bonsai_q1_register_weight_i32_bmma bonsai_gpu_mem_info bonsai_q1_resident_weight_bytes
+    bonsai_gpu_reservation_create bonsai_gpu_reservation_free bonsai_rmsnorm_gpu bonsai_attention_prefill_gpu
+    bonsai_buf_upload_i64 bonsai_prefill_forward_gpu bonsai_gpu_available bonsai_attention_decode_batched_gpu
+    bonsai_decode_ctx_create bonsai_decode_ctx_seed_seq bonsai_decode_step bonsai_decode_ctx_free
+    bonsai_gpu_abi_version bonsai_gpu_last_error_code bonsai_gpu_last_error""".split()
+    so = _lib.lib()
+    assert [n for n in names if not hasattr(so, n)] == []
+    assert so.bonsai_gpu_abi_version() == 3
+
+
+def test_dp4a_refusals_before_any_device_work():
+    """bonsai_q1_linear_dp4a_gpu argument refusals (bonsai_q1_gpu.cu:2249: rc 1 for |L| outside 1..8 or empty
+    shapes) are decided before the device is touched."""
+    so = _lib.lib()
+    x = np.zeros((1, 128), dtype=np.int64)
+    bits = np.zeros((1, 1, 16), dtype=np.uint8)
+    sc = np.ones((1, 1), dtype=np.int64)
+    out = np.zeros((1, 1), dtype=np.int64)
+    for L in (0, 9, -9):
+        assert so.bonsai_q1_linear_dp4a_gpu(x.ctypes.data, bits.ctypes.data, sc.ctypes.data, 1, 1, 1, 16, L,
+                                            out.ctypes.data) == 1
+    assert so.bonsai_q1_linear_dp4a_gpu(x.ctypes.data, bits.ctypes.data, sc.ctypes.data, 0, 1, 1, 16, 4,
+                                        out.ctypes.data) == 1
+    assert so.bonsai_q1_register_weight_i32_bmma(bits.ctypes.data, sc.astype(np.int32).ctypes.data, 1, 1) == -1
+
+
 def test_profile_metric_names_match_the_native_enum():
     """qk_profile_snapshot writes the counters in the order of the PM_* enum of csrc/nmc.hip; the Python names must
     match it one for one (qk_cuda.py:24-34 order)."""
