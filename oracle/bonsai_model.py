@@ -26,9 +26,16 @@ def head_rmsnorm(xh: np.ndarray, frac: int, gain: np.ndarray) -> np.ndarray:
     return fx.rmsnorm(xh.reshape(a * b, d), frac, 1, gain).reshape(a, b, d)
 
 
-def layer_forward(x, layer, cfg, cos, sin, frac, kcache, vcache, start, q1=q1_linear):
+def _silu_mul(gate, up, frac):
+    return fx.mulshift_wrap(fx.silu_wrap(gate, frac), up, frac)
+
+
+def layer_forward(x, layer, cfg, cos, sin, frac, kcache, vcache, start, q1=q1_linear, attn=attention_cached,
+                  silu_mul=_silu_mul):
     """One layer over M new positions [start, start+M). kcache/vcache (Hkv, start, hd) or None.
-    Returns (x_out (M,d), k_new (Hkv,M,hd) post-norm+RoPE, v_new (Hkv,M,hd))."""
+    Returns (x_out (M,d), k_new (Hkv,M,hd) post-norm+RoPE, v_new (Hkv,M,hd)). ``attn`` is pluggable like ``q1``
+    (the C restatement ``oracle.c_oracle.attention_cached`` for 2048-token prefills), and so is the FFN's
+    SiLU(gate)·up (``oracle.c_oracle.silu_mul``)."""
     M = x.shape[0]
     H, Hkv, hd = cfg["H"], cfg["Hkv"], cfg["hd"]
     n1 = fx.rmsnorm(x, frac, 1, layer["n1g"])
@@ -42,14 +49,36 @@ def layer_forward(x, layer, cfg, cos, sin, frac, kcache, vcache, start, q1=q1_li
     kh = apply_neox(kh, cos[start:start + M], sin[start:start + M], frac)
     K = kh if kcache is None else np.concatenate([kcache, kh], axis=1)
     V = vh if vcache is None else np.concatenate([vcache, vh], axis=1)
-    att = attention_cached(qh, K, V, start, frac, fx.inv_sqrt_fp(hd, frac))
+    att = attn(qh, K, V, start, frac, fx.inv_sqrt_fp(hd, frac))
     x = fx.add_wrap(x, q1(att.transpose(1, 0, 2).reshape(M, H * hd), *layer["wo"], frac))
     n2 = fx.rmsnorm(x, frac, 1, layer["n2g"])
     gate = q1(n2, *layer["w1"], frac)
     up = q1(n2, *layer["wu"], frac)
-    h = fx.mulshift_wrap(fx.silu_wrap(gate, frac), up, frac)
+    h = silu_mul(gate, up, frac)
     x = fx.add_wrap(x, q1(h, *layer["w2"], frac))
     return x, kh, vh
+
+
+def layer_forward_rowbuf(x, layer, cfg, cos, sin, frac, kbuf, vbuf, start, q1=q1_linear, silu_mul=_silu_mul):
+    """``layer_forward`` over M new positions [start, start+M) with the cache held in preallocated row buffers
+    kbuf/vbuf (Hkv, cap, hd) int64 (rows [0, start) filled): the new post-RoPE K and raw V rows are written in
+    place and attention runs over rows [0, start+M) with the C restatement (oracle.c_oracle.attention_ld), so a
+    32K-position decode appends without copying the cache. Returns x_out (M, d)."""
+    from .c_oracle import attention_ld
+    M = x.shape[0]
+    H, Hkv, hd = cfg["H"], cfg["Hkv"], cfg["hd"]
+    n1 = fx.rmsnorm(x, frac, 1, layer["n1g"])
+    qh = head_rmsnorm(q1(n1, *layer["wq"], frac).reshape(M, H, hd).transpose(1, 0, 2), frac, layer["qng"])
+    kh = head_rmsnorm(q1(n1, *layer["wk"], frac).reshape(M, Hkv, hd).transpose(1, 0, 2), frac, layer["kng"])
+    vh = q1(n1, *layer["wv"], frac).reshape(M, Hkv, hd).transpose(1, 0, 2)
+    qh = apply_neox(qh, cos[start:start + M], sin[start:start + M], frac)
+    kbuf[:, start:start + M] = apply_neox(kh, cos[start:start + M], sin[start:start + M], frac)
+    vbuf[:, start:start + M] = vh
+    att = attention_ld(qh, kbuf, vbuf, start + M, start, frac, fx.inv_sqrt_fp(hd, frac))
+    x = fx.add_wrap(x, q1(att.transpose(1, 0, 2).reshape(M, H * hd), *layer["wo"], frac))
+    n2 = fx.rmsnorm(x, frac, 1, layer["n2g"])
+    h = silu_mul(q1(n2, *layer["w1"], frac), q1(n2, *layer["wu"], frac), frac)
+    return fx.add_wrap(x, q1(h, *layer["w2"], frac))
 
 
 def layer_decode_batched(x, layer, cfg, cos, sin, frac, kcaches, vcaches, positions, q1=q1_linear):

@@ -7,6 +7,7 @@
 //                      wrapper falls back to the big-int numpy oracle)
 //   * attention        reference_bonsai.py:656-720 numpy path, INCLUDING the masked sentinel entries in the
 //                      softmax, and the fail-loud bounds of fixedpoint.py:207-227 (rc 2)
+//   * SiLU * up       reference_bonsai.py:245-264, :614 over fixedpoint.py:143-174
 //   * nmc linear       north-mini-code/src/nmc/cohere2.py:102-106 + qk_codec.py (exact int128 dot, one floor;
 //                      rc 2 when a result does not fit int64, where numpy's astype would raise)
 // Parity of this file with the numpy oracle is asserted in tests/test_oracle_c.py.
@@ -150,14 +151,46 @@ static int64_t exp2_neg(int64_t u, int64_t frac) {
   return poly >> kk;
 }
 
+// SiLU(gate) * up of the FFN (reference_bonsai.py:245-264 fixed_point_silu over fixedpoint.py:143-174 sigmoid,
+// then :614 mulshift): sig = (e1 << f) // (e0 + e1), e0 = 2^-min(max(x,0), dclip), e1 = 2^-min(max(x,0) - x, dclip)
+// (hard-capped dclip), silu = (x * sig) >> f, h = (silu * up) >> f, every product wrapping mod 2^64 as in numpy.
+int imo_silu_mul(const int64_t *gate, const int64_t *up, int64_t n, int64_t frac, int64_t *out) {
+  if (!gate || !up || !out || n < 0 || frac < 1 || frac > 29) return 1;
+  const int64_t log2e = scaled_log2e(frac);
+  const int64_t dca = ((frac + 2) << (2 * frac)) / log2e, dcb = ((int64_t)1 << 62) / log2e;
+  const int64_t dclip = dca < dcb ? dca : dcb;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t x = gate[i];
+    const int64_t m = x > 0 ? x : 0;
+    int64_t d0 = m < dclip ? m : dclip;
+    int64_t d1 = (int64_t)((uint64_t)m - (uint64_t)x);
+    d1 = d1 < dclip ? d1 : dclip;
+    const int64_t e0 = exp2_neg((int64_t)((uint64_t)d0 * (uint64_t)log2e) >> frac, frac);
+    const int64_t e1 = exp2_neg((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> frac, frac);
+    const int64_t z = (int64_t)((uint64_t)e0 + (uint64_t)e1);
+    int64_t sig = 0;
+    if (z != 0) {
+      const int64_t num = (int64_t)((uint64_t)e1 << frac);
+      sig = num / z;
+      if ((num % z) != 0 && ((num < 0) != (z < 0))) sig -= 1;
+    }
+    const int64_t silu = (int64_t)((uint64_t)x * (uint64_t)sig) >> frac;
+    out[i] = (int64_t)((uint64_t)silu * (uint64_t)up[i]) >> frac;
+  }
+  return 0;
+}
+
 static uint64_t absu(int64_t v) { return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v; }
 
-// q (H,M,hd); k,v (Hkv,L,hd) with L = start + M; out (H,M,hd). numpy path of reference_bonsai.py:708-719.
-// Scratch: per thread L int64. rc 2 where the numpy oracle raises OverflowError.
-int imo_attention(const int64_t *q, const int64_t *k, const int64_t *v, int64_t H, int64_t Hkv, int64_t hd,
-                  int64_t M, int64_t L, int64_t start, int64_t frac, int64_t inv_sqrt, int64_t *out) {
+// q (H,M,hd); k,v (Hkv,L,hd) with L = start + M, kv head h2's row j at (h2 * ldk + j) * hd (ldk >= L: a cache
+// with room for more rows); out (H,M,hd). numpy path of reference_bonsai.py:708-719. rc 2 where the numpy oracle
+// raises OverflowError. Sums wrap mod 2^64, so their order (here row-major over V) does not change them.
+int imo_attention_ld(const int64_t *q, const int64_t *k, const int64_t *v, int64_t H, int64_t Hkv, int64_t hd,
+                     int64_t M, int64_t L, int64_t ldk, int64_t start, int64_t frac, int64_t inv_sqrt,
+                     int64_t *out) {
   if (!q || !k || !v || !out || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || M <= 0 || L != start + M ||
-      frac < 1 || frac > 29)
+      ldk < L || frac < 1 || frac > 29)
     return 1;
   const int64_t rep = H / Hkv;
   const int64_t log2e = scaled_log2e(frac);
@@ -165,61 +198,68 @@ int imo_attention(const int64_t *q, const int64_t *k, const int64_t *v, int64_t 
   const int64_t dclip = dca < dcb ? dca : dcb;
   const int64_t neg = -((int64_t)1 << (frac + 30));
   int rc = 0;
-  // QK bound per head: max|q_h| * max|K_kv| * hd
-  for (int64_t h = 0; h < H; ++h) {
-    const int64_t kv = h / rep;
-    uint64_t mq = 0, mk = 0;
-    for (int64_t i = 0; i < M * hd; ++i) { const uint64_t a = absu(q[h * M * hd + i]); if (a > mq) mq = a; }
-    for (int64_t i = 0; i < L * hd; ++i) { const uint64_t a = absu(k[kv * L * hd + i]); if (a > mk) mk = a; }
-    if ((u128)mq * mk * (u128)hd > (u128)INT64_MAX) return 2;
-  }
-  int64_t *probs = (int64_t *)malloc((size_t)(H * M * L) * 8);
-  if (!probs) return 1;
-#pragma omp parallel for collapse(2) schedule(static)
-  for (int64_t h = 0; h < H; ++h)
-    for (int64_t m = 0; m < M; ++m) {
-      const int64_t kv = h / rep;
-      const int64_t *qr = q + (h * M + m) * hd;
-      int64_t *p = probs + (h * M + m) * L;
-      int64_t mx = INT64_MIN;
-      for (int64_t j = 0; j < L; ++j) {
-        int64_t s;
-        if (j > start + m) s = neg;
-        else {
-          uint64_t dot = 0;
-          const int64_t *kr = k + (kv * L + j) * hd;
-          for (int64_t d = 0; d < hd; ++d) dot += (uint64_t)qr[d] * (uint64_t)kr[d];
-          s = (int64_t)dot >> frac;
-          s = (int64_t)((uint64_t)s * (uint64_t)inv_sqrt) >> frac;
-        }
-        p[j] = s;
-        if (s > mx) mx = s;
-      }
-      uint64_t Z = 0;
-      for (int64_t j = 0; j < L; ++j) {
-        int64_t d = (int64_t)((uint64_t)mx - (uint64_t)p[j]);
-        if (d > dclip) d = dclip;
-        const int64_t u = (int64_t)((uint64_t)d * (uint64_t)log2e) >> frac;
-        p[j] = exp2_neg(u, frac);
-        Z += (uint64_t)p[j];
-      }
-      for (int64_t j = 0; j < L; ++j) {
-        if (Z == 0) p[j] = 0;
-        else {
-          const int64_t num = (int64_t)((uint64_t)p[j] << frac);
-          int64_t qq = num / (int64_t)Z;
-          if ((num % (int64_t)Z) != 0 && num < 0) qq -= 1;
-          p[j] = qq;
-        }
-      }
+  uint64_t *mk = (uint64_t *)calloc((size_t)(2 * Hkv), 8), *mv = mk + Hkv;
+  if (!mk) return 1;
+#pragma omp parallel for schedule(static)
+  for (int64_t kv = 0; kv < Hkv; ++kv)
+    for (int64_t i = 0; i < L * hd; ++i) {
+      const uint64_t a = absu(k[kv * ldk * hd + i]), b = absu(v[kv * ldk * hd + i]);
+      if (a > mk[kv]) mk[kv] = a;
+      if (b > mv[kv]) mv[kv] = b;
     }
-  // PV bound per head: max|P_h| * max|V_kv| * L
+  // QK bound per head: max|q_h| * max|K_kv| * hd
   for (int64_t h = 0; h < H && !rc; ++h) {
-    const int64_t kv = h / rep;
-    uint64_t mp = 0, mv = 0;
-    for (int64_t i = 0; i < M * L; ++i) { const uint64_t a = absu(probs[h * M * L + i]); if (a > mp) mp = a; }
-    for (int64_t i = 0; i < L * hd; ++i) { const uint64_t a = absu(v[kv * L * hd + i]); if (a > mv) mv = a; }
-    if ((u128)mp * mv * (u128)L > (u128)INT64_MAX) rc = 2;
+    uint64_t mq = 0;
+    for (int64_t i = 0; i < M * hd; ++i) { const uint64_t a = absu(q[h * M * hd + i]); if (a > mq) mq = a; }
+    if ((u128)mq * mk[h / rep] * (u128)hd > (u128)INT64_MAX) rc = 2;
+  }
+  int64_t *probs = rc ? NULL : (int64_t *)malloc((size_t)(H * M * L) * 8);
+  if (!rc && !probs) rc = 1;
+  if (!rc) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t h = 0; h < H; ++h)
+      for (int64_t m = 0; m < M; ++m) {
+        const int64_t kv = h / rep;
+        const int64_t *qr = q + (h * M + m) * hd;
+        int64_t *p = probs + (h * M + m) * L;
+        int64_t mx = INT64_MIN;
+        for (int64_t j = 0; j < L; ++j) {
+          int64_t s;
+          if (j > start + m) s = neg;
+          else {
+            uint64_t dot = 0;
+            const int64_t *kr = k + (kv * ldk + j) * hd;
+            for (int64_t d = 0; d < hd; ++d) dot += (uint64_t)qr[d] * (uint64_t)kr[d];
+            s = (int64_t)dot >> frac;
+            s = (int64_t)((uint64_t)s * (uint64_t)inv_sqrt) >> frac;
+          }
+          p[j] = s;
+          if (s > mx) mx = s;
+        }
+        uint64_t Z = 0;
+        for (int64_t j = 0; j < L; ++j) {
+          int64_t d = (int64_t)((uint64_t)mx - (uint64_t)p[j]);
+          if (d > dclip) d = dclip;
+          const int64_t u = (int64_t)((uint64_t)d * (uint64_t)log2e) >> frac;
+          p[j] = exp2_neg(u, frac);
+          Z += (uint64_t)p[j];
+        }
+        for (int64_t j = 0; j < L; ++j) {
+          if (Z == 0) p[j] = 0;
+          else {
+            const int64_t num = (int64_t)((uint64_t)p[j] << frac);
+            int64_t qq = num / (int64_t)Z;
+            if ((num % (int64_t)Z) != 0 && num < 0) qq -= 1;
+            p[j] = qq;
+          }
+        }
+      }
+    // PV bound per head: max|P_h| * max|V_kv| * L
+    for (int64_t h = 0; h < H && !rc; ++h) {
+      uint64_t mp = 0;
+      for (int64_t i = 0; i < M * L; ++i) { const uint64_t a = absu(probs[h * M * L + i]); if (a > mp) mp = a; }
+      if ((u128)mp * mv[h / rep] * (u128)L > (u128)INT64_MAX) rc = 2;
+    }
   }
   if (!rc) {
 #pragma omp parallel for collapse(2) schedule(static)
@@ -227,15 +267,47 @@ int imo_attention(const int64_t *q, const int64_t *k, const int64_t *v, int64_t 
       for (int64_t m = 0; m < M; ++m) {
         const int64_t kv = h / rep;
         const int64_t *p = probs + (h * M + m) * L;
-        for (int64_t d = 0; d < hd; ++d) {
-          uint64_t acc = 0;
-          for (int64_t j = 0; j < L; ++j) acc += (uint64_t)p[j] * (uint64_t)v[(kv * L + j) * hd + d];
-          out[(h * M + m) * hd + d] = (int64_t)acc >> frac;
+        uint64_t acc[256];
+        for (int64_t d = 0; d < hd; ++d) acc[d] = 0;
+        for (int64_t j = 0; j < L; ++j) {
+          const uint64_t pj = (uint64_t)p[j];
+          const int64_t *vr = v + (kv * ldk + j) * hd;
+          for (int64_t d = 0; d < hd; ++d) acc[d] += pj * (uint64_t)vr[d];
         }
+        for (int64_t d = 0; d < hd; ++d) out[(h * M + m) * hd + d] = (int64_t)acc[d] >> frac;
       }
   }
   free(probs);
+  free(mk);
   return rc;
+}
+
+int imo_attention(const int64_t *q, const int64_t *k, const int64_t *v, int64_t H, int64_t Hkv, int64_t hd,
+                  int64_t M, int64_t L, int64_t start, int64_t frac, int64_t inv_sqrt, int64_t *out) {
+  if (hd > 256) return 1;
+  return imo_attention_ld(q, k, v, H, Hkv, hd, M, L, L, start, frac, inv_sqrt, out);
+}
+
+// The synthetic stream of oracle/prng.py `uniform_int` (counter-based SplitMix64): element i of tensor (seed, tid)
+// is (mix(key + (i + 1) * gamma) mod span) + lo, key = mix(seed * 0x100000001B3 + tid * 0x9E3779B1 + c). Writes
+// elements i = i0 + r * C + c (r < R, c < C) to out[r * ld + c] (ld >= C).
+static inline uint64_t sm_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+int imo_uniform_fill(uint64_t seed, uint64_t tid, int64_t i0, int64_t R, int64_t C, int64_t ld, int64_t lo,
+                     uint64_t span, int64_t *out) {
+  if (!out || i0 < 0 || R < 0 || C < 0 || ld < C || span == 0) return 1;
+  const uint64_t key = sm_mix(seed * 0x100000001B3ull + tid * 0x9E3779B1ull + 0x632BE59BD9B4E019ull);
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t c = 0; c < C; ++c) {
+      const uint64_t i = (uint64_t)(i0 + r * C + c);
+      out[r * ld + c] = (int64_t)(sm_mix(key + (i + 1) * 0x9E3779B97F4A7C15ull) % span) + lo;
+    }
+  return 0;
 }
 
 // ---------------------------------------------------------------------------------------------------------

@@ -26,9 +26,14 @@ def lib():
     so.imo_rmsnorm.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]
     so.imo_attention.argtypes = [c_void_p] * 3 + [c_int64] * 8 + [c_void_p]
     so.imo_qk_linear.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_void_p]
+    so.imo_attention_ld.argtypes = [c_void_p] * 3 + [c_int64] * 9 + [c_void_p]
+    so.imo_uniform_fill.argtypes = [ctypes.c_uint64, ctypes.c_uint64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                    ctypes.c_uint64, c_void_p]
+    so.imo_silu_mul.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_void_p]
     so.imo_fp16_fixed.argtypes = [ctypes.c_uint16, c_int]
     so.imo_fp16_fixed.restype = c_int64
-    for f in (so.imo_q1_linear, so.imo_rmsnorm, so.imo_attention, so.imo_qk_linear):
+    for f in (so.imo_q1_linear, so.imo_rmsnorm, so.imo_attention, so.imo_qk_linear, so.imo_silu_mul,
+              so.imo_attention_ld, so.imo_uniform_fill):
         f.restype = c_int
     return so
 
@@ -62,6 +67,16 @@ def rmsnorm(x, frac, eps=1, gain=None):
     return out
 
 
+def silu_mul(gate, up, frac):
+    """(silu(gate) * up) >> frac, elementwise, wrapping (fx.mulshift_wrap(fx.silu_wrap(gate), up))."""
+    g = _c(gate)
+    u = _c(up)
+    assert g.shape == u.shape
+    out = np.empty(g.shape, dtype=np.int64)
+    assert lib().imo_silu_mul(g.ctypes.data, u.ctypes.data, g.size, int(frac), out.ctypes.data) == 0
+    return out
+
+
 def attention_cached(qh, k, v, start, frac, inv_sqrt):
     q = _c(qh)
     k = _c(k)
@@ -75,6 +90,30 @@ def attention_cached(qh, k, v, start, frac, inv_sqrt):
         raise OverflowError("fixed_point_matmul bound exceeded")
     assert rc == 0
     return out
+
+
+def attention_ld(qh, kbuf, vbuf, L, start, frac, inv_sqrt):
+    """attention_cached over the first L rows of per-kv-head row buffers kbuf/vbuf (Hkv, cap, hd), cap >= L."""
+    q = _c(qh)
+    assert kbuf.flags.c_contiguous and vbuf.flags.c_contiguous and kbuf.dtype == np.int64 == vbuf.dtype
+    H, M, hd = q.shape
+    Hkv, cap, _ = kbuf.shape
+    out = np.empty((H, M, hd), dtype=np.int64)
+    rc = lib().imo_attention_ld(q.ctypes.data, kbuf.ctypes.data, vbuf.ctypes.data, H, Hkv, hd, M, int(L), cap,
+                                int(start), int(frac), int(inv_sqrt), out.ctypes.data)
+    if rc == 2:
+        raise OverflowError("fixed_point_matmul bound exceeded")
+    assert rc == 0
+    return out
+
+
+def uniform_fill(seed: int, tid: int, out: np.ndarray, rows: int, cols: int, lo: int, hi: int, first: int = 0) -> None:
+    """Elements first .. first + rows*cols of the stream of prng.uniform_int(seed, tid, ..., lo, hi), as a (rows,
+    cols) block written into the first ``cols`` entries of the first ``rows`` rows of the 2-D int64 array ``out``
+    (row stride out.shape[1])."""
+    assert out.flags.c_contiguous and out.dtype == np.int64 and out.ndim == 2 and out.shape[1] >= cols
+    assert out.shape[0] >= rows
+    assert lib().imo_uniform_fill(seed, tid, int(first), rows, cols, out.shape[1], lo, hi - lo, out.ctypes.data) == 0
 
 
 def qk_linear(raw: np.ndarray, x, out_f: int, nb: int, fw: int, qtype: int):

@@ -106,3 +106,61 @@ def test_numpy_attention_equals_reference_c_kernels():
     outp = np.empty((H, M, hd), dtype=np.int64)
     assert pre(qp.ctypes.data, kp.ctypes.data, vp.ctypes.data, H, Hkv, hd, M, M, 0, 16, 5793, outp.ctypes.data) == 0
     assert np.array_equal(outp, attention_cached(qp, kp, vp, 0, 16, 5793))
+
+
+def _silu_inputs(seed, n=4000):
+    rng = np.random.default_rng(seed)
+    x = np.concatenate([rng.integers(-(1 << 24), 1 << 24, size=n), rng.integers(I64_MIN, I64_MAX, size=64),
+                        [0, 1, -1, I64_MIN, I64_MAX, I64_MIN + 1, 1 << 40, -(1 << 40)]]).astype(np.int64)
+    up = rng.integers(-(1 << 30), 1 << 30, size=x.size).astype(np.int64)
+    up[-8:] = [I64_MAX, I64_MIN, 3, -3, 1 << 62, -(1 << 62), 7, I64_MIN + 1]
+    return x, up
+
+
+@pytest.mark.parametrize("frac", [16, 1, 29])
+def test_c_silu_mul_equals_numpy(frac):
+    x, up = _silu_inputs(frac)
+    want = fx.mulshift_wrap(fx.silu_wrap(x, frac), up, frac)
+    assert np.array_equal(c_oracle.silu_mul(x, up, frac), want)
+
+
+def test_c_silu_mul_equals_reference_c_kernel():
+    """bonsai_q1_kernel.c:1729-1767 bonsai_silu_i64, then the mulshift of reference_bonsai.py:614."""
+    so = _ref("libbonsai_q1_kernel.so")
+    f = so.bonsai_silu_i64
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    x, up = _silu_inputs(3)
+    s = np.empty_like(x)
+    assert f(x.ctypes.data, x.size, 16, s.ctypes.data) == 0
+    assert np.array_equal(c_oracle.silu_mul(x, up, 16), fx.mulshift_wrap(s, up, 16))
+
+
+@pytest.mark.parametrize("H,Hkv,hd,M,start,extra", [(4, 2, 32, 1, 40, 9), (8, 2, 16, 3, 5, 1), (2, 1, 128, 1, 0, 64)])
+def test_c_attention_ld_equals_numpy_on_row_buffers(H, Hkv, hd, M, start, extra):
+    """Rows [0, L) of (Hkv, L + extra, hd) buffers give the contiguous attention's result (decode over a cache
+    with room for more rows)."""
+    L = start + M
+    rng = np.random.default_rng(H * 100 + L)
+    q = rng.integers(-(1 << 20), 1 << 20, size=(H, M, hd), dtype=np.int64)
+    kb = rng.integers(-(1 << 20), 1 << 20, size=(Hkv, L + extra, hd), dtype=np.int64)
+    vb = rng.integers(-(1 << 20), 1 << 20, size=(Hkv, L + extra, hd), dtype=np.int64)
+    kb[:, L:] = 1 << 40                                       # rows past L must not be read (bounds included)
+    vb[:, L:] = -(1 << 40)
+    want = attention_cached(q, kb[:, :L].copy(), vb[:, :L].copy(), start, 16, 5793)
+    assert np.array_equal(c_oracle.attention_ld(q, kb, vb, L, start, 16, 5793), want)
+
+
+def test_c_uniform_fill_equals_prng_stream():
+    from oracle import workloads
+    out = np.full((2 * 50, 40), 7, dtype=np.int64)
+    c_oracle.uniform_fill(13, 100000 + 1024 * 3 + 512 + 5, out, 2 * 37, 32, -(1 << 20), 1 << 20)
+    want = workloads.kv_fill_seq(13, 3, 1, 5, 2, 37, 32)
+    assert np.array_equal(out[:74, :32], want.reshape(74, 32)) and (out[:74, 32:] == 7).all()
+    assert (out[74:] == 7).all()
+    part = np.zeros((37, 32), dtype=np.int64)                 # kv head 1 alone: stream offset 37 * 32
+    c_oracle.uniform_fill(13, 100000 + 1024 * 3 + 512 + 5, part, 37, 32, -(1 << 20), 1 << 20, first=37 * 32)
+    assert np.array_equal(part, want[1])
+    big = np.empty((3, 5), dtype=np.int64)
+    c_oracle.uniform_fill(2, 9, big, 3, 5, -(1 << 61), 1 << 62)
+    assert np.array_equal(big, prng.uniform_int(2, 9, (3, 5), -(1 << 61), 1 << 62))

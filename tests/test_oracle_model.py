@@ -56,3 +56,26 @@ def test_head_rmsnorm_is_rowwise_rmsnorm():
     for a in range(4):
         for b in range(3):
             assert np.array_equal(out[a, b], fx.rmsnorm(xh[a, b][None], 16, 1, g)[0])
+
+
+def test_rowbuf_layer_equals_layer_forward():
+    """The in-place row-buffer form (used for 32K-position decodes) equals layer_forward: a 5-row prefill and two
+    single-row decodes, outputs and the cache rows, with the C silu/attention restatements."""
+    from oracle import c_oracle
+    model = workloads.small_bonsai(seed=8, ctx=64)
+    c = _cfg(model)
+    cfg = model["cfg"]
+    ids = prng.uniform_int(8, 1, (7,), 0, cfg["vocab"])
+    x = q1_rows(*model["embed"], ids)
+    layer = model["layers"][1]
+    kb = np.zeros((cfg["Hkv"], 20, cfg["hd"]), dtype=np.int64)
+    vb = np.zeros_like(kb)
+    k = v = None
+    for start, M in ((0, 5), (5, 1), (6, 1)):
+        want, kn, vn = obm.layer_forward(x[start:start + M], layer, c, model["cos"], model["sin"], 16, k, v, start)
+        k = kn if k is None else np.concatenate([k, kn], axis=1)
+        v = vn if v is None else np.concatenate([v, vn], axis=1)
+        got = obm.layer_forward_rowbuf(x[start:start + M], layer, c, model["cos"], model["sin"], 16, kb, vb, start,
+                                       silu_mul=c_oracle.silu_mul)
+        assert np.array_equal(got, want)
+        assert np.array_equal(kb[:, :start + M], k) and np.array_equal(vb[:, :start + M], v)
