@@ -79,6 +79,12 @@ int imie_q1_repack_host(const uint8_t *bits, const int64_t *scale, int64_t N, in
 /* device-pointer resident apply, asynchronous on `stream`. */
 int imie_q1_apply_dev(int64_t handle, const int64_t *x_dev, int64_t tokens, int64_t frac, int64_t *out_dev,
                       void *stream);
+/* No reference counterpart: imie_q1_apply_dev for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Same arguments and results; the digit-table workspace
+ * is a fixed 1.8 MiB device array held per device for the life of the process. tokens <= 7 and n_blocks <= 256
+ * (K <= 32768), else rc 1 (reason in imie_last_error). Calls overlapping on one device race on that array. */
+int imie_q1_apply_dev_noalloc(int64_t handle, const int64_t *x_dev, int64_t tokens, int64_t frac, int64_t *out_dev,
+                              void *stream);
 int imie_q1_weight_info(int64_t handle, int64_t *out_features, int64_t *n_blocks, int64_t *scale_bytes);
 /* exact thread-per-output kernel over natural-layout device buffers (cross-check path). */
 int imie_q1_linear_simple_dev(const int64_t *x_dev, const uint8_t *bits_dev, const int64_t *scale_dev,

@@ -51,6 +51,7 @@ SIGNATURES = {
     "bonsai_q1_resident_weight_bytes": (c_uint64, []),
     "imie_q1_repack_host": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "imie_q1_apply_dev": (c_int, [c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "imie_q1_apply_dev_noalloc": (c_int, [c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "imie_q1_weight_info": (c_int, [c_int64, c_void_p, c_void_p, c_void_p]),
     "imie_q1_linear_simple_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                           c_void_p, c_void_p]),

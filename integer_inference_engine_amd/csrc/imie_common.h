@@ -21,6 +21,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 void imie_note_error(hipError_t e, const char* what);
+void imie_note_message(const char* msg);        // a refusal's reason for imie_last_error (no HIP error)
 hipStream_t imie_stream();                 // the library's default stream (created on first use)
 std::recursive_mutex& imie_lock();         // the library is single-caller; ABI entry points take this lock
 int imie_device_ready();                   // 0 when a gfx9xx device is usable

@@ -1585,6 +1585,71 @@ int imie_q1_apply_dev(int64_t handle, const int64_t* x_dev, int64_t tokens, int6
   return q1_apply_dev(*w, x_dev, tokens, frac, out_dev, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+// ---- fixed scratch for callers that cannot allocate ------------------------------------------------------
+// The matvec path (T < kGemmMinT) keeps its per-call digit table (xq), block totals and slab limb counts in a
+// workspace; imie_q1_apply_dev_noalloc takes that workspace from this file-scope array instead of the allocator.
+// Sized for kNaMaxT tokens of up to kNaMaxSlabs 512-column slabs (K <= 32768). Each device holds its own copy for
+// the life of the process; host code reaches it only through the address hipGetSymbolAddress gives on that device.
+constexpr int64_t kNaMaxT = kGemmMinT - 1;
+constexpr int64_t kNaMaxSlabs = 64;
+constexpr size_t kNaXqBytes = (size_t)kNaMaxT * kMaxLimbs * (kNaMaxSlabs * kSlabBlocks) * 8 * 16;
+constexpr size_t kNaTotBytes = (size_t)kNaMaxT * (kNaMaxSlabs * kSlabBlocks) * 8;
+constexpr size_t kNaLsBytes = (size_t)kNaMaxT * kNaMaxSlabs * 4;
+constexpr size_t kNaAlign(size_t b) { return (b + 255) / 256 * 256; }
+constexpr size_t kNaBytes = kNaAlign(kNaXqBytes) + kNaAlign(kNaTotBytes) + kNaAlign(kNaLsBytes);
+static __device__ __align__(256) uint8_t scratch[kNaBytes];
+
+// this device's address of `scratch`, looked up once per device (nullptr if the lookup fails)
+static uint8_t* na_scratch_ptr() {
+  static std::vector<uint8_t*> per_dev;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+  if ((size_t)dev >= per_dev.size()) per_dev.resize((size_t)dev + 1, nullptr);
+  if (!per_dev[(size_t)dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) { imie_note_error(e, "hipGetSymbolAddress(scratch)"); return nullptr; }
+    per_dev[(size_t)dev] = (uint8_t*)p;
+  }
+  return per_dev[(size_t)dev];
+}
+
+extern "C" {
+
+// imie_q1_apply_dev without any allocation (no reference counterpart): for callers that cannot call hipMalloc
+// (graph capture, tight serving loops). tokens in 1..7 and n_blocks <= 256 (K <= 32768), else rc 1 with the reason
+// in imie_last_error. The digit-table workspace is the fixed device array above, shared by every call on this
+// device: calls that overlap on one device (two streams, two threads) race on it. Nothing in it must start at zero
+// (each call writes every entry it reads), and the K-split outputs are cleared by the call's own prep kernel.
+int imie_q1_apply_dev_noalloc(int64_t handle, const int64_t* x_dev, int64_t tokens, int64_t frac, int64_t* out_dev,
+                              void* stream) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  const Q1Weight* w = q1_get(handle);
+  if (!w || !x_dev || !out_dev || tokens < 0 || frac < 0) return IMIE_EARG;
+  if (tokens == 0) return IMIE_OK;
+  if (tokens > kNaMaxT || w->nslabs > kNaMaxSlabs) {
+    imie_note_message("imie_q1_apply_dev_noalloc: at most 7 tokens and 32768 input columns fit its fixed scratch");
+    return IMIE_EARG;
+  }
+  uint8_t* base = na_scratch_ptr();
+  if (!base) return IMIE_EARG;
+  Q1Ws wk;                                            // views into the fixed array: ensure() never allocates here
+  wk.xq.p = base;
+  wk.xq.cap = kNaXqBytes;
+  wk.totals.p = base + kNaAlign(kNaXqBytes);
+  wk.totals.cap = kNaTotBytes;
+  wk.lslab.p = base + kNaAlign(kNaXqBytes) + kNaAlign(kNaTotBytes);
+  wk.lslab.cap = kNaLsBytes;
+  const Q1Weight* ws[1] = {w};
+  int64_t* outs[1] = {out_dev};
+  const bool prof = imie_prof_suspend(true);          // the profiler's per-kernel events are created on demand
+  const int rc = q1_apply_multi(ws, 1, x_dev, tokens, frac, outs, 0, wk, (hipStream_t)stream);
+  imie_prof_suspend(prof);
+  return rc;
+}
+
 // Weight geometry of a handle: out_features, n_blocks, scale width in bytes (4 or 8).
 int imie_q1_weight_info(int64_t handle, int64_t* out_features, int64_t* n_blocks, int64_t* scale_bytes) {
   std::lock_guard<std::recursive_mutex> lk(imie_lock());

@@ -19,6 +19,11 @@ void imie_note_error(hipError_t e, const char* what) {
   snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(e));
 }
 
+void imie_note_message(const char* msg) {
+  g_last_error_code = 0;
+  snprintf(g_last_error, sizeof(g_last_error), "%s", msg);
+}
+
 int imie_device_ready() {
   if (g_ready >= 0) return g_ready == 1 ? 0 : 1;
   int n = 0;
