@@ -44,34 +44,54 @@ def matvec_bytes(scale_bytes: int) -> int:
     return K * NB * 16 + K * NB * scale_bytes + K * 8 + K * 8
 
 
-def cpu_worker(npz: str, seconds: float) -> None:
-    """Time the reference CPU kernel (or the C restatement) on the config-1 matvec; print one JSON line."""
-    import ctypes
-    d = np.load(npz)
-    x, bits, scale, gpu_out = d["x"], d["bits"], d["scale"], d["out"]
+def _ref_q1():
+    """(function, kind) of the CPU Q1 linear: the reference's C kernel built from its sources into oracle/_ref when
+    present ("reference"), else the C restatement of the oracle ("port")."""
     ref = ROOT / "oracle" / "_ref" / "libbonsai_q1_kernel.so"
     if ref.exists():
         so = ctypes.CDLL(str(ref))
         fn, kind = so.bonsai_q1_linear_i64, "reference"
     else:
         from oracle import c_oracle
-        so = c_oracle.lib()
-        fn, kind = so.imo_q1_linear, "port"
+        fn, kind = c_oracle.lib().imo_q1_linear, "port"
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_void_p]
+    return fn, kind
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_worker(npz: str, seconds: float, reps: int) -> None:
+    """Time the CPU Q1 linear on the config-1 matvec: ``reps`` repetitions of ``seconds`` each with the thread
+    count this process was given (OMP_NUM_THREADS); print one JSON line with the median."""
+    d = np.load(npz)
+    x, bits, scale, gpu_out = d["x"], d["bits"], d["scale"], d["out"]
+    fn, kind = _ref_q1()
     out = np.empty((1, K), dtype=np.int64)
     call = lambda: fn(x.ctypes.data, bits.ctypes.data, scale.ctypes.data, 1, K, NB, 16, out.ctypes.data)
     assert call() == 0
     match = bool(np.array_equal(out, gpu_out))
-    n, t0 = 0, time.perf_counter()
-    while True:
-        call()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    gbs = matvec_bytes(8) * n / el / 1e9
-    print(json.dumps({"value": gbs, "unit": "GB/s", "kind": kind, "calls": n, "seconds": el, "match": match}))
+    rates, calls = [], 0
+    for _ in range(reps):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            call()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        rates.append(matvec_bytes(8) * n / el / 1e9)
+        calls += n
+    print(json.dumps({"value": float(np.median(rates)), "reps": rates, "unit": "GB/s", "kind": kind,
+                      "calls": calls, "seconds": seconds * reps, "match": match}))
 
 
 def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, vocab: int = 151936,
@@ -352,7 +372,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--replicas", type=int, default=384)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=2.0, help="seconds per CPU-baseline repetition")
+    ap.add_argument("--cpu-reps", type=int, default=5, help="CPU-baseline repetitions (median reported)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=32, help="8B-shape b=1 decode leg (0 = skip)")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="config-3 layer prefill leg (0 = skip)")
@@ -363,7 +384,7 @@ def main() -> int:
                     help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     args = ap.parse_args()
     if args.cpu_worker:
-        cpu_worker(args.cpu_worker, args.cpu_seconds)
+        cpu_worker(args.cpu_worker, args.cpu_seconds, args.cpu_reps)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures ONE MI355X; --gpus {args.gpus} is not supported "
@@ -419,7 +440,7 @@ def main() -> int:
     torch.cuda.synchronize()
     exact = bool(torch.equal(chk[0], out[0, :K]))
 
-    so.imie_profile_begin()
+    # timed region: the K steps alone (no profiler events on the stream)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -429,6 +450,12 @@ def main() -> int:
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1)
+    # the dominant kernel's launch duration: the same K steps again with HIP events around each launch, on the
+    # stream the kernel runs on
+    so.imie_profile_begin()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
     kms, kcnt = ctypes.c_double(), ctypes.c_int64()
     so.imie_profile_read(1, ctypes.byref(kms), ctypes.byref(kcnt))
     pms, pcnt = ctypes.c_double(), ctypes.c_int64()
@@ -444,22 +471,45 @@ def main() -> int:
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
 
+    # byte-exactness of the timed launch: every replica's 4096 outputs against the CPU Q1 linear (the reference C
+    # kernel when built) on the same weights and x
+    out_host = out.cpu().numpy()
+    ref_fn, ref_kind = _ref_q1()
+    ref_out = np.empty((1, K), dtype=np.int64)
+    bad = 0
+    for r in range(R):
+        br = np.ascontiguousarray(bits[r * K:(r + 1) * K])
+        sr = np.ascontiguousarray(scale[r * K:(r + 1) * K])
+        assert ref_fn(x_host.ctypes.data, br.ctypes.data, sr.ctypes.data, 1, K, NB, 16, ref_out.ctypes.data) == 0
+        bad += int(not np.array_equal(ref_out[0], out_host[0, r * K:(r + 1) * K]))
+
     cpu = None
     if not args.no_cpu_baseline:
+        # the host's CPU share on the GPU box (OMP_NUM_THREADS there, else the cores this process may use), and one
+        # thread; each the median of --cpu-reps repetitions of --cpu-seconds
+        share = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+        res = {}
         with tempfile.TemporaryDirectory() as td:
             npz = os.path.join(td, "c1.npz")
-            np.savez(npz, x=x_host, bits=bits[:K], scale=scale[:K], out=out[:, :K].cpu().numpy())
-            cores = min(os.cpu_count() or 1, 16)
-            env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close")
-            r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-worker", npz, "--cpu-seconds",
-                                str(args.cpu_seconds)], env=env, capture_output=True, text=True, timeout=300)
-            if r.returncode == 0:
-                c = json.loads(r.stdout.strip().splitlines()[-1])
-                cpu = {"value": round(c["value"], 3), "unit": "GB/s", "cores": cores, "kind": c["kind"],
-                       "sample": f"config-1 4096x4096 Q1_0 matvec (int64 codec-range scales), {c['calls']} calls "
-                                 f"in {c['seconds']:.1f} s; output byte-equal to GPU: {c['match']}"}
-            else:
-                print(r.stderr[-2000:], file=sys.stderr)
+            np.savez(npz, x=x_host, bits=bits[:K], scale=scale[:K], out=out_host[:, :K])
+            for threads in (share, 1):
+                env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close")
+                r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-worker", npz, "--cpu-seconds",
+                                    str(args.cpu_seconds), "--cpu-reps", str(args.cpu_reps)], env=env,
+                                   capture_output=True, text=True, timeout=600)
+                if r.returncode != 0:
+                    print(r.stderr[-2000:], file=sys.stderr)
+                    break
+                res[threads] = json.loads(r.stdout.strip().splitlines()[-1])
+        if share in res and 1 in res:
+            c, c1 = res[share], res[1]
+            cpu = {"value": round(c["value"], 3), "unit": "GB/s", "cores": share, "kind": c["kind"],
+                   "single_thread_value": round(c1["value"], 3), "cpu_model": cpu_model(),
+                   "host_cpus": os.cpu_count(),
+                   "sample": f"config-1 4096x4096 Q1_0 matvec (int64 codec-range scales), median of "
+                             f"{args.cpu_reps} x {args.cpu_seconds:.0f} s runs at {share} threads "
+                             f"({c['calls']} calls) and at 1 thread ({c1['calls']} calls); output byte-equal "
+                             f"to GPU: {c['match'] and c1['match']}"}
 
     dec = None
     if args.decode_tokens > 0:
@@ -486,10 +536,14 @@ def main() -> int:
         "config": {"workload": f"config-1 Q1_0 matvec 4096x4096, b=1, rotated over {R} resident replicas "
                                f"(one launch = {R} matvecs, {step_bytes / 1e9:.2f} GB)",
                    "replicas": R, "scale_bytes": scale_bytes, "frac": 16, "byte_exact_replica0": exact,
+                   "byte_exact_all_replicas": bad == 0, "replicas_checked": R, "checked_against": ref_kind,
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
                    "us_per_matvec": round(ms / args.steps / R * 1e3, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/q1_matvec_c1_traffic.json: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE of this launch, copy-calibrated" if traffic else None,
+                     "frac_step": round(value / HBM_PEAK_GBS, 4),
                      "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,

@@ -1296,12 +1296,12 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
     for (int i = 0; i < cnt; ++i) { zero.p[i] = outs[i]; zero.n[i] = T * ws[i]->N; }
   }
   const int64_t K = w0.nb * 128;
-  imie_prof_mark(IMIE_K_Q1_PREP, st, true);
   if (!prepped) {
+    imie_prof_mark(IMIE_K_Q1_PREP, st, true);
     Q1PrepOut po = {(uint32_t*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, w0.nb, nbp, nslabs};
     hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, po, zero);
+    imie_prof_mark(IMIE_K_Q1_PREP, st, false);
   }
-  imie_prof_mark(IMIE_K_Q1_PREP, st, false);
   IMIE_HIP(hipGetLastError());
   const size_t budget = 48 * 1024;
   // staged limbs come in whole groups of four (a limb group reads either LDS or the global table)
