@@ -11,7 +11,10 @@ sentinel. The router's producer guard (nmc_qk_cuda.cu:615-638) refuses a row who
 ``router_logits`` raises OverflowError there (the producer's rc 3).
 
 Pinned by its parts: RMSNorm, softmax and sigmoid (oracle/fixedpoint.py), the exact Q4_K/Q6_K linear and the
-MoE (oracle/qk.py), and the interleaved RoPE against the NeoX form on a permuted head (tests/test_oracle_qk.py).
+MoE (oracle/qk.py), and the interleaved RoPE against the NeoX form on a permuted head (tests/test_oracle_qk.py);
+and as a whole by tests/test_oracle_nmc_block.py: at every position of a sequence, for windows None / 1 / 3 /
+S - 1 and with RoPE on sliding-window layers only, the decode step equals an independent full-sequence restatement
+of cohere2's masked attention (:85-92, :136-161) and parallel block (:191-199).
 """
 from __future__ import annotations
 
