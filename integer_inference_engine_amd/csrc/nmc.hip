@@ -18,6 +18,7 @@
 #include <stdlib.h>
 #include <algorithm>
 #include <map>
+#include <tuple>
 
 namespace {
 
@@ -216,7 +217,9 @@ __device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
 }
 
 __global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t* __restrict__ u, int64_t n, int fa,
-                                   int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status) {
+                                   int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status,
+                                   const int* __restrict__ run_gate = nullptr) {
+  if (run_gate && *run_gate == 0) return;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t x = g[i];
@@ -301,6 +304,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const int64_t* __restrict_
 }
 
 __global__ void qk_flag_reset_kernel(int* f) { *f = 0; }
+__global__ void qk_flags_reset_kernel(int* f, int n) { if ((int)threadIdx.x < n) f[threadIdx.x] = 0; }
 
 __device__ inline v4i mfma32(int64_t a, int64_t b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, c, 0, 0, 0);
@@ -596,6 +600,378 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Fused MoE expert kernels (the batched MoE of cohere2.py:168-188 with Q4_K gate/up and Q6_K down, the
+// north-mini-code layout): one item per expert = its gate/up/down weights and the (token, pair) list routed to it.
+//   moe_gateup : g = gate . h, u = up . h (the same activation operands feed both), then gu = (silu(g) * u) >> fa
+//                in the epilogue (the exact arithmetic of qk_silu_mul_kernel), written per pair
+//   moe_down   : d = down . gu per pair
+// int8 MFMA v_mfma_i32_16x16x32_i8 with the MFMA M rows = (token t, digit limb l) = 4 t + l: four tokens of up to
+// four balanced base-256 limbs per MFMA (a second MFMA takes limbs 4..7), weight rows in N, one sub-block (Q4_K:
+// 32 positions; Q6_K: 16, the other half of the K groups zeroed in A) per K = 32 step. D lane (t, n) then holds
+// the limb partial sums of token t for weight row n, recombined in place (no cross-lane traffic) into the
+// sub-block dot q.x per limb; S1 = sum_j sc_j q.x_j and S2 = sum_j m_j xsum_j are summed per limb in int32 and
+// recombined once per block into int64 (|x| < 127 (256^5-1)/255: |S1| < 2^57, |S2| < 2^53), and each 256-block
+// adds dq S1 - dmq S2 into a 128-bit (hi, lo) accumulator with one 64 x 64 -> 128 multiply per term. MFMA sums are
+// exact: |D| <= 32 * 128 * 32 < 2^31.
+// Workgroup = (64 weight rows, item), wave = 16 rows; the block loop is software-pipelined: the next block's digits
+// go to the other half of an LDS double buffer and its weights are in flight while a block computes.
+// ---------------------------------------------------------------------------------------------------------
+constexpr int kMoeTok = 4;         // tokens per MFMA row group (4 tokens x 4 limbs = 16 rows)
+constexpr int kMoeLimbs = 8;       // limbs staged (two MFMA row groups); the prep refuses rows beyond kQkLimbs
+
+struct MoeItem {
+  const uint8_t* wg;        // gate (Q4_K), up (Q4_K), down (Q6_K) of the expert
+  const uint8_t* wu;
+  const uint8_t* wd;
+  int first, count;         // into the pair arrays: ptok (activation row of h), ppair (gu / d row)
+};
+
+struct Acc128 {             // two's-complement 128-bit accumulator
+  uint64_t lo;
+  int64_t hi;
+};
+
+__device__ inline void acc_madd(Acc128& a, int64_t x, int64_t y) {
+  const uint64_t pl = (uint64_t)x * (uint64_t)y;
+  const int64_t ph = __mul64hi(x, y);
+  a.lo += pl;
+  a.hi += ph + (a.lo < pl ? 1 : 0);
+}
+
+// floor(acc / 2^fw) and whether it fits int64 (0 <= fw < 64)
+__device__ inline int64_t acc_shift(Acc128 a, int fw, bool* fits) {
+  const i128 v = (i128)(((unsigned __int128)(uint64_t)a.hi << 64) | a.lo);
+  const i128 y = v >> fw;
+  *fits = y <= (i128)INT64_MAX && y >= (i128)INT64_MIN;
+  return (int64_t)y;
+}
+
+// exact nmc SiLU * up of one element (qk_silu_mul_kernel): false when an intermediate leaves int64
+__device__ inline int64_t nmc_silu_mul(int64_t x, int64_t u, int fa, int64_t log2e, int64_t dclip, bool* ok) {
+  const int64_t m = x > 0 ? x : 0;
+  int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
+  if (d0 > dclip) d0 = dclip;
+  if (d1 > dclip) d1 = dclip;
+  const int64_t e0 = exp2_neg_fixed((int64_t)((uint64_t)d0 * (uint64_t)log2e) >> fa, fa);
+  const int64_t e1 = exp2_neg_fixed((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> fa, fa);
+  const int64_t z = e0 + e1;
+  const int64_t sig = z == 0 ? 0 : (int64_t)(((uint64_t)e1 << fa) / (uint64_t)z);
+  const i128 s = ((i128)x * sig) >> fa;
+  bool good = s <= (i128)INT64_MAX && s >= (i128)INT64_MIN;
+  const i128 gu = ((i128)(int64_t)s * u) >> fa;
+  good = good && gu <= (i128)INT64_MAX && gu >= (i128)INT64_MIN;
+  *ok = good;
+  return (int64_t)gu;
+}
+
+// Staging of one block's digits (L limbs x kMoeTok tokens x 256 bytes) as a register fetch issued before the
+// current block's compute and an LDS store after it. At most 8 x 4 x 16 = 512 uint4: two per thread. The thread's
+// two (source row, LDS slot) pairs are fixed for a token group (MoePlan); a block only adds its offset.
+struct MoePlan {
+  const int8_t* src[2];     // digits of (limb, token) row at 16-byte chunk c, block 0
+  int dst[2];               // LDS byte offset of [l][t][16 c]
+  bool on[2];
+};
+__device__ inline MoePlan moe_plan(const int* rowsel, int tn, int L, const int8_t* __restrict__ xd, int64_t rows,
+                                   int64_t K, int tid) {
+  MoePlan p;
+  const int n = L * tn * 16, nt = (int)blockDim.x;    // 256 or 512 threads: two or one chunks each
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + nt * k;
+    p.on[k] = i < n;
+    const int l = p.on[k] ? i / (tn * 16) : 0, rem = i - l * (tn * 16), t = p.on[k] ? rem >> 4 : 0, c = rem & 15;
+    p.src[k] = xd + ((int64_t)l * rows + rowsel[t]) * K + 16 * c;
+    p.dst[k] = (l * kMoeTok + t) * 256 + 16 * c;
+  }
+  return p;
+}
+struct MoeStage {
+  uint4 v[2];
+};
+__device__ inline MoeStage moe_fetch(const MoePlan& p, int64_t b) {
+  MoeStage r;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) r.v[k] = p.on[k] ? *(const uint4*)(p.src[k] + b * 256) : uint4{0, 0, 0, 0};
+  return r;
+}
+__device__ inline void moe_store(const MoeStage& r, const MoePlan& p, int8_t* buf) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    if (p.on[k]) *(uint4*)(buf + p.dst[k]) = r.v[k];
+}
+
+// The lane's A operand source: limb 4 lg + l of token t (row m = 4 t + l of the MFMA), K group kg; `ok` false
+// beyond the group's tokens / limbs (the lane then feeds zeros)
+struct MoeA {
+  int off;                  // byte offset of [l][t][8 kg] within one LDS buffer
+  bool ok0, ok1;            // limb groups 0 (limbs 0..3) and 1 (limbs 4..7)
+};
+__device__ inline MoeA moe_a_lane(int lane, int tn, int L) {
+  const int m = lane & 15, kg = lane >> 4, t = m >> 2, l = m & 3;
+  MoeA r;
+  r.off = (l * kMoeTok + t) * 256 + 8 * kg;
+  r.ok0 = t < tn && l < L;
+  r.ok1 = t < tn && 4 + l < L;
+  return r;
+}
+__device__ inline int64_t moe_a(const int8_t* buf, const MoeA& a, int lg, int p0, bool kon) {
+  const bool ok = (lg ? a.ok1 : a.ok0) && kon;
+  const int64_t v = *(const int64_t*)(buf + a.off + lg * 4 * kMoeTok * 256 + p0);   // always inside the buffer
+  return ok ? v : 0;                                  // a select, not a branch around the load
+}
+
+// sum_r T[r] << 8 (4 lg + r): a token's value from its per-limb partial sums (int32 per limb)
+__device__ inline int64_t limb_sum(v4i d, int lg) {
+  const int64_t v = (int64_t)d[0] + ((int64_t)d[1] << 8) + ((int64_t)d[2] << 16) + ((int64_t)d[3] << 24);
+  return lg ? (int64_t)((uint64_t)v << 32) : v;
+}
+
+// Q4_K weights of one block for B lanes (row n, K group kg): the 16-byte header (d, dmin, 12 scale bytes) and the
+// qs bytes 32 g + 8 kg .. + 7 for g = 0..3 (sub-blocks 2 g (low nibbles), 2 g + 1 (high nibbles))
+struct Q4Lane {
+  uint4 h;
+  uint2 q[4];
+};
+__device__ inline Q4Lane q4_lane_load(const uint8_t* blk, int kg) {
+  Q4Lane r;
+  r.h = *(const uint4*)blk;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) r.q[g] = *(const uint2*)(blk + 16 + 32 * g + 8 * kg);
+  return r;
+}
+
+// One Q4_K block: acc += dq S1 - dmq S2 for the lane's (token, row). Per limb r, S1's part sum_j sc_j D_j[r] stays
+// in int32 (|D| <= 32 * 128 * 15, 8 sub-blocks x 63: < 2^25) and S2's part sum_j m_j (sum of the sub-block's
+// digits) is an MFMA accumulation with B = m_j in every byte (|.| <= 8 * 63 * 32 * 128 < 2^21).
+__device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const MoeA& a, bool two, int fw,
+                                     Acc128& acc) {
+  const uint32_t hb = w.h.x;
+  const int64_t dq = fp16_fixed(hb & 0xFFFF, fw), dmq = fp16_fixed(hb >> 16, fw);
+  const uint32_t scw[3] = {w.h.y, w.h.z, w.h.w};
+  auto scb = [&](int i) { return (int)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+  int sc[8];
+  int64_t bq[8], bm[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int g = j >> 1, hi = j & 1;
+    const uint2 qv = w.q[g];
+    const uint32_t b0 = hi ? (qv.x >> 4) & 0x0F0F0F0Fu : qv.x & 0x0F0F0F0Fu;
+    const uint32_t b1 = hi ? (qv.y >> 4) & 0x0F0F0F0Fu : qv.y & 0x0F0F0F0Fu;
+    bq[j] = (int64_t)(((uint64_t)b1 << 32) | b0);
+    int mn;
+    if (j < 4) { sc[j] = scb(j) & 63; mn = scb(j + 4) & 63; }
+    else { sc[j] = (scb(j + 4) & 0xF) | ((scb(j - 4) >> 6) << 4); mn = (scb(j + 4) >> 4) | ((scb(j) >> 6) << 4); }
+    const uint32_t mb = (uint32_t)mn | ((uint32_t)mn << 8) | ((uint32_t)mn << 16) | ((uint32_t)mn << 24);
+    bm[j] = (int64_t)(((uint64_t)mb << 32) | mb);
+  }
+  int64_t S1 = 0, S2 = 0;
+#pragma unroll
+  for (int lg = 0; lg < 2; ++lg) {
+    if (lg == 1 && !two) break;
+    // the eight sub-block MFMAs are independent: issued back to back, their results consumed afterwards
+    v4i d[8];
+    v4i M = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t av = moe_a(buf, a, lg, 32 * j, true);
+      d[j] = mfma32(av, bq[j], v4i{0, 0, 0, 0});
+      M = mfma32(av, bm[j], M);
+    }
+    v4i T = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) T[r] += __mul24(sc[j], d[j][r]);   // 24-bit: |sc| < 2^6, |D| < 2^17
+    S1 += limb_sum(T, lg);
+    S2 += limb_sum(M, lg);
+  }
+  acc_madd(acc, dq, S1);
+  acc_madd(acc, -dmq, S2);
+}
+
+__global__ __launch_bounds__(256) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
+                                                         const int* __restrict__ ppair, const int8_t* __restrict__ xd,
+                                                         const int* __restrict__ Lrow, int64_t rows, int64_t K,
+                                                         int64_t e_ffn, int fw, int fa, int64_t log2e, int64_t dclip,
+                                                         int64_t* __restrict__ gu, int* __restrict__ status,
+                                                         const int* __restrict__ wide) {
+  __shared__ __align__(16) int8_t sx[2][kMoeLimbs][kMoeTok][256];
+  __shared__ int s_rows[kMoeTok];
+  if (*wide) return;                                  // the VALU fallback takes this call
+  const MoeItem it = items[blockIdx.y];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int64_t)blockIdx.x * 64 >= e_ffn) return;
+  const int n = lane & 15, kg = lane >> 4, t = lane >> 4;
+  const int64_t o = (int64_t)blockIdx.x * 64 + wave * 16 + n;
+  const bool orow = o < e_ffn;
+  const int64_t nb = K / 256;
+  const uint8_t* grow = it.wg + (orow ? o : 0) * nb * 144;
+  const uint8_t* urow = it.wu + (orow ? o : 0) * nb * 144;
+  for (int t0 = 0; t0 < it.count; t0 += kMoeTok) {
+    const int tn = min(kMoeTok, it.count - t0);
+    int L = 1;
+    for (int i = 0; i < tn; ++i) { const int lr = Lrow[ptok[it.first + t0 + i]]; L = lr > L ? lr : L; }
+    __syncthreads();                                  // the previous token group is done with the buffers
+    if (tid < tn) s_rows[tid] = ptok[it.first + t0 + tid];
+    __syncthreads();
+    const MoeA al = moe_a_lane(lane, tn, L);
+    Q4Lane g0 = q4_lane_load(grow, kg), u0 = q4_lane_load(urow, kg), g1 = g0, u1 = u0;
+    if (nb > 1) { g1 = q4_lane_load(grow + 144, kg); u1 = q4_lane_load(urow + 144, kg); }
+    const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
+    moe_store(moe_fetch(pl, 0), pl, &sx[0][0][0][0]);
+    __syncthreads();
+    Acc128 ag{0, 0}, au{0, 0};
+    for (int64_t b = 0; b < nb; b += 2) {
+      // even block: LDS buffer 0, weight registers slot 0; block b + 1 is fetched meanwhile
+      MoeStage nx{};
+      if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
+      q4_block_mfma(g0, &sx[0][0][0][0], al, L > 4, fw, ag);
+      q4_block_mfma(u0, &sx[0][0][0][0], al, L > 4, fw, au);
+      if (b + 2 < nb) { g0 = q4_lane_load(grow + (b + 2) * 144, kg); u0 = q4_lane_load(urow + (b + 2) * 144, kg); }
+      if (b + 1 >= nb) break;
+      moe_store(nx, pl, &sx[1][0][0][0]);
+      __syncthreads();
+      // odd block: LDS buffer 1, slot 1
+      if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
+      q4_block_mfma(g1, &sx[1][0][0][0], al, L > 4, fw, ag);
+      q4_block_mfma(u1, &sx[1][0][0][0], al, L > 4, fw, au);
+      if (b + 3 < nb) { g1 = q4_lane_load(grow + (b + 3) * 144, kg); u1 = q4_lane_load(urow + (b + 3) * 144, kg); }
+      if (b + 2 >= nb) break;
+      moe_store(nx, pl, &sx[0][0][0][0]);
+      __syncthreads();
+    }
+    if (orow && t < tn) {
+      bool f1, f2, f3;
+      const int64_t gy = acc_shift(ag, fw, &f1), uy = acc_shift(au, fw, &f2);
+      const int64_t v = nmc_silu_mul(gy, uy, fa, log2e, dclip, &f3);
+      if (!(f1 && f2 && f3)) atomicOr(status, IMIE_EOVF);
+      gu[(int64_t)ppair[it.first + t0 + t] * e_ffn + o] = v;
+    }
+  }
+}
+
+// Q6_K weights of one block for B lanes (row n, K group kg): per K step (half, qq) the ql bytes
+// 64 half + 32 (qq & 1) + 8 kg .. + 7 and the qh bytes 32 half + 8 kg .. + 7 (bits 2 qq, 2 qq + 1); the 16
+// int8 scales and d
+struct Q6Lane {
+  uint2 l[2][2];            // [half][qq & 1]
+  uint2 h[2];               // [half]
+  uint4 sc;
+  uint32_t d;
+};
+__device__ inline Q6Lane q6_lane_load(const uint8_t* blk, int kg) {
+  Q6Lane r;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int o = 0; o < 2; ++o) r.l[half][o] = *(const uint2*)(blk + 64 * half + 32 * o + 8 * kg);
+    r.h[half] = *(const uint2*)(blk + 128 + 32 * half + 8 * kg);
+  }
+  r.sc = *(const uint4*)(blk + 192);
+  r.d = (uint32_t)blk[208] | ((uint32_t)blk[209] << 8);
+  return r;
+}
+
+// One Q6_K block: acc += dq S1; per limb r, sum_j sc_j D_j[r] in int32 (|D| <= 32 * 128 * 32 = 2^17, 16
+// sub-blocks x 128: < 2^28)
+__device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const MoeA& a, bool two, int kg, int fw,
+                                     Acc128& acc) {
+  const int64_t dq = fp16_fixed(w.d, fw);
+  const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+  auto scs = [&](int i) { return (int)(int8_t)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+  const bool klo = kg < 2;
+  int64_t S1 = 0;
+#pragma unroll
+  for (int lg = 0; lg < 2; ++lg) {
+    if (lg == 1 && !two) break;
+    v4i T = {0, 0, 0, 0};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      // the 8 MFMAs of a half are independent: issued back to back, consumed afterwards
+      v4i d[4][2];
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const uint2 lv = w.l[half][qq & 1], hv = w.h[half];
+        const int sl = qq >= 2 ? 4 : 0, sh = 2 * qq;
+        uint32_t v0 = ((lv.x >> sl) & 0x0F0F0F0Fu) | (((hv.x >> sh) & 0x03030303u) << 4);
+        uint32_t v1 = ((lv.y >> sl) & 0x0F0F0F0Fu) | (((hv.y >> sh) & 0x03030303u) << 4);
+        v0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise q6 - 32 as int8
+        v1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        const int64_t bq = (int64_t)(((uint64_t)v1 << 32) | v0);
+        const int p0 = 128 * half + 32 * qq;
+        // the K step spans sub-blocks 8 half + 2 qq (K groups 0, 1) and + 1 (K groups 2, 3)
+        const int64_t av = moe_a(buf, a, lg, p0, true);
+        d[qq][0] = mfma32(klo ? av : 0, bq, v4i{0, 0, 0, 0});
+        d[qq][1] = mfma32(klo ? 0 : av, bq, v4i{0, 0, 0, 0});
+      }
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int s0 = scs(8 * half + 2 * qq), s1 = scs(8 * half + 2 * qq + 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) T[r] += __mul24(s0, d[qq][0][r]) + __mul24(s1, d[qq][1][r]);   // |s| < 2^8, |D| < 2^18
+      }
+    }
+    S1 += limb_sum(T, lg);
+  }
+  acc_madd(acc, dq, S1);
+}
+
+__global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ppair,
+                                                       const int8_t* __restrict__ xd, const int64_t* __restrict__ xs16,
+                                                       const int* __restrict__ Lrow, int64_t rows, int64_t K,
+                                                       int64_t d_model, int fw, int64_t* __restrict__ dout,
+                                                       int* __restrict__ status, const int* __restrict__ wide) {
+  __shared__ __align__(16) int8_t sx[2][kMoeLimbs][kMoeTok][256];
+  __shared__ int s_rows[kMoeTok];
+  if (*wide) return;
+  const MoeItem it = items[blockIdx.y];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int64_t)blockIdx.x * 64 >= d_model) return;
+  const int n = lane & 15, kg = lane >> 4, t = lane >> 4;
+  const int64_t o = (int64_t)blockIdx.x * 64 + wave * 16 + n;
+  const bool orow = o < d_model;
+  const int64_t nb = K / 256;
+  const uint8_t* drow = it.wd + (orow ? o : 0) * nb * 210;
+  for (int t0 = 0; t0 < it.count; t0 += kMoeTok) {
+    const int tn = min(kMoeTok, it.count - t0);
+    int L = 1;
+    for (int i = 0; i < tn; ++i) { const int lr = Lrow[ppair[it.first + t0 + i]]; L = lr > L ? lr : L; }
+    __syncthreads();
+    if (tid < tn) s_rows[tid] = ppair[it.first + t0 + tid];
+    __syncthreads();
+    const MoeA al = moe_a_lane(lane, tn, L);
+    Q6Lane w0 = q6_lane_load(drow, kg), w1 = w0;
+    if (nb > 1) w1 = q6_lane_load(drow + 210, kg);
+    const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
+    moe_store(moe_fetch(pl, 0), pl, &sx[0][0][0][0]);
+    __syncthreads();
+    Acc128 ad{0, 0};
+    for (int64_t b = 0; b < nb; b += 2) {
+      MoeStage nx{};
+      if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
+      q6_block_mfma(w0, &sx[0][0][0][0], al, L > 4, kg, fw, ad);
+      if (b + 2 < nb) w0 = q6_lane_load(drow + (b + 2) * 210, kg);
+      if (b + 1 >= nb) break;
+      moe_store(nx, pl, &sx[1][0][0][0]);
+      __syncthreads();
+      if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
+      q6_block_mfma(w1, &sx[1][0][0][0], al, L > 4, kg, fw, ad);
+      if (b + 3 < nb) w1 = q6_lane_load(drow + (b + 3) * 210, kg);
+      if (b + 2 >= nb) break;
+      moe_store(nx, pl, &sx[0][0][0][0]);
+      __syncthreads();
+    }
+    if (orow && t < tn) {
+      bool f;
+      const int64_t y = acc_shift(ad, fw, &f);
+      if (!f) atomicOr(status, IMIE_EOVF);
+      dout[(int64_t)ppair[it.first + t0 + t] * d_model + o] = y;
+    }
+  }
+}
+
 // int8-MFMA path on/off (IMIE_QK_MFMA=0 forces the VALU kernel; tests compare both)
 bool qk_mfma_enabled() {
   static const bool v = [] { const char* e = getenv("IMIE_QK_MFMA"); return !(e && atoi(e) == 0); }();
@@ -679,10 +1055,11 @@ int read_status_and(hipStream_t st, int* stat) {
 }
 
 // Batched MoE: P = m*k pairs (token-major, pair p belongs to token p / k). Pairs sharing a weight run in one
-// item, so each expert's gate/up/down are read once per call.
-int moe_batched(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
-                const int64_t* h_dev, const int64_t* gates_dev, int64_t d_model, int64_t e_ffn, int fa, int fw,
-                int64_t* out_dev, hipStream_t st) {
+// item, so each expert's gate/up/down are read once per call. This form runs each projection as its own item list
+// (any quantisation types); moe_batched below takes the fused expert kernels when the layout allows.
+int moe_batched_items(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                      const int64_t* h_dev, const int64_t* gates_dev, int64_t d_model, int64_t e_ffn, int fa, int fw,
+                      int64_t* out_dev, hipStream_t st) {
   const int64_t P = (int64_t)m * k;
   if (m <= 0 || k <= 0 || d_model <= 0 || e_ffn <= 0 || d_model % 256 || e_ffn % 256 || fa < 1 || fa > 28 || fw < 0 ||
       fw > 62)
@@ -729,6 +1106,113 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   if (rc) return rc;
   hipLaunchKernelGGL(qk_combine_kernel, dim3((unsigned)(((int64_t)m * d_model + 255) / 256)), dim3(256), 0, st, db,
                      m, k, d_model, gates_dev, fa, out_dev, status);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+// Batched MoE with the fused expert kernels (Q4_K gate/up, Q6_K down): one item per expert, its pairs listed
+// once. Sequence: prep(h) -> gate/up + SiLU*up -> prep(gu) -> down -> combine. When an activation row needs more
+// than kQkLimbs digit limbs, the prep sets a device flag: the fused kernels return at once and the exact VALU item
+// kernels (enqueued behind them, gated by the same flag) compute that stage instead, with no host round trip.
+int moe_batched(const long long* gate_h, const long long* up_h, const long long* down_h, int m, int k,
+                const int64_t* h_dev, const int64_t* gates_dev, int64_t d_model, int64_t e_ffn, int fa, int fw,
+                int64_t* out_dev, hipStream_t st) {
+  const int64_t P = (int64_t)m * k;
+  if (m <= 0 || k <= 0 || d_model <= 0 || e_ffn <= 0 || d_model % 256 || e_ffn % 256 || fa < 1 || fa > 28 || fw < 0 ||
+      fw > 62)
+    return IMIE_EARG;
+  bool fused = fw <= kMaxFw && qk_mfma_enabled();
+  for (int64_t p = 0; p < P && fused; ++p) {
+    const QKWeight *g = qk_get(gate_h[p]), *u = qk_get(up_h[p]), *d = qk_get(down_h[p]);
+    if (!g || !u || !d) return IMIE_EARG;
+    fused = g->qtype == 0 && u->qtype == 0 && d->qtype == 1;
+  }
+  if (!fused)
+    return moe_batched_items(gate_h, up_h, down_h, m, k, h_dev, gates_dev, d_model, e_ffn, fa, fw, out_dev, st);
+  for (int64_t p = 0; p < P; ++p) {
+    const QKWeight *g = qk_get(gate_h[p]), *u = qk_get(up_h[p]), *d = qk_get(down_h[p]);
+    if (g->out_f != e_ffn || g->nb * 256 != d_model || u->out_f != e_ffn || u->nb * 256 != d_model ||
+        d->out_f != d_model || d->nb * 256 != e_ffn)
+      return IMIE_EARG;
+  }
+  if (g_mws.g.ensure((size_t)(P * e_ffn) * 8) || g_mws.u.ensure((size_t)(P * e_ffn) * 8) ||
+      g_mws.d.ensure((size_t)(P * d_model) * 8) || g_mws.status.ensure(64))
+    return IMIE_EARG;
+  int64_t *gb = (int64_t*)g_mws.g.p, *ub = (int64_t*)g_mws.u.p, *db = (int64_t*)g_mws.d.p;
+  int* status = (int*)g_mws.status.p;
+  // experts = distinct (gate, up, down) handle triples; pairs listed expert by expert
+  std::map<std::tuple<long long, long long, long long>, std::vector<int>> groups;
+  for (int64_t p = 0; p < P; ++p) groups[std::make_tuple(gate_h[p], up_h[p], down_h[p])].push_back((int)p);
+  const size_t ne = groups.size();
+  std::vector<MoeItem> mi;
+  std::vector<Item> ig, iu, idn;
+  std::vector<int> ptok, ppair;
+  mi.reserve(ne);
+  for (auto& kv : groups) {
+    const QKWeight* g = qk_get(std::get<0>(kv.first));
+    const QKWeight* u = qk_get(std::get<1>(kv.first));
+    const QKWeight* d = qk_get(std::get<2>(kv.first));
+    const int first = (int)ptok.size(), count = (int)kv.second.size();
+    mi.push_back(MoeItem{g->p, u->p, d->p, first, count});
+    ig.push_back(Item{g->p, g->out_f, g->nb, g->qtype, first, count});
+    iu.push_back(Item{u->p, u->out_f, u->nb, u->qtype, first, count});
+    idn.push_back(Item{d->p, d->out_f, d->nb, d->qtype, first, count});
+    for (int p : kv.second) { ptok.push_back(p / k); ppair.push_back(p); }
+  }
+  // one upload: [MoeItem x ne][Item gate x ne][Item up x ne][Item down x ne][ptok P][ppair P]
+  static DevBuf meta;
+  const size_t o_items = 0, o_ig = o_items + ne * sizeof(MoeItem), o_iu = o_ig + ne * sizeof(Item),
+               o_id = o_iu + ne * sizeof(Item), o_pt = o_id + ne * sizeof(Item), o_pp = o_pt + (size_t)P * 4,
+               total = o_pp + (size_t)P * 4;
+  static std::vector<uint8_t> hb;                     // pageable staging: the async copy reads it before returning
+  hb.resize(total);
+  memcpy(hb.data() + o_items, mi.data(), ne * sizeof(MoeItem));
+  memcpy(hb.data() + o_ig, ig.data(), ne * sizeof(Item));
+  memcpy(hb.data() + o_iu, iu.data(), ne * sizeof(Item));
+  memcpy(hb.data() + o_id, idn.data(), ne * sizeof(Item));
+  memcpy(hb.data() + o_pt, ptok.data(), (size_t)P * 4);
+  memcpy(hb.data() + o_pp, ppair.data(), (size_t)P * 4);
+  if (meta.ensure(total)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(meta.p, hb.data(), total, hipMemcpyHostToDevice, st));
+  const uint8_t* mb = (const uint8_t*)meta.p;
+  const MoeItem* d_items = (const MoeItem*)(mb + o_items);
+  const Item *d_ig = (const Item*)(mb + o_ig), *d_iu = (const Item*)(mb + o_iu), *d_id = (const Item*)(mb + o_id);
+  const int *d_pt = (const int*)(mb + o_pt), *d_pp = (const int*)(mb + o_pp);
+  const int64_t prow = P > m ? P : m, pk = d_model > e_ffn ? d_model : e_ffn;
+  if (g_qprep.xd.ensure((size_t)(kQkLimbs * prow * pk)) || g_qprep.xs.ensure((size_t)(prow * (pk / 16)) * 8) ||
+      g_qprep.lr.ensure((size_t)prow * 4) || g_qprep.flag.ensure(64))
+    return IMIE_EARG;
+  int* flagA = (int*)g_qprep.flag.p;
+  int* flagB = flagA + 1;
+  int8_t* xdp = (int8_t*)g_qprep.xd.p;
+  int64_t* xsp = (int64_t*)g_qprep.xs.p;
+  int* lrp = (int*)g_qprep.lr.p;
+  int64_t log2e, dclip;
+  silu_consts_nmc(fa, &log2e, &dclip);
+  imie_prof_mark(IMIE_K_QK, st, true);
+  hipLaunchKernelGGL(qk_flags_reset_kernel, dim3(1), dim3(64), 0, st, flagA, 2);
+  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, xsp, lrp,
+                     flagA);
+  hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
+                     d_pt, d_pp, xdp, lrp, (int64_t)m, d_model, e_ffn, fw, fa, log2e, dclip, gb, status, flagA);
+  // exact VALU fallback of the gate/up stage (runs only when the prep flagged a wide activation row)
+  const dim3 ggrid((unsigned)((e_ffn + kRows - 1) / kRows), (unsigned)ne);
+  hipLaunchKernelGGL(qk_group_kernel, ggrid, dim3(256), 0, st, d_ig, d_pt, d_pp, h_dev, d_model, gb, e_ffn, fw, status,
+                     flagA);
+  hipLaunchKernelGGL(qk_group_kernel, ggrid, dim3(256), 0, st, d_iu, d_pt, d_pp, h_dev, d_model, ub, e_ffn, fw, status,
+                     flagA);
+  const int64_t n = P * e_ffn;
+  hipLaunchKernelGGL(qk_silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gb, ub, n, fa, log2e,
+                     dclip, gb, status, flagA);
+  // down over the P rows of gu
+  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)P), dim3(256), 0, st, gb, P, e_ffn, xdp, xsp, lrp, flagB);
+  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((d_model + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
+                     d_pp, xdp, xsp, lrp, P, e_ffn, d_model, fw, db, status, flagB);
+  hipLaunchKernelGGL(qk_group_kernel, dim3((unsigned)((d_model + kRows - 1) / kRows), (unsigned)ne), dim3(256), 0, st,
+                     d_id, d_pp, d_pp, gb, e_ffn, db, d_model, fw, status, flagB);
+  hipLaunchKernelGGL(qk_combine_kernel, dim3((unsigned)(((int64_t)m * d_model + 255) / 256)), dim3(256), 0, st, db,
+                     m, k, d_model, gates_dev, fa, out_dev, status);
+  imie_prof_mark(IMIE_K_QK, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

@@ -47,24 +47,28 @@ def test_resident_grouped_equals_individual(qkg):
     assert qkg.resident_count() == 0
 
 
-def _experts(seed, E, d, e_ffn):
-    return [dict(gate=qk.random_blocks(seed, 100 + 3 * e, e_ffn, d // 256, 0),
-                 up=qk.random_blocks(seed, 101 + 3 * e, e_ffn, d // 256, 0),
-                 down=qk.random_blocks(seed, 102 + 3 * e, d, e_ffn // 256, 1)) for e in range(E)]
+def _experts(seed, E, d, e_ffn, dq=(0.002, 0.01, 0.005)):
+    kw = dict(dlo=dq[0], dhi=dq[1], dminhi=dq[2])
+    return [dict(gate=qk.random_blocks(seed, 100 + 3 * e, e_ffn, d // 256, 0, **kw),
+                 up=qk.random_blocks(seed, 101 + 3 * e, e_ffn, d // 256, 0, **kw),
+                 down=qk.random_blocks(seed, 102 + 3 * e, d, e_ffn // 256, 1, **kw)) for e in range(E)]
 
 
-def _run_moe(qkg, seed, E, k, d, e_ffn, T, *, fast_oracle=False):
-    ex = _experts(seed, E, d, e_ffn)
+def _run_moe(qkg, seed, E, k, d, e_ffn, T, *, fast_oracle=False, hmag=16, oracle=True, dq=(0.002, 0.01, 0.005)):
+    ex = _experts(seed, E, d, e_ffn, dq)
     hs = [dict(gate=qkg.register_weight(x["gate"], e_ffn, d // 256, 0),
                up=qkg.register_weight(x["up"], e_ffn, d // 256, 0),
                down=qkg.register_weight(x["down"], d, e_ffn // 256, 1)) for x in ex]
-    h = prng.uniform_int(seed, 7, (T, d), -(1 << 16), 1 << 16)
+    h = prng.uniform_int(seed, 7, (T, d), -(1 << hmag), 1 << hmag)
     logits = prng.uniform_int(seed, 8, (T, E), -(1 << 20), 1 << 20)
     sel, gates = qk.moe_route(logits, k, 16)
     flat = sel.reshape(-1)
     got = qkg.moe_ffn_batched([hs[e]["gate"] for e in flat], [hs[e]["up"] for e in flat],
                               [hs[e]["down"] for e in flat], T, k, h, gates, d, e_ffn, 16, 24)
     used = sorted(set(int(e) for e in flat))
+    if not oracle:
+        qkg.free_all()
+        return got, None
     if fast_oracle:
         raw = {e: dict(gate=(ex[e]["gate"], e_ffn, d // 256, 0), up=(ex[e]["up"], e_ffn, d // 256, 0),
                        down=(ex[e]["down"], d, e_ffn // 256, 1)) for e in used}
@@ -81,6 +85,24 @@ def _run_moe(qkg, seed, E, k, d, e_ffn, T, *, fast_oracle=False):
 
 def test_moe_batched_small_matches_oracle(qkg):
     got, want = _run_moe(qkg, 1, E=8, k=3, d=512, e_ffn=256, T=5)
+    assert got is not None and np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("hmag,T,E,dq", [(16, 23, 4, (0.002, 0.01, 0.005)), (33, 9, 3, (1e-4, 1e-4, 5e-5)),
+                                         (41, 6, 4, (6e-8, 6e-8, 6e-8)), (2, 17, 2, (0.002, 0.01, 0.005)),
+                                         (45, 5, 3, (0.002, 0.01, 0.005))])
+def test_moe_fused_expert_kernels_limb_and_token_groups(qkg, hmag, T, E, dq):
+    """The fused expert kernels over every branch: more than 4 tokens per expert (several token groups), five
+    limbs (2^33: the second MFMA row group), activations beyond five limbs (2^41: the exact VALU fallback,
+    selected on the device; tiny block scales keep the oracle's int64 results in range), one-limb activations,
+    and a case whose results leave int64 (2^45 with ordinary scales: refused as the oracle raises)."""
+    try:
+        got, want = _run_moe(qkg, hmag + T, E=E, k=2, d=512, e_ffn=256, T=T, hmag=hmag, dq=dq)
+    except OverflowError:                                             # the oracle raises: the producer must refuse
+        qkg.free_all()
+        got, _ = _run_moe(qkg, hmag + T, E=E, k=2, d=512, e_ffn=256, T=T, hmag=hmag, oracle=False, dq=dq)
+        assert got is None
+        return
     assert got is not None and np.array_equal(got, want)
 
 
