@@ -195,6 +195,29 @@ uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d);
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);
 
+/* ---- host (CPU) re-execution for receipt verification (bonsai/src/trinote/infer_int/verify.py:156-272: the
+ * reference verifier re-derives turns on its CPU reference engine; this is that role, independent of the GPU). ---- */
+/* A host model over the caller's arrays (borrowed): 7 Q1_0 projections per layer (wq, wk, wv, wo, w1, wu, w2) as
+ * bits (out, in/128, 16) / int64 scales (out, in/128), 4 int64 gains per layer (n1, n2, q-norm, k-norm), the Q1_0
+ * embedding and output head, the final gain and the RoPE tables (rope_rows, hd/2). Handle >= 0 or -1. */
+int64_t imie_cpu_model_create(int64_t n_layers, int64_t H, int64_t Hkv, int64_t hd, int64_t d, int64_t dff,
+                              int64_t vocab, int64_t frac, int64_t eps, int64_t inv_sqrt,
+                              const uint8_t *const *w_bits, const int64_t *const *w_scale,
+                              const int64_t *const *gains, const uint8_t *embed_bits, const int64_t *embed_scale,
+                              const uint8_t *out_bits, const int64_t *out_scale, const int64_t *final_gain,
+                              const int64_t *cos, const int64_t *sin, int64_t rope_rows);
+void imie_cpu_model_free(int64_t model);
+/* worker threads of the host forward (0: the machine's hardware threads) */
+void imie_cpu_set_threads(int threads);
+/* ReferenceModelV2.forward (reference_bonsai.py:941-966, 790-827) of ids at positions 0..T-1 on the host: logits
+ * (T, vocab) or the last row only. rc 0; 1 bad arguments; 2 an attention / RoPE envelope the reference raises on;
+ * 4 RMSNorm (128-bit sum of squares exceeded, or the gain envelope). */
+int imie_cpu_forward(int64_t model, const int64_t *ids, int64_t T, int last_only, int64_t *logits);
+/* sample_token (sampler.py:403-437) on the host: cfg is an ImieSamplerConfig. rc 0; 1 bad arguments or a history
+ * id outside the vocabulary; 2 the temperature envelope. */
+int imie_cpu_sample_token(const int64_t *logits, int64_t vocab, const void *cfg, const int64_t *history,
+                          int64_t hist_len, int64_t position, int64_t *token);
+
 /* ---- integer samplers (bonsai/src/trinote/infer_int/sampler.py) ------------------------------------------ */
 /* Committed fixed-point sampler settings. mode 0 greedy, 1 temp, 2 top_k, 3 top_p, 4 min_p; inv_temp =
  * round(2^frac / T), top_p / min_p in 2^frac units (sampler.py:214-258); the field order and mode numbering follow

@@ -38,6 +38,12 @@ SIGNATURES = {
     "imie_profile_gemm_ops": (c_int, [c_void_p, c_int]),
     "imie_profile_read": (c_int, [c_int, c_void_p, c_void_p]),
     "imie_profile_end": (None, []),
+    # host re-execution (receipt verifier)
+    "imie_cpu_model_create": (c_int64, [c_int64] * 10 + [c_void_p] * 10 + [c_int64]),
+    "imie_cpu_model_free": (None, [c_int64]),
+    "imie_cpu_set_threads": (None, [c_int]),
+    "imie_cpu_forward": (c_int, [c_int64, c_void_p, c_int64, c_int, c_void_p]),
+    "imie_cpu_sample_token": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     # Q1_0 linear
     "bonsai_q1_linear_gpu": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "bonsai_q1_register_weight": (c_int64, [c_void_p, c_void_p, c_int64, c_int64]),

@@ -1,5 +1,6 @@
-"""Receipt re-execution on the device: full, sampled-audit, challenged and resampled verification of a committed
-Bonsai turn (``bonsai/src/trinote/infer_int/verify.py:27-272``).
+"""Receipt re-execution: full, sampled-audit, challenged and resampled verification of a committed Bonsai turn
+(``bonsai/src/trinote/infer_int/verify.py:27-272``), on the device (``DeviceVerifier``) or on the host CPU,
+independent of the GPU producer (``CpuVerifier``).
 
 A receipt commits ``inputIds`` and ``outputIds``; the verifier re-derives every output token from the artifact and
 checks it. The strategies, their names, the result dictionaries and the edge rules follow the reference:
@@ -21,7 +22,7 @@ all T positions, the LM head writes the (T, vocab) logits into HBM, and the sele
 penalties, or the seeded sampler) and the row digests (``imie_logits_digest_dev``) run on the device over the rows
 that predict output tokens. Only token ids and 32-byte digests cross PCIe (below 64 rows the rows themselves are
 hashed on the host, which is faster than one serial device SHA-256 lane). The cached replay runs the device decode
-loop (``imie_net_decode_dev`` / ``imie_net_decode_sampled_dev``). There is no host compute path.
+loop (``imie_net_decode_dev`` / ``imie_net_decode_sampled_dev``); the device verifier has no host compute path.
 """
 from __future__ import annotations
 
@@ -116,6 +117,12 @@ class DeviceVerifier:
     def teacher_forced_logits(self, ids) -> np.ndarray:
         return self.logits_dev(list(ids)).cpu().numpy()
 
+    def take_rows(self, full, idx):
+        return full.index_select(0, self.torch.tensor(list(idx), dtype=self.torch.int64, device="cuda"))
+
+    def cat_rows(self, rows):
+        return self.torch.cat(rows, 0)
+
     def forward(self, ids) -> np.ndarray:
         return self.teacher_forced_logits(ids)
 
@@ -184,6 +191,109 @@ class DeviceVerifier:
         from . import gpu_native
         self.net.close()
         gpu_native.q1_free_weights()
+
+
+class CpuVerifier:
+    """The same verifier on the host CPU: the ``model`` the verify functions take, re-deriving turns with the
+    library's host forward (``imie_cpu_forward``) and host sampler (``imie_cpu_sample_token``), which share no code
+    with the device producer. This is the reference's verifier role (verify.py:156-272 on its CPU reference engine):
+    a counterparty re-checks a receipt without trusting the GPU that produced it. It has no cached replay (the
+    strategies then stay teacher-forced, and an explicit ``cached-replay`` is refused as for any model without an
+    exact cached generator). ``threads`` = 0 uses every hardware thread."""
+
+    receipt_verify_cached_threshold = None
+    receipt_verify_strategy = "auto"
+
+    def __init__(self, artifact: dict, *, threads: int = 0):
+        self.lib = _lib.lib()
+        self.artifact = artifact
+        self.cfg = dict(artifact["config"])
+        self.cfg.setdefault("frac", 16)
+        self.cfg.setdefault("context_len", int(artifact["cos_fp"].shape[0]))
+        d = _artifact.dims(artifact)
+        self.dims = d
+        self.eff = min(int(self.cfg["context_len"]), int(artifact["cos_fp"].shape[0]))
+        self.vocab = d["vocab"]
+        c = lambda a, dt: np.ascontiguousarray(np.asarray(a), dtype=dt)
+        keep = []                                          # the host model borrows these arrays
+
+        def ptr(a):
+            keep.append(a)
+            return a.ctypes.data
+
+        layers = artifact["layers"]
+        wb = (ctypes.c_void_p * (7 * len(layers)))(*[ptr(c(l[f"{p}_bits"], np.uint8)) for l in layers
+                                                      for p in _artifact.PROJ])
+        ws = (ctypes.c_void_p * (7 * len(layers)))(*[ptr(c(l[f"{p}_scale_fp"], np.int64)) for l in layers
+                                                      for p in _artifact.PROJ])
+        gk = ("n1_gain_fp", "n2_gain_fp", "q_norm_gain_fp", "k_norm_gain_fp")
+        gs = (ctypes.c_void_p * (4 * len(layers)))(*[ptr(c(l[k], np.int64)) for l in layers for k in gk])
+        cos, sin = c(artifact["cos_fp"], np.int64), c(artifact["sin_fp"], np.int64)
+        inv = int(round((1.0 / np.sqrt(d["hd"])) * (1 << d["frac"])))
+        h = self.lib.imie_cpu_model_create(d["n_layers"], d["H"], d["Hkv"], d["hd"], d["d"], d["dff"], d["vocab"],
+                                           d["frac"], 1, inv, wb, ws, gs, ptr(c(artifact["embed_bits"], np.uint8)),
+                                           ptr(c(artifact["embed_scale_fp"], np.int64)),
+                                           ptr(c(artifact["output_bits"], np.uint8)),
+                                           ptr(c(artifact["output_scale_fp"], np.int64)),
+                                           ptr(c(artifact["final_norm_gain_fp"], np.int64)), ptr(cos), ptr(sin),
+                                           int(cos.shape[0]))
+        if h < 0:
+            raise ValueError("imie_cpu_model_create refused the artifact's shapes")
+        self.h, self._keep = int(h), (keep, wb, ws, gs)
+        self.lib.imie_cpu_set_threads(int(threads))
+
+    def logits_dev(self, ids, last_only: bool = False) -> np.ndarray:
+        ids = np.ascontiguousarray(np.asarray(list(ids), dtype=np.int64))
+        if not 0 < ids.size <= self.eff:
+            raise ValueError(f"prefill of {ids.size} tokens outside (0, {self.eff}]")
+        out = np.empty((1 if last_only else ids.size, self.vocab), dtype=np.int64)
+        rc = self.lib.imie_cpu_forward(self.h, ids.ctypes.data, ids.size, 1 if last_only else 0, out.ctypes.data)
+        if rc == 1:
+            raise ValueError("token id outside the vocabulary")
+        if rc == 2:
+            raise OverflowError("the reference forward raises on this turn (attention / RoPE int64 envelope)")
+        if rc != 0:
+            raise OverflowError(f"the reference forward raises on this turn (RMSNorm envelope, rc {rc})")
+        return out
+
+    def teacher_forced_logits(self, ids) -> np.ndarray:
+        return self.logits_dev(ids)
+
+    def forward(self, ids) -> np.ndarray:
+        return self.logits_dev(ids)
+
+    def take_rows(self, full, idx):
+        return full[np.asarray(list(idx), dtype=np.int64)]
+
+    def cat_rows(self, rows):
+        return np.concatenate(rows, 0)
+
+    def select(self, rows, cfg, positions, histories):
+        from .sampler_gpu import config_c
+        c = config_c(cfg, int(self.cfg["frac"]))
+        out = []
+        for r, pos, hist in zip(rows, positions, histories):
+            row = np.ascontiguousarray(r, dtype=np.int64)
+            hh = np.ascontiguousarray(np.asarray(hist, dtype=np.int64))
+            use = (cfg.rep_penalty or cfg.no_repeat_ngram) and hh.size
+            tok = ctypes.c_int64()
+            rc = self.lib.imie_cpu_sample_token(row.ctypes.data, row.shape[0], ctypes.byref(c),
+                                                hh.ctypes.data if use else None, int(hh.size) if use else 0,
+                                                int(pos), ctypes.byref(tok))
+            if rc == 2:
+                raise OverflowError("temperature scaling overflows int64; temperature too small for these logits")
+            if rc != 0:
+                raise ValueError(f"host sampler rejected the committed history (rc {rc})")
+            out.append(int(tok.value))
+        return out
+
+    def digests(self, rows) -> list[str]:
+        return [logits_digest(r) for r in rows]
+
+    def close(self) -> None:
+        if self.h >= 0:
+            self.lib.imie_cpu_model_free(self.h)
+            self.h = -1
 
 
 def logits_digest(row) -> str:
@@ -262,10 +372,9 @@ def _rows(model, input_ids, output_ids, idx):
     seq = list(input_ids) + list(output_ids)
     if len(seq) <= model.eff:
         full = model.logits_dev(seq)
-        sel = model.torch.tensor([n_in + i - 1 for i in idx], dtype=model.torch.int64, device="cuda")
-        return full.index_select(0, sel), "full"
+        return model.take_rows(full, [n_in + i - 1 for i in idx]), "full"
     rows = [model.logits_dev(seq[:n_in + i][-model.eff:], last_only=True) for i in idx]
-    return model.torch.cat(rows, 0), "sliding"
+    return model.cat_rows(rows), "sliding"
 
 
 def _teacher_forced(model, input_ids, output_ids, idx, cfg, keyed: bool):

@@ -186,3 +186,21 @@ def test_cached_replay_strategies(verifier):
     finally:
         v.receipt_verify_cached_threshold = None
         v.receipt_verify_strategy = "auto"
+
+
+def test_device_turn_verifies_on_the_host_verifier(verifier):
+    """A greedy turn generated by the device decode loop, re-derived by the independent host verifier
+    (CpuVerifier): the receipt check needs no trust in the GPU."""
+    from integer_inference_engine_amd import verify as V
+    from integer_inference_engine_amd.verify import CpuVerifier
+    v, model = verifier
+    inp = [7, 77, 177]
+    out = v.replay(inp, 9)
+    host = CpuVerifier(v.artifact, threads=8)
+    try:
+        res = V.verify_greedy(host, inp, out)
+        assert res["ok"] and res["checked"] == 9
+        dev = V.verify_greedy(v, inp, out)
+        assert [p["logitsDigest"] for p in res["positions"]] == [p["logitsDigest"] for p in dev["positions"]]
+    finally:
+        host.close()
