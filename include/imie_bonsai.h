@@ -191,6 +191,13 @@ int imie_net_fill_kv(int64_t ctx, uint64_t seed, const int64_t *lens, const int6
 uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo);
 uint64_t imie_fx_recip_u64(uint64_t d);
 uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d);
+/* CPU test hooks for the short paths of the single-token matvec prologue (no reference counterpart): the
+ * double-precision isqrt below 2^52; n = floor((x << frac) / rms) in double precision (returns 1 when that path
+ * applies, 0 when the integer routine would be taken); (silu(g) * u) >> frac by the two-exponential form
+ * (fast = 0) or the one-exponential form (fast = 1). */
+uint64_t imie_fx_isqrt_fast(uint64_t hi, uint64_t lo);
+int imie_fx_norm_f64(int64_t x, int frac, uint64_t rms, int64_t *out);
+int64_t imie_silu_mul_host(int64_t g, int64_t u, int64_t frac, int fast);
 /* Q1 embedding rows sign*scale (reference_bonsai.py:138-146) from device tables. */
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);

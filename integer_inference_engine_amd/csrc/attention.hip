@@ -476,6 +476,16 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     if (threadIdx.x < REP) d.cz[blockIdx.y * rows + b * d.H + kv * REP + threadIdx.x] = 0;
     return;
   }
+  // chunks of up to 256 keys (single-sequence decode): this thread's scores are requested before the row-max
+  // reduction that they do not depend on
+  const int64_t jend = min(j0 + d.chunk, L);
+  const bool one = d.chunk <= 256;
+  int64_t sv[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const int64_t j = j0 + threadIdx.x;
+    sv[r] = (one && j < jend) ? d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] : 0;
+  }
   // row max over the chunks that hold keys (wave r reduces row r)
   const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   for (int r = wave; r < REP; r += 4) {
@@ -489,14 +499,13 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     if (lane == 0) s_rmax[r] = m;
   }
   __syncthreads();
-  const int64_t jend = min(j0 + d.chunk, L);
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     const int64_t row = b * d.H + kv * REP + r;
     const int64_t mx = s_rmax[r];
     uint64_t z = 0;
     for (int64_t j = j0 + threadIdx.x; j < jend; j += blockDim.x) {
-      int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)d.scores[row * d.Lmax + j]);
+      int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)(one ? sv[r] : d.scores[row * d.Lmax + j]));
       if (dd > d.dclip) dd = d.dclip;
       const uint64_t e = (uint64_t)exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
       d.scores[row * d.Lmax + j] = (int64_t)e;
@@ -652,31 +661,33 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
   const int64_t L = dec_len(d, b);
   const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   const int64_t stride = rows * d.hd;
-  uint64_t acc = 0;
-  if (i < rows * d.hd) {
-    uint64_t s4[4] = {0, 0, 0, 0};
-    int64_t c = g;
-    for (; c + 24 < nlive; c += 32) {
+  // rounds of 8 chunks per thread with every load of a round issued before any is added (a loop-carried sum
+  // over single loads would wait for each in turn); the bound maxima of the first workgroup of a row ride along
+  const bool head = imie_umod32((int64_t)blockIdx.x * 32, d.hd) == 0;
+  const bool mx_lane = head && o == 0;
+  uint64_t acc = 0, mp = 0, mv = 0, mk = 0;
+  const bool live_o = i < rows * d.hd;
+  for (int64_t c0 = g; c0 < nlive; c0 += 64) {
+    uint64_t pv[8], ap[8], av[8], ak[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s4[u] += d.part[(c + 8 * u) * stride + i];
+    for (int u = 0; u < 8; ++u) {
+      const int64_t c = c0 + 8 * u;
+      const bool in = c < nlive;
+      pv[u] = (in && live_o) ? d.part[c * stride + i] : 0;
+      ap[u] = (in && mx_lane) ? d.cmp[c * rows + r] : 0;
+      av[u] = (in && mx_lane && !d.run_k) ? d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv] : 0;
+      ak[u] = (in && mx_lane && !d.run_k) ? d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv] : 0;
     }
-    for (; c < nlive; c += 8) s4[0] += d.part[c * stride + i];
-    acc = s4[0] + s4[1] + s4[2] + s4[3];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc += pv[u];
+      mp = ap[u] > mp ? ap[u] : mp;
+      mv = av[u] > mv ? av[u] : mv;
+      mk = ak[u] > mk ? ak[u] : mk;
+    }
   }
   s_sum[g][o] = acc;
-  const bool head = imie_umod32((int64_t)blockIdx.x * 32, d.hd) == 0;
-  if (head && o == 0) {
-    uint64_t mp = 0, mv = 0, mk = 0;
-    for (int64_t c = g; c < nlive; c += 8) {
-      const uint64_t a = d.cmp[c * rows + r];
-      const uint64_t v = d.run_k ? 0 : d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv];
-      const uint64_t k = d.run_k ? 0 : d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv];
-      mp = a > mp ? a : mp;
-      mv = v > mv ? v : mv;
-      mk = k > mk ? k : mk;
-    }
-    s_mx[0][g] = mp; s_mx[1][g] = mv; s_mx[2][g] = mk;
-  }
+  if (mx_lane) { s_mx[0][g] = mp; s_mx[1][g] = mv; s_mx[2][g] = mk; }
   __syncthreads();
   if (blockIdx.x == 0 && t == 0) check_rope_guard(d);
   if (t < 32 && i < rows * d.hd) {
@@ -686,7 +697,7 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
     d.out[qoff(d, r) + imie_umod32(i, d.hd)] = (int64_t)tot >> d.frac;
   }
   if (head && t == 0 && L > 0) {
-    uint64_t mp = 0, mv = 0, mk = 0;
+    mp = 0; mv = 0; mk = 0;
     for (int gg = 0; gg < 8; ++gg) {
       mp = s_mx[0][gg] > mp ? s_mx[0][gg] : mp;
       mv = s_mx[1][gg] > mv ? s_mx[1][gg] : mv;
@@ -764,61 +775,7 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
   const int64_t* qg = d.q + b * d.qsb + kv * REP * d.qsh;
   v4i av[RBH][2][2];
-  int Lq = 0;
-  if (d.qd) {
-    // digits prepared by the head stage: A operands straight from memory, no staging
-    for (int r = 0; r < REP; ++r) { const int lr = d.qlimbs[b * d.H + kv * REP + r]; Lq = lr > Lq ? lr : Lq; }
-#pragma unroll
-    for (int hb = 0; hb < RBH; ++hb)
-#pragma unroll
-      for (int lb = 0; lb < 2; ++lb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int r = 4 * hb + (m >> 2), lq = 4 * lb + (m & 3);
-          av[hb][lb][h] = (r < REP && lq < Lq && 64 * h + 16 * g < d.hd)
-                              ? *(const v4i*)(d.qd + ((b * d.H + kv * REP + r) * 8 + lq) * d.hd + 64 * h + 16 * g)
-                              : v4i{0, 0, 0, 0};
-        }
-  } else {
-    uint64_t mq = 0;
-    for (int i = tid; i < REP * d.hd; i += 256) {
-      const uint64_t a = imie_absu64(qg[imie_udiv32(i, d.hd) * d.qsh + imie_umod32(i, d.hd)]);
-      mq = a > mq ? a : mq;
-    }
-    mq = imie_wave_max_u64(mq);
-    if (lane == 0) s_mq[wave] = mq;
-    if (blockIdx.y == 0 && tid < REP) {
-      uint64_t mr = 0;
-      for (int c = 0; c < d.hd; ++c) { const uint64_t a = imie_absu64(qg[tid * d.qsh + c]); mr = a > mr ? a : mr; }
-      d.maxq[b * d.H + kv * REP + tid] = mr;
-    }
-    __syncthreads();
-    uint64_t mqa = s_mq[0];
-    for (int w = 1; w < 4; ++w) mqa = s_mq[w] > mqa ? s_mq[w] : mqa;
-    Lq = imie_limbs_needed(mqa);
-    // digits of every q element once (thread per element) into LDS rows [head block][4 (r % 4) + lq % 4][limb
-    // block][dim]; each lane then reads its 16-byte A operands directly
-    for (int i = tid; i < RBH * 2 * 16 * 128; i += 256) (&sQd[0][0][0][0])[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < REP * d.hd; i += 256) {
-      const int r = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
-      int64_t x = qg[r * d.qsh + c];
-      for (int lq = 0; lq < Lq; ++lq) {
-        const int64_t dg = ((x + 128) & 255) - 128;
-        x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
-        sQd[r >> 2][lq >> 2][4 * (r & 3) + (lq & 3)][c] = (int8_t)dg;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int hb = 0; hb < RBH; ++hb)
-#pragma unroll
-      for (int lb = 0; lb < 2; ++lb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
-  }
-  const int LB = (Lq + 3) / 4;
+  int Lq = 0, LB = 0;
   const int KS = (int)((d.hd + 63) / 64);
   int64_t smax[RBH];
 #pragma unroll
@@ -867,7 +824,73 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   };
   v4i bkA[4][2], bkB[4][2];
   int64_t t = j0 + 16 * wave;
-  if (t < jend) load_tile(t, bkA);
+  if (t < jend) load_tile(t, bkA);          // the first K tile in flight during the q setup
+  if (d.qd) {
+    // digits prepared by the head stage (all eight limb planes written): A operands straight from memory, loaded
+    // together with the limb counts and masked once those arrive
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int r = 4 * hb + (m >> 2), lq = 4 * lb + (m & 3);
+          av[hb][lb][h] = (r < REP && 64 * h + 16 * g < d.hd)
+                              ? *(const v4i*)(d.qd + ((b * d.H + kv * REP + r) * 8 + lq) * d.hd + 64 * h + 16 * g)
+                              : v4i{0, 0, 0, 0};
+        }
+    int lrs[REP];
+#pragma unroll
+    for (int r = 0; r < REP; ++r) lrs[r] = d.qlimbs[b * d.H + kv * REP + r];
+#pragma unroll
+    for (int r = 0; r < REP; ++r) Lq = lrs[r] > Lq ? lrs[r] : Lq;
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (4 * lb + (m & 3) >= Lq) av[hb][lb][h] = v4i{0, 0, 0, 0};
+  } else {
+    uint64_t mq = 0;
+    for (int i = tid; i < REP * d.hd; i += 256) {
+      const uint64_t a = imie_absu64(qg[imie_udiv32(i, d.hd) * d.qsh + imie_umod32(i, d.hd)]);
+      mq = a > mq ? a : mq;
+    }
+    mq = imie_wave_max_u64(mq);
+    if (lane == 0) s_mq[wave] = mq;
+    if (blockIdx.y == 0 && tid < REP) {
+      uint64_t mr = 0;
+      for (int c = 0; c < d.hd; ++c) { const uint64_t a = imie_absu64(qg[tid * d.qsh + c]); mr = a > mr ? a : mr; }
+      d.maxq[b * d.H + kv * REP + tid] = mr;
+    }
+    __syncthreads();
+    uint64_t mqa = s_mq[0];
+    for (int w = 1; w < 4; ++w) mqa = s_mq[w] > mqa ? s_mq[w] : mqa;
+    Lq = imie_limbs_needed(mqa);
+    // digits of every q element once (thread per element) into LDS rows [head block][4 (r % 4) + lq % 4][limb
+    // block][dim]; each lane then reads its 16-byte A operands directly
+    for (int i = tid; i < RBH * 2 * 16 * 128; i += 256) (&sQd[0][0][0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < REP * d.hd; i += 256) {
+      const int r = (int)imie_udiv32(i, d.hd), c = (int)imie_umod32(i, d.hd);
+      int64_t x = qg[r * d.qsh + c];
+      for (int lq = 0; lq < Lq; ++lq) {
+        const int64_t dg = ((x + 128) & 255) - 128;
+        x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+        sQd[r >> 2][lq >> 2][4 * (r & 3) + (lq & 3)][c] = (int8_t)dg;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
+  }
+  LB = (Lq + 3) / 4;
   while (t < jend) {
     const int64_t t2 = t + 64;
     if (t2 < jend) load_tile(t2, bkB);
@@ -913,6 +936,35 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
     if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
     return;
   }
+  const int64_t jend = min(j0 + d.chunk, L);
+  const int DT = (int)(d.hd / 16);
+  const int8_t* Vb = (const int8_t*)d.V;
+  // one 64-key step's operands: the V slices of this wave's dim tiles and the scores of thread (key tid % 64,
+  // heads tid / 64 + 4k); the first step's are requested before the Z reduction, later ones a step ahead
+  constexpr int RW = (REP + 3) / 4;
+  auto load_step = [&](int64_t t0, v4i (&bv)[2][4], int64_t (&sc)[RW]) {
+    const int64_t tn = min((int64_t)64, jend - t0);
+    int64_t pi, slot0;
+    page_split(d, t0, pi, slot0);
+    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tile = wave + 4 * tt;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        bv[tt][db] = tile < DT ? *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, 16 * tile + m, d.hd, d.P))
+                               : v4i{0, 0, 0, 0};
+    }
+    const int kk = tid & 63;
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+      const int r = (tid >> 6) + 4 * k;
+      sc[k] = (r < REP && kk < tn) ? d.scores[(b * d.H + kv * REP + r) * d.Lmax + t0 + kk] : 0;
+    }
+  };
+  v4i bvA[2][4], bvB[2][4];
+  int64_t scA[RW], scB[RW];
+  load_step(j0, bvA, scA);
   const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   for (int r = wave; r < REP; r += 4) {
     uint64_t z = 0;
@@ -924,8 +976,6 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   for (int i = tid; i < RBH * 16 * 64; i += 256) (&sPd[0][0][0])[i] = 0;
   __syncthreads();
   const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
-  const int64_t jend = min(j0 + d.chunk, L);
-  const int DT = (int)(d.hd / 16);
   uint64_t mp[REP];
 #pragma unroll
   for (int r = 0; r < REP; ++r) mp[r] = 0;
@@ -934,31 +984,36 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   for (int hb = 0; hb < RBH; ++hb)
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[hb][db][0] = acc[hb][db][1] = v4i{0, 0, 0, 0};
-  const int8_t* Vb = (const int8_t*)d.V;
   for (int64_t t0 = j0; t0 < jend; t0 += 64) {
     const int64_t tn = min((int64_t)64, jend - t0);
-    // this step's V slices first: their latency overlaps the p / digit work below
-    int64_t pi, slot0;
-    page_split(d, t0, pi, slot0);
-    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
     v4i bv[2][4];
+    int64_t scv[RW];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tile = wave + 4 * tt;
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-        bv[tt][db] = tile < DT ? *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, 16 * tile + m, d.hd, d.P))
-                               : v4i{0, 0, 0, 0};
+      for (int db = 0; db < 4; ++db) bv[tt][db] = bvA[tt][db];
+#pragma unroll
+    for (int k = 0; k < RW; ++k) scv[k] = scA[k];
+    if (t0 + 64 < jend) {
+      load_step(t0 + 64, bvB, scB);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) bvA[tt][db] = bvB[tt][db];
+#pragma unroll
+      for (int k = 0; k < RW; ++k) scA[k] = scB[k];
     }
     __syncthreads();                                  // previous step's digits consumed
     {
       const int kk = tid & 63;
-      for (int r = tid >> 6; r < REP; r += 4) {
-        const int64_t row = b * d.H + kv * REP + r;
+#pragma unroll
+      for (int k = 0; k < RW; ++k) {
+        const int r = (tid >> 6) + 4 * k;
+        if (r >= REP) break;
         const uint64_t Z = s_z[r];
         int64_t p = 0;
         if (kk < tn && Z != 0) {
-          const uint64_t num = (uint64_t)d.scores[row * d.Lmax + t0 + kk] << d.frac;
+          const uint64_t num = (uint64_t)scv[k] << d.frac;
           if (Z == 1) p = (int64_t)num;
           else {
             const uint64_t rz = s_rz[r];

@@ -6,49 +6,12 @@
 //   lowest-index argmax     reference_bonsai.py:812-827 (numpy first-max)
 #include "imie_common.h"
 #include "imie_kernels.h"
+#include "imie_silu.h"
 
 namespace {
 
+using namespace imie_silu;
 typedef unsigned __int128 u128;
-
-__device__ inline int64_t rshift_np(int64_t a, int64_t s) {   // numpy int64 `a >> s` incl. out-of-range counts
-  if (s < 0 || s >= 64) return a < 0 ? -1 : 0;
-  return a >> s;
-}
-
-__device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
-  const int64_t fp = (int64_t)1 << frac;
-  const int64_t k = u >> frac, f = u & (fp - 1);
-  const int sh = 16 - frac;
-  int64_t c0, c1, c2, c3;
-  if (sh >= 0) { c0 = 65536 >> sh; c1 = 45426 >> sh; c2 = 15743 >> sh; c3 = 3638 >> sh; }
-  else { c0 = (int64_t)65536 << -sh; c1 = (int64_t)45426 << -sh; c2 = (int64_t)15743 << -sh; c3 = (int64_t)3638 << -sh; }
-  const int64_t f2 = (int64_t)((uint64_t)f * (uint64_t)f) >> frac;
-  const int64_t f3 = (int64_t)((uint64_t)f2 * (uint64_t)f) >> frac;
-  int64_t poly = c0 - ((int64_t)((uint64_t)c1 * (uint64_t)f) >> frac) + ((int64_t)((uint64_t)c2 * (uint64_t)f2) >> frac) -
-                 ((int64_t)((uint64_t)c3 * (uint64_t)f3) >> frac);
-  if (poly < 0) poly = 0;
-  return rshift_np(poly, k < 63 ? k : 63);
-}
-
-__device__ inline int64_t sigmoid_fixed(int64_t x, int frac, int64_t log2e, int64_t dclip) {
-  const int64_t m = x > 0 ? x : 0;
-  int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
-  if (d0 > dclip) d0 = dclip;
-  if (d1 > dclip) d1 = dclip;
-  const int64_t e0 = exp2_neg_fixed((int64_t)((uint64_t)d0 * (uint64_t)log2e) >> frac, frac);
-  const int64_t e1 = exp2_neg_fixed((int64_t)((uint64_t)d1 * (uint64_t)log2e) >> frac, frac);
-  const int64_t z = e0 + e1;
-  if (z == 0) return 0;
-  const uint64_t num = (uint64_t)e1 << frac;               // e1 << frac >= 0 and fits (e1 <= c0 + c2)
-  if (num < ((uint64_t)1 << 52)) {                         // exact double quotient estimate, +-1 integer fix
-    uint64_t q = (uint64_t)((double)num / (double)z);
-    if (q * (uint64_t)z > num) --q;
-    else if (num - q * (uint64_t)z >= (uint64_t)z) ++q;
-    return (int64_t)q;
-  }
-  return (int64_t)(num / (uint64_t)z);
-}
 
 __global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t* __restrict__ up, int64_t n, int frac,
                                 int64_t log2e, int64_t dclip, int64_t* __restrict__ out) {
@@ -225,6 +188,8 @@ static void silu_consts(int64_t frac, int64_t* log2e, int64_t* dclip) {
   const int64_t a = ((frac + 2) << (2 * frac)) / *log2e, b = ((int64_t)1 << 62) / *log2e;
   *dclip = a < b ? a : b;
 }
+
+void imie_silu_consts(int64_t frac, int64_t* log2e, int64_t* dclip) { silu_consts(frac, log2e, dclip); }
 
 int imie_silu_mul_launch(const int64_t* gate, const int64_t* up, int64_t n, int64_t frac, int64_t* out,
                          hipStream_t st) {

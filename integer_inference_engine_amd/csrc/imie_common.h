@@ -52,7 +52,7 @@ __device__ __forceinline__ int64_t imie_floor_shift(int64_t v, int s) {
 __device__ __forceinline__ int64_t imie_udiv32(int64_t a, int64_t b) { return (int64_t)((uint32_t)a / (uint32_t)b); }
 __device__ __forceinline__ int64_t imie_umod32(int64_t a, int64_t b) { return (int64_t)((uint32_t)a % (uint32_t)b); }
 
-__device__ __forceinline__ uint64_t imie_absu64(int64_t v) {
+__host__ __device__ __forceinline__ uint64_t imie_absu64(int64_t v) {
   return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v;
 }
 

@@ -47,6 +47,37 @@ __host__ __device__ inline uint64_t isqrt_u128(u128 v) {
   return lo;
 }
 
+// floor(sqrt(v)) with a short path below 2^52: v converts exactly, the double root is within one of the answer,
+// and one integer check each way settles it (k <= 2^26, so the squares are 32 x 32 -> 64-bit products).
+__host__ __device__ inline uint64_t isqrt_u128_fast(u128 v) {
+  if ((v >> 52) == 0) {
+    const uint64_t u = (uint64_t)v;
+    uint64_t k = (uint64_t)sqrt((double)u);
+    if ((uint64_t)(uint32_t)k * (uint32_t)k > u) --k;
+    else if ((uint64_t)(uint32_t)(k + 1) * (uint32_t)(k + 1) <= u) ++k;
+    return k;
+  }
+  return isqrt_u128(v);
+}
+
+// n = floor((x << frac) / rms) in double precision where that is exact to settle: |x| << frac below 2^53 and rms
+// below 2^51. The quotient estimate num * (1 / rms) is within 2 of the answer; the remainder num - q * rms comes
+// exactly from one fma (|r| < 4 rms < 2^53) and steers the correction. Returns false where the bounds do not hold
+// (the caller takes the integer routine).
+__host__ __device__ inline bool norm_elem_f64(int64_t x, int frac, uint64_t rms, double rms_d, double rinv_d,
+                                              int64_t* out) {
+  const uint64_t ax = imie_absu64(x);
+  if (frac < 1 || frac > 52 || (ax >> (53 - frac)) != 0 || (rms >> 51) != 0) return false;
+  const double num = (double)(ax << frac);
+  double q = floor(num * rinv_d);
+  double r = fma(-q, rms_d, num);
+  while (r < 0) { q -= 1.0; r += rms_d; }
+  while (r >= rms_d) { q += 1.0; r -= rms_d; }
+  const uint64_t qi = (uint64_t)q;
+  *out = x < 0 ? -(int64_t)(qi + (r != 0 ? 1 : 0)) : (int64_t)qi;
+  return true;
+}
+
 // floor(num / d) for |num| < 2^127 given as sign + 128-bit magnitude, d > 0 (bitwise long division; rare path)
 __device__ inline int64_t floor_div_mag128(bool neg, u128 mag, uint64_t d, bool* fits) {
   u128 q = 0, r = 0;

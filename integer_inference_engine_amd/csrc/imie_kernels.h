@@ -36,6 +36,16 @@ int imie_rmsnorm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, int64
 int imie_silu_mul_prep_launch(const int64_t* gate, const int64_t* up, int64_t T, int64_t n, int64_t frac,
                               int64_t* out, const imie_q1::Q1PrepOut& po, hipStream_t st);
 
+// The SiLU constants for frac fraction bits (log2(e) in fixed point and the exponent clip).
+void imie_silu_consts(int64_t frac, int64_t* log2e, int64_t* dclip);
+// Single-token matvec whose workgroups derive the digit table of their slab range from the producer's inputs
+// (imie_q1::Q1Pro, kind kProCopy / kProSiluMul / kProNorm) in place of a prep kernel; pro.zero is cleared on the
+// way. K-split outputs are added into: with accumulate == 0 they must be clear before the launch.
+// imie_q1_pro_ok: whether the weights (same n_blocks, int32 scales, K == pro.cols) take this path.
+int imie_q1_pro_ok(const int64_t* handles, int cnt, int kind, int64_t cols);
+int imie_q1_launch_pro(const int64_t* handles, int cnt, const imie_q1::Q1Pro& pro, int kind, int64_t frac,
+                       int64_t* const* outs, int accumulate, hipStream_t st);
+
 // NeoX RoPE on rows x (rows, nh, hd); row r uses table row pos[r] (pos == nullptr: pos0 + r).
 // The fail-loud envelope 2*max|x|*max|cos,sin| <= INT64_MAX is checked exactly via `guard` scratch
 // (2 x uint64, zeroed by the caller) and reported in `status` by imie_rope_guard_check.

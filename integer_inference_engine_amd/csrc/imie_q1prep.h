@@ -37,6 +37,21 @@ struct Q1Zero {                    // outputs a producer clears before a K-split
   int cnt;
 };
 
+// Matvec prologue (single-token decode): the matvec workgroups derive their slab range's digit table from the
+// producer's inputs themselves instead of reading a table a separate kernel wrote.
+enum { kProNone = 0, kProCopy = 1, kProSiluMul = 2, kProNorm = 3 };
+struct Q1Pro {
+  const int64_t* x;                // activations (kProCopy), gate (kProSiluMul), the row to normalise (kProNorm)
+  const int64_t* x2;               // kProSiluMul: up
+  const int64_t* gain;             // kProNorm: gain (cols)
+  const uint64_t* gmax;            // kProNorm: max |gain| (one device word, written by an earlier kernel)
+  int64_t cols;                    // length of x (= the matvec's K)
+  int64_t eps, log2e, dclip;       // kProNorm: eps; kProSiluMul: log2(e) and the exponent clip
+  int frac;                        // the producer's fixed-point fraction bits
+  int* status;                     // kProNorm: refusal bit 4
+  Q1Zero zero;                     // outputs of a later K-split matvec, cleared by these workgroups
+};
+
 __device__ inline int64_t prep_pos(int lane, int64_t sl, int q) {
   const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
   const int d = 2 * dh + (q >> 2), c = q & 3;
@@ -73,6 +88,37 @@ __device__ inline void prep_slab(int64_t v[8], const Q1PrepOut& po, int64_t t, i
     }
     uint32_t* dst = po.xq + ((((t * kMaxLimbs + l) * po.nbp + blk) * 8 + s) * 4);
     *(uint2*)(dst + 2 * dh) = uint2{w0, w1};
+  }
+}
+
+// prep_slab into LDS: the slab's limb count, block totals and digits for a workgroup-local table laid out as the
+// global one of a single token (dst[l * 32 + block * 8 + s], eight limbs); every lane of the wave participates.
+__device__ inline void prep_slab_lds(int64_t v[8], uint4* dst, int* L_out, int64_t* tot_out) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 7, dh = (lane >> 3) & 1;
+  uint64_t mx = 0;
+  int64_t part = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint64_t a = imie_absu64(v[q]);
+    mx = a > mx ? a : mx;
+    part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
+  }
+  mx = imie_wave_max_u64_full(mx);
+  const int L = imie_limbs_needed(mx);
+  part = (int64_t)imie_row_sum_u64_full((uint64_t)part);
+  if ((lane & 15) == 0) tot_out[g] = part;
+  if (lane == 0) *L_out = L;
+  for (int l = 0; l < L; ++l) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t dig = ((v[q] + 128) & 255) - 128;
+      v[q] = (int64_t)(((uint64_t)v[q] - (uint64_t)dig)) >> 8;
+      const uint32_t byte = (uint32_t)(dig & 0xFF) << (8 * (q & 3));
+      if (q < 4) w0 |= byte; else w1 |= byte;
+    }
+    *(uint2*)((uint32_t*)(dst + l * 32 + g * 8 + s) + 2 * dh) = uint2{w0, w1};
   }
 }
 

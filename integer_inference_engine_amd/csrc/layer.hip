@@ -12,6 +12,7 @@
 // int64 cache). A dense reference cache (B, Hkv, cap, hd) is the case P = cap, mp = 1.
 #include "imie_common.h"
 #include "imie_kernels.h"
+#include <stdlib.h>
 #include "imie_attention.h"
 #include "imie_kvfmt.h"
 #include <string.h>
@@ -37,6 +38,40 @@ const int64_t* buf_get(int64_t h, int64_t need) {
 __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
+}
+
+// Start of a single-token pass with matvec prologues: workgroup i < ng writes max |gain_i| (over cols) for the
+// RMSNorm envelope check; every workgroup clears its share of the RoPE guards and of the zero list (the first
+// layer's q, k, v, which its K-split matvec adds into).
+__global__ __launch_bounds__(256) void pro_start_kernel(const int64_t* const* __restrict__ gains, int ng, int64_t cols,
+                                                        uint64_t* __restrict__ gmax, int64_t* __restrict__ guard,
+                                                        int64_t nguard, imie_q1::Q1Zero zero) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nguard; e += (int64_t)gridDim.x * 256) guard[e] = 0;
+  imie_q1::zero_share(zero, blockIdx.x, gridDim.x, threadIdx.x, 256);
+  if ((int)blockIdx.x >= ng) return;
+  const int64_t* g = gains[blockIdx.x];
+  uint64_t m = 0;
+  for (int64_t c0 = 0; c0 < cols; c0 += 16 * 256) {   // 16 loads in flight per thread
+    int64_t v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t c = c0 + threadIdx.x + 256 * k;
+      v[k] = g[c < cols ? c : 0];                      // unconditional: an in-range duplicate changes no maximum
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint64_t a = imie_absu64(v[k]);
+      m = a > m ? a : m;
+    }
+  }
+  m = imie_wave_max_u64(m);
+  __shared__ uint64_t s_m[4];
+  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) m = s_m[w] > m ? s_m[w] : m;
+    gmax[blockIdx.x] = m;
+  }
 }
 
 int fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t st) {
@@ -112,6 +147,7 @@ struct Net {
   std::vector<int64_t> len;           // host lengths per sequence
   // workspace
   DevBuf n, q, k, v, qn, kn, att, gate, up, h, pos, starts, attn, guard, status, x, logits, ids, lastx, amx, stepc;
+  DevBuf gtab, gmax;                  // device table of the 2 * nl RMSNorm gains (n1g, n2g per layer), their max |g|
   DevBuf kvrun;                       // kv8: running max|K|, max|V| per (layer, sequence, kv head): [nl][2][B*Hkv]
   DevBuf kvrow;                       // kv8: appended rows' maxima [2][rows*Hkv]
   DevBuf gpart;                       // many-row head stage: per-(row, head) RoPE envelope maxima [rows][H+Hkv][2]
@@ -150,7 +186,8 @@ void net_free(Net* n) {
   if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
                   &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx, &n->amx,
-                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow, &n->gpart};
+                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow, &n->gpart,
+                  &n->gtab, &n->gmax};
   for (auto b : bs) b->release();
   n->live = false;
 }
@@ -263,6 +300,20 @@ int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, i
   return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st);
 }
 
+// Whether every projection of every layer takes the prologue matvec (int32 scales, RMSNorm rows <= 4096), and
+// the device gain table is in place. IMIE_NO_PRO=1 keeps the separate producer kernels (comparison runs).
+bool pro_path_ok(Net& n) {
+  static const bool off = [] { const char* e = getenv("IMIE_NO_PRO"); return e && atoi(e) != 0; }();
+  if (off || !n.gtab.p || !n.gmax.p) return false;
+  const int64_t qd = n.H * n.hd;
+  for (const LayerW& L : n.layers) {
+    if (!imie_q1_pro_ok(L.w, 3, imie_q1::kProNorm, n.d) || !imie_q1_pro_ok(&L.w[3], 1, imie_q1::kProCopy, qd) ||
+        !imie_q1_pro_ok(&L.w[4], 2, imie_q1::kProNorm, n.d) || !imie_q1_pro_ok(&L.w[6], 1, imie_q1::kProSiluMul, n.dff))
+      return false;
+  }
+  return true;
+}
+
 // All layers over M new tokens per sequence; positions come from the device buffers n.pos (B*M) and n.starts
 // (B), so the launch sequence is independent of the positions (graph-capturable). lmax bounds the keys any row
 // sees and fixes the attention geometry. x: device (B*M, d), updated in place.
@@ -277,10 +328,39 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
   const int64_t* posd = (const int64_t*)n.pos.p;
   uint64_t* guard = (uint64_t*)n.guard.p;
   int* status = (int*)n.status.p;
-  CK(fill_i64((int64_t*)guard, 4 * n.nl, 0, st));   // per-layer RoPE envelope maxima
+  // one token: the matvecs build their digit tables in their own prologue (RMSNorm, copy, SiLU * up) instead of
+  // after a separate producer kernel; K-split outputs are cleared by the kernel before (q, k, v by the start
+  // kernel and by each layer's gate / up matvec, gate / up by the q, k, v matvec)
+  const bool pro = rows == 1 && pro_path_ok(n);
+  int64_t log2e = 0, dclip = 0;
+  imie_silu_consts(n.frac, &log2e, &dclip);
+  imie_q1::Q1Zero zq = {}, zg = {};
+  zq.cnt = 3; zq.p[0] = q; zq.p[1] = k; zq.p[2] = v; zq.n[0] = rows * qd; zq.n[1] = rows * kd; zq.n[2] = rows * kd;
+  zg.cnt = 2; zg.p[0] = gate; zg.p[1] = up; zg.n[0] = rows * n.dff; zg.n[1] = rows * n.dff;
+  if (pro) {
+    hipLaunchKernelGGL(pro_start_kernel, dim3((unsigned)(2 * n.nl)), dim3(256), 0, st,
+                       (const int64_t* const*)n.gtab.p, (int)(2 * n.nl), n.d, (uint64_t*)n.gmax.p, (int64_t*)guard,
+                       4 * n.nl, zq);
+    IMIE_HIP(hipGetLastError());
+  } else {
+    CK(fill_i64((int64_t*)guard, 4 * n.nl, 0, st));   // per-layer RoPE envelope maxima
+  }
+  auto pro_in = [&](const int64_t* a, const int64_t* b, const int64_t* g, int64_t cols, int gi,
+                    const imie_q1::Q1Zero& z) {
+    imie_q1::Q1Pro p = {};
+    p.x = a; p.x2 = b; p.gain = g; p.cols = cols; p.frac = (int)n.frac; p.eps = n.eps; p.status = status;
+    p.gmax = gi >= 0 ? (const uint64_t*)n.gmax.p + gi : nullptr;
+    p.log2e = log2e; p.dclip = dclip;
+    p.zero = z;
+    return p;
+  };
   for (int64_t l = 0; l < n.nl; ++l) {
     const LayerW& L = n.layers[(size_t)l];
-    {
+    if (pro) {
+      int64_t* outs[3] = {q, k, v};
+      const imie_q1::Q1Pro p = pro_in(x, nullptr, L.n1g, n.d, (int)(2 * l), zg);
+      CK(imie_q1_launch_pro(L.w, 3, p, imie_q1::kProNorm, n.frac, outs, 0, st));
+    } else {
       int64_t* outs[3] = {q, k, v};
       CK(norm_into_matvec(n, x, rows, L.n1g, xn, L.w, 3, outs, st));
     }
@@ -313,6 +393,17 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));
     }
     CK(imie_attention_launch(d, st));
+    if (pro) {
+      const imie_q1::Q1Zero none = {};
+      const imie_q1::Q1Pro po = pro_in(att, nullptr, nullptr, qd, -1, none);
+      CK(imie_q1_launch_pro(&L.w[3], 1, po, imie_q1::kProCopy, n.frac, &x, 1, st));
+      int64_t* outs[2] = {gate, up};
+      const imie_q1::Q1Pro pn = pro_in(x, nullptr, L.n2g, n.d, (int)(2 * l + 1), zq);
+      CK(imie_q1_launch_pro(&L.w[4], 2, pn, imie_q1::kProNorm, n.frac, outs, 0, st));
+      const imie_q1::Q1Pro ps = pro_in(gate, up, nullptr, n.dff, -1, none);
+      CK(imie_q1_launch_pro(&L.w[6], 1, ps, imie_q1::kProSiluMul, n.frac, &x, 1, st));
+      continue;
+    }
     CK(imie_q1_launch_multi(&L.w[3], 1, att, rows, n.frac, &x, 1, &n.q1w, st));
     {
       int64_t* outs[2] = {gate, up};
@@ -453,6 +544,14 @@ int64_t net_create(int64_t B, int64_t n_layers, int64_t H, int64_t Hkv, int64_t 
   n->sin = buf_get(sin_h, cap * (hd / 2));
   if (!n->cos || !n->sin) { delete n; return -1; }
   n->rope_rows = std::min(bufs()[(size_t)cos_h].n, bufs()[(size_t)sin_h].n) / (hd / 2);
+  {
+    std::vector<const int64_t*> gt;
+    for (const LayerW& L : n->layers) { gt.push_back(L.n1g); gt.push_back(L.n2g); }
+    if (n->gtab.ensure(gt.size() * sizeof(void*)) || n->gmax.ensure(gt.size() * 8) ||
+        hipMemcpy(n->gtab.p, gt.data(), gt.size() * sizeof(void*), hipMemcpyHostToDevice) != hipSuccess) {
+      n->gtab.release(); n->gmax.release(); delete n; return -1;
+    }
+  }
   n->live = true;
   if (net_alloc_kv(*n, std::vector<int64_t>((size_t)B, cap), page, kv32)) { net_free(n); delete n; return -1; }
   nets().push_back(n);

@@ -7,6 +7,7 @@
 #include "imie_common.h"
 #include "imie_kernels.h"
 #include "imie_fixed.h"
+#include "imie_silu.h"
 #include <stdlib.h>
 
 namespace {
@@ -436,6 +437,19 @@ int imie_rmsnorm_fused_gpu(const int64_t* x, int64_t rows, int64_t cols, int64_t
 
 uint64_t imie_fx_isqrt_u128(uint64_t hi, uint64_t lo) { return imie_fx::isqrt_u128(((imie_fx::u128)hi << 64) | lo); }
 uint64_t imie_fx_recip_u64(uint64_t d) { return imie_fx::recip_u64(d); }
+uint64_t imie_fx_isqrt_fast(uint64_t hi, uint64_t lo) {
+  return imie_fx::isqrt_u128_fast(((imie_fx::u128)hi << 64) | lo);
+}
+int imie_fx_norm_f64(int64_t x, int frac, uint64_t rms, int64_t* out) {
+  if (!out || rms == 0) return -1;
+  const double rd = (double)rms;
+  return imie_fx::norm_elem_f64(x, frac, rms, rd, 1.0 / rd, out) ? 1 : 0;
+}
+int64_t imie_silu_mul_host(int64_t g, int64_t u, int64_t frac, int fast) {
+  int64_t log2e, dclip;
+  imie_silu_consts(frac, &log2e, &dclip);
+  return fast ? imie_silu::silu_mul_fast(g, u, (int)frac, log2e, dclip) : imie_silu::silu_mul(g, u, (int)frac, log2e, dclip);
+}
 uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d) {
   return (uint64_t)imie_fx::div_u128_cols(((imie_fx::u128)hi << 64) | lo, d);
 }

@@ -22,6 +22,8 @@
 #include <vector>
 #include "imie_kernels.h"
 #include "imie_q1prep.h"
+#include "imie_fixed.h"
+#include "imie_silu.h"
 #include <string.h>
 #include <type_traits>
 #include <stdlib.h>
@@ -129,6 +131,79 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 //   * grid.y splits K: with ksplit > 1 the waves add their int64 partials into a zeroed output with 64-bit
 //     atomics (integer addition: order-free and exact).
 // ------------------------------------------------------------------------------------------------------
+// RMSNorm prologue statistics (single row, cols <= kProNormCols): every workgroup reduces the whole row's 128-bit
+// sum of squares itself and derives rms = isqrt(ssq // cols + eps) (fixedpoint.py:31-71). Waves whose |x| are all
+// below 2^26 sum 52-bit squares in one 64-bit word per lane (one wave reduction); others carry four 32-bit limbs.
+// Refusals decided here (block (0, 0) flags the status, every workgroup returns false): ssq of 2^128 or more, or
+// rms == 0. The envelope max|n| * max|gain| <= INT64_MAX is checked per element where n is formed.
+constexpr int kProNormCols = 4096;
+__device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, uint64_t& rms) {
+  using namespace imie_fx;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kPer = kProNormCols / 256;
+  int64_t v[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int64_t c = tid + 256 * k;
+    const int64_t x = p.x[c < p.cols ? c : 0];       // unconditional loads (no per-element branch)
+    v[k] = c < p.cols ? x : 0;
+  }
+  uint64_t amax = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint64_t a = imie_absu64(v[k]);
+    amax = a > amax ? a : amax;
+    s_x[tid + 256 * k] = v[k];                       // the row on chip for the element phase (after the barrier)
+  }
+  uint64_t lm[4];
+  if (!__any(amax >> 26 ? 1 : 0)) {
+    // 16 squares below 2^52 per lane, 64 lanes: the wave's sum stays below 2^62
+    uint64_t sq = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t a = (uint32_t)imie_absu64(v[k]);
+      sq += (uint64_t)a * a;
+    }
+    sq = imie_wave_sum_u64_full(sq);
+    lm[0] = sq & 0xFFFFFFFFull; lm[1] = sq >> 32; lm[2] = 0; lm[3] = 0;
+  } else {
+    uint64_t hi = 0, lo = 0;
+    int bad = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint64_t a = imie_absu64(v[k]);
+      const u128 sq = (u128)a * a;
+      const uint64_t sl = (uint64_t)sq, sh = (uint64_t)(sq >> 64);
+      const uint64_t nl = lo + sl;
+      const uint64_t cy = nl < lo ? 1 : 0;
+      const uint64_t nh = hi + sh;
+      bad |= (nh < hi ? 1 : 0) | (nh + cy < nh ? 1 : 0);
+      hi = nh + cy;
+      lo = nl;
+    }
+    u128_limbs(hi, lo, bad, lm);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lm[i] = imie_wave_sum_u64_full(lm[i]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_red[wave * 4 + i] = lm[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lm[i] = s_red[i] + s_red[4 + i] + s_red[8 + i] + s_red[12 + i];
+  uint64_t hi, lo;
+  int bad;
+  u128_fold(lm, hi, lo, bad);
+  rms = 0;
+  if (!bad) {
+    const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)p.cols);
+    if (mean <= ~(u128)0 - (u128)(uint64_t)p.eps) rms = isqrt_u128_fast(mean + (u128)(uint64_t)p.eps);
+  }
+  if (rms == 0 && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) atomicOr(p.status, IMIE_ERMS);
+  return rms != 0;
+}
+
 struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) applied to the same activations
   const uint4* bits[kMaxSegs];
   const void* scale[kMaxSegs];
@@ -138,10 +213,14 @@ struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) app
   int cnt;
 };
 
-template <bool S64, int R, int TT, int PF = 0>
+// PRO != kProNone (one token, R = 1, PF > 0, Lcap = 8): no digit table is read; the workgroup derives its slab
+// range's table from the producer's inputs (pro) into LDS -- element values thread-per-element into s_y, then one
+// wave per slab turns them into digits, limb counts and block totals -- while its weights are in flight.
+template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone>
 __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
-    int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out) {
+    int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, Q1Pro pro) {
+  static_assert(PRO == kProNone || (R == 1 && TT == 1 && PF > 0), "prologue: one token, one tile, prefetched range");
   extern __shared__ __align__(16) unsigned char smem[];
   uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
@@ -193,7 +272,7 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     // the slab's digit count and block total travel with its weights (one prefetch, one wait)
 #pragma unroll
     for (int t = 0; t < TT; ++t)
-      if (t < T) {
+      if (PRO == kProNone && t < T) {
         Lv[buf][t] = lslab[t * nslabs + sl];
         tv[buf][t] = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
       }
@@ -202,6 +281,11 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   // tiles; from LDS (staged limbs), the global table (limbs beyond Lcap), or the 8-entry zero slot for lanes
   // whose row is not their block or whose limb is beyond the slab's count
   const uint4* zslot = stage + (int64_t)TT * spk * Lcap * 32;
+  // PRO: slab limb counts, block totals and the element values after the zero slot
+  int* sL = (int*)(stage + (int64_t)TT * spk * Lcap * 32 + 8);
+  int64_t* stot = (int64_t*)(sL + 8);
+  // element values (PRO), aliasing the table: each wave reads its slab's values before writing digits over them
+  int64_t* s_y = (int64_t*)stage;
   const int arow_l = n & 3;
   auto compute = [&](int buf, int64_t sl) {
     uint64_t pos[TT][R];
@@ -212,7 +296,7 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       if (t >= T) break;
-      const int L = Lv[buf][t];
+      const int L = PRO != kProNone ? sL[sl - s0] : Lv[buf][t];
       if (L == 1) {
         // one limb (e.g. int8 activations): rows = (block, bit position mod 4) with mask-only B operands
         // (bytes 0 / 2^s, 0x80 reading as -128); 128 * pos = sum d0[q] << (7 - q) + sum d1[q] << (3 - q)
@@ -295,7 +379,8 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
       if (t >= T) break;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint64_t S = 2u * pos[t][r] - (uint64_t)tv[buf][t];
+        const int64_t tot = PRO != kProNone ? stot[(sl - s0) * 4 + g] : tv[buf][t];
+        const uint64_t S = 2u * pos[t][r] - (uint64_t)tot;
         const int64_t prod = (int64_t)(S * (uint64_t)(int64_t)sc[buf][r]);
         acc[t][r] += (uint64_t)imie_floor_shift(prod, frac);
       }
@@ -311,6 +396,83 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   } else if (live) {
     load(0, s0);
   }
+  if (PRO != kProNone) {
+    __shared__ uint64_t s_red[24];
+    // the range's inputs, element c0 + threadIdx.x + 256 k for k < 2 nsl, all requested before any use (a
+    // loop over a run-time count would wait for each load in turn)
+    constexpr int KY = PF > 0 ? 2 * PF : 1;
+    const int64_t c0 = s0 * 512;
+    int64_t ya[KY], yb[KY];
+#pragma unroll
+    for (int k = 0; k < KY; ++k) {
+      const int64_t c = c0 + threadIdx.x + 256 * k;
+      const int64_t cc = (k < 2 * nsl && c < pro.cols) ? c : 0;
+      ya[k] = PRO == kProNorm ? 0 : pro.x[cc];
+      yb[k] = PRO == kProSiluMul ? pro.x2[cc] : (PRO == kProNorm ? pro.gain[cc] : 0);
+    }
+    zero_share(pro.zero, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, (int64_t)gridDim.x * gridDim.y, threadIdx.x,
+               256);
+    const uint64_t gmax = PRO == kProNorm ? *pro.gmax : 0;
+    uint64_t rms = 0;
+    if (PRO == kProNorm) {
+      __shared__ int64_t s_x[kProNormCols];
+      if (!pro_norm_stats(pro, s_red, s_x, rms)) return;      // the same verdict in every workgroup
+#pragma unroll
+      for (int k = 0; k < KY; ++k) {                          // this range's x from the row staged in LDS
+        const int64_t c = c0 + threadIdx.x + 256 * k;
+        ya[k] = s_x[(k < 2 * nsl && c < pro.cols) ? c : 0];
+      }
+    }
+    // kProNorm: n = floor((x << f) / rms) in double precision where exact (the integer routine for the rest,
+    // with its reciprocal formed only when some lane needs it), then the envelope per element: |n| * max|gain|
+    // beyond INT64_MAX, or an n outside int64, flags the refusal (the oracle's check over the row's maxima)
+    const double rms_d = (double)rms, rinv_d = 1.0 / rms_d;
+    uint64_t rinv = 0;
+    if (PRO == kProNorm) {
+      bool slow = false;
+#pragma unroll
+      for (int k = 0; k < KY; ++k)
+        slow |= k < 2 * nsl && (pro.frac > 52 || (imie_absu64(ya[k]) >> (53 - pro.frac)) != 0 || (rms >> 51) != 0);
+      if (__any(slow ? 1 : 0)) rinv = imie_fx::recip_u64(rms);
+    }
+    uint64_t nmax = 0;
+    bool nfit = true;
+#pragma unroll
+    for (int k = 0; k < KY; ++k) {
+      const int64_t c = c0 + threadIdx.x + 256 * k;
+      if (k >= 2 * nsl) break;
+      int64_t y = 0;
+      if (c < pro.cols) {
+        if (PRO == kProCopy) {
+          y = ya[k];
+        } else if (PRO == kProSiluMul) {
+          y = imie_silu::silu_mul_fast(ya[k], yb[k], pro.frac, pro.log2e, pro.dclip);
+        } else {
+          int64_t nv;
+          if (!imie_fx::norm_elem_f64(ya[k], pro.frac, rms, rms_d, rinv_d, &nv)) {
+            bool f;
+            nv = imie_fx::norm_elem(ya[k], pro.frac, rms, rinv, &f);
+            nfit = nfit && f;
+          }
+          const uint64_t an = imie_absu64(nv);
+          nmax = an > nmax ? an : nmax;
+          y = imie_floor_shift((int64_t)((uint64_t)nv * (uint64_t)yb[k]), pro.frac);
+        }
+      }
+      s_y[threadIdx.x + 256 * k] = y;
+    }
+    if (PRO == kProNorm && (!nfit || (unsigned __int128)nmax * gmax > (unsigned __int128)INT64_MAX))
+      atomicOr(pro.status, IMIE_ERMS);
+    if (threadIdx.x < 8) stage[(int64_t)spk * Lcap * 32 + threadIdx.x] = uint4{0, 0, 0, 0};
+    __syncthreads();
+    for (int64_t j = wave; j < nsl; j += 4) {
+      int64_t v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = s_y[j * 512 + prep_pos(lane, 0, q)];
+      prep_slab_lds(v, stage + j * Lcap * 32, &sL[j], &stot[j * 4]);
+    }
+    __syncthreads();
+  } else {
   // stage the digit operands of this slab range (the same x for every wave of the workgroup)
   for (int t = 0; t < T; ++t)
     for (int64_t j = 0; j < nsl; ++j) {
@@ -323,6 +485,7 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     }
   if (threadIdx.x < 8) stage[(int64_t)TT * spk * Lcap * 32 + threadIdx.x] = uint4{0, 0, 0, 0};
   __syncthreads();
+  }
 
   if (!live) return;
 
@@ -1321,7 +1484,7 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
     const int* ls = (const int*)wk.lslab.p + t0 * nslabs;
 #define IMIE_Q1_LAUNCH(S64_, R_, TT_)                                                                        \
   hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, R_, TT_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs,  \
-                     nbp, tn, fr, spk, Lcap, mode)
+                     nbp, tn, fr, spk, Lcap, mode, Q1Pro{})
 #define IMIE_Q1_LAUNCH_R(S64_, TT_)                                                                          \
   if (R == 4) IMIE_Q1_LAUNCH(S64_, 4, TT_); else if (R == 2) IMIE_Q1_LAUNCH(S64_, 2, TT_); else IMIE_Q1_LAUNCH(S64_, 1, TT_)
 #define IMIE_Q1_LAUNCH_T(S64_)                                                                               \
@@ -1329,7 +1492,7 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   else if (R == 2) { IMIE_Q1_LAUNCH(S64_, 2, 4); } else { IMIE_Q1_LAUNCH(S64_, 1, 4); }
 #define IMIE_Q1_LAUNCH_PF(S64_, PF_)                                                                         \
   hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, 1, 1, PF_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs, \
-                     nbp, tn, fr, spk, Lcap, mode)
+                     nbp, tn, fr, spk, Lcap, mode, Q1Pro{})
     if (pf == 4) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 4); else IMIE_Q1_LAUNCH_PF(false, 4); }
     else if (pf == 2) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 2); else IMIE_Q1_LAUNCH_PF(false, 2); }
     else if (w0.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
@@ -1338,6 +1501,69 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
 #undef IMIE_Q1_LAUNCH_R
 #undef IMIE_Q1_LAUNCH
   }
+  imie_prof_mark(IMIE_K_Q1_GEMV, st, false);
+  IMIE_HIP(hipGetLastError());
+  return IMIE_OK;
+}
+
+// Single-token matvec whose workgroups build their own digit table from the producer's inputs (Q1Pro). The
+// K-split outputs must already be clear (accumulate == 0: a kernel before this one cleared them) or are added to
+// (accumulate != 0). Slab ranges of spk in {1, 2, 4, 8}: the largest that still leaves at least kProTargetWgs
+// workgroups (the prologue is per workgroup, so fewer, longer workgroups repeat less of it).
+static int q1_pro_target_wgs() {
+  static const int v = [] { const char* e = getenv("IMIE_PRO_WGS"); return e ? atoi(e) : 768; }();   // tuning: 768 measured best for the 8B decode
+  return v;
+}
+
+static bool q1_pro_shape_ok(const Q1Weight* const* ws, int cnt, int kind, int64_t cols) {
+  if (cnt < 1 || cnt > kMaxSegs || kind < kProCopy || kind > kProNorm) return false;
+  for (int i = 0; i < cnt; ++i)
+    if (ws[i]->scale64 || ws[i]->nb != ws[0]->nb) return false;
+  if (ws[0]->nb * 128 != cols) return false;
+  return kind != kProNorm || cols <= kProNormCols;
+}
+
+static int q1_apply_pro(const Q1Weight* const* ws, int cnt, const Q1Pro& pro, int kind, int64_t frac,
+                        int64_t* const* outs, int accumulate, hipStream_t st) {
+  if (!q1_pro_shape_ok(ws, cnt, kind, pro.cols)) return IMIE_EARG;
+  const int64_t nslabs = ws[0]->nslabs, nbp = nslabs * kSlabBlocks;
+  Q1Segs sg = {};
+  sg.cnt = cnt;
+  int64_t groups = 0;
+  for (int i = 0; i < cnt; ++i) {
+    sg.bits[i] = ws[i]->bits;
+    sg.scale[i] = ws[i]->scale;
+    sg.N[i] = ws[i]->N;
+    sg.ntiles[i] = ws[i]->ntiles;
+    sg.out[i] = outs[i];
+    sg.gbegin[i] = groups;
+    groups += ws[i]->ntiles;
+  }
+  sg.gbegin[cnt] = groups;
+  const int64_t wg_x = (groups + 3) / 4;
+  int64_t spk = 1;
+  for (int64_t c = 8; c >= 2; c >>= 1)
+    if (wg_x * ((nslabs + c - 1) / c) >= q1_pro_target_wgs()) { spk = c; break; }
+  if (spk > nslabs) spk = nslabs <= 1 ? 1 : (nslabs <= 2 ? 2 : (nslabs <= 4 ? 4 : 8));
+  const int64_t ksplit = (nslabs + spk - 1) / spk;
+  const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
+  const size_t lds = (size_t)spk * 8 * 512 + 128 + 32 + 256;   // table (values alias it), zero slot, L, totals
+  const int fr = (int)(frac > 63 ? 63 : frac);
+  const dim3 grid((unsigned)wg_x, (unsigned)ksplit);
+  imie_prof_mark(IMIE_K_Q1_GEMV, st, true);
+#define IMIE_Q1_PRO(PF_, PRO_)                                                                                 \
+  hipLaunchKernelGGL((q1_gemv_mfma_kernel<false, 1, 1, PF_, PRO_>), grid, dim3(256), lds, st, sg, nullptr,     \
+                     nullptr, nullptr, nslabs, nbp, 1, fr, spk, 8, mode, pro)
+#define IMIE_Q1_PRO_K(PF_)                                                                                     \
+  if (kind == kProCopy) IMIE_Q1_PRO(PF_, kProCopy);                                                           \
+  else if (kind == kProSiluMul) IMIE_Q1_PRO(PF_, kProSiluMul);                                                \
+  else IMIE_Q1_PRO(PF_, kProNorm)
+  if (spk == 8) { IMIE_Q1_PRO_K(8); }
+  else if (spk == 4) { IMIE_Q1_PRO_K(4); }
+  else if (spk == 2) { IMIE_Q1_PRO_K(2); }
+  else { IMIE_Q1_PRO_K(1); }
+#undef IMIE_Q1_PRO_K
+#undef IMIE_Q1_PRO
   imie_prof_mark(IMIE_K_Q1_GEMV, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
@@ -1426,6 +1652,23 @@ int imie_q1_launch_multi(const int64_t* handles, int cnt, const int64_t* x, int6
     if (rc) return rc;
   }
   return IMIE_OK;
+}
+
+int imie_q1_pro_ok(const int64_t* handles, int cnt, int kind, int64_t cols) {
+  if (cnt < 1 || cnt > kMaxSegs) return 0;
+  const Q1Weight* ws[kMaxSegs];
+  for (int i = 0; i < cnt; ++i)
+    if (!(ws[i] = q1_get(handles[i]))) return 0;
+  return q1_pro_shape_ok(ws, cnt, kind, cols) ? 1 : 0;
+}
+
+int imie_q1_launch_pro(const int64_t* handles, int cnt, const Q1Pro& pro, int kind, int64_t frac,
+                       int64_t* const* outs, int accumulate, hipStream_t st) {
+  if (cnt < 1 || cnt > kMaxSegs) return IMIE_EARG;
+  const Q1Weight* ws[kMaxSegs];
+  for (int i = 0; i < cnt; ++i)
+    if (!(ws[i] = q1_get(handles[i]))) return IMIE_EARG;
+  return q1_apply_pro(ws, cnt, pro, kind, frac, outs, accumulate, st);
 }
 
 int imie_q1_gemm_splits(int64_t handle, int64_t T) {

@@ -28,31 +28,55 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   const int64_t* gain = isq ? a.qng : a.kng;
   const int64_t x0 = act ? src[j] : 0, x1 = act ? src[j + half] : 0;
   const int64_t g0 = act ? gain[j] : 0, g1 = act ? gain[j + half] : 0;
-  // 128-bit sum of squares (two squares per lane cannot overflow 128 bits)
-  uint64_t hi, lo;
-  {
-    const uint64_t a0 = imie_absu64(x0), a1 = imie_absu64(x1);
+  // everything else this workgroup reads is requested before the norm's arithmetic: the RoPE entries of the
+  // row's position, and for a key head its V row and page
+  const int64_t p = a.pos[r];
+  const int64_t c = act ? a.cos[p * half + j] : 0, s = act ? a.sin[p * half + j] : 0;
+  const int64_t kvh = h - a.H, b = r / a.M;
+  int64_t v0 = 0, v1 = 0, pg = 0, slot = 0;
+  if (!isq) {
+    const uint32_t pq = (uint32_t)p / (uint32_t)a.P;            // positions are below 2^31
+    pg = a.pt[b * a.mp + pq];
+    slot = (uint32_t)p - pq * (uint32_t)a.P;
+    const int64_t* vr = a.v + (r * a.Hkv + kvh) * a.hd;
+    v0 = act ? vr[j] : 0;
+    v1 = act ? vr[j + half] : 0;
+  }
+  // 128-bit sum of squares (two squares per lane cannot overflow 128 bits); every |x| of the head below 2^26:
+  // 52-bit squares, the wave's sum in one 64-bit word (one reduction instead of four limb sums)
+  uint64_t hi = 0, lo = 0;
+  int bad = 0;
+  const uint64_t a0 = imie_absu64(x0), a1 = imie_absu64(x1);
+  if (!__any(((a0 | a1) >> 26) ? 1 : 0)) {
+    lo = imie_wave_sum_u64_full((uint64_t)(uint32_t)a0 * (uint32_t)a0 + (uint64_t)(uint32_t)a1 * (uint32_t)a1);
+  } else {
     const u128 sq = (u128)a0 * a0 + (u128)a1 * a1;
     hi = (uint64_t)(sq >> 64);
     lo = (uint64_t)sq;
+    wave_sum_u128_full(hi, lo, bad);   // every reduction here runs on the full wave
   }
-  int bad = 0;
-  wave_sum_u128_full(hi, lo, bad);   // every reduction here runs on the full wave
   uint64_t rms = 0;
   if (!bad) {
     const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)a.hd);
-    if (mean <= ~(u128)0 - (u128)(uint64_t)a.eps) rms = isqrt_u128(mean + (u128)(uint64_t)a.eps);
+    if (mean <= ~(u128)0 - (u128)(uint64_t)a.eps) rms = isqrt_u128_fast(mean + (u128)(uint64_t)a.eps);
   }
   if (rms == 0) {
     if (j == 0) atomicOr(a.status, IMIE_ERMS);
     if (j == 0 && a.gpart) { a.gpart[(r * (a.H + a.Hkv) + h) * 2] = 0; a.gpart[(r * (a.H + a.Hkv) + h) * 2 + 1] = 0; }
     return;
   }
-  const uint64_t rinv = recip_u64(rms);
+  // n in double precision where exact; the integer routine (and its reciprocal) only if some lane needs it
+  const double rd = (double)rms, rid = 1.0 / rd;
+  int64_t n0 = 0, n1 = 0;
+  const bool q0 = !act || norm_elem_f64(x0, a.frac, rms, rd, rid, &n0);
+  const bool q1 = !act || norm_elem_f64(x1, a.frac, rms, rd, rid, &n1);
   bool f0 = true, f1 = true;
-  const int64_t n0 = act ? norm_elem(x0, a.frac, rms, rinv, &f0) : 0;
-  const int64_t n1 = act ? norm_elem(x1, a.frac, rms, rinv, &f1) : 0;
-  const bool ok = imie_wave_max_u64_full((f0 && f1) ? 0 : 1) == 0;
+  if (__any((q0 && q1) ? 0 : 1)) {
+    const uint64_t rinv = recip_u64(rms);
+    if (!q0) n0 = norm_elem(x0, a.frac, rms, rinv, &f0);
+    if (!q1) n1 = norm_elem(x1, a.frac, rms, rinv, &f1);
+  }
+  const bool ok = __all((f0 && f1) ? 1 : 0) != 0;
   uint64_t mxn = imie_absu64(n0) > imie_absu64(n1) ? imie_absu64(n0) : imie_absu64(n1);
   uint64_t mxg = imie_absu64(g0) > imie_absu64(g1) ? imie_absu64(g0) : imie_absu64(g1);
   mxn = imie_wave_max_u64_full(mxn);
@@ -64,8 +88,6 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   }
   const int64_t y0 = imie_floor_shift((int64_t)((uint64_t)n0 * (uint64_t)g0), a.frac);
   const int64_t y1 = imie_floor_shift((int64_t)((uint64_t)n1 * (uint64_t)g1), a.frac);
-  const int64_t p = a.pos[r];
-  const int64_t c = act ? a.cos[p * half + j] : 0, s = act ? a.sin[p * half + j] : 0;
   const int64_t o0 = (int64_t)((uint64_t)y0 * (uint64_t)c - (uint64_t)y1 * (uint64_t)s) >> a.frac;
   const int64_t o1 = (int64_t)((uint64_t)y0 * (uint64_t)s + (uint64_t)y1 * (uint64_t)c) >> a.frac;
   {
@@ -108,11 +130,6 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     }
     return;
   }
-  const int64_t kvh = h - a.H, b = r / a.M;
-  const uint32_t pq = (uint32_t)p / (uint32_t)a.P;              // positions are below 2^31
-  const int64_t pg = a.pt[b * a.mp + pq], slot = (uint32_t)p - pq * (uint32_t)a.P;
-  const int64_t* vr = a.v + (r * a.Hkv + kvh) * a.hd;
-  const int64_t v0 = act ? vr[j] : 0, v1 = act ? vr[j + half] : 0;
   if (KV8) {
     uint64_t mk = imie_absu64(o0) > imie_absu64(o1) ? imie_absu64(o0) : imie_absu64(o1);
     uint64_t mv = imie_absu64(v0) > imie_absu64(v1) ? imie_absu64(v0) : imie_absu64(v1);

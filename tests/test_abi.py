@@ -73,6 +73,49 @@ def test_exact_norm_helpers_host():
             assert so.imie_fx_div_u128(v >> 64, v & ((1 << 64) - 1), d) == (v // d) & ((1 << 64) - 1), (v, d)
 
 
+def test_prologue_short_paths_host():
+    """The double-precision short paths of the single-token matvec prologue against exact integer arithmetic: the
+    isqrt below 2^52 (perfect squares and their neighbours up to the bound), n = floor((x << f) / rms) with the
+    oracle's floor toward -inf (exact multiples, remainders of rms - 1, the edges of the bounds), and the
+    one-exponential SiLU * up against the two-exponential form and the numpy oracle (fixedpoint.py:89-117)."""
+    import math
+    from oracle import fixedpoint as fx
+    so = _lib.lib()
+    rng = np.random.default_rng(11)
+    vals = [0, 1, 2, 3, (1 << 52) - 1, (1 << 52), (1 << 60) + 5, (1 << 100) + 3]
+    for r in [1, 2, 3, 1 << 13, (1 << 26) - 1, 1 << 26, 67108863, 94906265]:
+        vals += [r * r - 1, r * r, r * r + 1]
+    vals += [int(v) for v in rng.integers(0, 1 << 52, size=400)]
+    for v in vals:
+        if v >= 0:
+            assert so.imie_fx_isqrt_fast(v >> 64, v & ((1 << 64) - 1)) == math.isqrt(v), v
+    out = ctypes.c_int64()
+    cases = []
+    for frac in (1, 8, 16, 29):
+        lim = 1 << (53 - frac)
+        for rms in [1, 2, 3, 7, 65535, 65536, 1 << 26, (1 << 33) + 1, (1 << 51) - 1, 1 << 51]:
+            xs = [0, 1, -1, lim - 1, -(lim - 1), lim, -lim, rms, -rms, 2 * rms - 1, -(2 * rms - 1)]
+            xs += [int(v) for v in rng.integers(-lim, lim, size=60)]
+            cases += [(x, frac, rms) for x in xs]
+    fast = 0
+    for x, frac, rms in cases:
+        rc = so.imie_fx_norm_f64(x, frac, rms, ctypes.byref(out))
+        inside = abs(x) < (1 << (53 - frac)) and rms < (1 << 51)
+        assert rc == (1 if inside else 0), (x, frac, rms)
+        if rc == 1:
+            fast += 1
+            assert out.value == (x << frac) // rms, (x, frac, rms)
+    assert fast > 1000
+    for frac in (8, 16, 24, 29):
+        g = np.concatenate([rng.integers(-(1 << 40), 1 << 40, size=300), rng.integers(-(1 << 20), 1 << 20, size=300),
+                            np.array([0, 1, -1, (1 << 63) - 1, -(1 << 63), -(1 << 63) + 1, 1 << frac, -(1 << frac)])])
+        u = rng.integers(-(1 << 30), 1 << 30, size=g.size)
+        want = fx.mulshift_wrap(fx.silu_wrap(g.astype(np.int64), frac), u.astype(np.int64), frac)
+        for gi, ui, wi in zip(g.tolist(), u.tolist(), want.tolist()):
+            assert so.imie_silu_mul_host(gi, ui, frac, 1) == wi, (gi, ui, frac)
+            assert so.imie_silu_mul_host(gi, ui, frac, 0) == wi, (gi, ui, frac)
+
+
 def test_exports_every_symbol_the_reference_nmc_loader_requires():
     """north-mini-code/src/nmc/qk_cuda.py:39-72 (_REQUIRED_CUDA_SYMBOLS) and the ABI version it checks (:22, 83-92):
     the reference bridge binds this library unchanged."""
