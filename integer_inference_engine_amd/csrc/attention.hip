@@ -469,28 +469,36 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
   __shared__ uint64_t s_z[4][REP];
   const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t rows = d.B * d.H;
-  const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // requested before the sequence length arrives (none of them depends on it): this thread's scores (chunks of
+  // up to 256 keys; the row stride Lmax bounds the index, keys past the length are masked below) and the first
+  // 64 chunk maxima of the rows this wave reduces (an empty chunk's maximum is INT64_MIN)
+  const bool one = d.chunk <= 256;
+  const int64_t jt = j0 + threadIdx.x;
+  int64_t sv[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) sv[r] = (one && jt < d.Lmax) ? d.scores[(b * d.H + kv * REP + r) * d.Lmax + jt] : 0;
+  constexpr int RW = (REP + 3) / 4;
+  int64_t cm[RW];
+#pragma unroll
+  for (int k = 0; k < RW; ++k) {
+    const int r = wave + 4 * k;
+    cm[k] = (r < REP && lane < d.nch) ? d.cmax[(int64_t)lane * rows + b * d.H + kv * REP + r] : INT64_MIN;
+  }
+  const int64_t L = dec_len(d, b);
   if (j0 >= L) {
     if (threadIdx.x < REP) d.cz[blockIdx.y * rows + b * d.H + kv * REP + threadIdx.x] = 0;
     return;
   }
-  // chunks of up to 256 keys (single-sequence decode): this thread's scores are requested before the row-max
-  // reduction that they do not depend on
   const int64_t jend = min(j0 + d.chunk, L);
-  const bool one = d.chunk <= 256;
-  int64_t sv[REP];
+  // row max over all chunks (wave r reduces row r)
 #pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    const int64_t j = j0 + threadIdx.x;
-    sv[r] = (one && j < jend) ? d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] : 0;
-  }
-  // row max over the chunks that hold keys (wave r reduces row r)
-  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
-  for (int r = wave; r < REP; r += 4) {
-    int64_t m = INT64_MIN;
-    for (int64_t c = lane; c < nlive; c += 64) {
+  for (int k = 0; k < RW; ++k) {
+    const int r = wave + 4 * k;
+    if (r >= REP) break;
+    int64_t m = cm[k];
+    for (int64_t c = lane + 64; c < d.nch; c += 64) {
       const int64_t v = d.cmax[c * rows + b * d.H + kv * REP + r];
       m = v > m ? v : m;
     }
@@ -648,66 +656,67 @@ __global__ __launch_bounds__(256) void dec_pv_kernel(AttnDesc d) {
 }
 
 // WG = 32 consecutive outputs (within one row) x 8 chunk groups: thread (o, g) sums chunks g, g + 8, ... of
-// output o (all loads issued together), the 8 group sums are added through LDS. The first WG of a row also
-// reduces the chunk maxima for the bound checks (same split).
+// output o over all nch chunks (an empty chunk's partials are zero, so no sequence length is needed first; the
+// loads of a round are all issued before any is added), and the 8 group sums are added through LDS. The bound
+// checks run in separate workgroups at the end of the grid, alongside the sums: one wave per row reads the
+// row's chunk maxima (lane c: chunk c, c + 64, ...), the sequence length and the K / V maxima at once.
 __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
   __shared__ uint64_t s_sum[8][32];
-  __shared__ uint64_t s_mx[3][8];
   const int t = threadIdx.x, o = t & 31, g = t >> 5;
-  const int64_t i = (int64_t)blockIdx.x * 32 + o;
   const int64_t rows = d.B * d.H;
+  const int64_t nsum = (rows * d.hd + 31) / 32;
+  if ((int64_t)blockIdx.x >= nsum) {
+    const int lane = t & 63;
+    const int64_t r = ((int64_t)blockIdx.x - nsum) * 4 + (t >> 6);
+    if ((int64_t)blockIdx.x == nsum && t == 0) check_rope_guard(d);
+    if (r >= rows) return;
+    const int64_t b = imie_udiv32(r, d.H), kv = imie_udiv32(imie_umod32(r, d.H), d.H / d.Hkv);
+    const int64_t bkv = b * d.Hkv + kv;
+    const int64_t L = dec_len(d, b);
+    const uint64_t mq = d.maxq[r];
+    const uint64_t rk = d.run_k ? d.run_k[bkv] : 0, rv = d.run_k ? d.run_v[bkv] : 0;
+    uint64_t mp = 0, mv = 0, mk = 0;
+    for (int64_t c0 = 0; c0 < d.nch; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const bool in = c < d.nch;
+      const uint64_t a = in ? d.cmp[c * rows + r] : 0;
+      const uint64_t v = (in && !d.run_k) ? d.cvm[c * d.B * d.Hkv + bkv] : 0;
+      const uint64_t k = (in && !d.run_k) ? d.ckm[c * d.B * d.Hkv + bkv] : 0;
+      mp = a > mp ? a : mp;
+      mv = v > mv ? v : mv;
+      mk = k > mk ? k : mk;
+    }
+    mp = imie_wave_max_u64_full(mp);
+    if (d.run_k) { mk = rk; mv = rv; }
+    else { mv = imie_wave_max_u64_full(mv); mk = imie_wave_max_u64_full(mk); }
+    if (lane == 0 && L > 0) {
+      if ((u128)mp * mv > (u128)(INT64_MAX / L)) atomicOr(d.status, IMIE_EOVF);
+      if ((u128)mq * mk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+    }
+    return;
+  }
+  const int64_t i = (int64_t)blockIdx.x * 32 + o;
   const int64_t r = imie_udiv32((int64_t)blockIdx.x * 32, d.hd);
-  const int64_t b = imie_udiv32(r, d.H), kv = imie_udiv32(imie_umod32(r, d.H), d.H / d.Hkv);
-  const int64_t L = dec_len(d, b);
-  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
   const int64_t stride = rows * d.hd;
-  // rounds of 8 chunks per thread with every load of a round issued before any is added (a loop-carried sum
-  // over single loads would wait for each in turn); the bound maxima of the first workgroup of a row ride along
-  const bool head = imie_umod32((int64_t)blockIdx.x * 32, d.hd) == 0;
-  const bool mx_lane = head && o == 0;
-  uint64_t acc = 0, mp = 0, mv = 0, mk = 0;
   const bool live_o = i < rows * d.hd;
-  for (int64_t c0 = g; c0 < nlive; c0 += 64) {
-    uint64_t pv[8], ap[8], av[8], ak[8];
+  uint64_t acc = 0;
+  for (int64_t c0 = g; c0 < d.nch; c0 += 64) {
+    uint64_t pv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int64_t c = c0 + 8 * u;
-      const bool in = c < nlive;
-      pv[u] = (in && live_o) ? d.part[c * stride + i] : 0;
-      ap[u] = (in && mx_lane) ? d.cmp[c * rows + r] : 0;
-      av[u] = (in && mx_lane && !d.run_k) ? d.cvm[c * d.B * d.Hkv + b * d.Hkv + kv] : 0;
-      ak[u] = (in && mx_lane && !d.run_k) ? d.ckm[c * d.B * d.Hkv + b * d.Hkv + kv] : 0;
+      pv[u] = (c < d.nch && live_o) ? d.part[c * stride + i] : 0;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc += pv[u];
-      mp = ap[u] > mp ? ap[u] : mp;
-      mv = av[u] > mv ? av[u] : mv;
-      mk = ak[u] > mk ? ak[u] : mk;
-    }
+    for (int u = 0; u < 8; ++u) acc += pv[u];
   }
   s_sum[g][o] = acc;
-  if (mx_lane) { s_mx[0][g] = mp; s_mx[1][g] = mv; s_mx[2][g] = mk; }
   __syncthreads();
-  if (blockIdx.x == 0 && t == 0) check_rope_guard(d);
-  if (t < 32 && i < rows * d.hd) {
+  if (t < 32 && live_o) {
     uint64_t tot = 0;
 #pragma unroll
     for (int gg = 0; gg < 8; ++gg) tot += s_sum[gg][t];
     d.out[qoff(d, r) + imie_umod32(i, d.hd)] = (int64_t)tot >> d.frac;
-  }
-  if (head && t == 0 && L > 0) {
-    mp = 0; mv = 0; mk = 0;
-    for (int gg = 0; gg < 8; ++gg) {
-      mp = s_mx[0][gg] > mp ? s_mx[0][gg] : mp;
-      mv = s_mx[1][gg] > mv ? s_mx[1][gg] : mv;
-      mk = s_mx[2][gg] > mk ? s_mx[2][gg] : mk;
-    }
-    if (d.run_k) { mk = d.run_k[b * d.Hkv + kv]; mv = d.run_v[b * d.Hkv + kv]; }
-    const u128 pv = (u128)mp * mv;
-    if (pv > (u128)(INT64_MAX / L)) atomicOr(d.status, IMIE_EOVF);
-    const u128 qk = (u128)d.maxq[r] * mk;
-    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
   }
 }
 
@@ -783,9 +792,9 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   const int64_t jend = min(j0 + d.chunk, L);
   const int8_t* Kb = (const int8_t*)d.K;
   // 16-key tiles t = j0 + 16 wave + 64 i; the next tile's K slices are loaded before this tile's MFMAs
-  auto load_tile = [&](int64_t t, v4i (&bk)[4][2]) {
+  auto load_tile = [&](int64_t t, int64_t lim, v4i (&bk)[4][2]) {   // keys below lim (masked later by jend)
     const int64_t j = t + m;
-    const bool valid = j < jend;
+    const bool valid = j < lim;
     int64_t base = 0, slot = 0;
     if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
 #pragma unroll
@@ -824,7 +833,10 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   };
   v4i bkA[4][2], bkB[4][2];
   int64_t t = j0 + 16 * wave;
-  if (t < jend) load_tile(t, bkA);          // the first K tile in flight during the q setup
+  // the first K tile in flight during the q setup, bounded by the score row stride rather than the sequence length
+  // (no wait for the length): keys past it give scores that are never stored
+  const int64_t lim0 = min(j0 + d.chunk, d.Lmax);
+  if (t < lim0) load_tile(t, lim0, bkA);
   if (d.qd) {
     // digits prepared by the head stage (all eight limb planes written): A operands straight from memory, loaded
     // together with the limb counts and masked once those arrive
@@ -893,11 +905,11 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   LB = (Lq + 3) / 4;
   while (t < jend) {
     const int64_t t2 = t + 64;
-    if (t2 < jend) load_tile(t2, bkB);
+    if (t2 < jend) load_tile(t2, jend, bkB);
     score_tile(t, bkA);
     if (t2 >= jend) break;
     const int64_t t3 = t2 + 64;
-    if (t3 < jend) load_tile(t3, bkA);
+    if (t3 < jend) load_tile(t3, jend, bkA);
     score_tile(t2, bkB);
     t = t3;
   }
@@ -925,25 +937,19 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   __shared__ __align__(16) int8_t sPd[RBH][16][64];
   __shared__ uint64_t s_z[REP], s_rz[REP], s_mp[4][REP];
   const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
-  const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
   const int64_t rows = d.B * d.H;
   uint64_t* part = d.part + (int64_t)blockIdx.y * rows * d.hd;
-  if (j0 >= L) {
-    for (int i = tid; i < REP * d.hd; i += blockDim.x)
-      part[(b * d.H + kv * REP + imie_udiv32(i, d.hd)) * d.hd + imie_umod32(i, d.hd)] = 0;
-    if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
-    return;
-  }
-  const int64_t jend = min(j0 + d.chunk, L);
   const int DT = (int)(d.hd / 16);
   const int8_t* Vb = (const int8_t*)d.V;
   // one 64-key step's operands: the V slices of this wave's dim tiles and the scores of thread (key tid % 64,
-  // heads tid / 64 + 4k); the first step's are requested before the Z reduction, later ones a step ahead
+  // heads tid / 64 + 4k), bounded by `lim` (keys past the sequence length are masked where p is formed); the
+  // first step's, and the chunk Z sums (an empty chunk's is 0), are requested before the sequence length is
+  // known, later steps' one step ahead
   constexpr int RW = (REP + 3) / 4;
-  auto load_step = [&](int64_t t0, v4i (&bv)[2][4], int64_t (&sc)[RW]) {
-    const int64_t tn = min((int64_t)64, jend - t0);
+  auto load_step = [&](int64_t t0, int64_t lim, v4i (&bv)[2][4], int64_t (&sc)[RW]) {
+    const int64_t tn = min((int64_t)64, lim - t0);
     int64_t pi, slot0;
     page_split(d, t0, pi, slot0);
     const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
@@ -964,11 +970,27 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   };
   v4i bvA[2][4], bvB[2][4];
   int64_t scA[RW], scB[RW];
-  load_step(j0, bvA, scA);
-  const int64_t nlive = imie_udiv32(L + d.chunk - 1, d.chunk);
-  for (int r = wave; r < REP; r += 4) {
-    uint64_t z = 0;
-    for (int64_t c = lane; c < nlive; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
+  load_step(j0, d.Lmax, bvA, scA);
+  uint64_t cz0[RW];
+#pragma unroll
+  for (int k = 0; k < RW; ++k) {
+    const int r = wave + 4 * k;
+    cz0[k] = (r < REP && lane < d.nch) ? d.cz[(int64_t)lane * rows + b * d.H + kv * REP + r] : 0;
+  }
+  const int64_t L = dec_len(d, b);
+  if (j0 >= L) {
+    for (int i = tid; i < REP * d.hd; i += blockDim.x)
+      part[(b * d.H + kv * REP + imie_udiv32(i, d.hd)) * d.hd + imie_umod32(i, d.hd)] = 0;
+    if (tid < REP) d.cmp[blockIdx.y * rows + b * d.H + kv * REP + tid] = 0;
+    return;
+  }
+  const int64_t jend = min(j0 + d.chunk, L);
+#pragma unroll
+  for (int k = 0; k < RW; ++k) {
+    const int r = wave + 4 * k;
+    if (r >= REP) break;
+    uint64_t z = cz0[k];
+    for (int64_t c = lane + 64; c < d.nch; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
     if (lane == 0) { s_z[r] = z; s_rz[r] = z > 1 ? (~(uint64_t)0) / z : 0; }
@@ -995,7 +1017,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
 #pragma unroll
     for (int k = 0; k < RW; ++k) scv[k] = scA[k];
     if (t0 + 64 < jend) {
-      load_step(t0 + 64, bvB, scB);
+      load_step(t0 + 64, jend, bvB, scB);
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -1680,7 +1702,8 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
 #undef IMIE_DEC_R
 #undef IMIE_DEC
     IMIE_HIP(hipGetLastError());
-    hipLaunchKernelGGL(dec_final_kernel, dim3((unsigned)((rows * d.hd + 31) / 32)), dim3(256), 0, st, d);
+    hipLaunchKernelGGL(dec_final_kernel, dim3((unsigned)((rows * d.hd + 31) / 32 + (rows + 3) / 4)), dim3(256), 0, st,
+                       d);
     IMIE_HIP(hipGetLastError());
     imie_prof_mark(IMIE_K_ATTN, st, false);
     return IMIE_OK;
