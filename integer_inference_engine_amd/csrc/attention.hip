@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // requested before the sequence length arrives (none of them depends on it): this thread's scores (chunks of
   // up to 256 keys; the row stride Lmax bounds the index, keys past the length are masked below) and the first
-  // 64 chunk maxima of the rows this wave reduces (an empty chunk's maximum is INT64_MIN)
+  // 128 chunk maxima of the rows this wave reduces, two per lane (an empty chunk's maximum is INT64_MIN)
   const bool one = d.chunk <= 256;
   const int64_t jt = j0 + threadIdx.x;
   int64_t sv[REP];
@@ -484,7 +484,10 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
 #pragma unroll
   for (int k = 0; k < RW; ++k) {
     const int r = wave + 4 * k;
-    cm[k] = (r < REP && lane < d.nch) ? d.cmax[(int64_t)lane * rows + b * d.H + kv * REP + r] : INT64_MIN;
+    const int64_t a0 = (r < REP && lane < d.nch) ? d.cmax[(int64_t)lane * rows + b * d.H + kv * REP + r] : INT64_MIN;
+    const int64_t a1 =
+        (r < REP && lane + 64 < d.nch) ? d.cmax[(int64_t)(lane + 64) * rows + b * d.H + kv * REP + r] : INT64_MIN;
+    cm[k] = a0 > a1 ? a0 : a1;
   }
   const int64_t L = dec_len(d, b);
   if (j0 >= L) {
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     const int r = wave + 4 * k;
     if (r >= REP) break;
     int64_t m = cm[k];
-    for (int64_t c = lane + 64; c < d.nch; c += 64) {
+    for (int64_t c = lane + 128; c < d.nch; c += 64) {
       const int64_t v = d.cmax[c * rows + b * d.H + kv * REP + r];
       m = v > m ? v : m;
     }
@@ -676,15 +679,22 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
     const uint64_t mq = d.maxq[r];
     const uint64_t rk = d.run_k ? d.run_k[bkv] : 0, rv = d.run_k ? d.run_v[bkv] : 0;
     uint64_t mp = 0, mv = 0, mk = 0;
-    for (int64_t c0 = 0; c0 < d.nch; c0 += 64) {
-      const int64_t c = c0 + lane;
-      const bool in = c < d.nch;
-      const uint64_t a = in ? d.cmp[c * rows + r] : 0;
-      const uint64_t v = (in && !d.run_k) ? d.cvm[c * d.B * d.Hkv + bkv] : 0;
-      const uint64_t k = (in && !d.run_k) ? d.ckm[c * d.B * d.Hkv + bkv] : 0;
-      mp = a > mp ? a : mp;
-      mv = v > mv ? v : mv;
-      mk = k > mk ? k : mk;
+    for (int64_t c0 = 0; c0 < d.nch; c0 += 128) {
+      uint64_t a[2], v[2], k[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t c = c0 + 64 * h + lane;
+        const bool in = c < d.nch;
+        a[h] = in ? d.cmp[c * rows + r] : 0;
+        v[h] = (in && !d.run_k) ? d.cvm[c * d.B * d.Hkv + bkv] : 0;
+        k[h] = (in && !d.run_k) ? d.ckm[c * d.B * d.Hkv + bkv] : 0;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        mp = a[h] > mp ? a[h] : mp;
+        mv = v[h] > mv ? v[h] : mv;
+        mk = k[h] > mk ? k[h] : mk;
+      }
     }
     mp = imie_wave_max_u64_full(mp);
     if (d.run_k) { mk = rk; mv = rv; }
@@ -700,15 +710,15 @@ __global__ __launch_bounds__(256) void dec_final_kernel(AttnDesc d) {
   const int64_t stride = rows * d.hd;
   const bool live_o = i < rows * d.hd;
   uint64_t acc = 0;
-  for (int64_t c0 = g; c0 < d.nch; c0 += 64) {
-    uint64_t pv[8];
+  for (int64_t c0 = g; c0 < d.nch; c0 += 128) {
+    uint64_t pv[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 16; ++u) {
       const int64_t c = c0 + 8 * u;
       pv[u] = (c < d.nch && live_o) ? d.part[c * stride + i] : 0;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc += pv[u];
+    for (int u = 0; u < 16; ++u) acc += pv[u];
   }
   s_sum[g][o] = acc;
   __syncthreads();
@@ -975,7 +985,9 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
 #pragma unroll
   for (int k = 0; k < RW; ++k) {
     const int r = wave + 4 * k;
-    cz0[k] = (r < REP && lane < d.nch) ? d.cz[(int64_t)lane * rows + b * d.H + kv * REP + r] : 0;
+    const uint64_t z0 = (r < REP && lane < d.nch) ? d.cz[(int64_t)lane * rows + b * d.H + kv * REP + r] : 0;
+    const uint64_t z1 = (r < REP && lane + 64 < d.nch) ? d.cz[(int64_t)(lane + 64) * rows + b * d.H + kv * REP + r] : 0;
+    cz0[k] = z0 + z1;
   }
   const int64_t L = dec_len(d, b);
   if (j0 >= L) {
@@ -990,7 +1002,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
     const int r = wave + 4 * k;
     if (r >= REP) break;
     uint64_t z = cz0[k];
-    for (int64_t c = lane + 64; c < d.nch; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
+    for (int64_t c = lane + 128; c < d.nch; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
     if (lane == 0) { s_z[r] = z; s_rz[r] = z > 1 ? (~(uint64_t)0) / z : 0; }

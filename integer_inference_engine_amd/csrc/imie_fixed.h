@@ -78,6 +78,23 @@ __host__ __device__ inline bool norm_elem_f64(int64_t x, int frac, uint64_t rms,
   return true;
 }
 
+// norm_elem_f64 without the bounds test, for callers that have established them (|x| << frac < 2^53, rms < 2^51,
+// 1 <= frac <= 52): the quotient estimate is within 2, so two select-based steps each way settle it (no loop)
+__device__ inline int64_t norm_elem_f64_fast(int64_t x, int frac, double rms_d, double rinv_d) {
+  const uint64_t ax = imie_absu64(x);
+  const double num = (double)(ax << frac);
+  double q = floor(num * rinv_d);
+  double r = fma(-q, rms_d, num);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const bool lo = r < 0.0, hi = r >= rms_d;
+    q += lo ? -1.0 : (hi ? 1.0 : 0.0);
+    r += lo ? rms_d : (hi ? -rms_d : 0.0);
+  }
+  const uint64_t qi = (uint64_t)q;
+  return x < 0 ? -(int64_t)(qi + (r != 0.0 ? 1 : 0)) : (int64_t)qi;
+}
+
 // floor(num / d) for |num| < 2^127 given as sign + 128-bit magnitude, d > 0 (bitwise long division; rare path)
 __device__ inline int64_t floor_div_mag128(bool neg, u128 mag, uint64_t d, bool* fits) {
   u128 q = 0, r = 0;

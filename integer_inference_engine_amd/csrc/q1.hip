@@ -137,14 +137,15 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 // Refusals decided here (block (0, 0) flags the status, every workgroup returns false): ssq of 2^128 or more, or
 // rms == 0. The envelope max|n| * max|gain| <= INT64_MAX is checked per element where n is formed.
 constexpr int kProNormCols = 4096;
+template <int NT>
 __device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, uint64_t& rms) {
   using namespace imie_fx;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int kPer = kProNormCols / 256;
+  constexpr int kPer = kProNormCols / NT;
   int64_t v[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int64_t c = tid + 256 * k;
+    const int64_t c = tid + NT * k;
     const int64_t x = p.x[c < p.cols ? c : 0];       // unconditional loads (no per-element branch)
     v[k] = c < p.cols ? x : 0;
   }
@@ -153,11 +154,11 @@ __device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, ui
   for (int k = 0; k < kPer; ++k) {
     const uint64_t a = imie_absu64(v[k]);
     amax = a > amax ? a : amax;
-    s_x[tid + 256 * k] = v[k];                       // the row on chip for the element phase (after the barrier)
+    s_x[tid + NT * k] = v[k];                       // the row on chip for the element phase (after the barrier)
   }
   uint64_t lm[4];
   if (!__any(amax >> 26 ? 1 : 0)) {
-    // 16 squares below 2^52 per lane, 64 lanes: the wave's sum stays below 2^62
+    // at most 16 squares below 2^52 per lane, 64 lanes: the wave's sum stays below 2^62
     uint64_t sq = 0;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -191,7 +192,12 @@ __device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, ui
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lm[i] = s_red[i] + s_red[4 + i] + s_red[8 + i] + s_red[12 + i];
+  for (int i = 0; i < 4; ++i) {
+    uint64_t t = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) t += s_red[4 * w + i];
+    lm[i] = t;
+  }
   uint64_t hi, lo;
   int bad;
   u128_fold(lm, hi, lo, bad);
@@ -216,11 +222,12 @@ struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) app
 // PRO != kProNone (one token, R = 1, PF > 0, Lcap = 8): no digit table is read; the workgroup derives its slab
 // range's table from the producer's inputs (pro) into LDS -- element values thread-per-element into s_y, then one
 // wave per slab turns them into digits, limb counts and block totals -- while its weights are in flight.
-template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone>
-__global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
+template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone, int NT = 256>
+__global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
     Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
     int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, Q1Pro pro) {
   static_assert(PRO == kProNone || (R == 1 && TT == 1 && PF > 0), "prologue: one token, one tile, prefetched range");
+  static_assert(PRO != kProNone || NT == 256, "NT: workgroup size of the prologue variants");
   extern __shared__ __align__(16) unsigned char smem[];
   uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
@@ -230,7 +237,7 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
   const int64_t nsl = s1 - s0;
 
   // this wave's tile group -> (segment, first tile)
-  const int64_t gi_raw = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t gi_raw = (int64_t)blockIdx.x * (NT / 64) + wave;
   const bool live = gi_raw < sg.gbegin[sg.cnt];
   const int64_t gi = live ? gi_raw : sg.gbegin[sg.cnt] - 1;
   int seg = 0;
@@ -397,75 +404,97 @@ __global__ __launch_bounds__(256) void q1_gemv_mfma_kernel(
     load(0, s0);
   }
   if (PRO != kProNone) {
-    __shared__ uint64_t s_red[24];
-    // the range's inputs, element c0 + threadIdx.x + 256 k for k < 2 nsl, all requested before any use (a
-    // loop over a run-time count would wait for each load in turn)
-    constexpr int KY = PF > 0 ? 2 * PF : 1;
+    __shared__ uint64_t s_red[4 * (NT / 64)];
+    // the range's inputs, element c0 + threadIdx.x + NT k for threadIdx.x + NT k < 512 nsl, all requested before any
+    // use (a loop over a run-time count would wait for each load in turn)
+    constexpr int KY = PF * 512 / NT > 1 ? PF * 512 / NT : 1;
+    const int64_t nel = nsl * 512;
     const int64_t c0 = s0 * 512;
     int64_t ya[KY], yb[KY];
 #pragma unroll
     for (int k = 0; k < KY; ++k) {
-      const int64_t c = c0 + threadIdx.x + 256 * k;
-      const int64_t cc = (k < 2 * nsl && c < pro.cols) ? c : 0;
+      const int64_t c = c0 + threadIdx.x + NT * k;
+      const int64_t cc = (threadIdx.x + NT * k < nel && c < pro.cols) ? c : 0;
       ya[k] = PRO == kProNorm ? 0 : pro.x[cc];
       yb[k] = PRO == kProSiluMul ? pro.x2[cc] : (PRO == kProNorm ? pro.gain[cc] : 0);
     }
     zero_share(pro.zero, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, (int64_t)gridDim.x * gridDim.y, threadIdx.x,
-               256);
+               NT);
     const uint64_t gmax = PRO == kProNorm ? *pro.gmax : 0;
     uint64_t rms = 0;
     if (PRO == kProNorm) {
       __shared__ int64_t s_x[kProNormCols];
-      if (!pro_norm_stats(pro, s_red, s_x, rms)) return;      // the same verdict in every workgroup
+      if (!pro_norm_stats<NT>(pro, s_red, s_x, rms)) return;      // the same verdict in every workgroup
 #pragma unroll
       for (int k = 0; k < KY; ++k) {                          // this range's x from the row staged in LDS
-        const int64_t c = c0 + threadIdx.x + 256 * k;
-        ya[k] = s_x[(k < 2 * nsl && c < pro.cols) ? c : 0];
+        const int64_t c = c0 + threadIdx.x + NT * k;
+        ya[k] = s_x[(threadIdx.x + NT * k < nel && c < pro.cols) ? c : 0];
       }
     }
-    // kProNorm: n = floor((x << f) / rms) in double precision where exact (the integer routine for the rest,
-    // with its reciprocal formed only when some lane needs it), then the envelope per element: |n| * max|gain|
-    // beyond INT64_MAX, or an n outside int64, flags the refusal (the oracle's check over the row's maxima)
-    const double rms_d = (double)rms, rinv_d = 1.0 / rms_d;
-    uint64_t rinv = 0;
-    if (PRO == kProNorm) {
-      bool slow = false;
-#pragma unroll
-      for (int k = 0; k < KY; ++k)
-        slow |= k < 2 * nsl && (pro.frac > 52 || (imie_absu64(ya[k]) >> (53 - pro.frac)) != 0 || (rms >> 51) != 0);
-      if (__any(slow ? 1 : 0)) rinv = imie_fx::recip_u64(rms);
-    }
+    // kProNorm: n = floor((x << f) / rms) in double precision where exact, then y = (n * gain) >> f. A wave whose
+    // elements all meet the bounds of the short path (|x| << f < 2^53, rms < 2^51; |n|, |gain| < 2^31 for the
+    // 32 x 32 -> 64 product) runs it branch-free; any other wave takes the general routine per element (with the
+    // integer division and its reciprocal). Then the envelope per element: |n| * max|gain| beyond INT64_MAX, or an
+    // n outside int64, flags the refusal (the oracle's check over the row's maxima).
     uint64_t nmax = 0;
     bool nfit = true;
+    if (PRO == kProNorm) {
+      const double rms_d = (double)rms, rinv_d = 1.0 / rms_d;
+      // |n| <= |x| * 2^f / rms + 1, so |x| < 2^(30 - f) * rms, i.e. (|x| >> (30 - f)) < rms, keeps |n| below 2^31
+      bool fast = pro.frac >= 1 && pro.frac <= 29 && (rms >> 51) == 0;
 #pragma unroll
-    for (int k = 0; k < KY; ++k) {
-      const int64_t c = c0 + threadIdx.x + 256 * k;
-      if (k >= 2 * nsl) break;
-      int64_t y = 0;
-      if (c < pro.cols) {
-        if (PRO == kProCopy) {
-          y = ya[k];
-        } else if (PRO == kProSiluMul) {
-          y = imie_silu::silu_mul_fast(ya[k], yb[k], pro.frac, pro.log2e, pro.dclip);
-        } else {
-          int64_t nv;
-          if (!imie_fx::norm_elem_f64(ya[k], pro.frac, rms, rms_d, rinv_d, &nv)) {
-            bool f;
-            nv = imie_fx::norm_elem(ya[k], pro.frac, rms, rinv, &f);
-            nfit = nfit && f;
-          }
+      for (int k = 0; k < KY; ++k) {
+        const uint64_t ax = imie_absu64(ya[k]), ag = imie_absu64(yb[k]);
+        fast = fast && (ax >> (53 - pro.frac)) == 0 && (ax >> (30 - pro.frac)) < rms && (ag >> 31) == 0;
+      }
+      if (!__any(fast ? 0 : 1)) {
+#pragma unroll
+        for (int k = 0; k < KY; ++k) {
+          const int64_t c = c0 + threadIdx.x + NT * k;
+          if (threadIdx.x + NT * k >= nel) break;
+          const int64_t nv = imie_fx::norm_elem_f64_fast(ya[k], pro.frac, rms_d, rinv_d);
           const uint64_t an = imie_absu64(nv);
           nmax = an > nmax ? an : nmax;
-          y = imie_floor_shift((int64_t)((uint64_t)nv * (uint64_t)yb[k]), pro.frac);
+          const int64_t prod = (int64_t)(int32_t)nv * (int64_t)(int32_t)yb[k];
+          s_y[threadIdx.x + NT * k] = c < pro.cols ? (prod >> pro.frac) : 0;
+        }
+      } else {
+        const uint64_t rinv = imie_fx::recip_u64(rms);
+#pragma unroll
+        for (int k = 0; k < KY; ++k) {
+          const int64_t c = c0 + threadIdx.x + NT * k;
+          if (threadIdx.x + NT * k >= nel) break;
+          int64_t y = 0;
+          if (c < pro.cols) {
+            int64_t nv;
+            if (!imie_fx::norm_elem_f64(ya[k], pro.frac, rms, rms_d, rinv_d, &nv)) {
+              bool f;
+              nv = imie_fx::norm_elem(ya[k], pro.frac, rms, rinv, &f);
+              nfit = nfit && f;
+            }
+            const uint64_t an = imie_absu64(nv);
+            nmax = an > nmax ? an : nmax;
+            y = imie_floor_shift((int64_t)((uint64_t)nv * (uint64_t)yb[k]), pro.frac);
+          }
+          s_y[threadIdx.x + NT * k] = y;
         }
       }
-      s_y[threadIdx.x + 256 * k] = y;
+    } else {
+#pragma unroll
+      for (int k = 0; k < KY; ++k) {
+        const int64_t c = c0 + threadIdx.x + NT * k;
+        if (threadIdx.x + NT * k >= nel) break;
+        int64_t y = 0;
+        if (c < pro.cols)
+          y = PRO == kProCopy ? ya[k] : imie_silu::silu_mul_fast(ya[k], yb[k], pro.frac, pro.log2e, pro.dclip);
+        s_y[threadIdx.x + NT * k] = y;
+      }
     }
     if (PRO == kProNorm && (!nfit || (unsigned __int128)nmax * gmax > (unsigned __int128)INT64_MAX))
       atomicOr(pro.status, IMIE_ERMS);
     if (threadIdx.x < 8) stage[(int64_t)spk * Lcap * 32 + threadIdx.x] = uint4{0, 0, 0, 0};
     __syncthreads();
-    for (int64_t j = wave; j < nsl; j += 4) {
+    for (int64_t j = wave; j < nsl; j += NT / 64) {
       int64_t v[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) v[q] = s_y[j * 512 + prep_pos(lane, 0, q)];
@@ -1508,11 +1537,16 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
 
 // Single-token matvec whose workgroups build their own digit table from the producer's inputs (Q1Pro). The
 // K-split outputs must already be clear (accumulate == 0: a kernel before this one cleared them) or are added to
-// (accumulate != 0). Slab ranges of spk in {1, 2, 4, 8}: the largest that still leaves at least kProTargetWgs
-// workgroups (the prologue is per workgroup, so fewer, longer workgroups repeat less of it).
-static int q1_pro_target_wgs() {
-  static const int v = [] { const char* e = getenv("IMIE_PRO_WGS"); return e ? atoi(e) : 768; }();   // tuning: 768 measured best for the 8B decode
-  return v;
+// (accumulate != 0). Slab ranges of spk in {1, 2, 4, 8}: the largest that still leaves the target number of
+// workgroups (q1_pro_target_wgs).
+// Workgroups to aim for: a normalising prologue is repeated by every workgroup of a slab range, so RMSNorm launches
+// take fewer, longer workgroups (twice the tile-group count, at least 192; measured on the 8B q/k/v and gate/up
+// shapes), the cheap prologues 768 (IMIE_PRO_WGS overrides, tuning).
+static int64_t q1_pro_target_wgs(int kind, int64_t wg_x) {
+  static const int v = [] { const char* e = getenv("IMIE_PRO_WGS"); return e ? atoi(e) : 0; }();
+  if (v > 0) return v;
+  if (kind == kProNorm) return wg_x * 2 > 192 ? wg_x * 2 : 192;
+  return 768;
 }
 
 static bool q1_pro_shape_ok(const Q1Weight* const* ws, int cnt, int kind, int64_t cols) {
@@ -1540,10 +1574,11 @@ static int q1_apply_pro(const Q1Weight* const* ws, int cnt, const Q1Pro& pro, in
     groups += ws[i]->ntiles;
   }
   sg.gbegin[cnt] = groups;
-  const int64_t wg_x = (groups + 3) / 4;
+  constexpr int NT = 512;                            // 8 waves share one prologue (256 VGPRs per thread: no spills)
+  const int64_t wg_x = (groups + NT / 64 - 1) / (NT / 64);
   int64_t spk = 1;
   for (int64_t c = 8; c >= 2; c >>= 1)
-    if (wg_x * ((nslabs + c - 1) / c) >= q1_pro_target_wgs()) { spk = c; break; }
+    if (wg_x * ((nslabs + c - 1) / c) >= q1_pro_target_wgs(kind, wg_x)) { spk = c; break; }
   if (spk > nslabs) spk = nslabs <= 1 ? 1 : (nslabs <= 2 ? 2 : (nslabs <= 4 ? 4 : 8));
   const int64_t ksplit = (nslabs + spk - 1) / spk;
   const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
@@ -1552,7 +1587,7 @@ static int q1_apply_pro(const Q1Weight* const* ws, int cnt, const Q1Pro& pro, in
   const dim3 grid((unsigned)wg_x, (unsigned)ksplit);
   imie_prof_mark(IMIE_K_Q1_GEMV, st, true);
 #define IMIE_Q1_PRO(PF_, PRO_)                                                                                 \
-  hipLaunchKernelGGL((q1_gemv_mfma_kernel<false, 1, 1, PF_, PRO_>), grid, dim3(256), lds, st, sg, nullptr,     \
+  hipLaunchKernelGGL((q1_gemv_mfma_kernel<false, 1, 1, PF_, PRO_, NT>), grid, dim3(NT), lds, st, sg, nullptr,   \
                      nullptr, nullptr, nslabs, nbp, 1, fr, spk, 8, mode, pro)
 #define IMIE_Q1_PRO_K(PF_)                                                                                     \
   if (kind == kProCopy) IMIE_Q1_PRO(PF_, kProCopy);                                                           \
