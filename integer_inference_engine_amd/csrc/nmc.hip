@@ -80,16 +80,16 @@ struct Item {               // one weight applied to `count` x rows
 
 // y[yi[p]][o] = floor(W[o] . x[xi[p]] / 2^fw) for the pairs of one item.
 // run_gate (nullable): the launch runs only when *run_gate != 0 (the MFMA path found activations it cannot take)
-__global__ __launch_bounds__(256) void qk_group_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
-                                                       const int* __restrict__ yi, const int64_t* __restrict__ X,
-                                                       int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
-                                                       int* __restrict__ status, const int* __restrict__ run_gate) {
+// One (64-row tile bx, item by) of the exact int128 kernel; every thread of the workgroup calls it with the same
+// (bx, by).
+__device__ void qk_group_tile(const Item* __restrict__ items, const int* __restrict__ xi, const int* __restrict__ yi,
+                              const int64_t* __restrict__ X, int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
+                              int* __restrict__ status, int64_t bx, int64_t by) {
   __shared__ int64_t sx[kXRows][257];
   __shared__ int s_wide;
-  if (run_gate && *run_gate == 0) return;
-  const Item it = items[blockIdx.y];
-  const int64_t o = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 2);
-  if ((int64_t)blockIdx.x * kRows >= it.out_f) return;
+  const Item it = items[by];
+  const int64_t o = bx * kRows + (threadIdx.x >> 2);
+  if (bx * kRows >= it.out_f) return;
   const int slot = threadIdx.x & 3;
   const bool live = o < it.out_f;
   const int bs = it.qtype == 0 ? 144 : 210;
@@ -198,6 +198,29 @@ __global__ __launch_bounds__(256) void qk_group_kernel(const Item* __restrict__ 
   }
 }
 
+__global__ __launch_bounds__(256) void qk_group_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
+                                                       const int* __restrict__ yi, const int64_t* __restrict__ X,
+                                                       int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
+                                                       int* __restrict__ status, const int* __restrict__ run_gate) {
+  if (run_gate && *run_gate == 0) return;
+  qk_group_tile(items, xi, yi, X, K, Y, ldy, fw, status, blockIdx.x, blockIdx.y);
+}
+
+// The exact kernel as the fallback of a fused MoE stage: a small grid that ends at once unless the prep flagged a
+// wide activation row (*run_gate != 0); then its workgroups walk all (tile, item) pairs, ntx tiles per item.
+constexpr int kGatedWgs = 128;
+__global__ __launch_bounds__(256) void qk_group_gated_kernel(const Item* __restrict__ items, const int* __restrict__ xi,
+                                                             const int* __restrict__ yi, const int64_t* __restrict__ X,
+                                                             int64_t K, int64_t* __restrict__ Y, int64_t ldy, int fw,
+                                                             int* __restrict__ status, const int* __restrict__ run_gate,
+                                                             int64_t ntx, int64_t ne) {
+  if (*run_gate == 0) return;
+  for (int64_t t = blockIdx.x; t < ntx * ne; t += gridDim.x) {
+    qk_group_tile(items, xi, yi, X, K, Y, ldy, fw, status, t % ntx, t / ntx);
+    __syncthreads();                                  // the tile's shared buffers are free for the next one
+  }
+}
+
 // nmc SiLU*up: g <- ((g * sigmoid(g)) >> fa) exactly, then gu = (g * u) >> fa exactly (cohere2.py:109-111,
 // :183-185); sigmoid without the (1<<62)/log2e cap (north-mini-code/src/nmc/_bonsai/fixedpoint.py:148).
 __device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
@@ -220,8 +243,7 @@ __global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t*
                                    int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status,
                                    const int* __restrict__ run_gate = nullptr) {
   if (run_gate && *run_gate == 0) return;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
   const int64_t x = g[i];
   const int64_t m = x > 0 ? x : 0;
   int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
@@ -236,6 +258,7 @@ __global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t*
   const i128 gu = ((i128)(int64_t)s * u[i]) >> fa;
   if (gu > (i128)INT64_MAX || gu < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
   out[i] = (int64_t)gu;
+  }
 }
 
 // out[t][o] = sum_j (dd[t*k + j][o] * gates[t*k + j]) >> fa (exact; cohere2.py:187 then astype int64)
@@ -619,6 +642,12 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
 // ---------------------------------------------------------------------------------------------------------
 constexpr int kMoeTok = 4;         // tokens per MFMA row group (4 tokens x 4 limbs = 16 rows)
 constexpr int kMoeLimbs = 8;       // limbs staged (two MFMA row groups); the prep refuses rows beyond kQkLimbs
+// LDS row stride of the staged digits: 256 bytes + 16 of padding. A lane of row r (of the 16 (token, limb) rows)
+// and K group kg reads 8 bytes at r * 272 + 8 kg + 32 j, i.e. 8-byte slot 2 r + kg (mod 32): the 32 lanes of a
+// half-wave hit 32 distinct slots (with a 256-byte stride all 16 rows of a K group shared one slot: 16-way
+// bank conflicts).
+constexpr int kMoeRow = 272;
+constexpr int kMoeBuf = kMoeLimbs * kMoeTok * kMoeRow;
 
 struct MoeItem {
   const uint8_t* wg;        // gate (Q4_K), up (Q4_K), down (Q6_K) of the expert
@@ -683,7 +712,7 @@ __device__ inline MoePlan moe_plan(const int* rowsel, int tn, int L, const int8_
     p.on[k] = i < n;
     const int l = p.on[k] ? i / (tn * 16) : 0, rem = i - l * (tn * 16), t = p.on[k] ? rem >> 4 : 0, c = rem & 15;
     p.src[k] = xd + ((int64_t)l * rows + rowsel[t]) * K + 16 * c;
-    p.dst[k] = (l * kMoeTok + t) * 256 + 16 * c;
+    p.dst[k] = (l * kMoeTok + t) * kMoeRow + 16 * c;
   }
   return p;
 }
@@ -702,24 +731,24 @@ __device__ inline void moe_store(const MoeStage& r, const MoePlan& p, int8_t* bu
     if (p.on[k]) *(uint4*)(buf + p.dst[k]) = r.v[k];
 }
 
-// The lane's A operand source: limb 4 lg + l of token t (row m = 4 t + l of the MFMA), K group kg; `ok` false
-// beyond the group's tokens / limbs (the lane then feeds zeros)
+// The lane's A operand source: limb 4 lg + l of token t (row m = 4 t + l of the MFMA), K group kg. Rows beyond
+// the group's tokens / limbs are zero in LDS (cleared at the start of every token group, never staged), so the
+// lane reads its operand without a select.
 struct MoeA {
   int off;                  // byte offset of [l][t][8 kg] within one LDS buffer
-  bool ok0, ok1;            // limb groups 0 (limbs 0..3) and 1 (limbs 4..7)
 };
-__device__ inline MoeA moe_a_lane(int lane, int tn, int L) {
+__device__ inline MoeA moe_a_lane(int lane) {
   const int m = lane & 15, kg = lane >> 4, t = m >> 2, l = m & 3;
   MoeA r;
-  r.off = (l * kMoeTok + t) * 256 + 8 * kg;
-  r.ok0 = t < tn && l < L;
-  r.ok1 = t < tn && 4 + l < L;
+  r.off = (l * kMoeTok + t) * kMoeRow + 8 * kg;
   return r;
 }
-__device__ inline int64_t moe_a(const int8_t* buf, const MoeA& a, int lg, int p0, bool kon) {
-  const bool ok = (lg ? a.ok1 : a.ok0) && kon;
-  const int64_t v = *(const int64_t*)(buf + a.off + lg * 4 * kMoeTok * 256 + p0);   // always inside the buffer
-  return ok ? v : 0;                                  // a select, not a branch around the load
+__device__ inline int64_t moe_a(const int8_t* buf, const MoeA& a, int lg, int p0) {
+  return *(const int64_t*)(buf + a.off + lg * 4 * kMoeTok * kMoeRow + p0);
+}
+// both staging buffers to zero (threads tid of nt; the caller synchronizes before and after)
+__device__ inline void moe_clear(int8_t* sx, int tid, int nt) {
+  for (int i = tid; i < 2 * kMoeBuf / 16; i += nt) ((uint4*)sx)[i] = uint4{0, 0, 0, 0};
 }
 
 // sum_r T[r] << 8 (4 lg + r): a token's value from its per-limb partial sums (int32 per limb)
@@ -751,39 +780,45 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
   const int64_t dq = fp16_fixed(hb & 0xFFFF, fw), dmq = fp16_fixed(hb >> 16, fw);
   const uint32_t scw[3] = {w.h.y, w.h.z, w.h.w};
   auto scb = [&](int i) { return (int)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
-  int sc[8];
-  int64_t bq[8], bm[8];
+  int sc[8], mn[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int g = j >> 1, hi = j & 1;
-    const uint2 qv = w.q[g];
-    const uint32_t b0 = hi ? (qv.x >> 4) & 0x0F0F0F0Fu : qv.x & 0x0F0F0F0Fu;
-    const uint32_t b1 = hi ? (qv.y >> 4) & 0x0F0F0F0Fu : qv.y & 0x0F0F0F0Fu;
-    bq[j] = (int64_t)(((uint64_t)b1 << 32) | b0);
-    int mn;
-    if (j < 4) { sc[j] = scb(j) & 63; mn = scb(j + 4) & 63; }
-    else { sc[j] = (scb(j + 4) & 0xF) | ((scb(j - 4) >> 6) << 4); mn = (scb(j + 4) >> 4) | ((scb(j) >> 6) << 4); }
-    const uint32_t mb = (uint32_t)mn | ((uint32_t)mn << 8) | ((uint32_t)mn << 16) | ((uint32_t)mn << 24);
-    bm[j] = (int64_t)(((uint64_t)mb << 32) | mb);
+    if (j < 4) { sc[j] = scb(j) & 63; mn[j] = scb(j + 4) & 63; }
+    else { sc[j] = (scb(j + 4) & 0xF) | ((scb(j - 4) >> 6) << 4); mn[j] = (scb(j + 4) >> 4) | ((scb(j) >> 6) << 4); }
   }
+  // sub-block j's weights: the low / high nibbles of q bytes 32 (j / 2) + 8 kg ..; the min term's B operand has
+  // m_j in every byte
+  auto bq = [&](int j) {
+    const uint2 qv = w.q[j >> 1];
+    const uint32_t b0 = (j & 1) ? (qv.x >> 4) & 0x0F0F0F0Fu : qv.x & 0x0F0F0F0Fu;
+    const uint32_t b1 = (j & 1) ? (qv.y >> 4) & 0x0F0F0F0Fu : qv.y & 0x0F0F0F0Fu;
+    return (int64_t)(((uint64_t)b1 << 32) | b0);
+  };
+  auto bm = [&](int j) {
+    const uint32_t mb = __builtin_amdgcn_perm(0u, (uint32_t)mn[j], 0u);   // byte 0 in all four bytes
+    return (int64_t)(((uint64_t)mb << 32) | mb);
+  };
   int64_t S1 = 0, S2 = 0;
 #pragma unroll
   for (int lg = 0; lg < 2; ++lg) {
     if (lg == 1 && !two) break;
-    // the eight sub-block MFMAs are independent: issued back to back, their results consumed afterwards
-    v4i d[8];
-    v4i M = {0, 0, 0, 0};
+    v4i M = {0, 0, 0, 0}, T = {0, 0, 0, 0};
+    // two halves of four sub-blocks: four independent MFMAs issued back to back, their results consumed after
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t av = moe_a(buf, a, lg, 32 * j, true);
-      d[j] = mfma32(av, bq[j], v4i{0, 0, 0, 0});
-      M = mfma32(av, bm[j], M);
+    for (int hh = 0; hh < 2; ++hh) {
+      v4i d[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * hh + jj;
+        const int64_t av = moe_a(buf, a, lg, 32 * j);
+        d[jj] = mfma32(av, bq(j), v4i{0, 0, 0, 0});
+        M = mfma32(av, bm(j), M);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) T[r] += __mul24(sc[4 * hh + jj], d[jj][r]);   // 24-bit: |sc| < 2^6, |D| < 2^17
     }
-    v4i T = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) T[r] += __mul24(sc[j], d[j][r]);   // 24-bit: |sc| < 2^6, |D| < 2^17
     S1 += limb_sum(T, lg);
     S2 += limb_sum(M, lg);
   }
@@ -791,13 +826,13 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
   acc_madd(acc, -dmq, S2);
 }
 
-__global__ __launch_bounds__(256) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
+__global__ __launch_bounds__(256, 3) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
                                                          const int* __restrict__ ppair, const int8_t* __restrict__ xd,
                                                          const int* __restrict__ Lrow, int64_t rows, int64_t K,
                                                          int64_t e_ffn, int fw, int fa, int64_t log2e, int64_t dclip,
                                                          int64_t* __restrict__ gu, int* __restrict__ status,
                                                          const int* __restrict__ wide) {
-  __shared__ __align__(16) int8_t sx[2][kMoeLimbs][kMoeTok][256];
+  __shared__ __align__(16) int8_t sx[2][kMoeBuf];
   __shared__ int s_rows[kMoeTok];
   if (*wide) return;                                  // the VALU fallback takes this call
   const MoeItem it = items[blockIdx.y];
@@ -814,32 +849,36 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(const MoeItem* __restri
     int L = 1;
     for (int i = 0; i < tn; ++i) { const int lr = Lrow[ptok[it.first + t0 + i]]; L = lr > L ? lr : L; }
     __syncthreads();                                  // the previous token group is done with the buffers
+    moe_clear(&sx[0][0], tid, blockDim.x);
     if (tid < tn) s_rows[tid] = ptok[it.first + t0 + tid];
     __syncthreads();
-    const MoeA al = moe_a_lane(lane, tn, L);
-    Q4Lane g0 = q4_lane_load(grow, kg), u0 = q4_lane_load(urow, kg), g1 = g0, u1 = u0;
-    if (nb > 1) { g1 = q4_lane_load(grow + 144, kg); u1 = q4_lane_load(urow + 144, kg); }
+    const MoeA al = moe_a_lane(lane);
+    // one weight slot per projection: block b + 1 is requested as soon as block b has consumed the slot (the
+    // other waves of the SIMD cover the latency; a second slot costs the third wave its registers)
+    Q4Lane gw = q4_lane_load(grow, kg), uw = q4_lane_load(urow, kg);
     const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
-    moe_store(moe_fetch(pl, 0), pl, &sx[0][0][0][0]);
+    moe_store(moe_fetch(pl, 0), pl, &sx[0][0]);
     __syncthreads();
     Acc128 ag{0, 0}, au{0, 0};
     for (int64_t b = 0; b < nb; b += 2) {
-      // even block: LDS buffer 0, weight registers slot 0; block b + 1 is fetched meanwhile
+      // even block: LDS buffer 0; block b + 1's digits are fetched meanwhile
       MoeStage nx{};
       if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
-      q4_block_mfma(g0, &sx[0][0][0][0], al, L > 4, fw, ag);
-      q4_block_mfma(u0, &sx[0][0][0][0], al, L > 4, fw, au);
-      if (b + 2 < nb) { g0 = q4_lane_load(grow + (b + 2) * 144, kg); u0 = q4_lane_load(urow + (b + 2) * 144, kg); }
+      q4_block_mfma(gw, &sx[0][0], al, L > 4, fw, ag);
+      if (b + 1 < nb) gw = q4_lane_load(grow + (b + 1) * 144, kg);
+      q4_block_mfma(uw, &sx[0][0], al, L > 4, fw, au);
+      if (b + 1 < nb) uw = q4_lane_load(urow + (b + 1) * 144, kg);
       if (b + 1 >= nb) break;
-      moe_store(nx, pl, &sx[1][0][0][0]);
+      moe_store(nx, pl, &sx[1][0]);
       __syncthreads();
-      // odd block: LDS buffer 1, slot 1
+      // odd block: LDS buffer 1
       if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
-      q4_block_mfma(g1, &sx[1][0][0][0], al, L > 4, fw, ag);
-      q4_block_mfma(u1, &sx[1][0][0][0], al, L > 4, fw, au);
-      if (b + 3 < nb) { g1 = q4_lane_load(grow + (b + 3) * 144, kg); u1 = q4_lane_load(urow + (b + 3) * 144, kg); }
+      q4_block_mfma(gw, &sx[1][0], al, L > 4, fw, ag);
+      if (b + 2 < nb) gw = q4_lane_load(grow + (b + 2) * 144, kg);
+      q4_block_mfma(uw, &sx[1][0], al, L > 4, fw, au);
+      if (b + 2 < nb) uw = q4_lane_load(urow + (b + 2) * 144, kg);
       if (b + 2 >= nb) break;
-      moe_store(nx, pl, &sx[0][0][0][0]);
+      moe_store(nx, pl, &sx[0][0]);
       __syncthreads();
     }
     if (orow && t < tn) {
@@ -902,7 +941,7 @@ __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const M
         const int64_t bq = (int64_t)(((uint64_t)v1 << 32) | v0);
         const int p0 = 128 * half + 32 * qq;
         // the K step spans sub-blocks 8 half + 2 qq (K groups 0, 1) and + 1 (K groups 2, 3)
-        const int64_t av = moe_a(buf, a, lg, p0, true);
+        const int64_t av = moe_a(buf, a, lg, p0);
         d[qq][0] = mfma32(klo ? av : 0, bq, v4i{0, 0, 0, 0});
         d[qq][1] = mfma32(klo ? 0 : av, bq, v4i{0, 0, 0, 0});
       }
@@ -923,7 +962,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
                                                        const int* __restrict__ Lrow, int64_t rows, int64_t K,
                                                        int64_t d_model, int fw, int64_t* __restrict__ dout,
                                                        int* __restrict__ status, const int* __restrict__ wide) {
-  __shared__ __align__(16) int8_t sx[2][kMoeLimbs][kMoeTok][256];
+  __shared__ __align__(16) int8_t sx[2][kMoeBuf];
   __shared__ int s_rows[kMoeTok];
   if (*wide) return;
   const MoeItem it = items[blockIdx.y];
@@ -938,29 +977,30 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
     const int tn = min(kMoeTok, it.count - t0);
     int L = 1;
     for (int i = 0; i < tn; ++i) { const int lr = Lrow[ppair[it.first + t0 + i]]; L = lr > L ? lr : L; }
-    __syncthreads();
+    __syncthreads();                                  // the previous token group is done with the buffers
+    moe_clear(&sx[0][0], tid, blockDim.x);
     if (tid < tn) s_rows[tid] = ppair[it.first + t0 + tid];
     __syncthreads();
-    const MoeA al = moe_a_lane(lane, tn, L);
+    const MoeA al = moe_a_lane(lane);
     Q6Lane w0 = q6_lane_load(drow, kg), w1 = w0;
     if (nb > 1) w1 = q6_lane_load(drow + 210, kg);
     const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
-    moe_store(moe_fetch(pl, 0), pl, &sx[0][0][0][0]);
+    moe_store(moe_fetch(pl, 0), pl, &sx[0][0]);
     __syncthreads();
     Acc128 ad{0, 0};
     for (int64_t b = 0; b < nb; b += 2) {
       MoeStage nx{};
       if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
-      q6_block_mfma(w0, &sx[0][0][0][0], al, L > 4, kg, fw, ad);
+      q6_block_mfma(w0, &sx[0][0], al, L > 4, kg, fw, ad);
       if (b + 2 < nb) w0 = q6_lane_load(drow + (b + 2) * 210, kg);
       if (b + 1 >= nb) break;
-      moe_store(nx, pl, &sx[1][0][0][0]);
+      moe_store(nx, pl, &sx[1][0]);
       __syncthreads();
       if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
-      q6_block_mfma(w1, &sx[1][0][0][0], al, L > 4, kg, fw, ad);
+      q6_block_mfma(w1, &sx[1][0], al, L > 4, kg, fw, ad);
       if (b + 3 < nb) w1 = q6_lane_load(drow + (b + 3) * 210, kg);
       if (b + 2 >= nb) break;
-      moe_store(nx, pl, &sx[0][0][0][0]);
+      moe_store(nx, pl, &sx[0][0]);
       __syncthreads();
     }
     if (orow && t < tn) {
@@ -1196,20 +1236,20 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
                      d_pt, d_pp, xdp, lrp, (int64_t)m, d_model, e_ffn, fw, fa, log2e, dclip, gb, status, flagA);
   // exact VALU fallback of the gate/up stage (runs only when the prep flagged a wide activation row)
-  const dim3 ggrid((unsigned)((e_ffn + kRows - 1) / kRows), (unsigned)ne);
-  hipLaunchKernelGGL(qk_group_kernel, ggrid, dim3(256), 0, st, d_ig, d_pt, d_pp, h_dev, d_model, gb, e_ffn, fw, status,
-                     flagA);
-  hipLaunchKernelGGL(qk_group_kernel, ggrid, dim3(256), 0, st, d_iu, d_pt, d_pp, h_dev, d_model, ub, e_ffn, fw, status,
-                     flagA);
+  const int64_t ntg = (e_ffn + kRows - 1) / kRows;
+  hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_ig, d_pt, d_pp, h_dev, d_model, gb,
+                     e_ffn, fw, status, flagA, ntg, (int64_t)ne);
+  hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_iu, d_pt, d_pp, h_dev, d_model, ub,
+                     e_ffn, fw, status, flagA, ntg, (int64_t)ne);
   const int64_t n = P * e_ffn;
-  hipLaunchKernelGGL(qk_silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gb, ub, n, fa, log2e,
-                     dclip, gb, status, flagA);
+  hipLaunchKernelGGL(qk_silu_mul_kernel, dim3(kGatedWgs), dim3(256), 0, st, gb, ub, n, fa, log2e, dclip, gb, status,
+                     flagA);
   // down over the P rows of gu
   hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)P), dim3(256), 0, st, gb, P, e_ffn, xdp, xsp, lrp, flagB);
   hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((d_model + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
                      d_pp, xdp, xsp, lrp, P, e_ffn, d_model, fw, db, status, flagB);
-  hipLaunchKernelGGL(qk_group_kernel, dim3((unsigned)((d_model + kRows - 1) / kRows), (unsigned)ne), dim3(256), 0, st,
-                     d_id, d_pp, d_pp, gb, e_ffn, db, d_model, fw, status, flagB);
+  hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_id, d_pp, d_pp, gb, e_ffn, db,
+                     d_model, fw, status, flagB, (int64_t)((d_model + kRows - 1) / kRows), (int64_t)ne);
   hipLaunchKernelGGL(qk_combine_kernel, dim3((unsigned)(((int64_t)m * d_model + 255) / 256)), dim3(256), 0, st, db,
                      m, k, d_model, gates_dev, fa, out_dev, status);
   imie_prof_mark(IMIE_K_QK, st, false);
