@@ -267,23 +267,32 @@ def prefill_leg(so, torch, T: int = 2048) -> dict:
     torch.cuda.set_stream(net.stream)
     x.copy_(x0)
     st = net.forward(x, [0], T)                    # warm-up (sizes workspaces)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    x.copy_(x0)
+    # further untimed forwards for at least 0.25 s, so the timed ones run at the device's sustained clocks
+    t_end = time.perf_counter() + 0.25
+    while time.perf_counter() < t_end:
+        x.copy_(x0)
+        net.forward(x, [0], T)
+        net.stream.synchronize()
+    reps = 5
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     net.stream.synchronize()
     gops = ctypes.c_ulonglong()
     so.imie_profile_gemm_ops(ctypes.byref(gops), 1)
     so.imie_profile_begin()
-    e0.record(net.stream)
-    st = net.forward(x, [0], T)
-    e1.record(net.stream)
+    for e0, e1 in ev:                               # the input copy between forwards is outside the timed spans
+        x.copy_(x0)
+        e0.record(net.stream)
+        st = net.forward(x, [0], T)
+        e1.record(net.stream)
     net.stream.synchronize()
-    ms = e0.elapsed_time(e1)
+    ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / reps
     so.imie_profile_gemm_ops(ctypes.byref(gops), 1)
+    gops.value //= reps
     prof = {}
     for kid, name in ((0, "q1_prep"), (2, "q1_gemm"), (3, "attention")):
         kms, kcnt = ctypes.c_double(), ctypes.c_int64()
         so.imie_profile_read(kid, ctypes.byref(kms), ctypes.byref(kcnt))
-        prof[name + "_ms"] = round(kms.value, 3)
+        prof[name + "_ms"] = round(kms.value / reps, 3)
     so.imie_profile_end()
     net.close()
     so.bonsai_q1_free_weights()
@@ -344,6 +353,10 @@ def moe_leg(so, torch, E: int = 128, k: int = 8, d: int = 2048, e_ffn: int = 768
     so.imie_moe_status(1, sp)
     assert call() == 0
     st.synchronize()
+    t_end = time.perf_counter() + 0.25                 # untimed calls: the timed ones run at sustained clocks
+    while time.perf_counter() < t_end:
+        call()
+        st.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = 5
     e0.record(st)

@@ -18,28 +18,31 @@ __global__ void silu_mul_kernel(const int64_t* __restrict__ gate, const int64_t*
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t g = gate[i];
-  const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
+  const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed_fast(g, frac, log2e, dclip)) >> frac;
   out[i] = up ? (int64_t)((uint64_t)silu * (uint64_t)up[i]) >> frac : silu;
 }
 
-// silu_mul for the GEMM: one wave per (token, 512-slab) computes h at its eight table positions and writes the
-// GEMM digit table directly (the prep of the next projection, without h round-tripping through HBM)
-__global__ __launch_bounds__(64) void silu_mul_gemm_prep_kernel(const int64_t* __restrict__ gate,
-                                                                const int64_t* __restrict__ up, int64_t n, int frac,
-                                                                int64_t log2e, int64_t dclip, imie_q1::GemmPrepOut gp) {
-  const int lane = threadIdx.x;
-  const int64_t sl = blockIdx.x, t = blockIdx.y;
-  int64_t v[8];
+// silu_mul for the GEMM: one wave per (token, 512-slab), four slabs per workgroup, computes h at its eight table
+// positions and writes the GEMM digit table directly (the prep of the next projection, without h round-tripping
+// through HBM). Every gate / up load of the wave is issued before the first product.
+__global__ __launch_bounds__(256) void silu_mul_gemm_prep_kernel(const int64_t* __restrict__ gate,
+                                                                 const int64_t* __restrict__ up, int64_t n, int frac,
+                                                                 int64_t log2e, int64_t dclip,
+                                                                 imie_q1::GemmPrepOut gp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t sl = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
+  if (sl >= gp.nslabs) return;                        // whole wave
+  int64_t gv[8], uv[8], v[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int64_t p = imie_q1::prep_pos(lane, sl, q);
-    v[q] = 0;
-    if (p < n) {
-      const int64_t g = gate[t * n + p];
-      const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
-      v[q] = (int64_t)((uint64_t)silu * (uint64_t)up[t * n + p]) >> frac;
-    }
+    const int64_t pc = p < n ? p : 0;
+    gv[q] = gate[t * n + pc];
+    uv[q] = up[t * n + pc];
   }
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    v[q] = imie_q1::prep_pos(lane, sl, q) < n ? silu_mul_fast(gv[q], uv[q], frac, log2e, dclip) : 0;
   imie_q1::prep_gemm_slab(v, gp, t, sl);
 }
 
@@ -53,9 +56,7 @@ __global__ __launch_bounds__(512) void silu_mul_prep_kernel(const int64_t* __res
   const int64_t p = sl * 512 + threadIdx.x;
   int64_t h = 0;
   if (p < n) {
-    const int64_t g = gate[t * n + p];
-    const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;
-    h = (int64_t)((uint64_t)silu * (uint64_t)up[t * n + p]) >> frac;
+    h = silu_mul_fast(gate[t * n + p], up[t * n + p], frac, log2e, dclip);
     out[t * n + p] = h;
   }
   sh[threadIdx.x] = h;
@@ -220,7 +221,8 @@ int imie_silu_mul_gemm_prep_launch(const int64_t* gate, const int64_t* up, int64
   if (n != gp.nb * 128 || frac < 1 || frac > 62) return IMIE_EARG;
   int64_t log2e, dclip;
   silu_consts(frac, &log2e, &dclip);
-  hipLaunchKernelGGL(silu_mul_gemm_prep_kernel, dim3((unsigned)gp.nslabs, (unsigned)T), dim3(64), 0, st, gate, up, n,
+  hipLaunchKernelGGL(silu_mul_gemm_prep_kernel, dim3((unsigned)((gp.nslabs + 3) / 4), (unsigned)T), dim3(256), 0, st,
+                     gate, up, n,
                      (int)frac, log2e, dclip, gp);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;

@@ -143,10 +143,9 @@ __device__ inline void prep_gemm_slab(int64_t v[8], const GemmPrepOut& gp, int64
     mx = a > mx ? a : mx;
     part = (int64_t)((uint64_t)part + (uint64_t)v[q]);
   }
-  mx = imie_wave_max_u64(mx);
+  mx = imie_wave_max_u64_full(mx);
   const int L = imie_limbs_needed(mx);
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) part = (int64_t)((uint64_t)part + (uint64_t)__shfl_xor(part, o, 64));
+  part = (int64_t)imie_row_sum_u64_full((uint64_t)part);   // block total: the 16 lanes of group g (one DPP row)
   if ((lane & 15) == 0) gp.tg[blk * gp.Tp + t] = part;
   if (lane == 0) gp.lt[t * gp.nslabs + sl] = L;
   const int Lw = L > kGemmNarrowLimbs ? L : kGemmNarrowLimbs;

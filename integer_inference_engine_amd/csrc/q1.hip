@@ -599,9 +599,11 @@ __global__ void q1_linear_simple_kernel(const int64_t* __restrict__ x, const uin
 constexpr int kNarrowLimbs = kGemmNarrowLimbs;
 constexpr int kGemmMaxSlabs = 64;  // K <= 32768
 
-__global__ __launch_bounds__(64) void q1_prep_gemm_kernel(const int64_t* __restrict__ x, int64_t K, GemmPrepOut gp) {
-  const int lane = threadIdx.x;
-  const int64_t sl = blockIdx.x, t = blockIdx.y;
+// one wave per (token, slab), four slabs per workgroup
+__global__ __launch_bounds__(256) void q1_prep_gemm_kernel(const int64_t* __restrict__ x, int64_t K, GemmPrepOut gp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t sl = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
+  if (sl >= gp.nslabs) return;                        // whole wave
   int64_t v[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
@@ -1342,8 +1344,8 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
   const int64_t nslabs = gp.nslabs, nbp = gp.nbp, Tp = gp.Tp;
   if (!prepped) {
     imie_prof_mark(IMIE_K_Q1_PREP, st, true);
-    hipLaunchKernelGGL(q1_prep_gemm_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, w0.nb * 128,
-                       gp);
+    hipLaunchKernelGGL(q1_prep_gemm_kernel, dim3((unsigned)((nslabs + 3) / 4), (unsigned)T), dim3(256), 0, st, x_dev,
+                       w0.nb * 128, gp);
     imie_prof_mark(IMIE_K_Q1_PREP, st, false);
     IMIE_HIP(hipGetLastError());
   }
