@@ -17,6 +17,7 @@ int imie_q1_dims(int64_t handle, int64_t* N, int64_t* nb);
 // into a graph owns one, so no other call can reallocate the buffers the graph points at.
 struct Q1Ws {
   DevBuf xq, totals, lslab;
+  DevBuf wide;                     // GEMM: per 64-token tile, whether any slab needs more than 3 limbs
 };
 // Up to 3 weights with the same n_blocks applied to the same x in one prep + one matvec launch (wk == nullptr:
 // the library's shared workspace).

@@ -186,7 +186,7 @@ void net_free(Net* n) {
   if (n->gexec) { (void)hipGraphExecDestroy(n->gexec); n->gexec = nullptr; }
   DevBuf* bs[] = {&n->n, &n->q, &n->k, &n->v, &n->qn, &n->kn, &n->att, &n->gate, &n->up, &n->h, &n->pos,
                   &n->starts, &n->attn, &n->guard, &n->status, &n->x, &n->logits, &n->ids, &n->lastx, &n->amx,
-                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->kvrun, &n->kvrow, &n->gpart,
+                  &n->stepc, &n->q1w.xq, &n->q1w.totals, &n->q1w.lslab, &n->q1w.wide, &n->kvrun, &n->kvrow, &n->gpart,
                   &n->gtab, &n->gmax};
   for (auto b : bs) b->release();
   n->live = false;

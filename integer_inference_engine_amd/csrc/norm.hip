@@ -95,13 +95,31 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
     hi = nh + cy;
     lo = nl;
   };
+  // short path of a cached wave whose |x| are all below 2^26: the 32 x 32 -> 64-bit squares of the wave sum
+  // below 2^62 (kNormPer * 64 * 2^52), one 64-bit DPP sum
+  uint64_t amax = 0;
   if (cached) {
 #pragma unroll
-    for (int k = 0; k < kNormPer; ++k) add_sq(xv[k]);
-  } else {
-    for (int64_t c = tid; c < cols; c += nt) add_sq(xr[c]);
+    for (int k = 0; k < kNormPer; ++k) { const uint64_t a = imie_absu64(xv[k]); amax = a > amax ? a : amax; }
   }
-  wave_sum_u128(hi, lo, bad);
+  if (cached && kNormPer <= 16 && !__any((int)(amax >> 26) != 0)) {
+    uint64_t sq = 0;
+#pragma unroll
+    for (int k = 0; k < kNormPer; ++k) {
+      const uint32_t a = (uint32_t)imie_absu64(xv[k]);
+      sq += (uint64_t)a * a;
+    }
+    lo = imie_wave_sum_u64_full(sq);
+    hi = 0;
+  } else {
+    if (cached) {
+#pragma unroll
+      for (int k = 0; k < kNormPer; ++k) add_sq(xv[k]);
+    } else {
+      for (int64_t c = tid; c < cols; c += nt) add_sq(xr[c]);
+    }
+    wave_sum_u128(hi, lo, bad);
+  }
   if (lane == 0) { s_hi[wave] = hi; s_lo[wave] = lo; s_bad[wave] = bad; }
   __syncthreads();
   // every wave: combine the per-wave sums (lane w holds wave w's) and derive rms / reciprocal redundantly
@@ -112,19 +130,24 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
   uint64_t rms = 0;
   if (!bad) {
     const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)cols);
-    if (mean <= ~(u128)0 - (u128)(uint64_t)eps) rms = isqrt_u128(mean + (u128)(uint64_t)eps);
+    if (mean <= ~(u128)0 - (u128)(uint64_t)eps) rms = isqrt_u128_fast(mean + (u128)(uint64_t)eps);
   }
   if (rms == 0) {
     if (tid == 0) atomicOr(status, IMIE_ERMS);
     return;
   }
-  const uint64_t rinv = recip_u64(rms);
+  // short path of a cached wave: n = floor((x << f) / rms) in double precision when every |x| << f of the wave
+  // is below 2^53 and rms below 2^51 (1 <= f <= 52); otherwise the 64 / 128-bit integer routine
+  const bool fast = cached && frac >= 1 && frac <= 52 && (rms >> 51) == 0 &&
+                    !__any((int)((amax >> (53 - frac)) != 0));
+  const double rms_d = (double)rms, rinv_d = 1.0 / rms_d;
+  const uint64_t rinv = fast ? 0 : recip_u64(rms);
   uint64_t mxn = 0, mxg = 0;
   int nfit = 1;
   int64_t nvk[kNormPer];
   auto norm1 = [&](int64_t v, int64_t g, int64_t c, int64_t* keep) {
-    bool fits;
-    const int64_t nv = norm_elem(v, frac, rms, rinv, &fits);
+    bool fits = true;
+    const int64_t nv = fast ? norm_elem_f64_fast(v, frac, rms_d, rinv_d) : norm_elem(v, frac, rms, rinv, &fits);
     nfit &= fits ? 1 : 0;
     const uint64_t an = imie_absu64(nv);
     mxn = an > mxn ? an : mxn;
@@ -152,10 +175,9 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
     if (PREP == 2) { prep_row_gemm(s_y, row, gp, tid, nt); imie_q1::zero_share(zero, row, (int64_t)gridDim.x, tid, nt); }
     return;
   }
-  mxn = imie_wave_max_u64(mxn);
-  mxg = imie_wave_max_u64(mxg);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) nfit &= __shfl_xor(nfit, o, 64);
+  mxn = imie_wave_max_u64_full(mxn);
+  mxg = imie_wave_max_u64_full(mxg);
+  nfit = __all(nfit);
   if (lane == 0) { s_mn[wave] = mxn; s_mg[wave] = mxg; s_fit[wave] = nfit; }
   __syncthreads();
   mxn = lane < nw ? s_mn[lane] : 0;

@@ -626,6 +626,8 @@ struct GemmArgs {
   int kfold;                       // > 0: high-dword epilogue (narrow kernel), folded every kfold blocks
   int ksplit;                      // narrow kernel: blocks split over gridDim.y ranges, outputs added atomically
   int64_t* out;
+  int* wide_any;                   // set by q1_gemm_pm_kernel per 64-token tile: some slab needs > 3 limbs (the
+                                   // wide kernel's workgroups of other tiles end at once); nullptr: not known
 };
 
 // block bits of this lane's NT outputs (every K-group reads the same 16 bytes) and their scales
@@ -651,8 +653,9 @@ __device__ inline v4i expand_bits(const uint4 w, int sh) {
              (int)((w.w >> sh) & 0x01010101u)};
 }
 
-__device__ inline void gemm_tile(const GemmArgs& a, int wave, int64_t& t0w, int64_t& o0w, int64_t& t0g, bool& live) {
-  const int64_t wg = blockIdx.x;
+__device__ inline void gemm_tile(const GemmArgs& a, int wave, int64_t& t0w, int64_t& o0w, int64_t& t0g, bool& live,
+                                 int64_t wg = -1) {
+  if (wg < 0) wg = blockIdx.x;
   int64_t tt, ot;
   if (a.ntt >= 8) {
     // >= 8 token tiles: each XCD (blockIdx % 8) walks whole token tiles, so its L2 keeps those tiles' digits
@@ -1021,6 +1024,11 @@ __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg
   // per-lane physical chunk of K half h (the swizzle term (row >> 1) & 7 is (m >> 1) & 7 for every read row)
   const int pc0 = (0 + g) ^ ((m >> 1) & 7), pc1 = (4 + g) ^ ((m >> 1) & 7);
   __syncthreads();                                    // s_lw
+  if (ot == 0 && tid < 2 && t0g + 64 * tid < a.T) {   // one workgroup per token tile records its halves' flags
+    int any = 0;
+    for (int64_t sl = 0; sl < a.nslabs; ++sl) any |= s_lw[tid][sl] > kNarrowLimbs ? 1 : 0;
+    a.wide_any[tt * 2 + tid] = any;
+  }
   issue(0, sA0, sB0);
   if (tid < 128) sS0[tid] = load_scale(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1161,17 +1169,17 @@ __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg
     }
 }
 
-// blocks whose slab needs more than kNarrowLimbs limbs on the workgroup's tokens; adds into out
+// blocks whose slab needs more than kNarrowLimbs limbs on the tile's tokens; adds into out
 template <bool S64>
-__global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
+__device__ inline void gemm_wide_tile(const GemmArgs& a, int64_t wg, int* s_lw) {
   constexpr int MT = 2, NT = 4;
-  __shared__ int s_lw[kGemmMaxSlabs];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int64_t t0, o0, t0g;
   bool live;
-  gemm_tile(a, wave, t0, o0, t0g, live);
+  gemm_tile(a, wave, t0, o0, t0g, live, wg);
   if (!live) return;
+  if (a.wide_any && a.wide_any[t0g >> 6] == 0) return;
   gemm_slab_limbs(a, t0g, s_lw);
   bool any = false;
   for (int64_t sl = 0; sl < a.nslabs; ++sl) any = any || s_lw[sl] > kNarrowLimbs;
@@ -1265,6 +1273,14 @@ __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
     }
 }
 
+// One workgroup per (64-token, 128-output) tile; with the tile flags written by the sign-copy kernel
+// (a.wide_any) the workgroups of tiles no slab of which is wide end after one flag read.
+template <bool S64>
+__global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
+  __shared__ int s_lw[kGemmMaxSlabs];
+  gemm_wide_tile<S64>(a, blockIdx.x, s_lw);
+}
+
 // Executed int8 MFMA ops of one GEMM launch pair (profiling only): per (token tile, slab) the limb count the
 // kernels use (max over the tile's tokens) x the slab's blocks x the output tiles x 64 MFMAs of 2*16*16*64 ops.
 __global__ void gemm_opcount_kernel(const int* __restrict__ lt, int64_t T, int64_t nslabs, int64_t nb, int64_t nto,
@@ -1329,7 +1345,7 @@ static int gemm_table(Q1Ws& wk, int64_t nb, int64_t T, GemmPrepOut* gp) {
   const int64_t Tp = (T + kPmTok - 1) / kPmTok * kPmTok;
   if (nslabs > kGemmMaxSlabs) return IMIE_EARG;
   if (wk.xq.ensure((size_t)kMaxLimbs * nbp * Tp * 128) || wk.totals.ensure((size_t)nbp * Tp * 8) ||
-      wk.lslab.ensure((size_t)T * nslabs * 4))
+      wk.lslab.ensure((size_t)T * nslabs * 4) || wk.wide.ensure((size_t)(Tp / 64) * 4))
     return IMIE_EARG;
   *gp = GemmPrepOut{(uint4*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, nb, nbp, nslabs, Tp};
   return IMIE_OK;
@@ -1354,6 +1370,7 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     const Q1Weight& w = *ws[i];
     GemmArgs ga;
     ga.signs = nullptr;
+    ga.wide_any = nullptr;
     ga.ksplit = 1;
     ga.bitsT = w.bits; ga.scaleT = w.scale; ga.xg = (const uint4*)wk.xq.p; ga.tg = (const int64_t*)wk.totals.p;
     ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
@@ -1374,6 +1391,7 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     if (!w.scale64 && ga.kfold > 0 && T >= kPmMinT && gemm_pm() && xg_bytes < (1ull << 32) &&
         sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32) && q1_ensure_signs(const_cast<Q1Weight&>(w), st) == 0) {
       ga.signs = w.signs;
+      ga.wide_any = (int*)wk.wide.p;
       const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
       const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * ga.nto : ntt128 * ga.nto));
       hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
