@@ -198,6 +198,10 @@ uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d);
 uint64_t imie_fx_isqrt_fast(uint64_t hi, uint64_t lo);
 int imie_fx_norm_f64(int64_t x, int frac, uint64_t rms, int64_t *out);
 int64_t imie_silu_mul_host(int64_t g, int64_t u, int64_t frac, int fast);
+/* The softmax short paths (no reference counterpart; CPU tests pin them): exp2_neg_fixed((d * log2e) >> frac) of a
+   clipped difference (fast != 0: the 32-bit form when the constants allow), and floor((e << frac) / z). */
+int64_t imie_exp_clipped_host(int64_t d, int64_t frac, int fast);
+int64_t imie_prob_div_host(int64_t e, int64_t frac, uint64_t z);
 /* Q1 embedding rows sign*scale (reference_bonsai.py:138-146) from device tables. */
 int imie_embed_dev(const uint8_t *bits, const int64_t *scale, int64_t nb, const int64_t *ids, int64_t T, int64_t *out,
                    void *stream);

@@ -98,6 +98,8 @@ SIGNATURES = {
     "imie_fx_isqrt_fast": (c_uint64, [c_uint64, c_uint64]),
     "imie_fx_norm_f64": (c_int, [c_int64, c_int, c_uint64, c_void_p]),
     "imie_silu_mul_host": (c_int64, [c_int64, c_int64, c_int64, c_int]),
+    "imie_exp_clipped_host": (c_int64, [c_int64, c_int64, c_int]),
+    "imie_prob_div_host": (c_int64, [c_int64, c_int64, c_uint64]),
     "imie_fx_div_u128": (c_uint64, [c_uint64, c_uint64, c_uint32]),
     "imie_net_set_caps": (c_int, [c_int64, c_void_p]),
     "imie_net_fill_kv": (c_int, [c_int64, c_uint64, c_void_p, c_void_p, c_int64, c_int64]),

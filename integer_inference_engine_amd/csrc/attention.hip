@@ -22,6 +22,7 @@
 #include "imie_kernels.h"
 #include "imie_attention.h"
 #include "imie_kvfmt.h"
+#include "imie_silu.h"
 #include <stdlib.h>
 
 namespace {
@@ -30,25 +31,9 @@ typedef unsigned __int128 u128;
 constexpr int kRowTile = 16;
 constexpr int kKeyTile = 32;   // keeps every kernel's LDS under 64 KB
 
-__device__ inline int64_t rshift_np(int64_t a, int64_t s) {
-  if (s < 0 || s >= 64) return a < 0 ? -1 : 0;
-  return a >> s;
-}
-
-__device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
-  const int64_t fp = (int64_t)1 << frac;
-  const int64_t k = u >> frac, f = u & (fp - 1);
-  const int sh = 16 - frac;
-  int64_t c0, c1, c2, c3;
-  if (sh >= 0) { c0 = 65536 >> sh; c1 = 45426 >> sh; c2 = 15743 >> sh; c3 = 3638 >> sh; }
-  else { c0 = (int64_t)65536 << -sh; c1 = (int64_t)45426 << -sh; c2 = (int64_t)15743 << -sh; c3 = (int64_t)3638 << -sh; }
-  const int64_t f2 = (int64_t)((uint64_t)f * (uint64_t)f) >> frac;
-  const int64_t f3 = (int64_t)((uint64_t)f2 * (uint64_t)f) >> frac;
-  int64_t poly = c0 - ((int64_t)((uint64_t)c1 * (uint64_t)f) >> frac) + ((int64_t)((uint64_t)c2 * (uint64_t)f2) >> frac) -
-                 ((int64_t)((uint64_t)c3 * (uint64_t)f3) >> frac);
-  if (poly < 0) poly = 0;
-  return rshift_np(poly, k < 63 ? k : 63);
-}
+using imie_silu::exp2_neg_fixed;
+using imie_silu::exp_clipped;
+using imie_silu::prob_div;
 
 __device__ inline void amax_u64(uint64_t* p, uint64_t v) { atomicMax((unsigned long long*)p, (unsigned long long)v); }
 __device__ inline void amax_i64(int64_t* p, int64_t v) { atomicMax((long long*)p, (long long)v); }
@@ -495,6 +480,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     return;
   }
   const int64_t jend = min(j0 + d.chunk, L);
+  const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
   // row max over all chunks (wave r reduces row r)
 #pragma unroll
   for (int k = 0; k < RW; ++k) {
@@ -518,7 +504,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     for (int64_t j = j0 + threadIdx.x; j < jend; j += blockDim.x) {
       int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)(one ? sv[r] : d.scores[row * d.Lmax + j]));
       if (dd > d.dclip) dd = d.dclip;
-      const uint64_t e = (uint64_t)exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+      const uint64_t e = (uint64_t)exp_clipped(dd, d.frac, d.log2e, fx32);
       d.scores[row * d.Lmax + j] = (int64_t)e;
       z += e;
     }
@@ -945,7 +931,8 @@ template <int REP>
 __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   constexpr int RBH = (REP + 3) / 4;
   __shared__ __align__(16) int8_t sPd[RBH][16][64];
-  __shared__ uint64_t s_z[REP], s_rz[REP], s_mp[4][REP];
+  __shared__ uint64_t s_z[REP], s_mp[4][REP];
+  __shared__ double s_rzd[REP];
   const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
@@ -1005,7 +992,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
     for (int64_t c = lane + 128; c < d.nch; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
-    if (lane == 0) { s_z[r] = z; s_rz[r] = z > 1 ? (~(uint64_t)0) / z : 0; }
+    if (lane == 0) { s_z[r] = z; s_rzd[r] = z != 0 ? 1.0 / (double)z : 0.0; }
   }
   for (int i = tid; i < RBH * 16 * 64; i += 256) (&sPd[0][0][0])[i] = 0;
   __syncthreads();
@@ -1046,17 +1033,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
         if (r >= REP) break;
         const uint64_t Z = s_z[r];
         int64_t p = 0;
-        if (kk < tn && Z != 0) {
-          const uint64_t num = (uint64_t)scv[k] << d.frac;
-          if (Z == 1) p = (int64_t)num;
-          else {
-            const uint64_t rz = s_rz[r];
-            uint64_t qq = __umul64hi(num, rz);
-            uint64_t rem = num - qq * Z;
-            while (rem >= Z) { ++qq; rem -= Z; }
-            p = (int64_t)qq;
-          }
-        }
+        if (kk < tn && Z != 0) p = prob_div(scv[k], d.frac, Z, s_rzd[r]);
         mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
         int64_t x = p;
         for (int lp = 0; lp < 4; ++lp) {
@@ -1269,11 +1246,12 @@ __global__ __launch_bounds__(256) void pf_softmax8_kernel(AttnDesc d) {
   __syncthreads();
   const int64_t m = s_m;
   int64_t* s = d.scores + r * d.Lmax;
+  const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
   uint64_t z = 0;
   for (int64_t j = tid; j < ri.lv; j += 256) {
     int64_t dd = (int64_t)((uint64_t)m - (uint64_t)s[j]);
     if (dd > d.dclip) dd = d.dclip;
-    const int64_t e = exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+    const int64_t e = exp_clipped(dd, d.frac, d.log2e, fx32);
     s[j] = e;
     z += (uint64_t)e;
   }
@@ -1282,21 +1260,11 @@ __global__ __launch_bounds__(256) void pf_softmax8_kernel(AttnDesc d) {
   if ((tid & 63) == 0) red[tid >> 6] = z;
   __syncthreads();
   const uint64_t Z = red[0] + red[1] + red[2] + red[3];
-  const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
+  const double rzd = Z != 0 ? 1.0 / (double)Z : 0.0;
   const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
   uint64_t mp = 0;
   for (int64_t j = tid; j < ri.lv; j += 256) {
-    int64_t p = 0;
-    if (Z != 0) {
-      const uint64_t num = (uint64_t)s[j] << d.frac;
-      if (Z == 1) p = (int64_t)num;
-      else {
-        uint64_t qq = __umul64hi(num, rz);
-        uint64_t rem = num - qq * Z;
-        while (rem >= Z) { ++qq; rem -= Z; }
-        p = (int64_t)qq;
-      }
-    }
+    const int64_t p = Z != 0 ? prob_div(s[j], d.frac, Z, rzd) : 0;
     mp = (uint64_t)p > mp ? (uint64_t)p : mp;
     int64_t x = p;
     for (int lp = 0; lp < Lp; ++lp) {
@@ -1340,6 +1308,7 @@ __global__ __launch_bounds__(256) void pf_softmax8_wave_kernel(AttnDesc d) {
   }
   const int64_t m = (int64_t)(imie_wave_max_u64_full(mo) ^ 0x8000000000000000ull);
   const int64_t* s = d.scores + r * d.Lmax;
+  const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
   int64_t e[kSmPer];
   uint64_t z = 0;
 #pragma unroll
@@ -1349,36 +1318,27 @@ __global__ __launch_bounds__(256) void pf_softmax8_wave_kernel(AttnDesc d) {
     if (j < ri.lv) {
       int64_t dd = (int64_t)((uint64_t)m - (uint64_t)s[j]);
       if (dd > d.dclip) dd = d.dclip;
-      e[i] = exp2_neg_fixed((int64_t)((uint64_t)dd * (uint64_t)d.log2e) >> d.frac, d.frac);
+      e[i] = exp_clipped(dd, d.frac, d.log2e, fx32);
       z += (uint64_t)e[i];
     }
   }
   const uint64_t Z = imie_wave_sum_u64_full(z);
-  const uint64_t rz = Z > 1 ? (~(uint64_t)0) / Z : 0;
+  const double rzd = Z != 0 ? 1.0 / (double)Z : 0.0;
   const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
   uint64_t mp = 0;
 #pragma unroll
   for (int i = 0; i < kSmPer; ++i) {
     const int64_t j = lane + 64 * i;
     if (j >= ri.lv) continue;
-    int64_t p = 0;
-    if (Z != 0) {
-      const uint64_t num = (uint64_t)e[i] << d.frac;
-      if (Z == 1) p = (int64_t)num;
-      else {
-        uint64_t qq = __umul64hi(num, rz);
-        uint64_t rem = num - qq * Z;
-        while (rem >= Z) { ++qq; rem -= Z; }
-        p = (int64_t)qq;
-      }
-    }
+    const int64_t p = Z != 0 ? prob_div(e[i], d.frac, Z, rzd) : 0;
     mp = (uint64_t)p > mp ? (uint64_t)p : mp;
-    int64_t x = p;
+    // p <= 2^frac < 2^30: the balanced digits in 32-bit arithmetic
+    int32_t x = (int32_t)p;
 #pragma unroll
     for (int lp = 0; lp < 4; ++lp) {                  // Lp <= 4 (frac <= 29)
       if (lp >= Lp) break;
-      const int64_t dg = ((x + 128) & 255) - 128;
-      x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+      const int32_t dg = ((x + 128) & 255) - 128;
+      x = (x - dg) >> 8;
       d.pd[((int64_t)lp * rows + r) * d.pdL + j] = (int8_t)dg;
     }
   }

@@ -93,6 +93,29 @@ __host__ __device__ inline int64_t silu_mul_fast(int64_t g, int64_t u, int frac,
   return (int64_t)((uint64_t)silu * (uint64_t)u) >> frac;
 }
 
+// exp2_neg_fixed((d * log2e) >> frac) of a clipped softmax difference d (0 <= d <= dclip): one 32 x 32 product and
+// the 32-bit cubic when dclip and log2e are below 2^32 (fast, decided once per launch; frac <= 29), else the
+// general form. Same values.
+__host__ __device__ inline int64_t exp_clipped(int64_t d, int frac, int64_t log2e, bool fast) {
+  if (fast && d >= 0)
+    return exp2_neg_fixed32((int64_t)(((uint64_t)(uint32_t)d * (uint32_t)log2e) >> frac), frac);
+  return exp2_neg_fixed((int64_t)((uint64_t)d * (uint64_t)log2e) >> frac, frac);
+}
+
+// p = floor((e << frac) / z) for 0 <= e, 0 < z: below 2^52 (numerator and z) the double quotient num * (1 / z)
+// is within one of the answer and the exact remainder settles it; otherwise the integer division.
+__host__ __device__ inline int64_t prob_div(int64_t e, int frac, uint64_t z, double rz) {
+  const uint64_t num = (uint64_t)e << frac;
+  if ((num >> 52) == 0 && (z >> 52) == 0) {
+    uint64_t q = (uint64_t)((double)num * rz);
+    const int64_t r = (int64_t)(num - q * z);
+    if (r < 0) --q;
+    else if ((uint64_t)r >= z) ++q;
+    return (int64_t)q;
+  }
+  return (int64_t)(num / z);
+}
+
 // (silu(g) * u) >> frac with silu(g) = (g * sigmoid(g)) >> frac (wrapping int64 products, as the reference)
 __host__ __device__ inline int64_t silu_mul(int64_t g, int64_t u, int frac, int64_t log2e, int64_t dclip) {
   const int64_t silu = (int64_t)((uint64_t)g * (uint64_t)sigmoid_fixed(g, frac, log2e, dclip)) >> frac;

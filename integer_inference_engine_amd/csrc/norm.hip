@@ -472,6 +472,15 @@ int64_t imie_silu_mul_host(int64_t g, int64_t u, int64_t frac, int fast) {
   imie_silu_consts(frac, &log2e, &dclip);
   return fast ? imie_silu::silu_mul_fast(g, u, (int)frac, log2e, dclip) : imie_silu::silu_mul(g, u, (int)frac, log2e, dclip);
 }
+// the softmax short paths: exp_clipped (fast != 0: the 32-bit form) and prob_div
+int64_t imie_exp_clipped_host(int64_t d, int64_t frac, int fast) {
+  int64_t log2e, dclip;
+  imie_silu_consts(frac, &log2e, &dclip);
+  return imie_silu::exp_clipped(d, (int)frac, log2e, fast != 0 && (dclip >> 32) == 0 && (log2e >> 32) == 0);
+}
+int64_t imie_prob_div_host(int64_t e, int64_t frac, uint64_t z) {
+  return imie_silu::prob_div(e, (int)frac, z, 1.0 / (double)z);
+}
 uint64_t imie_fx_div_u128(uint64_t hi, uint64_t lo, uint32_t d) {
   return (uint64_t)imie_fx::div_u128_cols(((imie_fx::u128)hi << 64) | lo, d);
 }

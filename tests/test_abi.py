@@ -116,6 +116,29 @@ def test_prologue_short_paths_host():
             assert so.imie_silu_mul_host(gi, ui, frac, 0) == wi, (gi, ui, frac)
 
 
+def test_softmax_short_paths_host():
+    """The prefill softmax's short paths against the numpy oracle (fixedpoint.py:49-87): the exponential of a clipped
+    difference d in [0, dclip] by one 32 x 32 product and the 32-bit cubic (both forms, every fraction width the
+    kernels accept; the integer-part boundaries k * 2^frac and the clip edge included), and p = floor((e << frac)
+    / Z) by the double quotient with exact correction (exact multiples, remainders of Z - 1, e at 0 and 2^frac,
+    Z from 1 up to 2^52)."""
+    from oracle import fixedpoint as fx
+    so = _lib.lib()
+    rng = np.random.default_rng(12)
+    for frac in (1, 2, 8, 16, 24, 29):
+        log2e, dclip = fx.scaled_log2e(frac), fx.d_clip(frac)
+        ds = [0, 1, 2, dclip - 1, dclip] + [int(v) for v in rng.integers(0, dclip + 1, size=600)]
+        ds += [max(0, min(dclip, ((k << frac) * (1 << frac)) // log2e + o)) for k in range(0, 40) for o in (-1, 0, 1)]
+        want = fx.exp2_neg_fixed(np.array([(x * log2e) >> frac for x in ds], dtype=np.int64), frac)
+        for x, w in zip(ds, want.tolist()):
+            assert so.imie_exp_clipped_host(x, frac, 1) == w, (x, frac)
+            assert so.imie_exp_clipped_host(x, frac, 0) == w, (x, frac)
+        for z in [1, 2, 3, 1 << frac, (1 << frac) + 1, 12345677, (1 << 40) + 7, (1 << 52) - 1, 1 << 52]:
+            es = [0, 1, (1 << frac) - 1, 1 << frac, z % (1 << frac)] + [int(v) for v in rng.integers(0, (1 << frac) + 1, size=60)]
+            for e in es:
+                assert so.imie_prob_div_host(e, frac, z) == (e << frac) // z, (e, frac, z)
+
+
 def test_exports_every_symbol_the_reference_nmc_loader_requires():
     """north-mini-code/src/nmc/qk_cuda.py:39-72 (_REQUIRED_CUDA_SYMBOLS) and the ABI version it checks (:22, 83-92):
     the reference bridge binds this library unchanged."""
