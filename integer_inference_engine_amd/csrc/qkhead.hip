@@ -10,6 +10,7 @@
 #include "imie_kernels.h"
 #include "imie_fixed.h"
 #include "imie_kvfmt.h"
+#include "imie_head.h"
 
 namespace {
 
@@ -42,68 +43,21 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     v0 = act ? vr[j] : 0;
     v1 = act ? vr[j + half] : 0;
   }
-  // 128-bit sum of squares (two squares per lane cannot overflow 128 bits); every |x| of the head below 2^26:
-  // 52-bit squares, the wave's sum in one 64-bit word (one reduction instead of four limb sums)
-  uint64_t hi = 0, lo = 0;
-  int bad = 0;
-  const uint64_t a0 = imie_absu64(x0), a1 = imie_absu64(x1);
-  if (!__any(((a0 | a1) >> 26) ? 1 : 0)) {
-    lo = imie_wave_sum_u64_full((uint64_t)(uint32_t)a0 * (uint32_t)a0 + (uint64_t)(uint32_t)a1 * (uint32_t)a1);
-  } else {
-    const u128 sq = (u128)a0 * a0 + (u128)a1 * a1;
-    hi = (uint64_t)(sq >> 64);
-    lo = (uint64_t)sq;
-    wave_sum_u128_full(hi, lo, bad);   // every reduction here runs on the full wave
-  }
-  uint64_t rms = 0;
-  if (!bad) {
-    const u128 mean = div_u128_cols(((u128)hi << 64) | lo, (uint32_t)a.hd);
-    if (mean <= ~(u128)0 - (u128)(uint64_t)a.eps) rms = isqrt_u128_fast(mean + (u128)(uint64_t)a.eps);
-  }
-  if (rms == 0) {
+  int64_t o0, o1;
+  uint64_t mx, mc;
+  if (!imie_head::head_norm_rope(x0, x1, g0, g1, c, s, act, a.hd, a.frac, a.eps, o0, o1, mx, mc)) {
     if (j == 0) atomicOr(a.status, IMIE_ERMS);
     if (j == 0 && a.gpart) { a.gpart[(r * (a.H + a.Hkv) + h) * 2] = 0; a.gpart[(r * (a.H + a.Hkv) + h) * 2 + 1] = 0; }
     return;
   }
-  // n in double precision where exact; the integer routine (and its reciprocal) only if some lane needs it
-  const double rd = (double)rms, rid = 1.0 / rd;
-  int64_t n0 = 0, n1 = 0;
-  const bool q0 = !act || norm_elem_f64(x0, a.frac, rms, rd, rid, &n0);
-  const bool q1 = !act || norm_elem_f64(x1, a.frac, rms, rd, rid, &n1);
-  bool f0 = true, f1 = true;
-  if (__any((q0 && q1) ? 0 : 1)) {
-    const uint64_t rinv = recip_u64(rms);
-    if (!q0) n0 = norm_elem(x0, a.frac, rms, rinv, &f0);
-    if (!q1) n1 = norm_elem(x1, a.frac, rms, rinv, &f1);
-  }
-  const bool ok = __all((f0 && f1) ? 1 : 0) != 0;
-  uint64_t mxn = imie_absu64(n0) > imie_absu64(n1) ? imie_absu64(n0) : imie_absu64(n1);
-  uint64_t mxg = imie_absu64(g0) > imie_absu64(g1) ? imie_absu64(g0) : imie_absu64(g1);
-  mxn = imie_wave_max_u64_full(mxn);
-  mxg = imie_wave_max_u64_full(mxg);
-  if (!ok || (mxn != 0 && mxg > (uint64_t)INT64_MAX / mxn)) {
-    if (j == 0) atomicOr(a.status, IMIE_ERMS);
-    if (j == 0 && a.gpart) { a.gpart[(r * (a.H + a.Hkv) + h) * 2] = 0; a.gpart[(r * (a.H + a.Hkv) + h) * 2 + 1] = 0; }
-    return;
-  }
-  const int64_t y0 = imie_floor_shift((int64_t)((uint64_t)n0 * (uint64_t)g0), a.frac);
-  const int64_t y1 = imie_floor_shift((int64_t)((uint64_t)n1 * (uint64_t)g1), a.frac);
-  const int64_t o0 = (int64_t)((uint64_t)y0 * (uint64_t)c - (uint64_t)y1 * (uint64_t)s) >> a.frac;
-  const int64_t o1 = (int64_t)((uint64_t)y0 * (uint64_t)s + (uint64_t)y1 * (uint64_t)c) >> a.frac;
-  {
-    uint64_t mx = imie_absu64(y0) > imie_absu64(y1) ? imie_absu64(y0) : imie_absu64(y1);
-    uint64_t mc = imie_absu64(c) > imie_absu64(s) ? imie_absu64(c) : imie_absu64(s);
-    mx = imie_wave_max_u64_full(mx);
-    mc = imie_wave_max_u64_full(mc);
-    if (j == 0) {
-      if (a.gpart) {
-        uint64_t* gp = a.gpart + (r * (a.H + a.Hkv) + h) * 2;
-        gp[0] = mx;
-        gp[1] = mc;
-      } else {
-        amax_u64(&a.guard[isq ? 0 : 2], mx);
-        amax_u64(&a.guard[isq ? 1 : 3], mc);
-      }
+  if (j == 0) {
+    if (a.gpart) {
+      uint64_t* gp = a.gpart + (r * (a.H + a.Hkv) + h) * 2;
+      gp[0] = mx;
+      gp[1] = mc;
+    } else {
+      amax_u64(&a.guard[isq ? 0 : 2], mx);
+      amax_u64(&a.guard[isq ? 1 : 3], mc);
     }
   }
   if (isq) {
