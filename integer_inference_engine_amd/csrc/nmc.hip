@@ -239,12 +239,8 @@ __device__ inline int64_t exp2_neg_fixed(int64_t u, int frac) {
   return poly >> (k < 63 ? k : 63);
 }
 
-__global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t* __restrict__ u, int64_t n, int fa,
-                                   int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status,
-                                   const int* __restrict__ run_gate = nullptr) {
-  if (run_gate && *run_gate == 0) return;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-  const int64_t x = g[i];
+// (silu(x) * u) >> fa in int128 with the int64 range checks (status bit 2)
+__device__ inline int64_t qk_silu_elem(int64_t x, int64_t u, int fa, int64_t log2e, int64_t dclip, int* status) {
   const int64_t m = x > 0 ? x : 0;
   int64_t d0 = m, d1 = (int64_t)((uint64_t)m - (uint64_t)x);
   if (d0 > dclip) d0 = dclip;
@@ -255,17 +251,57 @@ __global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t*
   const int64_t sig = z == 0 ? 0 : (int64_t)(((uint64_t)e1 << fa) / (uint64_t)z);
   const i128 s = ((i128)x * sig) >> fa;
   if (s > (i128)INT64_MAX || s < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
-  const i128 gu = ((i128)(int64_t)s * u[i]) >> fa;
+  const i128 gu = ((i128)(int64_t)s * u) >> fa;
   if (gu > (i128)INT64_MAX || gu < (i128)INT64_MIN) atomicOr(status, IMIE_EOVF);
-  out[i] = (int64_t)gu;
+  return (int64_t)gu;
+}
+
+__global__ void qk_silu_mul_kernel(const int64_t* __restrict__ g, const int64_t* __restrict__ u, int64_t n, int fa,
+                                   int64_t log2e, int64_t dclip, int64_t* __restrict__ out, int* __restrict__ status,
+                                   const int* __restrict__ run_gate = nullptr) {
+  if (run_gate && *run_gate == 0) return;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = qk_silu_elem(g[i], u[i], fa, log2e, dclip, status);
+}
+
+// The exact gate and up kernels and SiLU * up as the fallback of the fused gate/up stage, in one launch: a small
+// grid that ends at once unless the prep flagged a wide activation row; then each workgroup takes (tile, item)
+// pairs, computes the gate tile and the up tile and turns its own tile's elements into silu(gate) * up.
+constexpr int kGatedWgs2 = 128;
+__global__ __launch_bounds__(256) void qk_gateup_gated_kernel(const Item* __restrict__ ig, const Item* __restrict__ iu,
+                                                              const int* __restrict__ xi, const int* __restrict__ yi,
+                                                              const int64_t* __restrict__ X, int64_t K,
+                                                              int64_t* __restrict__ gb, int64_t* __restrict__ ub,
+                                                              int64_t ldy, int fw, int fa, int64_t log2e,
+                                                              int64_t dclip, int* __restrict__ status,
+                                                              const int* __restrict__ run_gate, int64_t ntx,
+                                                              int64_t ne) {
+  if (*run_gate == 0) return;
+  for (int64_t t = blockIdx.x; t < ntx * ne; t += gridDim.x) {
+    const int64_t bx = t % ntx, by = t / ntx;
+    qk_group_tile(ig, xi, yi, X, K, gb, ldy, fw, status, bx, by);
+    __syncthreads();
+    qk_group_tile(iu, xi, yi, X, K, ub, ldy, fw, status, bx, by);
+    __threadfence_block();
+    __syncthreads();                                  // both tiles written (and the shared buffers free)
+    const Item it = ig[by];
+    const int64_t o0 = bx * kRows, no = it.out_f - o0 < kRows ? it.out_f - o0 : kRows;
+    if (no > 0)
+      for (int64_t e = threadIdx.x; e < (int64_t)it.count * no; e += blockDim.x) {
+        const int64_t idx = (int64_t)yi[it.first + e / no] * ldy + o0 + e % no;
+        gb[idx] = qk_silu_elem(gb[idx], ub[idx], fa, log2e, dclip, status);
+      }
+    __syncthreads();
   }
 }
 
 // out[t][o] = sum_j (dd[t*k + j][o] * gates[t*k + j]) >> fa (exact; cohere2.py:187 then astype int64)
+// flags (optional): the fused MoE's two wide-row flags, cleared here, after their last reader, for the next call
 __global__ void qk_combine_kernel(const int64_t* __restrict__ dd, int m, int k, int64_t d_model,
                                   const int64_t* __restrict__ gates, int fa, int64_t* __restrict__ out,
-                                  int* __restrict__ status) {
+                                  int* __restrict__ status, int* __restrict__ flags = nullptr) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (flags && idx < 2) flags[idx] = 0;
   if (idx >= (int64_t)m * d_model) return;
   const int64_t t = idx / d_model, o = idx % d_model;
   i128 acc = 0;
@@ -1230,20 +1266,16 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   int64_t log2e, dclip;
   silu_consts_nmc(fa, &log2e, &dclip);
   imie_prof_mark(IMIE_K_QK, st, true);
-  hipLaunchKernelGGL(qk_flags_reset_kernel, dim3(1), dim3(64), 0, st, flagA, 2);
+  // the wide-row flags start clear: the previous call's combine kernel cleared them (a fresh or foreign value
+  // only costs a run of the exact fallbacks, whose results equal the fused kernels')
   hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, xsp, lrp,
                      flagA);
   hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
                      d_pt, d_pp, xdp, lrp, (int64_t)m, d_model, e_ffn, fw, fa, log2e, dclip, gb, status, flagA);
   // exact VALU fallback of the gate/up stage (runs only when the prep flagged a wide activation row)
   const int64_t ntg = (e_ffn + kRows - 1) / kRows;
-  hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_ig, d_pt, d_pp, h_dev, d_model, gb,
-                     e_ffn, fw, status, flagA, ntg, (int64_t)ne);
-  hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_iu, d_pt, d_pp, h_dev, d_model, ub,
-                     e_ffn, fw, status, flagA, ntg, (int64_t)ne);
-  const int64_t n = P * e_ffn;
-  hipLaunchKernelGGL(qk_silu_mul_kernel, dim3(kGatedWgs), dim3(256), 0, st, gb, ub, n, fa, log2e, dclip, gb, status,
-                     flagA);
+  hipLaunchKernelGGL(qk_gateup_gated_kernel, dim3(kGatedWgs2), dim3(256), 0, st, d_ig, d_iu, d_pt, d_pp, h_dev,
+                     d_model, gb, ub, e_ffn, fw, fa, log2e, dclip, status, flagA, ntg, (int64_t)ne);
   // down over the P rows of gu
   hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)P), dim3(256), 0, st, gb, P, e_ffn, xdp, xsp, lrp, flagB);
   hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((d_model + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
@@ -1251,7 +1283,7 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_id, d_pp, d_pp, gb, e_ffn, db,
                      d_model, fw, status, flagB, (int64_t)((d_model + kRows - 1) / kRows), (int64_t)ne);
   hipLaunchKernelGGL(qk_combine_kernel, dim3((unsigned)(((int64_t)m * d_model + 255) / 256)), dim3(256), 0, st, db,
-                     m, k, d_model, gates_dev, fa, out_dev, status);
+                     m, k, d_model, gates_dev, fa, out_dev, status, flagA);
   imie_prof_mark(IMIE_K_QK, st, false);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
