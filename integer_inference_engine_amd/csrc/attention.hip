@@ -787,12 +787,27 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   for (int hb = 0; hb < RBH; ++hb) smax[hb] = INT64_MIN;
   const int64_t jend = min(j0 + d.chunk, L);
   const int8_t* Kb = (const int8_t*)d.K;
+  // page ids of the chunk's keys in lane registers (lane i: page pi0 + i, up to 64 pages): a tile's K addresses
+  // then come from a cross-lane move, not from a page-table load that would wait behind the previous tile's K
+  // loads (the vector memory counter is in order), so the next tile's loads really are in flight
+  int64_t pi0, pin0, pi1, pin1;
+  page_split(d, j0, pi0, pin0);
+  page_split(d, max(j0, min(j0 + d.chunk, d.Lmax) - 1), pi1, pin1);
+  const bool pgreg = pi1 - pi0 < 64;
+  const int64_t pgl = (pgreg && lane <= pi1 - pi0) ? d.pt[b * d.mp + pi0 + lane] : 0;
   // 16-key tiles t = j0 + 16 wave + 64 i; the next tile's K slices are loaded before this tile's MFMAs
   auto load_tile = [&](int64_t t, int64_t lim, v4i (&bk)[4][2]) {   // keys below lim (masked later by jend)
     const int64_t j = t + m;
     const bool valid = j < lim;
     int64_t base = 0, slot = 0;
-    if (valid) base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
+    if (pgreg) {                                      // every lane active here (t is wave-uniform)
+      int64_t pi;
+      page_split(d, valid ? j : j0, pi, slot);
+      const int64_t pg = __shfl(pgl, (int)(pi - pi0), 64);
+      base = imie_kv8::block_base(pg, kv, d.Hkv, d.hd, d.P) + imie_kv8::k_off(slot, 0, 0, d.hd);
+    } else if (valid) {
+      base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -945,11 +960,19 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   // first step's, and the chunk Z sums (an empty chunk's is 0), are requested before the sequence length is
   // known, later steps' one step ahead
   constexpr int RW = (REP + 3) / 4;
+  // page ids of the chunk's keys in lane registers (lane i: page pi0 + i, up to 64 pages): a step's V address
+  // comes from a lane read, not from a page-table load queued behind the previous step's V loads
+  int64_t pi0, pin0, pi1, pin1;
+  page_split(d, j0, pi0, pin0);
+  page_split(d, max(j0, min(j0 + d.chunk, d.Lmax) - 1), pi1, pin1);
+  const bool pgreg = pi1 - pi0 < 64;
+  const int64_t pgl = (pgreg && lane <= pi1 - pi0) ? d.pt[b * d.mp + pi0 + lane] : 0;
   auto load_step = [&](int64_t t0, int64_t lim, v4i (&bv)[2][4], int64_t (&sc)[RW]) {
     const int64_t tn = min((int64_t)64, lim - t0);
     int64_t pi, slot0;
     page_split(d, t0, pi, slot0);
-    const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, d.hd, d.P);
+    const int64_t pg = pgreg ? (int64_t)imie_readlane_u64((uint64_t)pgl, (int)(pi - pi0)) : d.pt[b * d.mp + pi];
+    const int8_t* vblk = Vb + imie_kv8::block_base(pg, kv, d.Hkv, d.hd, d.P);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int tile = wave + 4 * tt;
