@@ -673,17 +673,21 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
 // recombined once per block into int64 (|x| < 127 (256^5-1)/255: |S1| < 2^57, |S2| < 2^53), and each 256-block
 // adds dq S1 - dmq S2 into a 128-bit (hi, lo) accumulator with one 64 x 64 -> 128 multiply per term. MFMA sums are
 // exact: |D| <= 32 * 128 * 32 < 2^31.
-// Workgroup = (64 weight rows, item), wave = 16 rows; the block loop is software-pipelined: the next block's digits
-// go to the other half of an LDS double buffer and its weights are in flight while a block computes.
+// gate/up: workgroup = (64 RT weight rows, item), wave = RT tiles of 16 rows. Per token group the digit rows of up
+// to four limbs over the whole K are staged in LDS once (one barrier), and each wave then walks its tiles' blocks
+// with the next block's weights in flight and no barrier in the loop; a token group with more than four limbs
+// stages limbs 0..3 and 4..7 in turn per tile (two passes over the tile's weights).
+// down (K of a few blocks): workgroup = (64 weight rows, item); the block loop is software-pipelined, the next
+// block's digits going to the other half of an LDS double buffer while a block computes.
 // ---------------------------------------------------------------------------------------------------------
 constexpr int kMoeTok = 4;         // tokens per MFMA row group (4 tokens x 4 limbs = 16 rows)
-constexpr int kMoeLimbs = 8;       // limbs staged (two MFMA row groups); the prep refuses rows beyond kQkLimbs
-// LDS row stride of the staged digits: 256 bytes + 16 of padding. A lane of row r (of the 16 (token, limb) rows)
-// and K group kg reads 8 bytes at r * 272 + 8 kg + 32 j, i.e. 8-byte slot 2 r + kg (mod 32): the 32 lanes of a
-// half-wave hit 32 distinct slots (with a 256-byte stride all 16 rows of a K group shared one slot: 16-way
-// bank conflicts).
-constexpr int kMoeRow = 272;
-constexpr int kMoeBuf = kMoeLimbs * kMoeTok * kMoeRow;
+constexpr int kMoeRtGU = 1;        // 16-row weight tiles per wave of the gate/up kernel (config 4: 1 is fastest)
+// LDS row stride of the staged digits: K + 16 bytes (K a multiple of 256). A lane of row r (of the 16 (token, limb)
+// rows) and K group kg reads 8 bytes at r (K + 16) + 8 kg + 32 j, i.e. 8-byte slot 2 r + kg (mod 32): the 32 lanes
+// of a half-wave hit 32 distinct slots (with a K-byte stride all 16 rows of a K group shared one slot: 16-way bank
+// conflicts).
+__host__ __device__ inline int64_t moe_kp(int64_t K) { return K + 16; }
+__host__ __device__ inline size_t moe_lds_bytes(int64_t K) { return (size_t)(4 * kMoeTok) * (size_t)moe_kp(K); }
 
 struct MoeItem {
   const uint8_t* wg;        // gate (Q4_K), up (Q4_K), down (Q6_K) of the expert
@@ -730,6 +734,13 @@ __device__ inline int64_t nmc_silu_mul(int64_t x, int64_t u, int fa, int64_t log
   return (int64_t)gu;
 }
 
+// Per-block staging (the down kernel, whose K of a few blocks is walked with the next block's digits fetched while a
+// block computes): up to 8 limbs x kMoeTok tokens x 256 bytes per block, rows of 272 bytes (moe_kp(256)), double
+// buffered.
+constexpr int kMoeLimbs = 8;
+constexpr int kMoeRow = 272;
+constexpr int kMoeBuf = kMoeLimbs * kMoeTok * kMoeRow;
+
 // Staging of one block's digits (L limbs x kMoeTok tokens x 256 bytes) as a register fetch issued before the
 // current block's compute and an LDS store after it. At most 8 x 4 x 16 = 512 uint4: two per thread. The thread's
 // two (source row, LDS slot) pairs are fixed for a token group (MoePlan); a block only adds its offset.
@@ -767,24 +778,53 @@ __device__ inline void moe_store(const MoeStage& r, const MoePlan& p, int8_t* bu
     if (p.on[k]) *(uint4*)(buf + p.dst[k]) = r.v[k];
 }
 
-// The lane's A operand source: limb 4 lg + l of token t (row m = 4 t + l of the MFMA), K group kg. Rows beyond
-// the group's tokens / limbs are zero in LDS (cleared at the start of every token group, never staged), so the
-// lane reads its operand without a select.
-struct MoeA {
-  int off;                  // byte offset of [l][t][8 kg] within one LDS buffer
-};
-__device__ inline MoeA moe_a_lane(int lane) {
-  const int m = lane & 15, kg = lane >> 4, t = m >> 2, l = m & 3;
-  MoeA r;
-  r.off = (l * kMoeTok + t) * kMoeRow + 8 * kg;
-  return r;
-}
-__device__ inline int64_t moe_a(const int8_t* buf, const MoeA& a, int lg, int p0) {
-  return *(const int64_t*)(buf + a.off + lg * 4 * kMoeTok * kMoeRow + p0);
-}
 // both staging buffers to zero (threads tid of nt; the caller synchronizes before and after)
 __device__ inline void moe_clear(int8_t* sx, int tid, int nt) {
   for (int i = tid; i < 2 * kMoeBuf / 16; i += nt) ((uint4*)sx)[i] = uint4{0, 0, 0, 0};
+}
+
+// Stage limbs 4 p .. 4 p + 3 of the token group's activation rows over the whole K into LDS row [l][t] (l = limb
+// within the pass, t = token): 16 rows x K / 16 chunks of 16 bytes, the loads of four chunks per thread issued
+// before their stores. Rows of absent tokens (t >= tn) or limbs (4 p + l >= L) are written as zeros, so the MFMA
+// A operands need no selects. The caller synchronizes before (buffer free) and after (rows visible).
+__device__ inline void moe_stage(int8_t* sx, const int (&prow)[kMoeTok], int tn, int L, int p,
+                                 const int8_t* __restrict__ xd, int64_t rows, int64_t K, int tid, int nt) {
+  const int cpr = (int)(K >> 4), total = 16 * cpr;
+  const int64_t kp = moe_kp(K);
+  for (int i0 = tid; i0 < total; i0 += 4 * nt) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * nt;
+      const int r = i / cpr, c = i - r * cpr, l = r >> 2, t = r & 3;
+      const bool on = i < total && t < tn && 4 * p + l < L;
+      const int pr = t == 0 ? prow[0] : t == 1 ? prow[1] : t == 2 ? prow[2] : prow[3];
+      v[u] = on ? *(const uint4*)(xd + ((int64_t)(4 * p + l) * rows + pr) * K + 16 * c) : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * nt;
+      if (i < total) {
+        const int r = i / cpr, c = i - r * cpr;
+        *(uint4*)(sx + r * kp + 16 * c) = v[u];
+      }
+    }
+  }
+}
+
+// The lane's A operand source: limb l (of the staged pass) of token t (row m = 4 t + l of the MFMA), K group kg.
+struct MoeA {
+  int off;                  // byte offset of [l][t][8 kg]
+};
+__device__ inline MoeA moe_a_lane(int lane, int64_t K) {
+  const int m = lane & 15, kg = lane >> 4, t = m >> 2, l = m & 3;
+  MoeA r;
+  r.off = (l * kMoeTok + t) * (int)moe_kp(K) + 8 * kg;
+  return r;
+}
+// A operand at K position p0 (buf points at the block's first position)
+__device__ inline int64_t moe_a(const int8_t* buf, const MoeA& a, int p0) {
+  return *(const int64_t*)(buf + a.off + p0);
 }
 
 // sum_r T[r] << 8 (4 lg + r): a token's value from its per-limb partial sums (int32 per limb)
@@ -799,18 +839,39 @@ struct Q4Lane {
   uint4 h;
   uint2 q[4];
 };
+// Loads of weight bytes through global-address-space pointers of native vector types. The item pointers come from
+// memory, so plain loads through them are flat loads, which count against the LDS counter as well: every LDS wait
+// in the block compute would then also wait for the next block's weights in flight.
+typedef unsigned gv4u __attribute__((ext_vector_type(4)));
+typedef unsigned gv2u __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ inline T gload(const uint8_t* p);
+template <>
+__device__ inline uint4 gload<uint4>(const uint8_t* p) {
+  const gv4u v = *(__attribute__((address_space(1))) const gv4u*)p;
+  return uint4{v.x, v.y, v.z, v.w};
+}
+template <>
+__device__ inline uint2 gload<uint2>(const uint8_t* p) {
+  const gv2u v = *(__attribute__((address_space(1))) const gv2u*)p;
+  return uint2{v.x, v.y};
+}
+template <>
+__device__ inline uint8_t gload<uint8_t>(const uint8_t* p) {
+  return *(__attribute__((address_space(1))) const uint8_t*)p;
+}
 __device__ inline Q4Lane q4_lane_load(const uint8_t* blk, int kg) {
   Q4Lane r;
-  r.h = *(const uint4*)blk;
+  r.h = gload<uint4>(blk);
 #pragma unroll
-  for (int g = 0; g < 4; ++g) r.q[g] = *(const uint2*)(blk + 16 + 32 * g + 8 * kg);
+  for (int g = 0; g < 4; ++g) r.q[g] = gload<uint2>(blk + 16 + 32 * g + 8 * kg);
   return r;
 }
 
 // One Q4_K block: acc += dq S1 - dmq S2 for the lane's (token, row). Per limb r, S1's part sum_j sc_j D_j[r] stays
 // in int32 (|D| <= 32 * 128 * 15, 8 sub-blocks x 63: < 2^25) and S2's part sum_j m_j (sum of the sub-block's
 // digits) is an MFMA accumulation with B = m_j in every byte (|.| <= 8 * 63 * 32 * 128 < 2^21).
-__device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const MoeA& a, bool two, int fw,
+__device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const MoeA& a, int lg, int fw,
                                      Acc128& acc) {
   const uint32_t hb = w.h.x;
   const int64_t dq = fp16_fixed(hb & 0xFFFF, fw), dmq = fp16_fixed(hb >> 16, fw);
@@ -835,9 +896,7 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
     return (int64_t)(((uint64_t)mb << 32) | mb);
   };
   int64_t S1 = 0, S2 = 0;
-#pragma unroll
-  for (int lg = 0; lg < 2; ++lg) {
-    if (lg == 1 && !two) break;
+  {
     v4i M = {0, 0, 0, 0}, T = {0, 0, 0, 0};
     // two halves of four sub-blocks: four independent MFMAs issued back to back, their results consumed after
 #pragma unroll
@@ -846,7 +905,7 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int j = 4 * hh + jj;
-        const int64_t av = moe_a(buf, a, lg, 32 * j);
+        const int64_t av = moe_a(buf, a, 32 * j);
         d[jj] = mfma32(av, bq(j), v4i{0, 0, 0, 0});
         M = mfma32(av, bm(j), M);
       }
@@ -862,67 +921,88 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
   acc_madd(acc, -dmq, S2);
 }
 
+// The token group's activation rows (sel[first + t0 + t], absent tokens repeat the last one) and their largest
+// limb count: two load rounds, all issued at once
+__device__ inline int moe_group_rows(const int* __restrict__ sel, const int* __restrict__ Lrow, int first, int tn,
+                                     int (&prow)[kMoeTok]) {
+#pragma unroll
+  for (int i = 0; i < kMoeTok; ++i) prow[i] = sel[first + (i < tn ? i : tn - 1)];
+  int L = 1;
+#pragma unroll
+  for (int i = 0; i < kMoeTok; ++i) { const int lr = Lrow[prow[i]]; L = lr > L ? lr : L; }
+  return L;
+}
+
+// Step s of a wave's walk: tile s / (np nb), pass (s / nb) mod np, block s mod nb
+struct MoeStep {
+  int rt, p, b;
+};
+__device__ inline MoeStep moe_step(int s, int np, int nb) {
+  const int q = s / nb;
+  return MoeStep{q / np, q - (q / np) * np, s - q * nb};
+}
+
+template <int RT>
 __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
                                                          const int* __restrict__ ppair, const int8_t* __restrict__ xd,
                                                          const int* __restrict__ Lrow, int64_t rows, int64_t K,
                                                          int64_t e_ffn, int fw, int fa, int64_t log2e, int64_t dclip,
                                                          int64_t* __restrict__ gu, int* __restrict__ status,
                                                          const int* __restrict__ wide) {
-  __shared__ __align__(16) int8_t sx[2][kMoeBuf];
-  __shared__ int s_rows[kMoeTok];
+  extern __shared__ __align__(16) int8_t sx[];       // 16 rows x (K + 16)
   if (*wide) return;                                  // the VALU fallback takes this call
   const MoeItem it = items[blockIdx.y];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if ((int64_t)blockIdx.x * 64 >= e_ffn) return;
+  const int64_t r0 = (int64_t)blockIdx.x * 64 * RT;
+  if (r0 >= e_ffn) return;
   const int n = lane & 15, kg = lane >> 4, t = lane >> 4;
-  const int64_t o = (int64_t)blockIdx.x * 64 + wave * 16 + n;
-  const bool orow = o < e_ffn;
-  const int64_t nb = K / 256;
-  const uint8_t* grow = it.wg + (orow ? o : 0) * nb * 144;
-  const uint8_t* urow = it.wu + (orow ? o : 0) * nb * 144;
+  const int nb = (int)(K / 256);
+  const MoeA al = moe_a_lane(lane, K);
+  // weight row of tile rt (rows past e_ffn read row 0 and write nothing)
+  auto orow_of = [&](int rt) { return r0 + rt * 64 + wave * 16 + n; };
+  auto wrow = [&](const uint8_t* base, int rt) {
+    const int64_t o = orow_of(rt < RT ? rt : RT - 1);
+    return base + (o < e_ffn ? o : 0) * nb * 144;
+  };
   for (int t0 = 0; t0 < it.count; t0 += kMoeTok) {
     const int tn = min(kMoeTok, it.count - t0);
-    int L = 1;
-    for (int i = 0; i < tn; ++i) { const int lr = Lrow[ptok[it.first + t0 + i]]; L = lr > L ? lr : L; }
-    __syncthreads();                                  // the previous token group is done with the buffers
-    moe_clear(&sx[0][0], tid, blockDim.x);
-    if (tid < tn) s_rows[tid] = ptok[it.first + t0 + tid];
-    __syncthreads();
-    const MoeA al = moe_a_lane(lane);
-    // one weight slot per projection: block b + 1 is requested as soon as block b has consumed the slot (the
-    // other waves of the SIMD cover the latency; a second slot costs the third wave its registers)
-    Q4Lane gw = q4_lane_load(grow, kg), uw = q4_lane_load(urow, kg);
-    const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
-    moe_store(moe_fetch(pl, 0), pl, &sx[0][0]);
-    __syncthreads();
-    Acc128 ag{0, 0}, au{0, 0};
-    for (int64_t b = 0; b < nb; b += 2) {
-      // even block: LDS buffer 0; block b + 1's digits are fetched meanwhile
-      MoeStage nx{};
-      if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
-      q4_block_mfma(gw, &sx[0][0], al, L > 4, fw, ag);
-      if (b + 1 < nb) gw = q4_lane_load(grow + (b + 1) * 144, kg);
-      q4_block_mfma(uw, &sx[0][0], al, L > 4, fw, au);
-      if (b + 1 < nb) uw = q4_lane_load(urow + (b + 1) * 144, kg);
-      if (b + 1 >= nb) break;
-      moe_store(nx, pl, &sx[1][0]);
-      __syncthreads();
-      // odd block: LDS buffer 1
-      if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
-      q4_block_mfma(gw, &sx[1][0], al, L > 4, fw, ag);
-      if (b + 2 < nb) gw = q4_lane_load(grow + (b + 2) * 144, kg);
-      q4_block_mfma(uw, &sx[1][0], al, L > 4, fw, au);
-      if (b + 2 < nb) uw = q4_lane_load(urow + (b + 2) * 144, kg);
-      if (b + 2 >= nb) break;
-      moe_store(nx, pl, &sx[0][0]);
+    int prow[kMoeTok];
+    const int L = moe_group_rows(ptok, Lrow, it.first + t0, tn, prow);
+    const int np = L > 4 ? 2 : 1;
+    // one weight slot per projection, the first requested before the staging: step s + 1's block is requested as
+    // soon as step s has consumed the slot (the other waves of the SIMD cover the latency)
+    Q4Lane gw = q4_lane_load(wrow(it.wg, 0), kg), uw = q4_lane_load(wrow(it.wu, 0), kg);
+    __syncthreads();                                  // the previous token group is done with the buffer
+    if (np == 1) {
+      moe_stage(sx, prow, tn, L, 0, xd, rows, K, tid, blockDim.x);
       __syncthreads();
     }
-    if (orow && t < tn) {
-      bool f1, f2, f3;
-      const int64_t gy = acc_shift(ag, fw, &f1), uy = acc_shift(au, fw, &f2);
-      const int64_t v = nmc_silu_mul(gy, uy, fa, log2e, dclip, &f3);
-      if (!(f1 && f2 && f3)) atomicOr(status, IMIE_EOVF);
-      gu[(int64_t)ppair[it.first + t0 + t] * e_ffn + o] = v;
+    Acc128 ag{0, 0}, au{0, 0};
+    const int nsteps = RT * np * nb;
+    for (int s = 0; s < nsteps; ++s) {
+      const MoeStep c = moe_step(s, np, nb), nx = moe_step(s + 1, np, nb);
+      if (np == 2 && c.b == 0) {                      // two passes: this tile's limbs 4 p .. 4 p + 3
+        __syncthreads();
+        moe_stage(sx, prow, tn, L, c.p, xd, rows, K, tid, blockDim.x);
+        __syncthreads();
+      }
+      const int8_t* buf = sx + 256 * c.b;
+      q4_block_mfma(gw, buf, al, c.p, fw, ag);
+      gw = q4_lane_load(wrow(it.wg, nx.rt) + nx.b * 144, kg);
+      q4_block_mfma(uw, buf, al, c.p, fw, au);
+      uw = q4_lane_load(wrow(it.wu, nx.rt) + nx.b * 144, kg);
+      if (c.b == nb - 1 && c.p == np - 1) {           // tile c.rt complete
+        const int64_t o = orow_of(c.rt);
+        if (o < e_ffn && t < tn) {
+          bool f1, f2, f3;
+          const int64_t gy = acc_shift(ag, fw, &f1), uy = acc_shift(au, fw, &f2);
+          const int64_t v = nmc_silu_mul(gy, uy, fa, log2e, dclip, &f3);
+          if (!(f1 && f2 && f3)) atomicOr(status, IMIE_EOVF);
+          gu[(int64_t)ppair[it.first + t0 + t] * e_ffn + o] = v;
+        }
+        ag = Acc128{0, 0};
+        au = Acc128{0, 0};
+      }
     }
   }
 }
@@ -941,26 +1021,24 @@ __device__ inline Q6Lane q6_lane_load(const uint8_t* blk, int kg) {
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
 #pragma unroll
-    for (int o = 0; o < 2; ++o) r.l[half][o] = *(const uint2*)(blk + 64 * half + 32 * o + 8 * kg);
-    r.h[half] = *(const uint2*)(blk + 128 + 32 * half + 8 * kg);
+    for (int o = 0; o < 2; ++o) r.l[half][o] = gload<uint2>(blk + 64 * half + 32 * o + 8 * kg);
+    r.h[half] = gload<uint2>(blk + 128 + 32 * half + 8 * kg);
   }
-  r.sc = *(const uint4*)(blk + 192);
-  r.d = (uint32_t)blk[208] | ((uint32_t)blk[209] << 8);
+  r.sc = gload<uint4>(blk + 192);
+  r.d = (uint32_t)gload<uint8_t>(blk + 208) | ((uint32_t)gload<uint8_t>(blk + 209) << 8);
   return r;
 }
 
 // One Q6_K block: acc += dq S1; per limb r, sum_j sc_j D_j[r] in int32 (|D| <= 32 * 128 * 32 = 2^17, 16
 // sub-blocks x 128: < 2^28)
-__device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const MoeA& a, bool two, int kg, int fw,
+__device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const MoeA& a, int lg, int kg, int fw,
                                      Acc128& acc) {
   const int64_t dq = fp16_fixed(w.d, fw);
   const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
   auto scs = [&](int i) { return (int)(int8_t)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
   const bool klo = kg < 2;
   int64_t S1 = 0;
-#pragma unroll
-  for (int lg = 0; lg < 2; ++lg) {
-    if (lg == 1 && !two) break;
+  {
     v4i T = {0, 0, 0, 0};
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -977,7 +1055,7 @@ __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const M
         const int64_t bq = (int64_t)(((uint64_t)v1 << 32) | v0);
         const int p0 = 128 * half + 32 * qq;
         // the K step spans sub-blocks 8 half + 2 qq (K groups 0, 1) and + 1 (K groups 2, 3)
-        const int64_t av = moe_a(buf, a, lg, p0);
+        const int64_t av = moe_a(buf, a, p0);
         d[qq][0] = mfma32(klo ? av : 0, bq, v4i{0, 0, 0, 0});
         d[qq][1] = mfma32(klo ? 0 : av, bq, v4i{0, 0, 0, 0});
       }
@@ -991,6 +1069,13 @@ __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const M
     S1 += limb_sum(T, lg);
   }
   acc_madd(acc, dq, S1);
+}
+
+// One Q6_K block over both staged limb groups of the per-block buffer (limbs 4..7 when two)
+__device__ inline void q6_block_pair(const Q6Lane& w, const int8_t* buf, const MoeA& a, bool two, int kg, int fw,
+                                     Acc128& acc) {
+  q6_block_mfma(w, buf, a, 0, kg, fw, acc);
+  if (two) q6_block_mfma(w, buf + 4 * kMoeTok * kMoeRow, a, 1, kg, fw, acc);
 }
 
 __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ppair,
@@ -1017,7 +1102,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
     moe_clear(&sx[0][0], tid, blockDim.x);
     if (tid < tn) s_rows[tid] = ppair[it.first + t0 + tid];
     __syncthreads();
-    const MoeA al = moe_a_lane(lane);
+    const MoeA al = moe_a_lane(lane, 256);   // the 272-byte rows of one block
     Q6Lane w0 = q6_lane_load(drow, kg), w1 = w0;
     if (nb > 1) w1 = q6_lane_load(drow + 210, kg);
     const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
@@ -1027,13 +1112,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
     for (int64_t b = 0; b < nb; b += 2) {
       MoeStage nx{};
       if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
-      q6_block_mfma(w0, &sx[0][0], al, L > 4, kg, fw, ad);
+      q6_block_pair(w0, &sx[0][0], al, L > 4, kg, fw, ad);
       if (b + 2 < nb) w0 = q6_lane_load(drow + (b + 2) * 210, kg);
       if (b + 1 >= nb) break;
       moe_store(nx, pl, &sx[1][0]);
       __syncthreads();
       if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
-      q6_block_mfma(w1, &sx[1][0], al, L > 4, kg, fw, ad);
+      q6_block_pair(w1, &sx[1][0], al, L > 4, kg, fw, ad);
       if (b + 3 < nb) w1 = q6_lane_load(drow + (b + 3) * 210, kg);
       if (b + 2 >= nb) break;
       moe_store(nx, pl, &sx[0][0]);
@@ -1270,7 +1355,8 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   // only costs a run of the exact fallbacks, whose results equal the fused kernels')
   hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, xsp, lrp,
                      flagA);
-  hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
+  hipLaunchKernelGGL(moe_gateup_kernel<kMoeRtGU>, dim3((unsigned)((e_ffn + 64 * kMoeRtGU - 1) / (64 * kMoeRtGU)),
+                     (unsigned)ne), dim3(256), moe_lds_bytes(d_model), st, d_items,
                      d_pt, d_pp, xdp, lrp, (int64_t)m, d_model, e_ffn, fw, fa, log2e, dclip, gb, status, flagA);
   // exact VALU fallback of the gate/up stage (runs only when the prep flagged a wide activation row)
   const int64_t ntg = (e_ffn + kRows - 1) / kRows;
