@@ -673,21 +673,22 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
 // recombined once per block into int64 (|x| < 127 (256^5-1)/255: |S1| < 2^57, |S2| < 2^53), and each 256-block
 // adds dq S1 - dmq S2 into a 128-bit (hi, lo) accumulator with one 64 x 64 -> 128 multiply per term. MFMA sums are
 // exact: |D| <= 32 * 128 * 32 < 2^31.
-// gate/up: workgroup = (64 RT weight rows, item), wave = RT tiles of 16 rows. Per token group the digit rows of up
-// to four limbs over the whole K are staged in LDS once (one barrier), and each wave then walks its tiles' blocks
-// with the next block's weights in flight and no barrier in the loop; a token group with more than four limbs
-// stages limbs 0..3 and 4..7 in turn per tile (two passes over the tile's weights).
+// gate/up: workgroup = (64 weight rows, item), wave = 16 rows. Up to eight tokens share one walk over the weights:
+// with at most four limbs, two token groups of four are staged (32 digit rows, K in two halves, one barrier each)
+// and every block's decode (scales, mins, nibbles) feeds both groups' MFMAs; otherwise one group of four at a time
+// stages its rows over the whole K (limbs 0..3, then 4..7 in a second pass when there are more than four). The
+// block loop has no barrier; the next block's weights are in flight while a block computes.
 // down (K of a few blocks): workgroup = (64 weight rows, item); the block loop is software-pipelined, the next
 // block's digits going to the other half of an LDS double buffer while a block computes.
 // ---------------------------------------------------------------------------------------------------------
 constexpr int kMoeTok = 4;         // tokens per MFMA row group (4 tokens x 4 limbs = 16 rows)
-constexpr int kMoeRtGU = 1;        // 16-row weight tiles per wave of the gate/up kernel (config 4: 1 is fastest)
 // LDS row stride of the staged digits: K + 16 bytes (K a multiple of 256). A lane of row r (of the 16 (token, limb)
 // rows) and K group kg reads 8 bytes at r (K + 16) + 8 kg + 32 j, i.e. 8-byte slot 2 r + kg (mod 32): the 32 lanes
 // of a half-wave hit 32 distinct slots (with a K-byte stride all 16 rows of a K group shared one slot: 16-way bank
 // conflicts).
 __host__ __device__ inline int64_t moe_kp(int64_t K) { return K + 16; }
-__host__ __device__ inline size_t moe_lds_bytes(int64_t K) { return (size_t)(4 * kMoeTok) * (size_t)moe_kp(K); }
+// gate/up staging: 16 rows x (K + 16) (one token group) or 32 rows x (K / 2 + 16) (two groups, K in halves)
+__host__ __device__ inline size_t moe_lds_bytes(int64_t K) { return (size_t)16 * (size_t)K + 512; }
 
 struct MoeItem {
   const uint8_t* wg;        // gate (Q4_K), up (Q4_K), down (Q6_K) of the expert
@@ -783,23 +784,26 @@ __device__ inline void moe_clear(int8_t* sx, int tid, int nt) {
   for (int i = tid; i < 2 * kMoeBuf / 16; i += nt) ((uint4*)sx)[i] = uint4{0, 0, 0, 0};
 }
 
-// Stage limbs 4 p .. 4 p + 3 of the token group's activation rows over the whole K into LDS row [l][t] (l = limb
-// within the pass, t = token): 16 rows x K / 16 chunks of 16 bytes, the loads of four chunks per thread issued
-// before their stores. Rows of absent tokens (t >= tn) or limbs (4 p + l >= L) are written as zeros, so the MFMA
-// A operands need no selects. The caller synchronizes before (buffer free) and after (rows visible).
-__device__ inline void moe_stage(int8_t* sx, const int (&prow)[kMoeTok], int tn, int L, int p,
-                                 const int8_t* __restrict__ xd, int64_t rows, int64_t K, int tid, int nt) {
-  const int cpr = (int)(K >> 4), total = 16 * cpr;
-  const int64_t kp = moe_kp(K);
+// Stage limbs 4 p .. 4 p + 3 of up to 8 tokens' activation rows, K positions kbeg .. kbeg + klen, into LDS row
+// r = 16 grp + 4 l + t (token 4 grp + t, limb 4 p + l) at stride kp: 16 ngrp rows x klen / 16 chunks of 16 bytes, the
+// loads of four chunks per thread issued before their stores. Rows of absent tokens (>= tn) or limbs (>= L) are
+// written as zeros, so the MFMA A operands need no selects. The caller synchronizes before (buffer free) and after
+// (rows visible).
+__device__ inline void moe_stage(int8_t* sx, const int (&prow)[2 * kMoeTok], int tn, int L, int p, int ngrp,
+                                 int64_t kbeg, int64_t klen, int64_t kp, const int8_t* __restrict__ xd, int64_t rows,
+                                 int64_t K, int tid, int nt) {
+  const int cpr = (int)(klen >> 4), total = 16 * ngrp * cpr;
   for (int i0 = tid; i0 < total; i0 += 4 * nt) {
     uint4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * nt;
-      const int r = i / cpr, c = i - r * cpr, l = r >> 2, t = r & 3;
-      const bool on = i < total && t < tn && 4 * p + l < L;
-      const int pr = t == 0 ? prow[0] : t == 1 ? prow[1] : t == 2 ? prow[2] : prow[3];
-      v[u] = on ? *(const uint4*)(xd + ((int64_t)(4 * p + l) * rows + pr) * K + 16 * c) : uint4{0, 0, 0, 0};
+      const int r = i / cpr, c = i - r * cpr, l = (r >> 2) & 3, tok = 4 * (r >> 4) + (r & 3);
+      const bool on = i < total && tok < tn && 4 * p + l < L;
+      int pr = prow[0];
+#pragma unroll
+      for (int q = 1; q < 2 * kMoeTok; ++q) pr = tok == q ? prow[q] : pr;
+      v[u] = on ? *(const uint4*)(xd + ((int64_t)(4 * p + l) * rows + pr) * K + kbeg + 16 * c) : uint4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -816,10 +820,10 @@ __device__ inline void moe_stage(int8_t* sx, const int (&prow)[kMoeTok], int tn,
 struct MoeA {
   int off;                  // byte offset of [l][t][8 kg]
 };
-__device__ inline MoeA moe_a_lane(int lane, int64_t K) {
+__device__ inline MoeA moe_a_lane(int lane, int64_t kp) {
   const int m = lane & 15, kg = lane >> 4, t = m >> 2, l = m & 3;
   MoeA r;
-  r.off = (l * kMoeTok + t) * (int)moe_kp(K) + 8 * kg;
+  r.off = (l * kMoeTok + t) * (int)kp + 8 * kg;
   return r;
 }
 // A operand at K position p0 (buf points at the block's first position)
@@ -871,8 +875,9 @@ __device__ inline Q4Lane q4_lane_load(const uint8_t* blk, int kg) {
 // One Q4_K block: acc += dq S1 - dmq S2 for the lane's (token, row). Per limb r, S1's part sum_j sc_j D_j[r] stays
 // in int32 (|D| <= 32 * 128 * 15, 8 sub-blocks x 63: < 2^25) and S2's part sum_j m_j (sum of the sub-block's
 // digits) is an MFMA accumulation with B = m_j in every byte (|.| <= 8 * 63 * 32 * 128 < 2^21).
-__device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const MoeA& a, int lg, int fw,
-                                     Acc128& acc) {
+template <int NG>
+__device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, int gstride, const MoeA& a, int lg, int fw,
+                                     Acc128 (&acc)[NG], bool two) {
   const uint32_t hb = w.h.x;
   const int64_t dq = fp16_fixed(hb & 0xFFFF, fw), dmq = fp16_fixed(hb >> 16, fw);
   const uint32_t scw[3] = {w.h.y, w.h.z, w.h.w};
@@ -895,8 +900,11 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
     const uint32_t mb = __builtin_amdgcn_perm(0u, (uint32_t)mn[j], 0u);   // byte 0 in all four bytes
     return (int64_t)(((uint64_t)mb << 32) | mb);
   };
-  int64_t S1 = 0, S2 = 0;
-  {
+  // the weight decode above is shared by the NG token groups (16 MFMA rows each, gstride bytes apart in LDS)
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    if (gi > 0 && !two) break;                        // wave-uniform
+    const int8_t* gb = buf + gi * gstride;
     v4i M = {0, 0, 0, 0}, T = {0, 0, 0, 0};
     // two halves of four sub-blocks: four independent MFMAs issued back to back, their results consumed after
 #pragma unroll
@@ -905,7 +913,7 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int j = 4 * hh + jj;
-        const int64_t av = moe_a(buf, a, 32 * j);
+        const int64_t av = moe_a(gb, a, 32 * j);
         d[jj] = mfma32(av, bq(j), v4i{0, 0, 0, 0});
         M = mfma32(av, bm(j), M);
       }
@@ -914,95 +922,112 @@ __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, const M
 #pragma unroll
         for (int r = 0; r < 4; ++r) T[r] += __mul24(sc[4 * hh + jj], d[jj][r]);   // 24-bit: |sc| < 2^6, |D| < 2^17
     }
-    S1 += limb_sum(T, lg);
-    S2 += limb_sum(M, lg);
+    acc_madd(acc[gi], dq, limb_sum(T, lg));
+    acc_madd(acc[gi], -dmq, limb_sum(M, lg));
   }
-  acc_madd(acc, dq, S1);
-  acc_madd(acc, -dmq, S2);
 }
 
-// The token group's activation rows (sel[first + t0 + t], absent tokens repeat the last one) and their largest
-// limb count: two load rounds, all issued at once
+// The token groups' activation rows (sel[first + t], absent tokens repeat the last one) and their limb counts
+// (two load rounds, all issued at once); returns the largest
 __device__ inline int moe_group_rows(const int* __restrict__ sel, const int* __restrict__ Lrow, int first, int tn,
-                                     int (&prow)[kMoeTok]) {
+                                     int (&prow)[2 * kMoeTok], int (&lr)[2 * kMoeTok]) {
 #pragma unroll
-  for (int i = 0; i < kMoeTok; ++i) prow[i] = sel[first + (i < tn ? i : tn - 1)];
+  for (int i = 0; i < 2 * kMoeTok; ++i) prow[i] = sel[first + (i < tn ? i : tn - 1)];
   int L = 1;
 #pragma unroll
-  for (int i = 0; i < kMoeTok; ++i) { const int lr = Lrow[prow[i]]; L = lr > L ? lr : L; }
+  for (int i = 0; i < 2 * kMoeTok; ++i) { lr[i] = Lrow[prow[i]]; L = lr[i] > L ? lr[i] : L; }
   return L;
 }
 
-// Step s of a wave's walk: tile s / (np nb), pass (s / nb) mod np, block s mod nb
-struct MoeStep {
-  int rt, p, b;
-};
-__device__ inline MoeStep moe_step(int s, int np, int nb) {
-  const int q = s / nb;
-  return MoeStep{q / np, q - (q / np) * np, s - q * nb};
-}
-
-template <int RT>
-__global__ __launch_bounds__(256, 3) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
+__global__ __launch_bounds__(256, 2) void moe_gateup_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ptok,
                                                          const int* __restrict__ ppair, const int8_t* __restrict__ xd,
                                                          const int* __restrict__ Lrow, int64_t rows, int64_t K,
                                                          int64_t e_ffn, int fw, int fa, int64_t log2e, int64_t dclip,
                                                          int64_t* __restrict__ gu, int* __restrict__ status,
                                                          const int* __restrict__ wide) {
-  extern __shared__ __align__(16) int8_t sx[];       // 16 rows x (K + 16)
+  extern __shared__ __align__(16) int8_t sx[];       // moe_lds_bytes(K)
   if (*wide) return;                                  // the VALU fallback takes this call
   const MoeItem it = items[blockIdx.y];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t r0 = (int64_t)blockIdx.x * 64 * RT;
-  if (r0 >= e_ffn) return;
+  if ((int64_t)blockIdx.x * 64 >= e_ffn) return;
   const int n = lane & 15, kg = lane >> 4, t = lane >> 4;
   const int nb = (int)(K / 256);
-  const MoeA al = moe_a_lane(lane, K);
-  // weight row of tile rt (rows past e_ffn read row 0 and write nothing)
-  auto orow_of = [&](int rt) { return r0 + rt * 64 + wave * 16 + n; };
-  auto wrow = [&](const uint8_t* base, int rt) {
-    const int64_t o = orow_of(rt < RT ? rt : RT - 1);
-    return base + (o < e_ffn ? o : 0) * nb * 144;
+  const int64_t o = (int64_t)blockIdx.x * 64 + wave * 16 + n;
+  const bool orow = o < e_ffn;
+  const uint8_t* grow = it.wg + (orow ? o : 0) * nb * 144;
+  const uint8_t* urow = it.wu + (orow ? o : 0) * nb * 144;
+  auto emit = [&](const Acc128& ag, const Acc128& au, int tok) {
+    bool f1, f2, f3;
+    const int64_t gy = acc_shift(ag, fw, &f1), uy = acc_shift(au, fw, &f2);
+    const int64_t v = nmc_silu_mul(gy, uy, fa, log2e, dclip, &f3);
+    if (!(f1 && f2 && f3)) atomicOr(status, IMIE_EOVF);
+    gu[(int64_t)ppair[it.first + tok] * e_ffn + o] = v;
   };
-  for (int t0 = 0; t0 < it.count; t0 += kMoeTok) {
-    const int tn = min(kMoeTok, it.count - t0);
-    int prow[kMoeTok];
-    const int L = moe_group_rows(ptok, Lrow, it.first + t0, tn, prow);
-    const int np = L > 4 ? 2 : 1;
-    // one weight slot per projection, the first requested before the staging: step s + 1's block is requested as
-    // soon as step s has consumed the slot (the other waves of the SIMD cover the latency)
-    Q4Lane gw = q4_lane_load(wrow(it.wg, 0), kg), uw = q4_lane_load(wrow(it.wu, 0), kg);
-    __syncthreads();                                  // the previous token group is done with the buffer
-    if (np == 1) {
-      moe_stage(sx, prow, tn, L, 0, xd, rows, K, tid, blockDim.x);
-      __syncthreads();
-    }
-    Acc128 ag{0, 0}, au{0, 0};
-    const int nsteps = RT * np * nb;
-    for (int s = 0; s < nsteps; ++s) {
-      const MoeStep c = moe_step(s, np, nb), nx = moe_step(s + 1, np, nb);
-      if (np == 2 && c.b == 0) {                      // two passes: this tile's limbs 4 p .. 4 p + 3
+  for (int t0 = 0; t0 < it.count; t0 += 2 * kMoeTok) {
+    const int tn8 = min(2 * kMoeTok, it.count - t0);
+    int prow[2 * kMoeTok], lr[2 * kMoeTok];
+    const int L8 = moe_group_rows(ptok, Lrow, it.first + t0, tn8, prow, lr);
+    // one weight slot per projection, the first requested before the staging: block b + 1 is requested as soon as
+    // block b has consumed the slot (the other waves of the SIMD cover the latency)
+    Q4Lane gw = q4_lane_load(grow, kg), uw = q4_lane_load(urow, kg);
+    if (tn8 > kMoeTok && L8 <= 4 && (nb & 1) == 0) {
+      // two token groups of four in one walk over the weights (the block decode shared): K staged in halves of
+      // 32 rows x (K / 2 + 16)
+      const int64_t kp = K / 2 + 16;
+      const MoeA al = moe_a_lane(lane, kp);
+      Acc128 ag[2] = {{0, 0}, {0, 0}}, au[2] = {{0, 0}, {0, 0}};
+      for (int h = 0; h < 2; ++h) {
+        __syncthreads();                              // the buffer is free
+        moe_stage(sx, prow, tn8, L8, 0, 2, h * (K / 2), K / 2, kp, xd, rows, K, tid, blockDim.x);
         __syncthreads();
-        moe_stage(sx, prow, tn, L, c.p, xd, rows, K, tid, blockDim.x);
-        __syncthreads();
-      }
-      const int8_t* buf = sx + 256 * c.b;
-      q4_block_mfma(gw, buf, al, c.p, fw, ag);
-      gw = q4_lane_load(wrow(it.wg, nx.rt) + nx.b * 144, kg);
-      q4_block_mfma(uw, buf, al, c.p, fw, au);
-      uw = q4_lane_load(wrow(it.wu, nx.rt) + nx.b * 144, kg);
-      if (c.b == nb - 1 && c.p == np - 1) {           // tile c.rt complete
-        const int64_t o = orow_of(c.rt);
-        if (o < e_ffn && t < tn) {
-          bool f1, f2, f3;
-          const int64_t gy = acc_shift(ag, fw, &f1), uy = acc_shift(au, fw, &f2);
-          const int64_t v = nmc_silu_mul(gy, uy, fa, log2e, dclip, &f3);
-          if (!(f1 && f2 && f3)) atomicOr(status, IMIE_EOVF);
-          gu[(int64_t)ppair[it.first + t0 + t] * e_ffn + o] = v;
+        for (int bb = 0; bb < nb / 2; ++bb) {
+          const int b = h * (nb / 2) + bb, bn = b + 1 < nb ? b + 1 : b;
+          const int8_t* buf = sx + 256 * bb;
+          q4_block_mfma<2>(gw, buf, (int)(16 * kp), al, 0, fw, ag, true);
+          gw = q4_lane_load(grow + bn * 144, kg);
+          q4_block_mfma<2>(uw, buf, (int)(16 * kp), al, 0, fw, au, true);
+          uw = q4_lane_load(urow + bn * 144, kg);
         }
-        ag = Acc128{0, 0};
-        au = Acc128{0, 0};
       }
+      if (orow) {
+        emit(ag[0], au[0], t0 + t);
+        if (kMoeTok + t < tn8) emit(ag[1], au[1], t0 + kMoeTok + t);
+      }
+      continue;
+    }
+    // one token group of four at a time; more than four limbs take two passes per group (limbs 0..3, 4..7)
+    const int64_t kp = K + 16;
+    const MoeA al = moe_a_lane(lane, kp);
+    for (int s0 = 0; s0 < tn8; s0 += kMoeTok) {
+      const int tn = min(kMoeTok, tn8 - s0);
+      int pr4[2 * kMoeTok];
+      int L = 1;
+#pragma unroll
+      for (int i = 0; i < 2 * kMoeTok; ++i) {
+        const int q = s0 + (i < tn ? i : tn - 1);
+        int v = prow[0], lv = lr[0];
+#pragma unroll
+        for (int z = 1; z < 2 * kMoeTok; ++z) { v = q == z ? prow[z] : v; lv = q == z ? lr[z] : lv; }
+        pr4[i] = v;
+        L = i < tn && lv > L ? lv : L;
+      }
+      const int np = L > 4 ? 2 : 1;
+      Acc128 ag[1] = {{0, 0}}, au[1] = {{0, 0}};
+      for (int p = 0; p < np; ++p) {
+        __syncthreads();                              // the buffer is free
+        moe_stage(sx, pr4, tn, L, p, 1, 0, K, kp, xd, rows, K, tid, blockDim.x);
+        __syncthreads();
+        for (int b = 0; b < nb; ++b) {
+          // the next block of this walk: this group's next pass or the following group start again at block 0
+          const int bn = b + 1 < nb ? b + 1 : 0;
+          const int8_t* buf = sx + 256 * b;
+          q4_block_mfma<1>(gw, buf, 0, al, p, fw, ag, false);
+          gw = q4_lane_load(grow + bn * 144, kg);
+          q4_block_mfma<1>(uw, buf, 0, al, p, fw, au, false);
+          uw = q4_lane_load(urow + bn * 144, kg);
+        }
+      }
+      if (orow && t < tn) emit(ag[0], au[0], t0 + s0 + t);
     }
   }
 }
@@ -1102,7 +1127,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
     moe_clear(&sx[0][0], tid, blockDim.x);
     if (tid < tn) s_rows[tid] = ppair[it.first + t0 + tid];
     __syncthreads();
-    const MoeA al = moe_a_lane(lane, 256);   // the 272-byte rows of one block
+    const MoeA al = moe_a_lane(lane, kMoeRow);
     Q6Lane w0 = q6_lane_load(drow, kg), w1 = w0;
     if (nb > 1) w1 = q6_lane_load(drow + 210, kg);
     const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
@@ -1355,7 +1380,7 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   // only costs a run of the exact fallbacks, whose results equal the fused kernels')
   hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, xsp, lrp,
                      flagA);
-  hipLaunchKernelGGL(moe_gateup_kernel<kMoeRtGU>, dim3((unsigned)((e_ffn + 64 * kMoeRtGU - 1) / (64 * kMoeRtGU)),
+  hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64),
                      (unsigned)ne), dim3(256), moe_lds_bytes(d_model), st, d_items,
                      d_pt, d_pp, xdp, lrp, (int64_t)m, d_model, e_ffn, fw, fa, log2e, dclip, gb, status, flagA);
   // exact VALU fallback of the gate/up stage (runs only when the prep flagged a wide activation row)
