@@ -679,7 +679,9 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
 // stages its rows over the whole K (limbs 0..3, then 4..7 in a second pass when there are more than four). The
 // block loop has no barrier; the next block's weights are in flight while a block computes.
 // down (K of a few blocks): workgroup = (64 weight rows, item); the block loop is software-pipelined, the next
-// block's digits going to the other half of an LDS double buffer while a block computes.
+// block's digits going to the other half of an LDS double buffer while a block computes. The buffer's second
+// 16-row group holds tokens 4..7 (up to eight tokens of at most four limbs share each block's unpacked weights)
+// or limbs 4..7 of up to four tokens.
 // ---------------------------------------------------------------------------------------------------------
 constexpr int kMoeTok = 4;         // tokens per MFMA row group (4 tokens x 4 limbs = 16 rows)
 // LDS row stride of the staged digits: K + 16 bytes (K a multiple of 256). A lane of row r (of the 16 (token, limb)
@@ -760,7 +762,9 @@ __device__ inline MoePlan moe_plan(const int* rowsel, int tn, int L, const int8_
     p.on[k] = i < n;
     const int l = p.on[k] ? i / (tn * 16) : 0, rem = i - l * (tn * 16), t = p.on[k] ? rem >> 4 : 0, c = rem & 15;
     p.src[k] = xd + ((int64_t)l * rows + rowsel[t]) * K + 16 * c;
-    p.dst[k] = (l * kMoeTok + t) * kMoeRow + 16 * c;
+    // row 16 gi + 4 (l mod 4) + (t mod 4): the second 16-row group holds limbs 4..7 (tn <= 4) or tokens 4..7 (L <= 4)
+    const int gi = (l >= 4 || t >= kMoeTok) ? 1 : 0;
+    p.dst[k] = (16 * gi + 4 * (l & 3) + (t & 3)) * kMoeRow + 16 * c;
   }
   return p;
 }
@@ -1056,14 +1060,31 @@ __device__ inline Q6Lane q6_lane_load(const uint8_t* blk, int kg) {
 
 // One Q6_K block: acc += dq S1; per limb r, sum_j sc_j D_j[r] in int32 (|D| <= 32 * 128 * 32 = 2^17, 16
 // sub-blocks x 128: < 2^28)
-__device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const MoeA& a, int lg, int kg, int fw,
-                                     Acc128& acc) {
+// The second group (gstride bytes further in LDS) is either limbs 4..7 of the same tokens (added into acc0 with
+// lg1 = 1) or limbs 0..3 of four more tokens (acc1, lg1 = 0); the block's unpacked weights and scales serve both.
+__device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, int gstride, const MoeA& a, int kg, int fw,
+                                     Acc128& acc0, Acc128& acc1, int lg1, bool two) {
   const int64_t dq = fp16_fixed(w.d, fw);
   const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
   auto scs = [&](int i) { return (int)(int8_t)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
   const bool klo = kg < 2;
-  int64_t S1 = 0;
-  {
+  int64_t bq[2][4];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const uint2 lv = w.l[half][qq & 1], hv = w.h[half];
+      const int sl = qq >= 2 ? 4 : 0, sh = 2 * qq;
+      uint32_t v0 = ((lv.x >> sl) & 0x0F0F0F0Fu) | (((hv.x >> sh) & 0x03030303u) << 4);
+      uint32_t v1 = ((lv.y >> sl) & 0x0F0F0F0Fu) | (((hv.y >> sh) & 0x03030303u) << 4);
+      v0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise q6 - 32 as int8
+      v1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+      bq[half][qq] = (int64_t)(((uint64_t)v1 << 32) | v0);
+    }
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    if (gi == 1 && !two) break;                       // wave-uniform
+    const int8_t* gb = buf + gi * gstride;
     v4i T = {0, 0, 0, 0};
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -1071,18 +1092,10 @@ __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const M
       v4i d[4][2];
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const uint2 lv = w.l[half][qq & 1], hv = w.h[half];
-        const int sl = qq >= 2 ? 4 : 0, sh = 2 * qq;
-        uint32_t v0 = ((lv.x >> sl) & 0x0F0F0F0Fu) | (((hv.x >> sh) & 0x03030303u) << 4);
-        uint32_t v1 = ((lv.y >> sl) & 0x0F0F0F0Fu) | (((hv.y >> sh) & 0x03030303u) << 4);
-        v0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise q6 - 32 as int8
-        v1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-        const int64_t bq = (int64_t)(((uint64_t)v1 << 32) | v0);
-        const int p0 = 128 * half + 32 * qq;
         // the K step spans sub-blocks 8 half + 2 qq (K groups 0, 1) and + 1 (K groups 2, 3)
-        const int64_t av = moe_a(buf, a, p0);
-        d[qq][0] = mfma32(klo ? av : 0, bq, v4i{0, 0, 0, 0});
-        d[qq][1] = mfma32(klo ? 0 : av, bq, v4i{0, 0, 0, 0});
+        const int64_t av = moe_a(gb, a, 128 * half + 32 * qq);
+        d[qq][0] = mfma32(klo ? av : 0, bq[half][qq], v4i{0, 0, 0, 0});
+        d[qq][1] = mfma32(klo ? 0 : av, bq[half][qq], v4i{0, 0, 0, 0});
       }
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
@@ -1091,16 +1104,9 @@ __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, const M
         for (int r = 0; r < 4; ++r) T[r] += __mul24(s0, d[qq][0][r]) + __mul24(s1, d[qq][1][r]);   // |s| < 2^8, |D| < 2^18
       }
     }
-    S1 += limb_sum(T, lg);
+    if (gi == 0) acc_madd(acc0, dq, limb_sum(T, 0));
+    else acc_madd(acc1, dq, limb_sum(T, lg1));
   }
-  acc_madd(acc, dq, S1);
-}
-
-// One Q6_K block over both staged limb groups of the per-block buffer (limbs 4..7 when two)
-__device__ inline void q6_block_pair(const Q6Lane& w, const int8_t* buf, const MoeA& a, bool two, int kg, int fw,
-                                     Acc128& acc) {
-  q6_block_mfma(w, buf, a, 0, kg, fw, acc);
-  if (two) q6_block_mfma(w, buf + 4 * kMoeTok * kMoeRow, a, 1, kg, fw, acc);
 }
 
 __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict__ items, const int* __restrict__ ppair,
@@ -1109,7 +1115,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
                                                        int64_t d_model, int fw, int64_t* __restrict__ dout,
                                                        int* __restrict__ status, const int* __restrict__ wide) {
   __shared__ __align__(16) int8_t sx[2][kMoeBuf];
-  __shared__ int s_rows[kMoeTok];
+  __shared__ int s_rows[2 * kMoeTok];
   if (*wide) return;
   const MoeItem it = items[blockIdx.y];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1119,10 +1125,18 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
   const bool orow = o < d_model;
   const int64_t nb = K / 256;
   const uint8_t* drow = it.wd + (orow ? o : 0) * nb * 210;
-  for (int t0 = 0; t0 < it.count; t0 += kMoeTok) {
-    const int tn = min(kMoeTok, it.count - t0);
-    int L = 1;
-    for (int i = 0; i < tn; ++i) { const int lr = Lrow[ppair[it.first + t0 + i]]; L = lr > L ? lr : L; }
+  for (int t0 = 0; t0 < it.count;) {
+    // up to eight tokens with at most four limbs (the second 16-row group holds tokens 4..7), else up to four
+    // tokens (the second group holds limbs 4..7 when there are more than four)
+    const int tn8 = min(2 * kMoeTok, it.count - t0);
+    int L4 = 1, L8 = 1;
+    for (int i = 0; i < tn8; ++i) {
+      const int lr = Lrow[ppair[it.first + t0 + i]];
+      L8 = lr > L8 ? lr : L8;
+      if (i < kMoeTok) L4 = L8;
+    }
+    const bool tok2 = tn8 > kMoeTok && L8 <= 4;
+    const int tn = tok2 ? tn8 : min(kMoeTok, tn8), L = tok2 ? L8 : L4;
     __syncthreads();                                  // the previous token group is done with the buffers
     moe_clear(&sx[0][0], tid, blockDim.x);
     if (tid < tn) s_rows[tid] = ppair[it.first + t0 + tid];
@@ -1133,17 +1147,21 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
     const MoePlan pl = moe_plan(s_rows, tn, L, xd, rows, K, tid);
     moe_store(moe_fetch(pl, 0), pl, &sx[0][0]);
     __syncthreads();
-    Acc128 ad{0, 0};
+    Acc128 ad{0, 0}, ad1{0, 0};
+    Acc128& a2 = tok2 ? ad1 : ad;
+    const int lg1 = tok2 ? 0 : 1;
+    const bool two = tok2 || L > 4;
+    constexpr int gstride = 4 * kMoeTok * kMoeRow;
     for (int64_t b = 0; b < nb; b += 2) {
       MoeStage nx{};
       if (b + 1 < nb) nx = moe_fetch(pl, b + 1);
-      q6_block_pair(w0, &sx[0][0], al, L > 4, kg, fw, ad);
+      q6_block_mfma(w0, &sx[0][0], gstride, al, kg, fw, ad, a2, lg1, two);
       if (b + 2 < nb) w0 = q6_lane_load(drow + (b + 2) * 210, kg);
       if (b + 1 >= nb) break;
       moe_store(nx, pl, &sx[1][0]);
       __syncthreads();
       if (b + 2 < nb) nx = moe_fetch(pl, b + 2);
-      q6_block_pair(w1, &sx[1][0], al, L > 4, kg, fw, ad);
+      q6_block_mfma(w1, &sx[1][0], gstride, al, kg, fw, ad, a2, lg1, two);
       if (b + 3 < nb) w1 = q6_lane_load(drow + (b + 3) * 210, kg);
       if (b + 2 >= nb) break;
       moe_store(nx, pl, &sx[0][0]);
@@ -1155,6 +1173,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const MoeItem* __restrict
       if (!f) atomicOr(status, IMIE_EOVF);
       dout[(int64_t)ppair[it.first + t0 + t] * d_model + o] = y;
     }
+    if (orow && tok2 && kMoeTok + t < tn) {
+      bool f;
+      const int64_t y = acc_shift(ad1, fw, &f);
+      if (!f) atomicOr(status, IMIE_EOVF);
+      dout[(int64_t)ppair[it.first + t0 + kMoeTok + t] * d_model + o] = y;
+    }
+    t0 += tn;
   }
 }
 
