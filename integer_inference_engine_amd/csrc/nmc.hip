@@ -332,19 +332,45 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const int64_t* __restrict_
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint64_t mx = 0;
-  for (int64_t c = tid; c < K; c += 256) {
-    int64_t v = X[r * K + c];
-    const uint64_t a = imie_absu64(v);
-    mx = a > mx ? a : mx;
+  // eight consecutive activations per thread: their digits of each limb plane packed into one 64-bit store
+  for (int64_t c0 = 8 * (int64_t)tid; c0 < K; c0 += 8 * 256) {
+    if (c0 + 8 <= K) {
+      int64_t v[8];
 #pragma unroll
-    for (int l = 0; l < kQkLimbs; ++l) {
-      const int64_t dg = ((v + 128) & 255) - 128;
-      v = (int64_t)((uint64_t)v - (uint64_t)dg) >> 8;
-      xd[((int64_t)l * rows + r) * K + c] = (int8_t)dg;
+      for (int e = 0; e < 8; ++e) v[e] = X[r * K + c0 + e];
+      uint64_t pk[kQkLimbs];
+#pragma unroll
+      for (int l = 0; l < kQkLimbs; ++l) pk[l] = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint64_t a = imie_absu64(v[e]);
+        mx = a > mx ? a : mx;
+        int64_t x = v[e];
+#pragma unroll
+        for (int l = 0; l < kQkLimbs; ++l) {
+          const int64_t dg = ((x + 128) & 255) - 128;
+          x = (int64_t)((uint64_t)x - (uint64_t)dg) >> 8;
+          pk[l] |= (uint64_t)(uint8_t)dg << (8 * e);
+        }
+      }
+#pragma unroll
+      for (int l = 0; l < kQkLimbs; ++l) *(uint64_t*)&xd[((int64_t)l * rows + r) * K + c0] = pk[l];
+    } else {
+      for (int64_t c = c0; c < K; ++c) {
+        int64_t v = X[r * K + c];
+        const uint64_t a = imie_absu64(v);
+        mx = a > mx ? a : mx;
+#pragma unroll
+        for (int l = 0; l < kQkLimbs; ++l) {
+          const int64_t dg = ((v + 128) & 255) - 128;
+          v = (int64_t)((uint64_t)v - (uint64_t)dg) >> 8;
+          xd[((int64_t)l * rows + r) * K + c] = (int8_t)dg;
+        }
+      }
     }
   }
-  // sums of 16 consecutive activations (thread per group)
-  for (int64_t gq = tid; gq < K / 16; gq += 256) {
+  // sums of 16 consecutive activations (thread per group; callers whose kernels read no sums pass none)
+  for (int64_t gq = tid; xs16 && gq < K / 16; gq += 256) {
     int64_t sm = 0;
 #pragma unroll
     for (int e = 0; e < 16; ++e) sm = (int64_t)((uint64_t)sm + (uint64_t)X[r * K + 16 * gq + e]);
@@ -1403,7 +1429,8 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   imie_prof_mark(IMIE_K_QK, st, true);
   // the wide-row flags start clear: the previous call's combine kernel cleared them (a fresh or foreign value
   // only costs a run of the exact fallbacks, whose results equal the fused kernels')
-  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, xsp, lrp,
+  // the fused expert kernels read no 16-element sums (their min terms are MFMA accumulations)
+  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)m), dim3(256), 0, st, h_dev, (int64_t)m, d_model, xdp, nullptr, lrp,
                      flagA);
   hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((e_ffn + 63) / 64),
                      (unsigned)ne), dim3(256), moe_lds_bytes(d_model), st, d_items,
@@ -1413,7 +1440,7 @@ int moe_batched(const long long* gate_h, const long long* up_h, const long long*
   hipLaunchKernelGGL(qk_gateup_gated_kernel, dim3(kGatedWgs2), dim3(256), 0, st, d_ig, d_iu, d_pt, d_pp, h_dev,
                      d_model, gb, ub, e_ffn, fw, fa, log2e, dclip, status, flagA, ntg, (int64_t)ne);
   // down over the P rows of gu
-  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)P), dim3(256), 0, st, gb, P, e_ffn, xdp, xsp, lrp, flagB);
+  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)P), dim3(256), 0, st, gb, P, e_ffn, xdp, nullptr, lrp, flagB);
   hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((d_model + 63) / 64), (unsigned)ne), dim3(256), 0, st, d_items,
                      d_pp, xdp, xsp, lrp, P, e_ffn, d_model, fw, db, status, flagB);
   hipLaunchKernelGGL(qk_group_gated_kernel, dim3(kGatedWgs), dim3(256), 0, st, d_id, d_pp, d_pp, gb, e_ffn, db,
