@@ -51,24 +51,20 @@ struct MoeWs {
   int64_t grows = 0;
 } g_mws;
 
+// round(fp16 h * 2^fw) to the nearest integer, ties to even, without branches (lanes of different rows take
+// different exponents): a normal h is (1024 + mant) 2^(e - 25), a subnormal mant 2^-24. A left shift (sh >= 0) is
+// exact; a right shift by s rounds m >> s with the remainder against half; every shift of 12 or more gives 0 (m <
+// 2^11), so s is clamped to 12, as the 32-bit remainder arithmetic needs.
 __device__ inline int64_t fp16_fixed(uint32_t h, int fw) {
-  const int sign = (h >> 15) & 1, e = (h >> 10) & 31;
-  const int64_t mant = h & 0x3FF;
-  int64_t m;
-  int sh;
-  if (e == 0) { m = mant; sh = fw - 24; }
-  else { m = mant | 0x400; sh = e - 25 + fw; }
-  int64_t r;
-  if (sh >= 0) r = m << sh;
-  else {
-    const int s = -sh;
-    if (s >= 63) r = 0;
-    else {
-      const int64_t q = m >> s, rem = m & (((int64_t)1 << s) - 1), half = (int64_t)1 << (s - 1);
-      r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
-    }
-  }
-  return sign ? -r : r;
+  const uint32_t e = (h >> 10) & 31, mant = h & 0x3FF;
+  const uint32_t m = e == 0 ? mant : (mant | 0x400);
+  const int sh = (e == 0 ? 1 : (int)e) - 25 + fw;
+  const int64_t rp = (int64_t)m << (sh > 0 ? sh : 0);
+  const uint32_t s = sh < 0 ? (uint32_t)(-sh < 12 ? -sh : 12) : 1u;
+  const uint32_t q = m >> s, rem = m & ((1u << s) - 1u), half = 1u << (s - 1u);
+  const uint32_t rn = q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+  const int64_t r = sh >= 0 ? rp : (int64_t)rn;
+  return ((h >> 15) & 1) ? -r : r;
 }
 
 struct Item {               // one weight applied to `count` x rows
