@@ -222,12 +222,17 @@ struct Q1Segs {                    // up to kMaxSegs weights (same n_blocks) app
 // PRO != kProNone (one token, R = 1, PF > 0, Lcap = 8): no digit table is read; the workgroup derives its slab
 // range's table from the producer's inputs (pro) into LDS -- element values thread-per-element into s_y, then one
 // wave per slab turns them into digits, limb counts and block totals -- while its weights are in flight.
-template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone, int NT = 256>
+// PERS (one token, one weight, one K range, two-slab pipeline): a grid of about two rounds of resident waves; each
+// wave walks tile groups gi, gi + W, gi + 2W, ... (W waves in the grid), so the digit staging is paid once per
+// workgroup and the pipeline runs on across group boundaries (the next group's first slab is in flight while the
+// current group's last slab computes).
+template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone, int NT = 256, bool PERS = false>
 __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
     Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
     int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, Q1Pro pro) {
   static_assert(PRO == kProNone || (R == 1 && TT == 1 && PF > 0), "prologue: one token, one tile, prefetched range");
   static_assert(PRO != kProNone || NT == 256, "NT: workgroup size of the prologue variants");
+  static_assert(!PERS || (TT == 1 && PF == 0 && PRO == kProNone), "persistent: one token, pipelined slabs");
   extern __shared__ __align__(16) unsigned char smem[];
   uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
@@ -267,10 +272,10 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
   ScT sc[NB][R];
   int Lv[NB][TT];
   int64_t tv[NB][TT];
-  auto load = [&](int buf, int64_t sl) {
+  auto load_t = [&](int buf, int64_t tb, int64_t sl) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t tl = tile0 + r < ntiles ? tile0 + r : tile0;
+      const int64_t tl = tb + r < ntiles ? tb + r : tb;
       const int64_t idx = (tl * nslabs + sl) * 64 + lane;
       const v4i wv = __builtin_nontemporal_load(&((const v4i*)bitsT)[idx]);
       wb[buf][r] = uint4{(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
@@ -284,6 +289,10 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
         tv[buf][t] = totals[(int64_t)t * nbp + sl * kSlabBlocks + g];
       }
   };
+  auto load = [&](int buf, int64_t sl) { load_t(buf, tile0, sl); };
+  // persistent mode: unit u = (group gi_raw + (u / nsl) W, slab s0 + u % nsl)
+  const int64_t W = (int64_t)gridDim.x * (NT / 64);
+  auto load_unit = [&](int buf, int64_t u) { load_t(buf, (gi_raw + (u / nsl) * W) * R, s0 + u % nsl); };
   // A operands of (token t, limb group lg): the 8 bit positions' digit rows, loaded once and shared by the R
   // tiles; from LDS (staged limbs), the global table (limbs beyond Lcap), or the 8-entry zero slot for lanes
   // whose row is not their block or whose limb is beyond the slab's count
@@ -401,7 +410,8 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
     for (int j = 0; j < PF; ++j)
       if (live && j < nsl) load(j, s0 + j);
   } else if (live) {
-    load(0, s0);
+    if (PERS) load_unit(0, 0);
+    else load(0, s0);
   }
   if (PRO != kProNone) {
     __shared__ uint64_t s_red[4 * (NT / 64)];
@@ -518,6 +528,38 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
 
   if (!live) return;
 
+  if (PERS) {
+    // a group's row totals are complete after its last slab: reduce the 4 blocks of each row and store them
+    auto flush = [&](int64_t tb) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        uint64_t v = acc[0][r];
+        v += (uint64_t)__shfl_xor((int64_t)v, 16, 64);
+        v += (uint64_t)__shfl_xor((int64_t)v, 32, 64);
+        const int64_t row = (tb + r) * kTileRows + n;
+        if (g == 0 && tb + r < ntiles && row < N) {
+          if (atomic_out == 2) out[row] = (int64_t)((uint64_t)out[row] + v);
+          else out[row] = (int64_t)v;
+        }
+        acc[0][r] = 0;
+      }
+    };
+    const int64_t ngroups = sg.gbegin[1];
+    const int64_t nu = ((ngroups - 1 - gi_raw) / W + 1) * nsl;   // live: gi_raw < ngroups
+    auto step = [&](int buf, int64_t u) {
+      compute(buf, s0 + u % nsl);
+      if ((u + 1) % nsl == 0) flush((gi_raw + (u / nsl) * W) * R);
+    };
+    int64_t u = 0;
+    for (; u + 1 < nu; u += 2) {
+      load_unit(1, u + 1);
+      step(0, u);
+      if (u + 2 < nu) load_unit(0, u + 2);
+      step(1, u + 1);
+    }
+    if (u < nu) step(0, u);
+    return;
+  }
   if (PF > 0) {
 #pragma unroll
     for (int j = 0; j < PF; ++j)
@@ -1499,7 +1541,10 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
     ksplit = (nslabs + spk - 1) / spk;
   }
   const int TT = T <= 1 ? 1 : (T <= 2 ? 2 : 4);
-  if (TT == 4 && R == 4) return IMIE_EARG;            // not instantiated: R is 4 only for T == 1
+  if (TT == 4 && R == 4) return IMIE_EARG;
+  // large single-token launches on one weight: persistent waves (IMIE_Q1_PERS = workgroups per CU, 0 = off)
+  static const int pers_wpc = [] { const char* e = getenv("IMIE_Q1_PERS"); return e ? atoi(e) : 3; }();
+  const bool pers = pers_wpc > 0 && R == 4 && T == 1 && cnt == 1 && ksplit == 1 && pf == 0;            // not instantiated: R is 4 only for T == 1
   const int Tc = TT;
   // the prep kernel clears the outputs when the matvec adds into them (K-split) and no residual is kept
   Q1Zero zero = {};
@@ -1522,6 +1567,16 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   const size_t lds = (size_t)Tc * spk * Lcap * 512 + 128;   // + the zero slot (8 x 16 B)
   const int fr = (int)(frac > 63 ? 63 : frac);
   const dim3 grid((unsigned)((groups + 3) / 4), (unsigned)ksplit);
+  dim3 pgrid = grid;
+  if (pers) {
+    static int cus_of[64] = {};
+    int dev = 0;
+    IMIE_HIP(hipGetDevice(&dev));
+    int& cus = cus_of[dev & 63];
+    if (cus == 0) IMIE_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int64_t cap = (int64_t)cus * pers_wpc;
+    if ((int64_t)pgrid.x > cap) pgrid.x = (unsigned)cap;
+  }
   const int mode = ksplit > 1 ? 1 : (accumulate ? 2 : 0);
   imie_prof_mark(IMIE_K_Q1_GEMV, st, true);
   for (int64_t t0 = 0; t0 < T; t0 += Tc) {
@@ -1542,7 +1597,14 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
 #define IMIE_Q1_LAUNCH_PF(S64_, PF_)                                                                         \
   hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, 1, 1, PF_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs, \
                      nbp, tn, fr, spk, Lcap, mode, Q1Pro{})
-    if (pf == 4) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 4); else IMIE_Q1_LAUNCH_PF(false, 4); }
+    if (pers) {
+      if (w0.scale64)
+        hipLaunchKernelGGL((q1_gemv_mfma_kernel<true, 4, 1, 0, kProNone, 256, true>), pgrid, dim3(256), lds, st, sgt,
+                           xq, tot, ls, nslabs, nbp, tn, fr, spk, Lcap, mode, Q1Pro{});
+      else
+        hipLaunchKernelGGL((q1_gemv_mfma_kernel<false, 4, 1, 0, kProNone, 256, true>), pgrid, dim3(256), lds, st, sgt,
+                           xq, tot, ls, nslabs, nbp, tn, fr, spk, Lcap, mode, Q1Pro{});
+    } else if (pf == 4) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 4); else IMIE_Q1_LAUNCH_PF(false, 4); }
     else if (pf == 2) { if (w0.scale64) IMIE_Q1_LAUNCH_PF(true, 2); else IMIE_Q1_LAUNCH_PF(false, 2); }
     else if (w0.scale64) { IMIE_Q1_LAUNCH_T(true); } else { IMIE_Q1_LAUNCH_T(false); }
 #undef IMIE_Q1_LAUNCH_PF

@@ -154,3 +154,20 @@ def test_q1_c1_shape_int8_activations(gpu):
     x = prng.uniform_int(11, 3, (1, K), -127, 128)
     got = gpu.q1_apply_gpu(x, bits, scale, 16)
     assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("nb,xmag,smag", [(12, 7, 20), (12, 40, 20), (8, 7, 40), (20, 40, 40)])
+def test_q1_large_single_token_persistent_waves(gpu, nb, xmag, smag):
+    """Single-token launches of more than 65536 tiles on one weight run persistent waves that walk tile groups
+    gi, gi + W, ... with the slab pipeline running across group boundaries: a ragged last tile and group
+    (N = 16 * 65539 + 3), odd and even slab counts (nb 12 -> 3 slabs, 20 -> 5, 8 -> 2), one-limb (|x| < 2^7) and
+    multi-limb activations, int32 and int64 scales. Checked against the C restatement of the Q1 linear."""
+    from oracle import c_oracle
+    N = 16 * 65539 + 3
+    rng = np.random.default_rng(nb * 100 + xmag + smag)
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    scale = rng.integers(-(1 << smag), 1 << smag, size=(N, nb), dtype=np.int64)
+    x = rng.integers(-(1 << xmag) + 1, 1 << xmag, size=(1, nb * 128), dtype=np.int64)
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    want = c_oracle.q1_linear(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, want)
