@@ -813,7 +813,7 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
         bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
-                        ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
+                        ? *(const v4i*)(Kb + base + imie_kv8::k_piece(db, 64 * h + 16 * g, d.hd))
                         : v4i{0, 0, 0, 0};
   };
   auto score_tile = [&](int64_t t, const v4i (&bk)[4][2]) {
@@ -1188,7 +1188,7 @@ __global__ __launch_bounds__(256) void pf_scores8_kernel(AttnDesc d) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
-                          ? *(const v4i*)(Kb + base + db * d.hd + 64 * h + 16 * g)
+                          ? *(const v4i*)(Kb + base + imie_kv8::k_piece(db, 64 * h + 16 * g, d.hd))
                           : v4i{0, 0, 0, 0};
       v4i T[8];
 #pragma unroll

@@ -3,8 +3,10 @@
 // bytes directly. 4 bytes per element, like an int32 cache; representable values are |v| <= 2139062143
 // (= 127 * (256^4 - 1) / 255), anything larger is refused (status bit 2) and needs the int64 cache.
 //
-// Per (page, kv head) block of P slots (P a multiple of 64), 4 * hd * P bytes:
-//   K: [slot j][digit b][dim c]   -- a key row is 4 * hd contiguous bytes, one hd-byte plane per digit
+// Per (page, kv head) block of P slots (P a multiple of 64, hd a multiple of 16), 4 * hd * P bytes:
+//   K: [slot tile j / 16][digit b][dim group c / 16][slot j % 16][dim c % 16] -- the 16-byte pieces of one
+//      (digit, dim group) for 16 consecutive slots are contiguous, so the 64 lanes of one MFMA operand load
+//      (16 keys x 4 dim groups) read 1 KB contiguous
 //   V: [digit b][dim c][slot j]   -- for one (digit, dim), the P slots are contiguous (keys on the MFMA K axis)
 #pragma once
 #include "imie_common.h"
@@ -35,7 +37,11 @@ __host__ __device__ inline int64_t decode4(int8_t d0, int8_t d1, int8_t d2, int8
 __host__ __device__ inline int64_t block_base(int64_t pg, int64_t kv, int64_t Hkv, int64_t hd, int64_t P) {
   return (pg * Hkv + kv) * 4 * hd * P;
 }
-__host__ __device__ inline int64_t k_off(int64_t j, int b, int64_t c, int64_t hd) { return (j * 4 + b) * hd + c; }
+__host__ __device__ inline int64_t k_off(int64_t j, int b, int64_t c, int64_t hd) {
+  return (((j >> 4) * 4 + b) * (hd >> 4) + (c >> 4)) * 256 + (j & 15) * 16 + (c & 15);
+}
+// offset of the 16-byte piece (digit b, dims c .. c + 15; c a multiple of 16) of slot j from k_off(j, 0, 0, hd)
+__host__ __device__ inline int64_t k_piece(int b, int64_t c, int64_t hd) { return ((int64_t)b * hd + c) * 16; }
 __host__ __device__ inline int64_t v_off(int64_t j, int b, int64_t c, int64_t hd, int64_t P) {
   return ((int64_t)b * hd + c) * P + j;
 }

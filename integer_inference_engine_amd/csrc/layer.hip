@@ -195,7 +195,8 @@ void net_free(Net* n) {
 // Allocate the paged cache: sequence b gets ceil(caps[b] / P) pages, contiguous in the pool; its page-table row
 // (mp = the largest page count) lists them and repeats its first page past its own count (never addressed).
 int net_alloc_kv(Net& n, const std::vector<int64_t>& caps, int64_t P, int kv32) {
-  if (P <= 0 || (kv32 && P % 64 != 0)) return IMIE_EARG;   // kv8 MFMA steps take 64 slots of one page
+  // kv8 MFMA steps take 64 slots of one page; its K pieces are 16 dims wide
+  if (P <= 0 || (kv32 && (P % 64 != 0 || n.hd % 16 != 0))) return IMIE_EARG;
   n.kv32 = kv32;
   n.P = P;
   n.pg0.assign((size_t)n.B, 0);
