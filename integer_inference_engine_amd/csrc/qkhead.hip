@@ -101,7 +101,10 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     }
     if (!act) return;
     int8_t* blk = (int8_t*)a.kpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
-    const uint32_t wk0 = imie_kv8::encode(o0), wk1 = imie_kv8::encode(o1);
+    // an element beyond the format's range is stored as 0 (its row is refused through the status bit above),
+    // never as the digits of a wrapped value
+    const uint32_t wk0 = imie_kv8::encode(imie_kv8::fits(o0) ? o0 : 0);
+    const uint32_t wk1 = imie_kv8::encode(imie_kv8::fits(o1) ? o1 : 0);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       blk[imie_kv8::k_off(slot, db, j, a.hd)] = (int8_t)(wk0 >> (8 * db));
@@ -109,7 +112,8 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
     }
     if (a.gpart) return;                              // V planes: kv8_v_append_kernel (coalesced over slots)
     int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
-    const uint32_t wv0 = imie_kv8::encode(v0), wv1 = imie_kv8::encode(v1);
+    const uint32_t wv0 = imie_kv8::encode(imie_kv8::fits(v0) ? v0 : 0);
+    const uint32_t wv1 = imie_kv8::encode(imie_kv8::fits(v1) ? v1 : 0);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       vblk[imie_kv8::v_off(slot, db, j, a.hd, a.P)] = (int8_t)(wv0 >> (8 * db));

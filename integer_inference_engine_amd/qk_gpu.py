@@ -8,8 +8,10 @@ serialized by a process lock as in the reference (qk_cuda.py:35-38).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -314,7 +316,8 @@ def resident_layer_available() -> bool:
 
 
 class ResidentLayerHidden:
-    """Marker for the M=1 residual a bank retains between MoE layers (no host activation)."""
+    """Marker for the M=1 residual a bank retains between MoE layers (no host activation). It is valid only for
+    the bank and the bank epoch that produced it."""
 
     __slots__ = ("_cache", "_generation", "shape")
 
@@ -323,199 +326,202 @@ class ResidentLayerHidden:
         self.shape = (1, cache.d_model)
 
 
+@dataclass
+class _BankLayer:
+    """Host-side view of one bank layer: tokens held on the device and the MoE shape it was configured with."""
+    length: int = 0
+    moe: "tuple | None" = None          # (n_experts, n_used, d_model, expert_ffn)
+
+
+def _why(rc: int, *, cold_rc: bool = False) -> str:
+    """Caller-facing reason for a nonzero bank status."""
+    if rc == 3:
+        return "exact overflow guard fired"
+    if cold_rc and rc == 4:
+        return "selected cold experts remain unbound"
+    return f"native status {rc}"
+
+
 class ResidentAttentionCache:
     """Request-scoped device K/V bank with the exact M=1 attention sublayer and the MoE layer begin / continue
-    chain (qk_cuda.py:476-715). A failed native call poisons the layer and raises CudaContextError."""
+    chain (interface: qk_cuda.py:476-715; native side: ``qk_attention_bank_*``). A failed native call poisons
+    the layer on the device and raises CudaContextError.
+
+    State kept here: one ``_BankLayer`` per layer, the layer whose MoE half is open between ``begin`` and
+    ``continue`` (at most one), and an epoch that every reset / continuation / close advances so that stale
+    ``ResidentLayerHidden`` markers are rejected."""
 
     def __init__(self, n_layers: int, max_length: int, d_model: int, n_heads: int, n_kv: int, head_dim: int,
                  fa: int, cos, sin):
         lib = _dev()
         if lib is None:
             raise CudaContextError("resident attention context API is unavailable")
-        n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa = (
-            int(v) for v in (n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa))
-        if min(n_layers, max_length, d_model, n_heads, n_kv, head_dim) <= 0 or n_heads % n_kv or head_dim % 2 or \
-                not 1 <= fa <= 29 or d_model % 256 or (n_heads * head_dim) % 256:
+        dims = tuple(int(v) for v in (n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa))
+        n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa = dims
+        shape_ok = min(dims[:6]) > 0 and n_heads % n_kv == 0 and head_dim % 2 == 0
+        native_ok = 1 <= fa <= 29 and d_model % 256 == 0 and (n_heads * head_dim) % 256 == 0
+        if not (shape_ok and native_ok):
             raise ValueError("invalid resident attention dimensions")
-        c = np.ascontiguousarray(np.asarray(cos, dtype=np.int64))
-        s = np.ascontiguousarray(np.asarray(sin, dtype=np.int64))
-        if c.shape != (max_length, head_dim // 2) or s.shape != c.shape:
+        tables = [np.ascontiguousarray(np.asarray(t, dtype=np.int64)) for t in (cos, sin)]
+        if any(t.shape != (max_length, head_dim // 2) for t in tables):
             raise ValueError(f"resident attention RoPE tables must both have shape {(max_length, head_dim // 2)}")
         with _LOCK:
-            self.handle = int(lib.qk_attention_bank_create(n_layers, max_length, d_model, n_heads, n_kv, head_dim, fa,
-                                                           c.ctypes.data, s.ctypes.data))
+            self.handle = int(lib.qk_attention_bank_create(*dims, tables[0].ctypes.data, tables[1].ctypes.data))
         if self.handle < 0:
             raise CudaContextError("resident attention context creation failed")
         self.n_layers, self.max_length, self.d_model = n_layers, max_length, d_model
         self.n_heads, self.n_kv, self.head_dim, self.fa = n_heads, n_kv, head_dim, fa
         self.q_width = n_heads * head_dim
-        self._lengths = [0] * n_layers
-        self._moe = {}
-        self._generation = 0
-        self._pending = None
+        self.inv_sqrt = int(round((1 << fa) / float(np.sqrt(head_dim))))
+        self._layers = [_BankLayer() for _ in range(n_layers)]
+        self._open_layer = None
+        self._epoch = 0
         self._closed = False
 
-    def _lib(self):
+    # -- helpers ---------------------------------------------------------------------------------------------------
+    def _native(self, fn: str, *args) -> int:
+        """Call ``qk_attention_bank_<fn>(handle, *args)`` under the process lock; the open check comes first."""
         if self._closed:
             raise CudaContextError("resident attention context is closed")
-        return _lib.lib()
+        with _LOCK:
+            rc = getattr(_lib.lib(), "qk_attention_bank_" + fn)(self.handle, *args)
+        return 0 if rc is None else int(rc)
 
-    def _inv_sqrt(self) -> int:
-        import math
-        return int(round((1.0 / math.sqrt(self.head_dim)) * (1 << self.fa)))
+    def _layer(self, layer) -> "_BankLayer | None":
+        layer = int(layer)
+        return self._layers[layer] if 0 <= layer < self.n_layers else None
+
+    def _row(self, hidden, what: str) -> np.ndarray:
+        x = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
+        if x.shape != (1, self.d_model):
+            raise ValueError(f"resident {what} expects hidden shape (1, {self.d_model})")
+        return x
+
+    def _room(self, layer) -> bool:
+        st = self._layer(layer)
+        return st is not None and st.length < self.max_length
+
+    @property
+    def _generation(self) -> int:
+        return self._epoch
 
     def length(self, layer=0):
-        return self._lengths[layer]
+        return self._layers[layer].length
 
+    # -- K/V and the attention sublayer ----------------------------------------------------------------------------
     def import_layer(self, layer: int, k, v) -> None:
-        lib = self._lib()
-        kk = np.ascontiguousarray(np.asarray(k, dtype=np.int64))
-        vv = np.ascontiguousarray(np.asarray(v, dtype=np.int64))
+        kk, vv = (np.ascontiguousarray(np.asarray(t, dtype=np.int64)) for t in (k, v))
         if kk.shape != vv.shape or kk.ndim != 3 or kk.shape[0] != self.n_kv or kk.shape[2] != self.head_dim:
             raise ValueError("resident attention import expects matching [n_kv, length, head_dim] K/V")
-        if not 0 <= int(layer) < self.n_layers or kk.shape[1] > self.max_length:
+        st = self._layer(layer)
+        if st is None or kk.shape[1] > self.max_length:
             raise ValueError("resident attention import exceeds layer or context bounds")
-        with _LOCK:
-            rc = lib.qk_attention_bank_import(self.handle, int(layer), kk.ctypes.data, vv.ctypes.data, kk.shape[1])
-        if rc != 0:
+        if self._native("import", int(layer), kk.ctypes.data, vv.ctypes.data, kk.shape[1]) != 0:
             raise CudaContextError(f"resident attention K/V import failed for layer {layer}")
-        self._lengths[int(layer)] = int(kk.shape[1])
+        st.length = int(kk.shape[1])
 
     def apply(self, layer: int, q_handle: int, k_handle: int, v_handle: int, o_handle: int, hidden, fw: int,
               window, rope: bool):
-        lib = self._lib()
-        layer = int(layer)
-        if not 0 <= layer < self.n_layers or self._lengths[layer] >= self.max_length:
+        if not self._room(layer):
             raise ValueError("resident attention decode exceeds layer or context bounds")
-        x = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
-        if x.shape != (1, self.d_model):
-            raise ValueError(f"resident attention apply expects hidden shape (1, {self.d_model})")
-        out = np.empty((1, self.d_model), dtype=np.int64)
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_apply(self.handle, layer, int(q_handle), int(k_handle), int(v_handle),
-                                                 int(o_handle), x.ctypes.data, int(fw), -1 if window is None else int(window),
-                                                 int(bool(rope)), self._inv_sqrt(), out.size, out.ctypes.data))
+        x = self._row(hidden, "attention apply")
+        out = np.empty_like(x)
+        rc = self._native("apply", int(layer), int(q_handle), int(k_handle), int(v_handle), int(o_handle),
+                          x.ctypes.data, int(fw), -1 if window is None else int(window), int(bool(rope)),
+                          self.inv_sqrt, out.size, out.ctypes.data)
         if rc != 0:
-            why = "exact overflow guard fired" if rc == 3 else f"native status {rc}"
-            raise CudaContextError(f"resident attention apply failed for layer {layer}: {why}")
-        self._lengths[layer] += 1
+            raise CudaContextError(f"resident attention apply failed for layer {layer}: {_why(rc)}")
+        self._layers[int(layer)].length += 1
         return out
 
+    # -- MoE layers ------------------------------------------------------------------------------------------------
     def configure_moe_layer(self, layer: int, n_experts: int, n_used: int, d_model: int, expert_ffn: int) -> None:
-        lib = self._lib()
-        cfg = tuple(int(v) for v in (n_experts, n_used, d_model, expert_ffn))
-        layer = int(layer)
-        if not 0 <= layer < self.n_layers or cfg[0] <= 0 or not 0 < cfg[1] <= cfg[0] or cfg[2] != self.d_model or \
-                cfg[3] <= 0 or cfg[2] % 256 or cfg[3] % 256:
+        shape = tuple(int(v) for v in (n_experts, n_used, d_model, expert_ffn))
+        n_exp, used, width, ffn = shape
+        st = self._layer(layer)
+        if st is None or not (0 < used <= n_exp) or width != self.d_model or width % 256 or ffn <= 0 or ffn % 256:
             raise ValueError("invalid resident MoE layer dimensions")
-        if layer in self._moe and self._moe[layer] != cfg:
+        if st.moe not in (None, shape):
             raise ValueError("resident MoE layer cannot be reconfigured with different dimensions")
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_moe_configure(self.handle, layer, *cfg))
-        if rc != 0:
+        if self._native("moe_configure", int(layer), *shape) != 0:
             raise CudaContextError(f"resident MoE layer configuration failed for layer {layer}")
-        self._moe[layer] = cfg
+        st.moe = shape
 
     def bind_moe_expert(self, layer: int, expert: int, gate_handle: int, up_handle: int, down_handle: int) -> None:
-        lib = self._lib()
-        layer, expert = int(layer), int(expert)
-        if layer not in self._moe or not 0 <= expert < self._moe[layer][0]:
+        st = self._layer(layer)
+        if st is None or st.moe is None or not 0 <= int(expert) < st.moe[0]:
             raise ValueError("resident MoE expert binding is outside the configured layer")
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_moe_bind(self.handle, layer, expert, int(gate_handle), int(up_handle),
-                                                    int(down_handle)))
-        if rc != 0:
+        if self._native("moe_bind", int(layer), int(expert), int(gate_handle), int(up_handle), int(down_handle)):
             raise CudaContextError(f"resident MoE expert binding failed for layer {layer}, expert {expert}")
 
     def begin_moe_layer(self, layer: int, gain_handle: int, router_handle: int, q_handle: int, k_handle: int,
                         v_handle: int, o_handle: int, hidden, fw: int, eps: int, window, rope: bool) -> tuple:
-        lib = self._lib()
-        layer = int(layer)
-        if layer not in self._moe or self._pending is not None or self._lengths[layer] >= self.max_length:
+        st = self._layer(layer)
+        if st is None or st.moe is None or self._open_layer is not None or st.length >= self.max_length:
             raise ValueError("resident MoE layer begin violates configuration, pending, or context bounds")
-        retained = isinstance(hidden, ResidentLayerHidden)
-        if retained:
-            if hidden._cache is not self or hidden._generation != self._generation:
+        if isinstance(hidden, ResidentLayerHidden):
+            if hidden._cache is not self or hidden._generation != self._epoch:
                 raise ValueError("resident hidden marker is stale or belongs to another request")
-            xp = None
+            x_ptr, retained = None, 1
         else:
-            x = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
-            if x.shape != (1, self.d_model):
-                raise ValueError(f"resident MoE layer begin expects hidden shape (1, {self.d_model})")
-            xp = x.ctypes.data
-        used = self._moe[layer][1]
-        cold = np.empty(used, dtype=np.int32)
-        count = ctypes.c_int(0)
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_moe_begin(
-                self.handle, layer, int(gain_handle), int(router_handle), int(q_handle), int(k_handle),
-                int(v_handle), int(o_handle), xp, int(retained), int(fw), int(eps),
-                -1 if window is None else int(window), int(bool(rope)), self._inv_sqrt(), cold.size,
-                ctypes.byref(count), cold.ctypes.data))
+            x = self._row(hidden, "MoE layer begin")
+            x_ptr, retained = x.ctypes.data, 0
+        cold = np.empty(st.moe[1], dtype=np.int32)
+        n_cold = ctypes.c_int(0)
+        rc = self._native("moe_begin", int(layer), int(gain_handle), int(router_handle), int(q_handle),
+                          int(k_handle), int(v_handle), int(o_handle), x_ptr, retained, int(fw), int(eps),
+                          -1 if window is None else int(window), int(bool(rope)), self.inv_sqrt, cold.size,
+                          ctypes.byref(n_cold), cold.ctypes.data)
         if rc != 0:
-            why = "exact overflow guard fired" if rc == 3 else f"native status {rc}"
-            raise CudaContextError(f"resident MoE layer begin failed for layer {layer}: {why}")
-        n = int(count.value)
-        if not 0 <= n <= used:
+            raise CudaContextError(f"resident MoE layer begin failed for layer {layer}: {_why(rc)}")
+        if not 0 <= n_cold.value <= cold.size:
             raise CudaContextError("resident MoE layer returned an invalid cold-route count")
-        self._lengths[layer] += 1
-        self._pending = layer
-        return tuple(int(e) for e in cold[:n])
+        st.length += 1
+        self._open_layer = int(layer)
+        return tuple(cold[:n_cold.value].tolist())
 
     def continue_moe_layer(self, layer: int, fw: int, *, publish: bool = False):
-        lib = self._lib()
-        layer = int(layer)
-        if self._pending != layer:
+        if self._open_layer is None or self._open_layer != int(layer):
             raise ValueError("resident MoE continuation has no matching prepared layer")
         out = np.empty((1, self.d_model), dtype=np.int64) if publish else None
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_moe_continue(self.handle, layer, int(fw), int(bool(publish)),
-                                                        0 if out is None else out.size,
-                                                        None if out is None else out.ctypes.data))
+        rc = self._native("moe_continue", int(layer), int(fw), int(bool(publish)),
+                          0 if out is None else out.size, None if out is None else out.ctypes.data)
         if rc != 0:
-            why = ("selected cold experts remain unbound" if rc == 4 else
-                   "exact overflow guard fired" if rc == 3 else f"native status {rc}")
-            raise CudaContextError(f"resident MoE continuation failed for layer {layer}: {why}")
-        self._pending = None
-        self._generation += 1
-        return out if publish else ResidentLayerHidden(self, self._generation)
+            raise CudaContextError(f"resident MoE continuation failed for layer {layer}: {_why(rc, cold_rc=True)}")
+        self._open_layer = None
+        self._epoch += 1
+        return out if publish else ResidentLayerHidden(self, self._epoch)
 
     def export_moe_hidden(self) -> np.ndarray:
-        lib = self._lib()
-        if self._pending is not None:
+        if self._open_layer is not None:
             raise CudaContextError("resident MoE hidden cannot be exported from this context state")
         out = np.empty((1, self.d_model), dtype=np.int64)
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_moe_export(self.handle, out.size, out.ctypes.data))
-        if rc != 0:
+        if self._native("moe_export", out.size, out.ctypes.data) != 0:
             raise CudaContextError("resident MoE hidden export failed")
         return out
 
+    # -- lifetime --------------------------------------------------------------------------------------------------
     def workspace_bytes(self) -> int:
-        lib = self._lib()
-        with _LOCK:
-            v = int(lib.qk_attention_bank_workspace_bytes(self.handle))
+        v = self._native("workspace_bytes")
         if v == (1 << 64) - 1:
             raise CudaContextError("resident attention workspace accounting failed")
         return v
 
     def reset(self) -> None:
-        lib = self._lib()
-        with _LOCK:
-            rc = int(lib.qk_attention_bank_reset(self.handle))
-        if rc != 0:
+        if self._native("reset") != 0:
             raise CudaContextError("resident attention context reset failed")
-        self._lengths = [0] * self.n_layers
-        self._generation += 1
-        self._pending = None
+        for st in self._layers:
+            st.length = 0
+        self._open_layer = None
+        self._epoch += 1
 
     def close(self) -> None:
-        if not self._closed:
-            with _LOCK:
-                _lib.lib().qk_attention_bank_destroy(self.handle)
-            self._closed = True
-            self._pending = None
-            self._generation += 1
+        if self._closed:
+            return
+        self._native("destroy")
+        self._closed = True
+        self._open_layer = None
+        self._epoch += 1
 
 
 # ---- telemetry and capability probes (qk_cuda.py:24-34, 870-910, 1029-1101) ---------------------------------------
@@ -606,9 +612,6 @@ def moe_ffn_batched_dp4a_available() -> bool:
 
 
 # ---- retained MoE token chain (qk_cuda.py:726-868) ------------------------------------------------------------------
-from dataclasses import dataclass
-
-
 @dataclass(frozen=True)
 class ResidentMoeLayerSpec:
     """Resident dense-handle inputs of one M = 1 MoE layer."""
@@ -623,109 +626,117 @@ class ResidentMoeLayerSpec:
     rope: bool
 
 
+def _expert_handles(value, where: str):
+    """A (gate, up, down) triple of non-negative resident handles, or CudaContextError naming ``where``."""
+    try:
+        triple = tuple(int(h) for h in value)
+    except (TypeError, ValueError):
+        triple = None
+    if triple is None or len(triple) != 3 or min(triple) < 0:
+        raise CudaContextError(f"{where} did not return a valid gate/up/down handle triplet")
+    return triple
+
+
 class ResidentMoeTokenExecutor:
     """One token through consecutive MoE layers of a ResidentAttentionCache with the hidden state retained on the
-    device between layers. ``lookup_expert(layer, e)`` returns an already resident (gate, up, down) triplet or None
-    (no side effects); ``load_expert(layer, e)`` is called only for the experts the device reports unbound. Any
-    error poisons the executor: the caller resets or destroys the bank instead of mixing partly advanced K/V with
-    another path."""
+    device between layers (interface: qk_cuda.py:726-868, used by engine.py's resident decode).
+
+    ``lookup_expert(layer, e)`` returns an already resident (gate, up, down) triplet or None, with no side
+    effects; ``load_expert(layer, e)`` is called only for the experts the device reports unbound after routing.
+    Any error raised while touching the bank poisons the executor: the caller resets or destroys the bank instead
+    of mixing partly advanced K/V with another path.
+
+    Per layer the executor keeps one entry in ``_ready``: the set of experts bound to the bank for that layer. A
+    layer gets its entry once it is configured and every expert ``lookup_expert`` knows has been bound."""
 
     def __init__(self, cache: "ResidentAttentionCache", *, first_layer: int, layer_count: int, n_experts: int,
                  n_used: int, d_model: int, expert_ffn: int, fw: int, eps: int, lookup_expert, load_expert):
         if not isinstance(cache, ResidentAttentionCache) or cache._closed:
             raise ValueError("resident token executor requires an open attention bank")
-        first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps = (
-            int(v) for v in (first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps))
-        if (first_layer < 0 or layer_count <= 0 or first_layer + layer_count > cache.n_layers or n_experts <= 0
-                or not 0 < n_used <= n_experts or d_model != cache.d_model or d_model % 256 or expert_ffn <= 0
-                or expert_ffn % 256 or not 0 <= fw <= 62 or not 0 <= eps <= (1 << 64) - 1):
+        first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps = map(
+            int, (first_layer, layer_count, n_experts, n_used, d_model, expert_ffn, fw, eps))
+        layers_ok = first_layer >= 0 and layer_count > 0 and first_layer + layer_count <= cache.n_layers
+        moe_ok = n_experts > 0 and 0 < n_used <= n_experts and expert_ffn > 0 and expert_ffn % 256 == 0
+        width_ok = d_model == cache.d_model and d_model % 256 == 0
+        fixed_ok = 0 <= fw <= 62 and 0 <= eps < (1 << 64)
+        if not (layers_ok and moe_ok and width_ok and fixed_ok):
             raise ValueError("invalid resident token executor dimensions")
-        if not callable(lookup_expert) or not callable(load_expert):
+        if not (callable(lookup_expert) and callable(load_expert)):
             raise TypeError("resident token executor requires expert lookup and lazy-load callables")
         self.cache = cache
         self.first_layer, self.layer_count = first_layer, layer_count
         self.n_experts, self.n_used, self.d_model, self.expert_ffn = n_experts, n_used, d_model, expert_ffn
         self.fw, self.eps = fw, eps
         self.lookup_expert, self.load_expert = lookup_expert, load_expert
-        self._configured, self._scanned, self._bound = set(), set(), set()
+        self._ready: "dict[int, set[int]]" = {}
         self._poisoned = False
 
     @property
     def poisoned(self) -> bool:
         return self._poisoned
 
-    @staticmethod
-    def _triplet(value, *, allow_none: bool, label: str):
-        if value is None and allow_none:
-            return None
+    @contextlib.contextmanager
+    def _guarded(self):
+        """Refuse work once poisoned; poison on any exception raised inside."""
+        if self._poisoned:
+            raise CudaContextError("resident token executor is poisoned; destroy or reset the request bank")
         try:
-            hs = tuple(int(h) for h in value)
-        except (TypeError, ValueError):
-            hs = ()
-        if len(hs) != 3 or any(h < 0 for h in hs):
-            raise CudaContextError(f"{label} did not return a valid gate/up/down handle triplet")
-        return hs
+            yield
+        except BaseException:
+            self._poisoned = True
+            raise
 
-    def _configure_and_bind_known(self, layer: int) -> None:
-        if layer not in self._configured:
-            self.cache.configure_moe_layer(layer, self.n_experts, self.n_used, self.d_model, self.expert_ffn)
-            self._configured.add(layer)
-        if layer in self._scanned:
-            return
-        for e in range(self.n_experts):
-            hs = self._triplet(self.lookup_expert(layer, e), allow_none=True,
-                               label=f"resident expert lookup for layer {layer}, expert {e}")
-            if hs is not None:
-                self.cache.bind_moe_expert(layer, e, *hs)
-                self._bound.add((layer, e))
-        self._scanned.add(layer)
-
-    def _specs(self, layers):
-        specs = tuple(layers)
-        want = tuple(range(self.first_layer, self.first_layer + self.layer_count))
-        if (len(specs) != self.layer_count or any(not isinstance(s, ResidentMoeLayerSpec) for s in specs)
-                or tuple(int(s.layer) for s in specs) != want):
-            raise ValueError(f"resident token executor requires consecutive layers {want[0]}..{want[-1]}")
+    def _check_specs(self, layers) -> "list[ResidentMoeLayerSpec]":
+        specs = list(layers)
+        last = self.first_layer + self.layer_count - 1
+        good = len(specs) == self.layer_count and all(
+            isinstance(s, ResidentMoeLayerSpec) and int(s.layer) == self.first_layer + i for i, s in enumerate(specs))
+        if not good:
+            raise ValueError(f"resident token executor requires consecutive layers {self.first_layer}..{last}")
         return specs
+
+    def _bind(self, layer: int, expert: int, triple) -> None:
+        self.cache.bind_moe_expert(layer, expert, *triple)
+        self._ready[layer].add(expert)
+
+    def _make_ready(self, layer: int) -> None:
+        if layer in self._ready:
+            return
+        self.cache.configure_moe_layer(layer, self.n_experts, self.n_used, self.d_model, self.expert_ffn)
+        self._ready[layer] = set()
+        for expert in range(self.n_experts):
+            found = self.lookup_expert(layer, expert)
+            if found is not None:
+                where = f"resident expert lookup for layer {layer}, expert {expert}"
+                self._bind(layer, expert, _expert_handles(found, where))
 
     def prepare(self, layers):
         """Configure every layer and bind the experts already resident, before any K/V changes."""
         if self._poisoned:
             raise CudaContextError("resident token executor is poisoned; destroy or reset the request bank")
-        specs = self._specs(layers)
-        try:
-            for s in specs:
-                self._configure_and_bind_known(int(s.layer))
-            return specs
-        except Exception:
-            self._poisoned = True
-            raise
+        specs = self._check_specs(layers)
+        with self._guarded():
+            for spec in specs:
+                self._make_ready(int(spec.layer))
+        return tuple(specs)
 
     def run(self, hidden, layers) -> np.ndarray:
-        if self._poisoned:
-            raise CudaContextError("resident token executor is poisoned; destroy or reset the request bank")
         specs = self.prepare(layers)
         state = np.ascontiguousarray(np.asarray(hidden, dtype=np.int64))
         if state.shape != (1, self.d_model):
             raise ValueError(f"resident token executor expects hidden shape (1, {self.d_model})")
-        try:
-            for i, s in enumerate(specs):
-                layer = int(s.layer)
-                self._configure_and_bind_known(layer)
-                cold = self.cache.begin_moe_layer(layer, int(s.gain_handle), int(s.router_handle), int(s.q_handle),
-                                                  int(s.k_handle), int(s.v_handle), int(s.o_handle), state, self.fw,
-                                                  self.eps, s.window, bool(s.rope))
-                if len(cold) != len(set(cold)) or any(not 0 <= e < self.n_experts for e in cold):
+        with self._guarded():
+            for spec in specs:
+                layer = int(spec.layer)
+                cold = self.cache.begin_moe_layer(
+                    layer, int(spec.gain_handle), int(spec.router_handle), int(spec.q_handle), int(spec.k_handle),
+                    int(spec.v_handle), int(spec.o_handle), state, self.fw, self.eps, spec.window, bool(spec.rope))
+                if len(set(cold)) != len(cold) or not all(0 <= e < self.n_experts for e in cold):
                     raise CudaContextError(f"resident layer {layer} returned invalid cold expert IDs")
-                for e in cold:
-                    hs = self._triplet(self.load_expert(layer, e), allow_none=False,
-                                       label=f"lazy expert loader for layer {layer}, expert {e}")
-                    self.cache.bind_moe_expert(layer, e, *hs)
-                    self._bound.add((layer, e))
-                state = self.cache.continue_moe_layer(layer, self.fw, publish=i + 1 == self.layer_count)
-            if not isinstance(state, np.ndarray) or state.shape != (1, self.d_model):
+                for expert in cold:
+                    where = f"lazy expert loader for layer {layer}, expert {expert}"
+                    self._bind(layer, expert, _expert_handles(self.load_expert(layer, expert), where))
+                state = self.cache.continue_moe_layer(layer, self.fw, publish=spec is specs[-1])
+            if not (isinstance(state, np.ndarray) and state.shape == (1, self.d_model)):
                 raise CudaContextError("resident token executor did not publish its final residual")
-            return state
-        except Exception:
-            self._poisoned = True
-            raise
+        return state

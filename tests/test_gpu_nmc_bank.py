@@ -133,7 +133,6 @@ def test_bank_moe_chain_matches_oracle(gpu):
         if layer == 0 and cold:                         # continuing with a cold expert unbound fails closed (rc 4)
             with pytest.raises(qk_gpu.CudaContextError):
                 bank.continue_moe_layer(layer, FW)
-            bank._pending = layer
         for e in cold:
             bank.bind_moe_expert(layer, e, *eh[e])
         state = bank.continue_moe_layer(layer, FW, publish=layer == 1)
