@@ -46,6 +46,7 @@ struct Q1Weight {
   uint4* signs = nullptr;          // prefill copy: +-1 int8 per weight in MFMA operand order (made on first use)
   int scale64 = 0;
   int64_t maxsc = 0;               // max |scale| (host-side bounds for the GEMM epilogue)
+  uint64_t rsum[8] = {};           // [r - 1]: max over rows and over r equal block ranges of sum |scale|
   size_t bytes = 0;
   bool live = false;
 };
@@ -666,6 +667,7 @@ struct GemmArgs {
   int64_t ntiles16;                // 16 * tiles: rows of the tiled scale layout
   int frac, accumulate;
   int kfold;                       // > 0: high-dword epilogue (narrow kernel), folded every kfold blocks
+  int rlen;                        // q1_gemm_ps_kernel<.., 2>: first block of the second int32 partial sum
   int ksplit;                      // narrow kernel: blocks split over gridDim.y ranges, outputs added atomically
   int64_t* out;
   int* wide_any;                   // set by q1_gemm_pm_kernel per 64-token tile: some slab needs > 3 limbs (the
@@ -1212,20 +1214,12 @@ __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg
 }
 
 // blocks whose slab needs more than kNarrowLimbs limbs on the tile's tokens; adds into out
-template <bool S64>
-__device__ inline void gemm_wide_tile(const GemmArgs& a, int64_t wg, int* s_lw) {
-  constexpr int MT = 2, NT = 4;
+// One wave's 16 MT x 16 NT sub-tile at (t0, o0): the blocks whose slab needs more than kNarrowLimbs limbs over
+// the wave's 64-token tile (s_lw[slab] from gemm_slab_limbs), exact in int64 with any limb count, added into out
+// (ATOMIC: with 64-bit atomic adds, for callers that stored the narrow blocks' sums to the same outputs).
+template <bool S64, int MT, int NT, bool ATOMIC>
+__device__ inline void gemm_wide_wave(const GemmArgs& a, int64_t t0, int64_t o0, const int* s_lw) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int64_t t0, o0, t0g;
-  bool live;
-  gemm_tile(a, wave, t0, o0, t0g, live, wg);
-  if (!live) return;
-  if (a.wide_any && a.wide_any[t0g >> 6] == 0) return;
-  gemm_slab_limbs(a, t0g, s_lw);
-  bool any = false;
-  for (int64_t sl = 0; sl < a.nslabs; ++sl) any = any || s_lw[sl] > kNarrowLimbs;
-  if (!any) return;
   const int m = lane & 15, g = lane >> 4;
   int64_t ta[MT];
 #pragma unroll
@@ -1310,9 +1304,27 @@ __device__ inline void gemm_wide_tile(const GemmArgs& a, int64_t wg, int* s_lw) 
         const int64_t t = t0 + 16 * i + 4 * g + r;
         if (t >= a.T) continue;
         int64_t* dst = a.out + t * a.N + o;
-        *dst = (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]);
+        if (ATOMIC) atomicAdd((unsigned long long*)dst, (unsigned long long)acc[i][jj][r]);
+        else *dst = (int64_t)((uint64_t)*dst + (uint64_t)acc[i][jj][r]);
       }
     }
+}
+
+
+template <bool S64>
+__device__ inline void gemm_wide_tile(const GemmArgs& a, int64_t wg, int* s_lw) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int64_t t0, o0, t0g;
+  bool live;
+  gemm_tile(a, wave, t0, o0, t0g, live, wg);
+  if (!live) return;
+  if (a.wide_any && a.wide_any[t0g >> 6] == 0) return;
+  gemm_slab_limbs(a, t0g, s_lw);
+  bool any = false;
+  for (int64_t sl = 0; sl < a.nslabs; ++sl) any = any || s_lw[sl] > kNarrowLimbs;
+  if (!any) return;
+  gemm_wide_wave<S64, 2, 4, false>(a, t0, o0, s_lw);
 }
 
 // One workgroup per (64-token, 128-output) tile; with the tile flags written by the sign-copy kernel
@@ -1321,6 +1333,223 @@ template <bool S64>
 __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
   __shared__ int s_lw[kGemmMaxSlabs];
   gemm_wide_tile<S64>(a, blockIdx.x, s_lw);
+}
+
+// ------------------------------------------------------------------------------------------------------
+// Prefill GEMM over the sign copy, several weights per launch (q1_gemm_ps_kernel). The same operands, LDS ring
+// and swizzle as q1_gemm_pm_kernel, with three changes:
+// * Int32 partial sums without folds. Each block's floor(S * scale / 2^frac) is added into an int32 partial; the
+//   host proves, from the weight's row sums of |scale| and |S| < 2^30 (3 limbs), that the sum over the partial's
+//   block range stays below 2^31 in magnitude, so the partial is exact after sign extension whatever it wrapped
+//   through on the way (NP = 2: the second half of the blocks in a second partial). No int64 accumulators: a
+//   16 x 32 .. 32 x 32 sub-tile per wave fits 128 VGPRs, so 16 waves (four per SIMD) hide one another's MFMA ->
+//   VALU dependencies and barrier waits.
+// * The copies of block b + 1 are issued in three parts, one before each limb's MFMAs of block b, so the copy
+//   traffic is spread over the block instead of queueing in front of it.
+// * Slabs needing more than 3 limbs over a 64-token half (rare: activations beyond 2^23) are computed by the same
+//   workgroup after its sums are stored (gemm_wide_wave, 64-bit atomic adds), so no second launch runs.
+// One launch covers up to kMaxSegs weights of the same n_blocks (q / k / v, gate / up): their output tiles are
+// concatenated, so the small k / v projections share the grid with q instead of each filling part of the chip.
+// ------------------------------------------------------------------------------------------------------
+struct PsArgs {
+  GemmArgs s[kMaxSegs];
+  int64_t tend[kMaxSegs];          // cumulative output tiles through segment i
+  uint32_t sg_bytes[kMaxSegs], sc_bytes[kMaxSegs];
+  uint32_t xg_bytes;
+  int cnt;
+};
+
+template <int MT, int NT, int NP>
+__global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) {
+  constexpr int NW = 64 / (MT * NT);             // waves of 16 MT x 16 NT covering the 128 x 128 tile
+  constexpr int WO = 128 / (16 * NT);            // waves along the outputs
+  constexpr int QA = 48 / NW, QB = 16 / NW;      // 1 KB copies per wave and block: A (3 limbs x 16 row groups), B
+  static_assert(NW == 8 || NW == 16, "8 or 16 waves");
+  __shared__ int s_lw[2][kGemmMaxSlabs];
+  __shared__ v4i sA0[kNarrowLimbs][kPmTok * 8], sA1[kNarrowLimbs][kPmTok * 8];   // 2 x 48 KB
+  __shared__ v4i sB0[128 * 8], sB1[128 * 8];                                      // 2 x 16 KB
+  __shared__ int32_t sS0[128], sS1[128];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t T = P.s[0].T, ntt = (T + kPmTok - 1) / kPmTok, nto = P.tend[P.cnt - 1], wg = blockIdx.x;
+  int64_t tt, ot;
+  bool live;
+  if (ntt >= 8) {                                     // each XCD walks whole token tiles (their digits stay in L2)
+    const int64_t xcd = wg & 7, j = wg >> 3, tpx = (ntt + 7) / 8;
+    tt = xcd + 8 * (j / nto);
+    ot = j % nto;
+    live = tt < ntt && (j / nto) < tpx;
+  } else {
+    tt = wg / nto;
+    ot = wg % nto;
+    live = tt < ntt;
+  }
+  if (!live) return;
+  const int seg = (ot >= P.tend[0] ? 1 : 0) + (P.cnt > 2 && ot >= P.tend[1] ? 1 : 0);
+  const GemmArgs a = seg == 0 ? P.s[0] : (seg == 1 ? P.s[1] : P.s[2]);
+  const uint32_t sg_bytes = seg == 0 ? P.sg_bytes[0] : (seg == 1 ? P.sg_bytes[1] : P.sg_bytes[2]);
+  const uint32_t sc_bytes = seg == 0 ? P.sc_bytes[0] : (seg == 1 ? P.sc_bytes[1] : P.sc_bytes[2]);
+  if (seg) ot -= P.tend[seg - 1];
+  const int64_t t0g = tt * kPmTok, o0g = ot * 128;
+  for (int64_t q = wave; q < 2 * a.nslabs; q += NW) {  // (half, slab) limb maxima over 64 tokens each
+    const int hh = (int)(q & 1);
+    const int64_t sl = q >> 1, t = t0g + 64 * hh + lane;
+    int L = t < T ? a.lt[t * a.nslabs + sl] : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const int w2 = __shfl_xor(L, o, 64); L = w2 > L ? w2 : L; }
+    if (lane == 0) s_lw[hh][sl] = L;
+  }
+  const int m = lane & 15, g = lane >> 4;
+  const int tb = (wave / WO) * 16 * MT, ob = (wave % WO) * 16 * NT, half = tb >> 6;
+  const __amdgpu_buffer_rsrc_t rA = pm_rsrc(a.xg, P.xg_bytes), rB = pm_rsrc(a.signs, sg_bytes),
+                               rS = pm_rsrc(a.scaleT, sc_bytes);
+  // copy roles: lane L of a 1 KB copy fills slot L & 7 of row L >> 3 of an 8-row group
+  const int drow = lane >> 3, dslot = lane & 7;
+  uint32_t voA[QA], voB[QB];
+#pragma unroll
+  for (int q = 0; q < QA; ++q) {
+    const int rg = (wave * QA + q) & 15, t = rg * 8 + drow;
+    voA[q] = (uint32_t)(t0g + t) * 128u + (uint32_t)(dslot ^ ((t >> 1) & 7)) * 16u;
+  }
+#pragma unroll
+  for (int q = 0; q < QB; ++q) {
+    const int r = (wave * QB + q) * 8 + drow;
+    const int64_t o = o0g + r < a.N ? o0g + r : a.N - 1;                     // clamp: padding columns unused
+    voB[q] = (uint32_t)o * (uint32_t)a.nb * 128u + (uint32_t)(dslot ^ ((r >> 1) & 7)) * 16u;
+  }
+  const int64_t so_ = o0g + (tid & 127) < a.ntiles16 ? o0g + (tid & 127) : a.ntiles16 - 1;
+  const uint32_t voS = (uint32_t)(((so_ >> 4) * a.nslabs * 64 + (so_ & 15)) * 4);
+  const uint32_t limb_stride = (uint32_t)a.nbp * (uint32_t)a.Tp * 128u, blk_stride = (uint32_t)a.Tp * 128u;
+  // part ph (0..2) of block b's copies, or all of them (ph < 0); all three limbs are copied (the table holds zero
+  // digits above a token's limb count)
+  auto issue = [&](int64_t b, v4i (*dA)[kPmTok * 8], v4i* dB, int ph) {
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      if (ph >= 0 && q / (QA / 3) != ph) continue;
+      const int qi = wave * QA + q, l = qi >> 4, rg = qi & 15;
+      pm_dma(rA, &dA[l][rg * 64], voA[q], (uint32_t)l * limb_stride + (uint32_t)b * blk_stride);
+    }
+    if (ph < 0 || ph == 2)
+#pragma unroll
+      for (int q = 0; q < QB; ++q) pm_dma(rB, &dB[(wave * QB + q) * 64], voB[q], (uint32_t)b * 128u);
+  };
+  auto load_scale = [&](int64_t b) -> int32_t {
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rS, (int)voS, (int)((((b >> 2) * 64) + 16 * (b & 3)) * 4), 0);
+  };
+  // NP int32 partial sums (NP = 2: blocks from a.rlen on go to `part` after `sav` took the first range)
+  int32_t part[MT][NT][4], sav[MT][NT][NP == 2 ? 4 : 1];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[i][jj][r] = 0;
+#pragma unroll
+      for (int r = 0; r < (NP == 2 ? 4 : 1); ++r) sav[i][jj][r] = 0;
+    }
+  const int64_t t0 = t0g + tb, o0 = o0g + ob;
+  // per-lane physical chunk of K half h (the swizzle term (row >> 1) & 7 is (m >> 1) & 7 for every read row)
+  const int pc0 = (0 + g) ^ ((m >> 1) & 7), pc1 = (4 + g) ^ ((m >> 1) & 7);
+  __syncthreads();                                    // s_lw
+  bool wide0 = false, wide1 = false;
+  for (int64_t sl = 0; sl < a.nslabs; ++sl) {
+    wide0 = wide0 || s_lw[0][sl] > kNarrowLimbs;
+    wide1 = wide1 || s_lw[1][sl] > kNarrowLimbs;
+  }
+  issue(0, sA0, sB0, -1);
+  if (tid < 128) sS0[tid] = load_scale(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // block b from (cA, cB, cS) while block b + 1 is copied into (nA, nB, nS)
+  auto step = [&](int64_t b, const v4i (*cA)[kPmTok * 8], const v4i* cB, const int32_t* cS, v4i (*nA)[kPmTok * 8],
+                  v4i* nB, int32_t* nS) {
+    const bool more = b + 1 < a.nb;
+    int32_t ps = 0;
+    if (more && tid < 128) ps = load_scale(b + 1);
+    if constexpr (NP == 2) {
+      if (b == a.rlen) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { sav[i][jj][q] = part[i][jj][q]; part[i][jj][q] = 0; }
+      }
+    }
+    const int lw = s_lw[half][b >> 2];               // this wave's 64-token half
+    if (lw <= kNarrowLimbs) {
+      v4i bx[NT][2];
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) {
+        const int r = ob + 16 * jj + m;
+        bx[jj][0] = cB[r * 8 + pc0];
+        bx[jj][1] = cB[r * 8 + pc1];
+      }
+      int32_t scp[NT];
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) scp[jj] = (int32_t)((uint32_t)cS[ob + 16 * jj + m] << (32 - a.frac));
+      // limbs outermost: S = ((D2 * 256) + D1) * 256 + D0 per chain, each limb's operands read once
+      v4i c[MT][NT];
+#pragma unroll
+      for (int l = kNarrowLimbs - 1; l >= 0; --l) {
+        if (more) issue(b + 1, nA, nB, kNarrowLimbs - 1 - l);
+        v4i av[MT][2];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int r = tb + 16 * i + m;
+          av[i][0] = cA[l][r * 8 + pc0];
+          av[i][1] = cA[l][r * 8 + pc1];
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NT; ++jj) {
+            v4i x = l == kNarrowLimbs - 1 ? v4i{0, 0, 0, 0}
+                                          : v4i{(int)((uint32_t)c[i][jj][0] << 8), (int)((uint32_t)c[i][jj][1] << 8),
+                                                (int)((uint32_t)c[i][jj][2] << 8), (int)((uint32_t)c[i][jj][3] << 8)};
+            x = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][0], bx[jj][0], x, 0, 0, 0);
+            c[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i][1], bx[jj][1], x, 0, 0, 0);
+          }
+      }
+      // high dword of S * (scale << (32 - frac)) = floor(S * scale / 2^frac)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            part[i][jj][q] = (int32_t)((uint32_t)part[i][jj][q] + (uint32_t)__mulhi(c[i][jj][q], scp[jj]));
+    } else if (more) {
+      issue(b + 1, nA, nB, -1);
+    }
+    if (more && tid < 128) nS[tid] = ps;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of block b + 1 have landed
+    __syncthreads();                                  // ... and every wave's; block b's half is free again
+  };
+  for (int64_t b = 0; b < a.nb; b += 2) {
+    step(b, sA0, sB0, sS0, sA1, sB1, sS1);
+    if (b + 1 < a.nb) step(b + 1, sA1, sB1, sS1, sA0, sB0, sS0);
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      const int64_t o = o0 + 16 * jj + m;
+      if (o >= a.N) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t t = t0 + 16 * i + 4 * g + q;
+        if (t >= T) continue;
+        int64_t v = (int64_t)part[i][jj][q];
+        if constexpr (NP == 2) v += (int64_t)sav[i][jj][q];
+        int64_t* dst = a.out + t * a.N + o;
+        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)v) : v;
+      }
+    }
+  if (wide0 || wide1) {                               // uniform over the workgroup
+    __threadfence();
+    if (half ? wide1 : wide0) gemm_wide_wave<false, MT, NT, true>(a, t0, o0, s_lw[half]);
+  }
 }
 
 // Executed int8 MFMA ops of one GEMM launch pair (profiling only): per (token tile, slab) the limb count the
@@ -1361,6 +1590,12 @@ __global__ void q1_zero_kernel(int64_t* __restrict__ p, int64_t n) {
 // +-1 sign GEMM for T >= kPmMinT (IMIE_GEMM_PM=0 disables; tuning and tests)
 static bool gemm_pm() {
   static const bool v = [] { const char* e = getenv("IMIE_GEMM_PM"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
+// the multi-weight unfolded-partial kernel where its bounds hold (IMIE_GEMM_PS=0 disables; tuning and tests)
+static bool gemm_ps() {
+  static const bool v = [] { const char* e = getenv("IMIE_GEMM_PS"); return !(e && atoi(e) == 0); }();
   return v;
 }
 
@@ -1408,9 +1643,13 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     IMIE_HIP(hipGetLastError());
   }
   imie_prof_mark(IMIE_K_Q1_GEMM, st, true);
+  GemmArgs gas[kMaxSegs];
+  int nps[kMaxSegs];
+  bool all_ps = T >= kPmMinT && gemm_pm() && gemm_ps();
+  const uint64_t xg_bytes = (uint64_t)kNarrowLimbs * nbp * Tp * 128;
   for (int i = 0; i < cnt; ++i) {
     const Q1Weight& w = *ws[i];
-    GemmArgs ga;
+    GemmArgs& ga = gas[i];
     ga.signs = nullptr;
     ga.wide_any = nullptr;
     ga.ksplit = 1;
@@ -1418,8 +1657,6 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     ga.lt = (const int*)wk.lslab.p; ga.T = T; ga.Tp = Tp; ga.N = w.N; ga.nb = w.nb; ga.nbp = nbp;
     ga.nslabs = nslabs; ga.ntt = (T + 63) / 64; ga.nto = (w.N + 127) / 128; ga.ntiles16 = w.ntiles * 16;
     ga.frac = (int)(frac > 63 ? 63 : frac); ga.accumulate = accumulate; ga.out = outs[i];
-    const dim3 grid((unsigned)(ga.ntt >= 8 ? 8 * ((ga.ntt + 7) / 8) * ga.nto : ga.ntt * ga.nto));
-    const int nbuf = gemm_nbuf();
     // high-dword epilogue: int32 scales below 2^(frac-1); |q| = |floor(S * scale / 2^frac)| <= max_q with
     // |S| < 2^30 (narrow blocks); fold before |A| + max_q could reach 2^31
     ga.kfold = 0;
@@ -1428,48 +1665,91 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
       const int64_t k = (((int64_t)1 << 31) - 1) / max_q - 1;
       ga.kfold = (int)(k < 1 ? 1 : (k > (1 << 20) ? (1 << 20) : k));
     }
-    const uint64_t xg_bytes = (uint64_t)kNarrowLimbs * nbp * Tp * 128, sg_bytes = (uint64_t)w.N * w.nb * 128,
-                   sc_bytes = (uint64_t)w.ntiles * nslabs * 64 * 4;
-    if (!w.scale64 && ga.kfold > 0 && T >= kPmMinT && gemm_pm() && xg_bytes < (1ull << 32) &&
-        sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32) && q1_ensure_signs(const_cast<Q1Weight&>(w), st) == 0) {
-      ga.signs = w.signs;
-      ga.wide_any = (int*)wk.wide.p;
-      const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
-      const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * ga.nto : ntt128 * ga.nto));
-      hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
-                         (uint32_t)sc_bytes);
-      hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
-    } else {
-      // few token tiles (batched decode): split K over grid.y so the launch fills the chip; each split adds its
-      // partial sums with 64-bit atomics (exact: integer sums mod 2^64 in any order)
-      const int64_t tiles = (int64_t)grid.x;
-      ga.ksplit = 1;
-      if (tiles < 256 && w.nb >= 8) {
-        const int64_t want = (512 + tiles - 1) / tiles, cap = w.nb / 4;
-        ga.ksplit = (int)(want < cap ? want : cap);
-        if (ga.ksplit < 1) ga.ksplit = 1;
+    // unfolded int32 partials (q1_gemm_ps_kernel): over a range of blocks the sum of |floor(S * scale / 2^frac)|
+    // with |S| < 2^30 is at most ((2^30 * range sum of |scale|) >> frac) + blocks, which must stay below 2^31;
+    // one range, or two halves
+    nps[i] = 0;
+    if (ga.kfold > 0)
+      for (int r = 1; r <= 2 && !nps[i]; ++r) {
+        const int64_t rl = (w.nb + r - 1) / r;
+        const unsigned __int128 bound = (((unsigned __int128)w.rsum[r - 1] << 30) >> ga.frac) + (uint64_t)rl;
+        if (bound < ((unsigned __int128)1 << 31) - 1) { nps[i] = r; ga.rlen = (int)rl; }
       }
-      const dim3 ngrid(grid.x, (unsigned)ga.ksplit);
-      if (ga.ksplit > 1 && !accumulate && prepped != 3) {   // prepped == 3: the producer cleared the outputs
-        const int64_t n = T * w.N;
-        hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, outs[i], n);
-      }
-      if (w.scale64) {
-        if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), ngrid, dim3(256), 0, st, ga);
-        else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), ngrid, dim3(256), 0, st, ga);
-        hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
-      } else {
-        if (ga.kfold > 0) {
-          if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, true>), ngrid, dim3(256), 0, st, ga);
-          else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, true>), ngrid, dim3(256), 0, st, ga);
-        } else {
-          if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, false>), ngrid, dim3(256), 0, st, ga);
-          else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, false>), ngrid, dim3(256), 0, st, ga);
-        }
-        hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
-      }
+    const uint64_t sg_bytes = (uint64_t)w.N * w.nb * 128, sc_bytes = (uint64_t)w.ntiles * nslabs * 64 * 4;
+    all_ps = all_ps && nps[i] > 0 && xg_bytes < (1ull << 32) && sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32);
+  }
+  for (int i = 0; i < cnt && all_ps; ++i) all_ps = q1_ensure_signs(const_cast<Q1Weight&>(*ws[i]), st) == 0;
+  if (all_ps) {
+    // one launch for every weight: their output tiles side by side
+    PsArgs P;
+    int np = 1;
+    int64_t tiles = 0;
+    for (int i = 0; i < cnt; ++i) {
+      gas[i].signs = ws[i]->signs;
+      P.s[i] = gas[i];
+      tiles += gas[i].nto;
+      P.tend[i] = tiles;
+      P.sg_bytes[i] = (uint32_t)((uint64_t)ws[i]->N * ws[i]->nb * 128);
+      P.sc_bytes[i] = (uint32_t)((uint64_t)ws[i]->ntiles * nslabs * 64 * 4);
+      np = nps[i] > np ? nps[i] : np;
     }
+    for (int i = cnt; i < kMaxSegs; ++i) { P.s[i] = gas[0]; P.tend[i] = tiles; P.sg_bytes[i] = P.sc_bytes[i] = 0; }
+    P.xg_bytes = (uint32_t)xg_bytes;
+    P.cnt = cnt;
+    const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
+    const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * tiles : ntt128 * tiles));
+    // one partial: 16 waves of 32 x 32 (128 VGPRs); two: 8 waves of 32 x 64 (the second partial's registers)
+    if (np == 1) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1>), pgrid, dim3(1024), 0, st, P);
+    else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2>), pgrid, dim3(512), 0, st, P);
     IMIE_HIP(hipGetLastError());
+  } else {
+    for (int i = 0; i < cnt; ++i) {
+      const Q1Weight& w = *ws[i];
+      GemmArgs& ga = gas[i];
+      const dim3 grid((unsigned)(ga.ntt >= 8 ? 8 * ((ga.ntt + 7) / 8) * ga.nto : ga.ntt * ga.nto));
+      const int nbuf = gemm_nbuf();
+      const uint64_t sg_bytes = (uint64_t)w.N * w.nb * 128, sc_bytes = (uint64_t)w.ntiles * nslabs * 64 * 4;
+      if (!w.scale64 && ga.kfold > 0 && T >= kPmMinT && gemm_pm() && xg_bytes < (1ull << 32) &&
+          sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32) && q1_ensure_signs(const_cast<Q1Weight&>(w), st) == 0) {
+        ga.signs = w.signs;
+        ga.wide_any = (int*)wk.wide.p;
+        const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
+        const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * ga.nto : ntt128 * ga.nto));
+        hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
+                           (uint32_t)sc_bytes);
+        hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+      } else {
+        // few token tiles (batched decode): split K over grid.y so the launch fills the chip; each split adds its
+        // partial sums with 64-bit atomics (exact: integer sums mod 2^64 in any order)
+        const int64_t tiles = (int64_t)grid.x;
+        ga.ksplit = 1;
+        if (tiles < 256 && w.nb >= 8) {
+          const int64_t want = (512 + tiles - 1) / tiles, cap = w.nb / 4;
+          ga.ksplit = (int)(want < cap ? want : cap);
+          if (ga.ksplit < 1) ga.ksplit = 1;
+        }
+        const dim3 ngrid(grid.x, (unsigned)ga.ksplit);
+        if (ga.ksplit > 1 && !accumulate && prepped != 3) {   // prepped == 3: the producer cleared the outputs
+          const int64_t n = T * w.N;
+          hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, outs[i], n);
+        }
+        if (w.scale64) {
+          if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 1, false>), ngrid, dim3(256), 0, st, ga);
+          else hipLaunchKernelGGL((q1_gemm_narrow_kernel<true, 2, false>), ngrid, dim3(256), 0, st, ga);
+          hipLaunchKernelGGL(q1_gemm_wide_kernel<true>, grid, dim3(256), 0, st, ga);
+        } else {
+          if (ga.kfold > 0) {
+            if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, true>), ngrid, dim3(256), 0, st, ga);
+            else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, true>), ngrid, dim3(256), 0, st, ga);
+          } else {
+            if (nbuf == 1) hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 1, false>), ngrid, dim3(256), 0, st, ga);
+            else hipLaunchKernelGGL((q1_gemm_narrow_kernel<false, 2, false>), ngrid, dim3(256), 0, st, ga);
+          }
+          hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
+        }
+      }
+      IMIE_HIP(hipGetLastError());
+    }
   }
   imie_prof_mark(IMIE_K_Q1_GEMM, st, false);
   if (imie_prof_on() && !imie_prof_suspend(true)) {   // count outside the timed window
@@ -1723,6 +2003,19 @@ static int64_t q1_register(const uint8_t* bits, const void* scale, int64_t N, in
   }
   w.scale64 = scale64;
   w.maxsc = maxsc > (uint64_t)INT64_MAX ? INT64_MAX : (int64_t)maxsc;
+  for (int64_t o = 0; o < N; ++o)                   // range sums of |scale| per row (saturating)
+    for (int r = 1; r <= 8; ++r) {
+      const int64_t rl = (nb + r - 1) / r;
+      for (int64_t b0 = 0; b0 < nb; b0 += rl) {
+        uint64_t sum = 0;
+        for (int64_t b = b0; b < nb && b < b0 + rl; ++b) {
+          const int64_t v = s64[(size_t)(o * nb + b)];
+          const uint64_t av = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+          sum = sum + av < sum ? UINT64_MAX : sum + av;
+        }
+        w.rsum[r - 1] = sum > w.rsum[r - 1] ? sum : w.rsum[r - 1];
+      }
+    }
   w.bytes = hb.size() + hs.size();
   w.live = true;
   g_resident_bytes += w.bytes;

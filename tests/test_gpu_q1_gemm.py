@@ -167,3 +167,26 @@ def test_gemm_sign_copy_resident_lifecycle(gpu):
         assert gpu.gpu_memory_info()["resident_weight_bytes"] == base + N * nb * 128
     gpu.q1_free_weights()
     assert gpu.gpu_memory_info()["resident_weight_bytes"] == 0
+
+
+@pytest.mark.parametrize("nb,s", [(32, 4095), (32, 8191), (96, 1365), (96, 2730), (32, 16383)])
+def test_gemm_sign_copy_partial_ranges(gpu, nb, s):
+    """The multi-weight sign-copy kernel sums each block's floor into an int32 partial without folding, over all
+    blocks or over each half (two partials); the host uses it only where the worst-case sum (|S| < 2^30 at 3 limbs
+    times the row's sum of |scale| over the range) stays below 2^31. Uniform |scale| = s at the largest value
+    that allows one partial and two partials (nb 32 and 96), and one that allows neither (the folded kernel runs);
+    activations at the 3-limb maximum, rows of all-ones bits, mixed scale signs."""
+    cap3 = 127 * (1 + 256 + 65536)
+    N, T = 48, 320
+    rng = np.random.default_rng(nb * 7 + s)
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    bits[:8] = 0xFF
+    bits[8:12] = 0
+    scale = np.full((N, nb), s, dtype=np.int64)
+    scale[16:32] *= rng.choice(np.array([1, -1], dtype=np.int64), size=(16, nb))
+    scale[40:] = -s
+    x = rng.choice(np.array([cap3, -cap3, cap3 - 1, 0], dtype=np.int64), size=(T, nb * 128))
+    x[:16] = cap3
+    x[16:24] = -cap3
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
