@@ -44,11 +44,11 @@ def matvec_bytes(scale_bytes: int) -> int:
     return K * NB * 16 + K * NB * scale_bytes + K * 8 + K * 8
 
 
-def _ref_q1():
+def _ref_q1(port: bool = False):
     """(function, kind) of the CPU Q1 linear: the reference's C kernel built from its sources into oracle/_ref when
-    present ("reference"), else the C restatement of the oracle ("port")."""
+    present ("reference"), else (or with port=True) the C restatement of the oracle ("port")."""
     ref = ROOT / "oracle" / "_ref" / "libbonsai_q1_kernel.so"
-    if ref.exists():
+    if ref.exists() and not port:
         so = ctypes.CDLL(str(ref))
         fn, kind = so.bonsai_q1_linear_i64, "reference"
     else:
@@ -60,21 +60,28 @@ def _ref_q1():
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with the family / model / stepping numbers (a virtualized host may
+    report only a generic model name)."""
+    info = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (t.strip() for t in line.split(":", 1))
+                info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    ids = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    extra = ", ".join(x for x in (ids, f"{info['cache size']} cache" if "cache size" in info else "") if x)
+    return f"{name} ({extra})" if extra else name
 
 
-def cpu_worker(npz: str, seconds: float, reps: int) -> None:
+def cpu_worker(npz: str, seconds: float, reps: int, port: bool = False) -> None:
     """Time the CPU Q1 linear on the config-1 matvec: ``reps`` repetitions of ``seconds`` each with the thread
     count this process was given (OMP_NUM_THREADS); print one JSON line with the median."""
     d = np.load(npz)
     x, bits, scale, gpu_out = d["x"], d["bits"], d["scale"], d["out"]
-    fn, kind = _ref_q1()
+    fn, kind = _ref_q1(port)
     out = np.empty((1, K), dtype=np.int64)
     call = lambda: fn(x.ctypes.data, bits.ctypes.data, scale.ctypes.data, 1, K, NB, 16, out.ctypes.data)
     assert call() == 0
@@ -393,11 +400,12 @@ def main() -> int:
     ap.add_argument("--c5-tokens", type=int, default=64, help="config-5 ragged batch decode leg (0 = skip)")
     ap.add_argument("--moe-tokens", type=int, default=64, help="config-4 MoE block leg (0 = skip)")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-port", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     args = ap.parse_args()
     if args.cpu_worker:
-        cpu_worker(args.cpu_worker, args.cpu_seconds, args.cpu_reps)
+        cpu_worker(args.cpu_worker, args.cpu_seconds, args.cpu_reps, args.cpu_port)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures ONE MI355X; --gpus {args.gpus} is not supported "
@@ -505,24 +513,29 @@ def main() -> int:
         with tempfile.TemporaryDirectory() as td:
             npz = os.path.join(td, "c1.npz")
             np.savez(npz, x=x_host, bits=bits[:K], scale=scale[:K], out=out_host[:, :K])
-            for threads in (share, 1):
+            # the reference C kernel at the job's share and at one thread, then the repo's own C restatement
+            # (oracle/c) at the share: the restatement is the baseline that does not need the reference tree
+            for key, threads, impl in (("ref", share, []), ("ref1", 1, []), ("port", share, ["--cpu-port"])):
                 env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close")
                 r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-worker", npz, "--cpu-seconds",
-                                    str(args.cpu_seconds), "--cpu-reps", str(args.cpu_reps)], env=env,
+                                    str(args.cpu_seconds), "--cpu-reps", str(args.cpu_reps), *impl], env=env,
                                    capture_output=True, text=True, timeout=600)
                 if r.returncode != 0:
                     print(r.stderr[-2000:], file=sys.stderr)
                     break
-                res[threads] = json.loads(r.stdout.strip().splitlines()[-1])
-        if share in res and 1 in res:
-            c, c1 = res[share], res[1]
+                res[key] = json.loads(r.stdout.strip().splitlines()[-1])
+        if "ref" in res and "ref1" in res:
+            c, c1 = res["ref"], res["ref1"]
+            cp = res.get("port")
             cpu = {"value": round(c["value"], 3), "unit": "GB/s", "cores": share, "kind": c["kind"],
-                   "single_thread_value": round(c1["value"], 3), "cpu_model": cpu_model(),
+                   "single_thread_value": round(c1["value"], 3),
+                   "port_value": round(cp["value"], 3) if cp else None, "cpu_model": cpu_model(),
                    "host_cpus": os.cpu_count(),
                    "sample": f"config-1 4096x4096 Q1_0 matvec (int64 codec-range scales), median of "
                              f"{args.cpu_reps} x {args.cpu_seconds:.0f} s runs at {share} threads "
-                             f"({c['calls']} calls) and at 1 thread ({c1['calls']} calls); output byte-equal "
-                             f"to GPU: {c['match'] and c1['match']}"}
+                             f"({c['calls']} calls) and at 1 thread ({c1['calls']} calls); port_value: the repo's C "
+                             f"restatement (oracle/c) at {share} threads; output byte-equal to GPU: "
+                             f"{c['match'] and c1['match'] and (cp is None or cp['match'])}"}
 
     dec = None
     if args.decode_tokens > 0:

@@ -1568,6 +1568,446 @@ __global__ __launch_bounds__(512) void pf_pv8w_kernel(AttnDesc d) {
     }
 }
 
+// Prefill attention over the kv8 cache in one launch (M > 1). Workgroup = (b, head h, 16 consecutive query rows);
+// wave w takes keys 16 w .. 16 w + 15 of every 64-key step. The integer softmax needs the row maximum before any
+// e_j and Z before any p_j, so the keys are walked three times and QK^T is recomputed each time instead of being
+// stored: pass 1 the row maxima, pass 2 Z = sum e_j, pass 3 p_j = floor((e_j << f) / Z) as balanced digits into
+// LDS and the PV MFMAs (wave w owns dim tiles 2 w, 2 w + 1). Nothing but q, K, V and the outputs touches HBM.
+// Scores: per 16-key tile T_e = sum over (q limb lq, K digit db) with lq + db = e of the int8 MFMA products
+// (|T_e| < 2^23), S = sum_e T_e << 8 e in int64 (256^e = 0 mod 2^64 for e >= 8), s = ((S >> f) * inv_sqrt) >> f.
+// PV: T'_e (e = lp + db) in int32 over up to 64 steps (|T'_e| < 2^28), folded into int64.
+constexpr int kFfRows = 16;
+// rows padded from 128 to 144 bytes: the 16-byte operand reads of 8 consecutive rows then start in distinct banks
+constexpr int kFfPad = 144;
+struct FfShared {
+  int8_t sQ[8][kFfRows][kFfPad];                               // q digit planes (limb, row, dim)
+  int8_t sP[2][4][kFfRows][kFfPad];                            // p digit planes of one key step, double buffer
+  uint64_t s_red[8][kFfRows];
+  uint64_t s_mq[kFfRows];
+};
+
+template <int LQ, int HD, bool F32, int PASSES, int NW>
+__device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, int64_t b, int64_t h, int64_t kv, int64_t pt,
+                               int64_t row0, int64_t len);
+
+// MODE 0: head dim 128, frac 16 and tiles whose scores fit the 32-bit form (see pf_fused8_body), the common case;
+// a workgroup whose tile does not records it in d.rowmax[workgroup] and leaves the tile to the MODE 1 launch that
+// follows, which does only those tiles (or every tile when the head dim is not 128) in general int64 arithmetic.
+template <int MODE, int NW>
+__global__ __launch_bounds__(64 * NW) void pf_fused8_kernel(AttnDesc d) {
+  __shared__ __align__(16) FfShared S;
+  if (MODE == 1 && d.hd == 128 && d.rowmax[blockIdx.x] == 0) return;
+  if (MODE == 2 && d.rowmax[blockIdx.x] != 0) return;
+  auto& sQ = S.sQ;
+  auto& s_mq = S.s_mq;
+  const int64_t npt = (d.M + kFfRows - 1) / kFfRows;
+  const int64_t bh = imie_udiv32(blockIdx.x, npt);
+  const int64_t pt = npt - 1 - imie_umod32(blockIdx.x, npt);   // longest rows first
+  const int64_t b = imie_udiv32(bh, d.H), h = imie_umod32(bh, d.H), kv = imie_udiv32(h, d.H / d.Hkv);
+  const int64_t bkv = b * d.Hkv + kv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  if (blockIdx.x == 0 && tid == 0) check_rope_guard(d);
+  const int64_t row0 = bh * d.M + pt * kFfRows;                // query row r = (b * H + h) * M + m
+  const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
+  auto row_lv = [&](int i) -> int64_t {                         // keys visible to tile row i (0: no row)
+    const int64_t mm = pt * kFfRows + i;
+    if (mm >= d.M) return 0;
+    return d.starts ? d.starts[b] + mm + 1 : len;
+  };
+  int64_t vis = 0;
+  for (int i = 0; i < kFfRows; ++i) vis = max(vis, row_lv(i));
+  // q of the tile: thread -> row tid / 16, dims 8 (tid % 16) .. + 7 (threads 0 .. 255); digits of every limb the
+  // tile needs
+  {
+    const int qi = (tid >> 4) & 15, qc = 8 * (tid & 15);
+    const bool qrow = tid < 256 && pt * kFfRows + qi < d.M;
+    int64_t qv[8];
+    uint64_t mq = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      qv[c] = (qrow && qc + c < d.hd) ? d.q[qoff(d, row0 + qi) + qc + c] : 0;
+      const uint64_t a = imie_absu64(qv[c]);
+      mq = a > mq ? a : mq;
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) { const uint64_t w2 = __shfl_xor(mq, o, 64); mq = w2 > mq ? w2 : mq; }
+    if ((tid & 15) == 0 && tid < 256) s_mq[qi] = mq;
+    __syncthreads();
+    uint64_t mqa = 0;
+    for (int i = 0; i < kFfRows; ++i) mqa = s_mq[i] > mqa ? s_mq[i] : mqa;
+    const int Lq0 = imie_limbs_needed(mqa);
+    if (tid < 256)
+      for (int lq = 0; lq < 8; ++lq)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sQ[lq][qi][qc + c] = lq < Lq0 ? (int8_t)bal_digit(qv[c], lq) : (int8_t)0;
+    __syncthreads();
+  }
+  uint64_t mqa = 0;
+  for (int i = 0; i < kFfRows; ++i) mqa = s_mq[i] > mqa ? s_mq[i] : mqa;
+  const int Lq = imie_limbs_needed(mqa);
+  // the limb count is uniform over the workgroup: one specialization per count range (no per-limb predication)
+  if (MODE == 0) {
+    const int64_t bkv = b * d.Hkv + kv;
+    const bool fast = Lq <= 3 && d.frac == 16 && d.inv_sqrt < ((int64_t)1 << 31) && len <= 16384 &&
+                      d.dclip >= 0 && d.dclip < ((int64_t)1 << 20) && d.log2e >= 0 && d.log2e < ((int64_t)1 << 17) &&
+                      (u128)mqa * d.run_k[bkv] * 128 < ((u128)1 << 47);
+    if (tid == 0) d.rowmax[blockIdx.x] = fast ? 0 : 1;
+    if (fast) pf_fused8_body<3, 128, true, 1, NW>(d, S, b, h, kv, pt, row0, len);
+  } else if (MODE == 2) {
+    pf_fused8_body<3, 128, true, 2, NW>(d, S, b, h, kv, pt, row0, len);
+  } else {
+    pf_fused8_body<8, 0, false, 3, NW>(d, S, b, h, kv, pt, row0, len);  // any hd (multiple of 16, <= 128), any limbs
+  }
+}
+
+// F32 (frac 16, head dim 128, at most 3 q limbs, 128 max|q| max|K| < 2^47 so |q . k| < 2^47): the scores are formed
+// in 32-bit arithmetic. With 3 limbs every T_e sums at most 3 products of 128-term int8 dots (|.| <= 2^21 each),
+// so U0 = T0 + 256 T1, U1 = T2 + 256 T3, U2 = T4 + 256 T5 are exact int32 and S = U0 + 2^16 U1 + 2^32 U2; then
+// S >> 16 = U1 + 2^16 U2 + (U0 >> 16) fits int32 (evaluated mod 2^32, exact since the result fits) and
+// ((S >> 16) * inv_sqrt) >> 16 comes from one 32 x 32 -> 64 product.
+// PASSES: 1 = passes 1 and 2 (the row maxima and Z go to d.acc[r] and d.acc[rows + r]), 2 = pass 3 from them,
+// 3 = all three in one launch.
+// NW waves: wave w scores keys 16 w .. 16 w + 15 of every 16 NW-key step and (pass 3) owns 8 / NW of the 16-dim
+// output tiles.
+template <int LQ, int HD, bool F32, int PASSES, int NW>
+__device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, int64_t b, int64_t h, int64_t kv, int64_t pt,
+                               int64_t row0, int64_t len) {
+  constexpr int STEP = 16 * NW, DPW = 8 / NW, KSP = NW / 4;   // keys per step, dim tiles per wave, 64-key K steps
+  auto& sQ = S.sQ;
+  auto& sP = S.sP;
+  auto& s_red = S.s_red;
+  auto& s_mq = S.s_mq;
+  constexpr int NE = LQ + 3 < 8 ? LQ + 3 : 8;                 // exponents lq + db below 8 (256^8 = 0 mod 2^64)
+  // F32: scores, row maxima, Z (at most 16384 keys: Z < 2^30) and p (<= 2^16) in 32 bits, 3 p limbs
+  using ST = std::conditional_t<F32, int32_t, int64_t>;
+  using UT = std::conditional_t<F32, uint32_t, uint64_t>;
+  constexpr ST SMIN = F32 ? (ST)INT32_MIN : (ST)INT64_MIN;
+  constexpr UT SBIT = (UT)1 << (8 * sizeof(UT) - 1);
+  constexpr int NTP = F32 ? 6 : 7;                             // PV exponents lp + db (lp < 3 when F32)
+  const int64_t bkv = b * d.Hkv + kv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  auto row_lv = [&](int i) -> int64_t {                         // keys visible to tile row i (0: no row)
+    const int64_t mm = pt * kFfRows + i;
+    if (mm >= d.M) return 0;
+    return d.starts ? d.starts[b] + mm + 1 : len;
+  };
+  int64_t vis = 0;
+  for (int i = 0; i < kFfRows; ++i) vis = max(vis, row_lv(i));
+  const int64_t HDv = HD ? HD : d.hd;                          // head dim (compile-time for the 128 case)
+  const int KS = (int)((HDv + 63) / 64);
+  int32_t lvr[4];                                              // visible keys of this lane's rows 4 g + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lvr[i] = (int32_t)row_lv(4 * g + i);
+  const int8_t* Kb = (const int8_t*)d.K;
+  // K digits of the 16-key tile t (keys t .. t + 15 lie in one page: pages hold a multiple of 64 keys and t is a
+  // multiple of 16): the page is wave-uniform, lane m takes key t + m
+  auto load_k = [&](int64_t t, v4i (&bk)[4][2]) {
+    const int64_t tu = (int64_t)__builtin_amdgcn_readfirstlane((int)t);   // wave-uniform: scalar page arithmetic
+    int64_t pi, slot;
+    page_split(d, tu, pi, slot);
+    const int8_t* kblk = Kb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P) +
+                         imie_kv8::k_off(slot, 0, 0, HDv);
+    // keys past the sequence length are loaded from their (allocated) slots and masked where the scores are used
+    const int8_t* kl = kblk + 16 * m;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        if (hh >= KS) { bk[db][hh] = v4i{0, 0, 0, 0}; continue; }
+        const int c = 64 * hh + 16 * g;
+        const v4i v = *(const v4i*)(kl + imie_kv8::k_piece(db, c < HDv ? c : 0, HDv));
+        bk[db][hh] = c < HDv ? v : v4i{0, 0, 0, 0};
+      }
+  };
+  // scores of the lane's 4 rows for key t + m from the tile's K digits; invalid entries INT64_MIN
+  auto scores = [&](int64_t t, const v4i (&bk)[4][2], ST sc[4]) {
+    const int32_t j = (int32_t)t + m;
+    v4i T[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) T[e] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int lq = 0; lq < LQ; ++lq) {                          // limbs above the tile's count hold zero digits
+      v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
+      v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
+      if (16 * g >= HDv) a0 = v4i{0, 0, 0, 0};
+      if (64 + 16 * g >= HDv) a1 = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        if (lq + db >= NE) continue;
+        v4i x = mfma8(a0, bk[db][0], T[lq + db]);
+        if (KS > 1) x = mfma8(a1, bk[db][1], x);
+        T[lq + db] = x;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int64_t s;
+      if constexpr (F32) {
+        static_assert(NE == 6, "3 q limbs");
+        const uint32_t U0 = (uint32_t)T[0][i] + ((uint32_t)T[1][i] << 8);
+        const uint32_t U1 = (uint32_t)T[2][i] + ((uint32_t)T[3][i] << 8);
+        const uint32_t U2 = (uint32_t)T[4][i] + ((uint32_t)T[5][i] << 8);
+        const int32_t V = (int32_t)(U1 + (U2 << 16) + (uint32_t)((int32_t)U0 >> 16));
+        s = (int64_t)V * (int32_t)d.inv_sqrt >> 16;
+      } else {
+        uint64_t Sx = 0;
+#pragma unroll
+        for (int e = NE - 1; e >= 0; --e) Sx = (Sx << 8) + (uint64_t)(int64_t)T[e][i];
+        s = (int64_t)Sx >> d.frac;
+        s = (int64_t)((uint64_t)s * (uint64_t)d.inv_sqrt) >> d.frac;
+      }
+      sc[i] = j < lvr[i] ? (ST)s : SMIN;
+    }
+  };
+  // cross-lane (16 keys) and cross-wave reduction of per-row values held as lanes (g, i)
+  auto reduce_rows = [&](uint64_t v[4], bool is_max, uint64_t out[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) {
+        const uint64_t w2 = (uint64_t)__shfl_xor((int64_t)v[i], o, 64);
+        v[i] = is_max ? (w2 > v[i] ? w2 : v[i]) : v[i] + w2;
+      }
+      if (m == 0) s_red[wave][4 * g + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint64_t a = s_red[0][4 * g + i];
+      for (int w = 1; w < NW; ++w) a = is_max ? (s_red[w][4 * g + i] > a ? s_red[w][4 * g + i] : a) : a + s_red[w][4 * g + i];
+      out[i] = a;
+    }
+    __syncthreads();
+  };
+  // pass 1: row maxima (signed max as the unsigned max of values offset by INT64_MIN)
+  // this wave's tiles t = 16 wave, + 64, ... below vis, the next tile's K in flight while one is scored
+  auto walk = [&](auto&& use) {
+    v4i bkA[4][2], bkB[4][2];
+    int64_t t = 16 * wave;
+    if (t < vis) load_k(t, bkA);
+    while (t < vis) {
+      const int64_t t2 = t + STEP;
+      if (t2 < vis) load_k(t2, bkB);
+      ST sc[4];
+      scores(t, bkA, sc);
+      use(sc);
+      if (t2 >= vis) break;
+      const int64_t t3 = t2 + STEP;
+      if (t3 < vis) load_k(t3, bkA);
+      scores(t2, bkB, sc);
+      use(sc);
+      t = t3;
+    }
+  };
+  ST Mx[4];
+  UT Z[4];
+  const int64_t rows_all = d.B * d.H * d.M;
+  const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
+  auto expv = [&](ST s, int i) -> int64_t {
+    if (s == SMIN) return 0;
+    if constexpr (F32) {
+      // exp2_neg_fixed32 at frac 16 with dclip < 2^20 and log2e < 2^17: every product fits 32 bits
+      uint32_t dd = (uint32_t)(Mx[i] - s);
+      if (dd > (uint32_t)d.dclip) dd = (uint32_t)d.dclip;
+      const uint32_t u = (uint32_t)(((uint64_t)dd * (uint32_t)d.log2e) >> 16);
+      const uint32_t k = u >> 16, f = u & 0xFFFFu;
+      const uint32_t f2 = (f * f) >> 16, f3 = (f2 * f) >> 16;
+      const int32_t poly = 65536 - (int32_t)((45426u * f) >> 16) + (int32_t)((15743u * f2) >> 16) -
+                           (int32_t)((3638u * f3) >> 16);
+      return poly <= 0 ? 0 : (int64_t)((uint32_t)poly >> k);      // k < 32 (u < 2^21)
+    } else {
+      int64_t dd = (int64_t)((uint64_t)Mx[i] - (uint64_t)s);
+      if (dd > d.dclip) dd = d.dclip;
+      return exp_clipped(dd, d.frac, d.log2e, fx32);
+    }
+  };
+  if constexpr (PASSES != 2) {
+  UT mo[4] = {0, 0, 0, 0};
+  walk([&](const ST (&sc)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const UT v = (UT)sc[i] ^ SBIT;
+      mo[i] = v > mo[i] ? v : mo[i];
+    }
+  });
+  uint64_t M4[4];
+  {
+    uint64_t mo64[4] = {mo[0], mo[1], mo[2], mo[3]};
+    reduce_rows(mo64, true, M4);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) Mx[i] = (ST)((UT)M4[i] ^ SBIT);
+  // pass 2: Z
+  UT zs[4] = {0, 0, 0, 0};
+  walk([&](const ST (&sc)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) zs[i] += (UT)expv(sc[i], i);
+  });
+  {
+    uint64_t z64[4] = {zs[0], zs[1], zs[2], zs[3]}, zo[4];
+    reduce_rows(z64, false, zo);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Z[i] = (UT)zo[i];
+  }
+  }
+  if constexpr (PASSES == 1) {                                 // hand the row maxima and Z to the pass-3 launch
+    if (m == 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (lvr[i] == 0 || wave != 0) continue;
+        d.acc[row0 + 4 * g + i] = (uint64_t)(int64_t)Mx[i];
+        d.acc[rows_all + row0 + 4 * g + i] = (uint64_t)Z[i];
+      }
+    return;
+  }
+  if constexpr (PASSES == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      Mx[i] = lvr[i] ? (ST)(int64_t)d.acc[row0 + 4 * g + i] : (ST)0;
+      Z[i] = lvr[i] ? (UT)d.acc[rows_all + row0 + 4 * g + i] : (UT)0;
+    }
+  }
+  double rz[4];
+  float rzf[4];                                                 // F32: 2^16 / Z for the single-precision quotient
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    rz[i] = Z[i] != 0 ? 1.0 / (double)Z[i] : 0.0;
+    rzf[i] = Z[i] != 0 ? (float)(65536.0 / (double)Z[i]) : 0.0f;
+  }
+  // p = floor((e << frac) / Z). F32 (e <= 2^16, Z < 2^30): the float estimate e * (2^16 / Z) is within 2^-5 of the
+  // quotient (< 2^17), so its floor is off by at most one; the remainder (e << 16) - q Z lies in (-Z, 2Z), below
+  // 2^31 in magnitude, so it is exact in wrapping 32-bit arithmetic and settles q
+  auto probv = [&](int64_t e, int i) -> int64_t {
+    if (Z[i] == 0) return 0;
+    if constexpr (F32) {
+      uint32_t q = (uint32_t)((float)(uint32_t)e * rzf[i]);
+      const int32_t r = (int32_t)(((uint32_t)e << 16) - q * (uint32_t)Z[i]);
+      if (r < 0) --q;
+      else if ((uint32_t)r >= (uint32_t)Z[i]) ++q;
+      return (int64_t)q;
+    } else {
+      return prob_div(e, d.frac, Z[i], rz[i]);
+    }
+  };
+  // pass 3: p digits of each 64-key step into LDS, then PV
+  const int Lp = F32 ? 3 : imie_limbs_needed((uint64_t)1 << d.frac);   // <= 4 (frac <= 29); 3 at frac 16
+  const int DT = (int)(d.hd / 16);
+  const int8_t* Vb = (const int8_t*)d.V;
+  v4i Tp[DPW][NTP];
+  uint64_t O[DPW][4];
+#pragma unroll
+  for (int tt = 0; tt < DPW; ++tt) {
+#pragma unroll
+    for (int e = 0; e < NTP; ++e) Tp[tt][e] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[tt][i] = 0;
+  }
+  auto fold = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < DPW; ++tt)
+#pragma unroll
+      for (int e = 0; e < NTP; ++e) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[tt][i] += (uint64_t)(int64_t)Tp[tt][e][i] << (8 * e);
+        Tp[tt][e] = v4i{0, 0, 0, 0};
+      }
+  };
+  UT mp[4] = {0, 0, 0, 0};
+  int steps = 0, buf = 0;
+  // K of this wave's tile and V of the step are loaded one step ahead, into the registers the current step has
+  // just consumed: the loads are in flight during the p digits, the barrier and the PV MFMAs
+  auto load_v = [&](int64_t t0, v4i (&bv)[DPW][KSP][4]) {
+#pragma unroll
+    for (int ks = 0; ks < KSP; ++ks) {                         // each 64 keys lie in one page
+      const int64_t tu = (int64_t)__builtin_amdgcn_readfirstlane((int)(t0 + 64 * ks));
+      int64_t pi, slot0;
+      page_split(d, tu, pi, slot0);
+      const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P);
+      const bool live = tu < vis;
+#pragma unroll
+      for (int tt = 0; tt < DPW; ++tt) {
+        const int tile = DPW * wave + tt;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          bv[tt][ks][db] = (live && tile < DT)
+                               ? *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, 16 * tile + m, HDv, d.P))
+                               : v4i{0, 0, 0, 0};
+      }
+    }
+  };
+  v4i bk[4][2], bv[DPW][KSP][4];
+  if (16 * wave < vis) load_k(16 * wave, bk);
+  load_v(0, bv);
+  for (int64_t t0 = 0; t0 < vis; t0 += STEP, buf ^= 1) {
+    const int64_t t = t0 + 16 * wave;
+    ST sc[4] = {SMIN, SMIN, SMIN, SMIN};
+    if (t < vis) scores(t, bk, sc);
+    if (t + STEP < vis) load_k(t + STEP, bk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e = expv(sc[i], i);
+      const int64_t p = probv(e, i);
+      mp[i] = (UT)p > mp[i] ? (UT)p : mp[i];
+      // balanced base-256 digits of 0 <= p <= 2^frac < 2^30: the bytes of p + 0x80808080, each less 0x80
+      const uint32_t dg = ((uint32_t)p + 0x80808080u) ^ 0x80808080u;
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp)
+        if (lp < Lp) sP[buf][lp][4 * g + i][16 * wave + m] = (int8_t)(dg >> (8 * lp));
+    }
+    __syncthreads();                                          // the step's p digits are in LDS
+#pragma unroll
+    for (int ks = 0; ks < KSP; ++ks)
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp) {
+        if (lp >= Lp) break;
+        const v4i a = *(const v4i*)&sP[buf][lp][m][64 * ks + 16 * g];
+#pragma unroll
+        for (int tt = 0; tt < DPW; ++tt) {
+          if (DPW * wave + tt >= DT) continue;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+            if (lp + db < NTP) Tp[tt][lp + db] = mfma8(a, bv[tt][ks][db], Tp[tt][lp + db]);
+        }
+      }
+    if (t0 + STEP < vis) load_v(t0 + STEP, bv);
+    if (++steps == 64) { fold(); steps = 0; }
+  }
+  fold();
+  // p maxima of the rows for the PV bound (lanes of one g share rows)
+  uint64_t MP[4];
+  {
+    uint64_t mp64[4] = {mp[0], mp[1], mp[2], mp[3]};
+    reduce_rows(mp64, true, MP);
+  }
+#pragma unroll
+  for (int tt = 0; tt < DPW; ++tt) {
+    const int tile = DPW * wave + tt;
+    if (tile >= DT) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * g + i;
+      if (lvr[i] == 0) continue;
+      d.out[qoff(d, row0 + rr) + 16 * tile + m] = (int64_t)O[tt][i] >> d.frac;
+    }
+  }
+  if (tid < kFfRows && row_lv(tid) > 0) {
+    const int64_t r = row0 + tid;
+    d.maxq[r] = s_mq[tid];
+    uint64_t mpr = 0;
+    for (int w = 0; w < NW; ++w) mpr = s_red[w][tid] > mpr ? s_red[w][tid] : mpr;
+    const u128 qk = (u128)s_mq[tid] * d.run_k[bkv];
+    if (qk > (u128)(INT64_MAX / d.hd)) atomicOr(d.status, IMIE_EOVF);
+    const u128 pv = (u128)mpr * d.run_v[bkv];
+    if (pv > (u128)(INT64_MAX / row_lv(tid))) atomicOr(d.status, IMIE_EOVF);
+  }
+}
+
+// the one-launch prefill attention (IMIE_PF_FUSED=0 selects the three-kernel path; tuning and tests)
+bool pf_fused() {
+  static const bool v = [] { const char* e = getenv("IMIE_PF_FUSED"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
 // prefill PV with 64-row workgroups (IMIE_PV_WIDE=0 selects the 16-row kernel; tuning and tests)
 bool pv_wide() {
   static const bool v = [] { const char* e = getenv("IMIE_PV_WIDE"); return !(e && atoi(e) == 0); }();
@@ -1705,6 +2145,17 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
   }
   if (d.kv32) {                                      // kv8 prefill: MFMA scores, softmax to p digits, MFMA PV
     if (d.hd % 16 != 0 || !d.run_k || !d.run_v) return IMIE_EARG;
+    if (d.hd <= 128 && pf_fused()) {
+      const int64_t npt = (d.M + kFfRows - 1) / kFfRows;
+      if (d.hd == 128) {
+        hipLaunchKernelGGL((pf_fused8_kernel<0, 4>), dim3((unsigned)(d.B * d.H * npt)), dim3(256), 0, st, d);
+        hipLaunchKernelGGL((pf_fused8_kernel<2, 4>), dim3((unsigned)(d.B * d.H * npt)), dim3(256), 0, st, d);
+      }
+      hipLaunchKernelGGL((pf_fused8_kernel<1, 4>), dim3((unsigned)(d.B * d.H * npt)), dim3(256), 0, st, d);
+      IMIE_HIP(hipGetLastError());
+      imie_prof_mark(IMIE_K_ATTN, st, false);
+      return IMIE_OK;
+    }
     const int64_t nrt16 = (grows + 15) / 16, nkt8 = (d.Lmax + kPfKeys - 1) / kPfKeys;
     const int64_t nkg = (nkt8 + kPfTilesPerWg - 1) / kPfTilesPerWg;
     hipLaunchKernelGGL(pf_scores8_kernel, dim3((unsigned)(d.B * d.Hkv * nrt16), (unsigned)nkg), dim3(256), 0, st, d);

@@ -1490,6 +1490,7 @@ __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) 
       for (int jj = 0; jj < NT; ++jj) scp[jj] = (int32_t)((uint32_t)cS[ob + 16 * jj + m] << (32 - a.frac));
       // limbs outermost: S = ((D2 * 256) + D1) * 256 + D0 per chain, each limb's operands read once
       v4i c[MT][NT];
+      __builtin_amdgcn_s_setprio(1);               // favour this wave's MFMA issue over the others' epilogues
 #pragma unroll
       for (int l = kNarrowLimbs - 1; l >= 0; --l) {
         if (more) issue(b + 1, nA, nB, kNarrowLimbs - 1 - l);
@@ -1519,6 +1520,7 @@ __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) 
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             part[i][jj][q] = (int32_t)((uint32_t)part[i][jj][q] + (uint32_t)__mulhi(c[i][jj][q], scp[jj]));
+      __builtin_amdgcn_s_setprio(0);
     } else if (more) {
       issue(b + 1, nA, nB, -1);
     }
