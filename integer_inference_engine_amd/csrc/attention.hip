@@ -1577,6 +1577,17 @@ __global__ __launch_bounds__(512) void pf_pv8w_kernel(AttnDesc d) {
 // (|T_e| < 2^23), S = sum_e T_e << 8 e in int64 (256^e = 0 mod 2^64 for e >= 8), s = ((S >> f) * inv_sqrt) >> f.
 // PV: T'_e (e = lp + db) in int32 over up to 64 steps (|T'_e| < 2^28), folded into int64.
 constexpr int kFfRows = 16;
+// 16 bytes at a wave-uniform base plus a 32-bit lane offset, as a buffer load (the base goes to scalar registers,
+// no 64-bit address arithmetic per lane); bytes: the extent of the block read from the base
+__device__ inline v4i ld16u(const void* base, uint32_t off, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;                        // wave-uniform by the caller's construction
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)u, (short)0, (int)bytes, 0x00020000);
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
 // rows padded from 128 to 144 bytes: the 16-byte operand reads of 8 consecutive rows then start in distinct banks
 constexpr int kFfPad = 144;
 struct FfShared {
@@ -1705,17 +1716,18 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     const int64_t tu = (int64_t)__builtin_amdgcn_readfirstlane((int)t);   // wave-uniform: scalar page arithmetic
     int64_t pi, slot;
     page_split(d, tu, pi, slot);
+    // wave-uniform 64-bit base (scalar registers) plus 32-bit lane offsets: no 64-bit address arithmetic per load
     const int8_t* kblk = Kb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P) +
                          imie_kv8::k_off(slot, 0, 0, HDv);
     // keys past the sequence length are loaded from their (allocated) slots and masked where the scores are used
-    const int8_t* kl = kblk + 16 * m;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         if (hh >= KS) { bk[db][hh] = v4i{0, 0, 0, 0}; continue; }
         const int c = 64 * hh + 16 * g;
-        const v4i v = *(const v4i*)(kl + imie_kv8::k_piece(db, c < HDv ? c : 0, HDv));
+        const uint32_t off = 16u * (uint32_t)m + ((uint32_t)db * (uint32_t)HDv + (uint32_t)(c < HDv ? c : 0)) * 16u;
+        const v4i v = ld16u(kblk, off, (uint32_t)(4 * 16 * HDv));
         bk[db][hh] = c < HDv ? v : v4i{0, 0, 0, 0};
       }
   };
@@ -1924,14 +1936,15 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
       page_split(d, tu, pi, slot0);
       const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P);
       const bool live = tu < vis;
+      const int8_t* vs = vblk + slot0;                         // uniform; lane offsets below are 32-bit
 #pragma unroll
       for (int tt = 0; tt < DPW; ++tt) {
         const int tile = DPW * wave + tt;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-          bv[tt][ks][db] = (live && tile < DT)
-                               ? *(const v4i*)(vblk + imie_kv8::v_off(slot0 + 16 * g, db, 16 * tile + m, HDv, d.P))
-                               : v4i{0, 0, 0, 0};
+        for (int db = 0; db < 4; ++db) {
+          const uint32_t off = ((uint32_t)db * (uint32_t)HDv + (uint32_t)(16 * tile + m)) * (uint32_t)d.P + 16u * g;
+          bv[tt][ks][db] = (live && tile < DT) ? ld16u(vs, off, (uint32_t)(4 * HDv * d.P)) : v4i{0, 0, 0, 0};
+        }
       }
     }
   };
