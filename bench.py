@@ -128,6 +128,10 @@ def decode_leg(so, torch, tokens: int, ctx: int = 4096, n_layers: int = 36, voca
     hscale = rng.integers(1, 4097, size=(vocab, d // 128), dtype=np.int64)
     w["out_head"], w["out_head_vocab"] = gn.q1_register_weight(hbits, hscale), vocab
     g["finalg"] = gn.buf_upload_i64(rng.integers(1 << 15, (1 << 17) + 1, size=(d,), dtype=np.int64))
+    if tokens <= 0:                                   # config 5 alone (profiling it without the b=1 leg's kernels)
+        ebits = torch.from_numpy(hbits).cuda()
+        escale = torch.from_numpy(hscale).cuda()
+        return {"_c5": c5_leg(so, torch, w, g, ebits, escale, c5_tokens) if c5_tokens > 0 else None}
     cap = ctx + tokens + 2 + 8 + 4 + 64
     cos, sin = bonsai8b_tables(cap)
     g["cos_h"], g["sin_h"] = gn.buf_upload_i64(cos), gn.buf_upload_i64(sin)
@@ -538,7 +542,7 @@ def main() -> int:
                              f"{c['match'] and c1['match'] and (cp is None or cp['match'])}"}
 
     dec = None
-    if args.decode_tokens > 0:
+    if args.decode_tokens > 0 or args.c5_tokens > 0:
         del bits, scale
         so.bonsai_q1_free_weights()
         print("[bench] 8B-shape decode leg", file=sys.stderr, flush=True)
@@ -573,7 +577,7 @@ def main() -> int:
                      "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,
-        "decode_8b_b1": {k: v for k, v in dec.items() if k != "_c5"} if dec else None,
+        "decode_8b_b1": {k: v for k, v in dec.items() if k != "_c5"} if dec and args.decode_tokens > 0 else None,
         "decode_c5_batch32": dec.get("_c5") if dec else None,
         "prefill_8b_layer": pre,
         "moe_c4": moe,

@@ -1351,12 +1351,14 @@ __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
 // One launch covers up to kMaxSegs weights of the same n_blocks (q / k / v, gate / up): their output tiles are
 // concatenated, so the small k / v projections share the grid with q instead of each filling part of the chip.
 // ------------------------------------------------------------------------------------------------------
+constexpr int kPsBt = 4, kPsBo = 8;                  // q1_gemm_ps_kernel block of token x output tiles per XCD round
 struct PsArgs {
   GemmArgs s[kMaxSegs];
   int64_t tend[kMaxSegs];          // cumulative output tiles through segment i
   uint32_t sg_bytes[kMaxSegs], sc_bytes[kMaxSegs];
   uint32_t xg_bytes;
   int cnt;
+  int map;                         // 1: blocked tile order (see the kernel)
 };
 
 template <int MT, int NT, int NP>
@@ -1374,7 +1376,16 @@ __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) 
   const int64_t T = P.s[0].T, ntt = (T + kPmTok - 1) / kPmTok, nto = P.tend[P.cnt - 1], wg = blockIdx.x;
   int64_t tt, ot;
   bool live;
-  if (ntt >= 8) {                                     // each XCD walks whole token tiles (their digits stay in L2)
+  if (P.map) {
+    // blocks of kPsBt token tiles x kPsBo output tiles, one block per XCD round (the XCD's 32 CUs run one
+    // workgroup each): every sign tile of the block is fetched for kPsBt workgroups and every digit tile for kPsBo
+    // through the XCD's L2, instead of the sign tiles of 32 output tiles once each
+    const int64_t xcd = wg & 7, j = wg >> 3, G = (j / (kPsBt * kPsBo)) * 8 + xcd, r = j % (kPsBt * kPsBo);
+    const int64_t ntb = (ntt + kPsBt - 1) / kPsBt;
+    tt = (G % ntb) * kPsBt + r / kPsBo;
+    ot = (G / ntb) * kPsBo + r % kPsBo;
+    live = tt < ntt && ot < nto;
+  } else if (ntt >= 8) {                              // each XCD walks whole token tiles (their digits stay in L2)
     const int64_t xcd = wg & 7, j = wg >> 3, tpx = (ntt + 7) / 8;
     tt = xcd + 8 * (j / nto);
     ot = j % nto;
@@ -1595,6 +1606,8 @@ static bool gemm_pm() {
   return v;
 }
 
+static int ps_map() { const char* e = getenv("IMIE_PS_MAP"); return e ? atoi(e) : 1; }
+
 // the multi-weight unfolded-partial kernel where its bounds hold (IMIE_GEMM_PS=0 disables; tuning and tests)
 static bool gemm_ps() {
   static const bool v = [] { const char* e = getenv("IMIE_GEMM_PS"); return !(e && atoi(e) == 0); }();
@@ -1699,7 +1712,10 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     P.xg_bytes = (uint32_t)xg_bytes;
     P.cnt = cnt;
     const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
-    const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * tiles : ntt128 * tiles));
+    P.map = ps_map();
+    const int64_t nblk = ((ntt128 + kPsBt - 1) / kPsBt) * ((tiles + kPsBo - 1) / kPsBo);
+    const dim3 pgrid((unsigned)(P.map ? (nblk + 7) / 8 * 8 * (kPsBt * kPsBo)
+                                      : (ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * tiles : ntt128 * tiles)));
     // one partial: 16 waves of 32 x 32 (128 VGPRs); two: 8 waves of 32 x 64 (the second partial's registers)
     if (np == 1) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1>), pgrid, dim3(1024), 0, st, P);
     else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2>), pgrid, dim3(512), 0, st, P);
