@@ -1218,7 +1218,8 @@ __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg
 // the wave's 64-token tile (s_lw[slab] from gemm_slab_limbs), exact in int64 with any limb count, added into out
 // (ATOMIC: with 64-bit atomic adds, for callers that stored the narrow blocks' sums to the same outputs).
 template <bool S64, int MT, int NT, bool ATOMIC>
-__device__ inline void gemm_wide_wave(const GemmArgs& a, int64_t t0, int64_t o0, const int* s_lw) {
+__device__ inline void gemm_wide_wave(const GemmArgs& a, int64_t t0, int64_t o0, const int* s_lw, int64_t bbeg = 0,
+                                      int64_t bend = -1) {
   const int lane = threadIdx.x & 63;
   const int m = lane & 15, g = lane >> 4;
   int64_t ta[MT];
@@ -1231,7 +1232,8 @@ __device__ inline void gemm_wide_wave(const GemmArgs& a, int64_t t0, int64_t o0,
     for (int jj = 0; jj < NT; ++jj)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][jj][r] = 0;
-  for (int64_t b = 0; b < a.nb; ++b) {
+  if (bend < 0) bend = a.nb;
+  for (int64_t b = bbeg; b < bend; ++b) {
     const int lwg = s_lw[b >> 2];
     if (lwg <= kNarrowLimbs) continue;
     const int64_t sl = b >> 2;
@@ -1565,6 +1567,246 @@ __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) 
   }
 }
 
+// ------------------------------------------------------------------------------------------------------
+// Batched-decode GEMM (kGemmMinT <= T <= 64 tokens, one token tile). The weights are streamed once and a launch
+// moves only a few MB, so the kernel is built around having the bytes in flight early:
+// * Workgroup = 128 outputs x 16 MT tokens over a K range of at most kBtMaxBlk blocks (the whole K, or a few
+//   ranges added with 64-bit atomics when the output count alone cannot fill the chip); 4 MT waves, wave = 32
+//   outputs (2 MFMA tiles) x one 16-token group, so a SIMD holds MT waves to overlap one another's LDS and MFMA
+//   latencies.
+// * At entry the workgroup copies ALL of its range's weight bits and scales into LDS (buffer_load ... lds, no
+//   registers): the whole matrix is requested in the first microseconds instead of a few blocks at a time. The
+//   digit rows of each block (3 limbs x 16 MT tokens, L2-resident) and its negated totals go through a ring of RA
+//   slots, RA - 1 blocks ahead. The copies are inline asm, so the compiler adds no waits of its own; each block
+//   waits with s_waitcnt vmcnt for the copies issued after it, then a bare s_barrier (no release fence, which would
+//   drain the ring).
+// * Per block the narrow kernel's arithmetic: pos by Horner over the limbs (int32 exact, |pos| <= 2^30), S = 2 pos
+//   - total, q = floor(S * scale / 2^frac) as the high dword of S * (scale << (32 - frac)) (int32 scales below
+//   2^(frac - 1)); q summed in an int32 partial folded into int64 every kf blocks, kf from the weight's largest
+//   |scale| (kf ((2^30 max|scale|) >> frac) + kf < 2^31).
+// * A slab needing more than 3 limbs over the T tokens is skipped here and computed afterwards by gemm_wide_wave
+//   over the same range (int64, any limb count, 64-bit atomics).
+// ------------------------------------------------------------------------------------------------------
+constexpr int kBtMaxBlk = 32;      // blocks per workgroup range (the range's weights sit in LDS)
+struct BtArgs {
+  GemmArgs s[kMaxSegs];
+  int64_t tend[kMaxSegs];          // cumulative output groups of 128 through segment i
+  uint32_t bt_bytes[kMaxSegs], sc_bytes[kMaxSegs];
+  uint32_t xg_bytes, tg_bytes;
+  int cnt, nkr, kf;
+};
+
+template <int MT>
+struct __align__(16) BtASlot {
+  v4i A[kNarrowLimbs * 16 * MT * 8];   // [limb][token][chunk slot], slot = chunk ^ ((token >> 1) & 7)
+  int64_t tot[64];
+};
+
+template <int N>
+__device__ inline void bt_wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// LDS DMA issued as inline asm: the compiler does not track it, so it inserts no waits of its own before the LDS
+// reads (its tracking cannot tell ring slots apart and would drain every copy in flight); every wait on these
+// copies is the kernel's explicit s_waitcnt vmcnt, and the "memory" clobber keeps a block's LDS reads after the
+// wait that covers it
+__device__ inline void bt_dma(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+  soff = __builtin_amdgcn_readfirstlane(soff);       // uniform by construction; the operand must be an SGPR
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(r), "s"(soff), "{m0}"(base)
+               : "memory");
+}
+
+template <int MT, int RA>
+__global__ __launch_bounds__(256 * MT) void q1_gemm_bt_kernel(BtArgs P) {
+  constexpr int NT = 2, NW = 4 * MT, ROWS = 16 * MT, NJA = 6 * MT + 1, QA = (NJA + NW - 1) / NW;
+  static_assert((RA - 2) * QA <= 63, "vmcnt range");
+  __shared__ uint4 sWb[kBtMaxBlk][128];               // [block][tile][row]
+  __shared__ int32_t sWs[kBtMaxBlk][128];
+  __shared__ BtASlot<MT> SA[RA];
+  __shared__ int s_lw[kGemmMaxSlabs];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tw = wave & 3, ig = wave >> 2;            // output tile pair, 16-token group
+  int64_t og = blockIdx.x;
+  const int seg = (og >= P.tend[0] ? 1 : 0) + (P.cnt > 2 && og >= P.tend[1] ? 1 : 0);
+  const GemmArgs& a = seg == 0 ? P.s[0] : (seg == 1 ? P.s[1] : P.s[2]);
+  const uint32_t bt_bytes = seg == 0 ? P.bt_bytes[0] : (seg == 1 ? P.bt_bytes[1] : P.bt_bytes[2]);
+  const uint32_t sc_bytes = seg == 0 ? P.sc_bytes[0] : (seg == 1 ? P.sc_bytes[1] : P.sc_bytes[2]);
+  if (seg) og -= P.tend[seg - 1];
+  const int64_t b0 = (int64_t)blockIdx.y * a.nb / P.nkr, b1 = ((int64_t)blockIdx.y + 1) * a.nb / P.nkr;
+  const int64_t nbr = b1 - b0;                        // <= kBtMaxBlk (host)
+  const int m = lane & 15, g = lane >> 4;
+  const int64_t o0 = og * 128, o0w = o0 + 32 * tw;
+  const __amdgpu_buffer_rsrc_t rA = pm_rsrc(a.xg, P.xg_bytes), rT = pm_rsrc(a.tg, P.tg_bytes),
+                               rB = pm_rsrc(a.bitsT, bt_bytes), rS = pm_rsrc(a.scaleT, sc_bytes);
+  const int64_t ntl = a.ntiles16 >> 4;
+  // the range's blocks in a rotated order (workgroup-dependent start), so workgroups running together read
+  // different blocks' digit rows
+  const int64_t rot = nbr > 1 ? ((int64_t)blockIdx.x * 7) % nbr : 0;
+  auto phys = [&](int64_t k) { const int64_t v = k + rot; return b0 + (v >= nbr ? v - nbr : v); };
+  // slab limb counts over the T tokens (wave 0; T <= 64: one lane per token), loaded before any copy is issued
+  // (the compiler's wait for these loads then drains nothing else)
+  if (wave == 0)
+    for (int64_t sl = b0 >> 2; sl <= (b1 - 1) >> 2; ++sl) {
+      int L = lane < a.T ? a.lt[(int64_t)lane * a.nslabs + sl] : 0;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) { const int w2 = __shfl_xor(L, o, 64); L = w2 > L ? w2 : L; }
+      if (lane == 0) s_lw[sl] = L;
+    }
+  // every weight copy of the range first: job j = (logical block j / 3, part j % 3: bits of tiles 0-3, 4-7, scales)
+  {
+    const int64_t otb = min((o0 >> 4) + (lane >> 4), ntl - 1), otb2 = min((o0 >> 4) + 4 + (lane >> 4), ntl - 1);
+    const int64_t ots = min((o0 >> 4) + (lane >> 2), ntl - 1);
+    const uint32_t vb0 = (uint32_t)((otb * a.nslabs * 64 + (lane & 15)) * 16);
+    const uint32_t vb1 = (uint32_t)((otb2 * a.nslabs * 64 + (lane & 15)) * 16);
+    const uint32_t vs = (uint32_t)((ots * a.nslabs * 64 + 4 * (lane & 3)) * 4);
+    for (int j = wave; j < 3 * nbr; j += NW) {
+      const int kb = j / 3, part = j - 3 * kb;
+      const int64_t b = phys(kb);
+      const uint32_t sb = (uint32_t)(((b >> 2) * 64) + 16 * (b & 3));
+      if (part < 2) bt_dma(rB, &sWb[kb][64 * part], part ? vb1 : vb0, sb * 16u);
+      else if (lane < 32) bt_dma(rS, &sWs[kb][0], vs, sb * 4u);
+    }
+  }
+  // digit-row copy jobs of a block: 0 the totals, 1.. 8 rows of 128 B each; a wave's jobs beyond the last repeat
+  // it (the same bytes to the same place)
+  const uint32_t limb_stride = (uint32_t)a.nbp * (uint32_t)a.Tp * 128u;
+  int ja[QA];
+  uint32_t va[QA];
+#pragma unroll
+  for (int q = 0; q < QA; ++q) {
+    const int j = min(wave + NW * q, NJA - 1);
+    ja[q] = j;
+    if (j == 0) {
+      va[q] = (uint32_t)lane * 16u;
+    } else {
+      const int rr = 8 * (j - 1) + (lane >> 3), l = rr / ROWS, t = rr - l * ROWS;
+      va[q] = (uint32_t)l * limb_stride + (uint32_t)t * 128u + (uint32_t)((lane & 7) ^ ((t >> 1) & 7)) * 16u;
+    }
+  }
+  auto issue_a = [&](int64_t b, BtASlot<MT>& d) {
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      const int j = ja[q];
+      if (j == 0) {
+        if (lane < 8 * MT) bt_dma(rT, &d.tot[0], va[q], (uint32_t)b * (uint32_t)a.Tp * 8u);
+      } else {
+        bt_dma(rA, &d.A[64 * (j - 1)], va[q], (uint32_t)b * (uint32_t)a.Tp * 128u);
+      }
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < RA - 1; ++k)
+    if (k < nbr) issue_a(phys(k), SA[k]);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();                       // s_lw (a bare barrier: the copies stay in flight)
+  int64_t acc[NT][4];
+  int32_t part[NT][4];
+#pragma unroll
+  for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { acc[jj][r] = 0; part[jj][r] = 0; }
+  int fc = 0;
+  // the range's slab limb counts in one register: 4 bits per slab from the first (the range spans <= 9 slabs)
+  const int64_t sl0 = b0 >> 2;
+  uint64_t lwm = 0;
+  bool wide = false;
+  for (int64_t sl = sl0; sl <= (b1 - 1) >> 2; ++sl) {
+    const int v = s_lw[sl];
+    wide = wide || v > kNarrowLimbs;
+    lwm |= (uint64_t)(v > kNarrowLimbs ? 15 : v) << (4 * (sl - sl0));
+  }
+  const int sw = (m >> 1) & 7;
+  // one block with L limbs: every LDS operand read issued together, then the Horner chains of the two tiles
+  auto block = [&](auto LC, int64_t k, const BtASlot<MT>& c) {
+    constexpr int L = decltype(LC)::value;
+    uint4 w[NT];
+    int32_t sc[NT];
+    v4i av[L][2];
+    int64_t tv[4];
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      w[jj] = sWb[k][(2 * tw + jj) * 16 + m];
+      sc[jj] = sWs[k][(2 * tw + jj) * 16 + m];
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) av[l][h] = c.A[(l * ROWS + 16 * ig + m) * 8 + ((4 * h + g) ^ sw)];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tv[r] = c.tot[16 * ig + 4 * g + r];
+    v4i bx[NT][2];
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      bx[jj][0] = expand_bits(w[jj], g);
+      bx[jj][1] = expand_bits(w[jj], 4 + g);
+    }
+    v4i D[NT];
+#pragma unroll
+    for (int l = L - 1; l >= 0; --l)
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj) {
+        v4i x = v4i{0, 0, 0, 0};
+        if (l < L - 1)
+          x = v4i{(int)((uint32_t)D[jj][0] << 8), (int)((uint32_t)D[jj][1] << 8), (int)((uint32_t)D[jj][2] << 8),
+                  (int)((uint32_t)D[jj][3] << 8)};
+        x = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[l][0], bx[jj][0], x, 0, 0, 0);
+        D[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[l][1], bx[jj][1], x, 0, 0, 0);
+      }
+#pragma unroll
+    for (int jj = 0; jj < NT; ++jj) {
+      const int32_t scp = (int32_t)((uint32_t)sc[jj] << (32 - a.frac));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t S = (int32_t)(((uint32_t)D[jj][r] << 1) - (uint32_t)tv[r]);
+        part[jj][r] = (int32_t)((uint32_t)part[jj][r] + (uint32_t)__mulhi(S, scp));
+      }
+    }
+  };
+  for (int64_t k = 0; k < nbr; ++k) {
+    if (k + RA - 2 < nbr) bt_wait_vm<(RA - 2) * QA>();
+    else bt_wait_vm<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (k + RA - 1 < nbr) issue_a(phys(k + RA - 1), SA[(k + RA - 1) % RA]);
+    const int lw = (int)((lwm >> (4 * ((phys(k) >> 2) - sl0))) & 15);
+    if (lw > kNarrowLimbs || lw == 0) continue;   // wide slab (done afterwards) or all-zero digits
+    const BtASlot<MT>& c = SA[k % RA];
+    if (lw == 3) block(std::integral_constant<int, 3>{}, k, c);
+    else if (lw == 2) block(std::integral_constant<int, 2>{}, k, c);
+    else block(std::integral_constant<int, 1>{}, k, c);
+    if (++fc == P.kf) {
+      fc = 0;
+#pragma unroll
+      for (int jj = 0; jj < NT; ++jj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[jj][r] = (int64_t)((uint64_t)acc[jj][r] + (uint64_t)(int64_t)part[jj][r]);
+          part[jj][r] = 0;
+        }
+    }
+  }
+  const bool atomic = P.nkr > 1;
+#pragma unroll
+  for (int jj = 0; jj < NT; ++jj) {
+    const int64_t o = o0w + 16 * jj + m;
+    if (o >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = 16 * ig + 4 * g + r;
+      if (t >= a.T) continue;
+      const int64_t v = (int64_t)((uint64_t)acc[jj][r] + (uint64_t)(int64_t)part[jj][r]);
+      int64_t* dst = a.out + t * a.N + o;
+      if (atomic) atomicAdd((unsigned long long*)dst, (unsigned long long)v);
+      else *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)v) : v;
+    }
+  }
+  if (wide && o0w < a.N) {                            // uniform over the workgroup
+    __threadfence();
+    gemm_wide_wave<false, 1, NT, true>(a, 16 * ig, o0w, s_lw, b0, b1);
+  }
+}
+
 // Executed int8 MFMA ops of one GEMM launch pair (profiling only): per (token tile, slab) the limb count the
 // kernels use (max over the tile's tokens) x the slab's blocks x the output tiles x 64 MFMAs of 2*16*16*64 ops.
 __global__ void gemm_opcount_kernel(const int* __restrict__ lt, int64_t T, int64_t nslabs, int64_t nb, int64_t nto,
@@ -1586,6 +1828,18 @@ static int gemm_nbuf() {
     const int n = e ? atoi(e) : 0;
     return n == 1 || n == 2 ? n : 1;
   }();
+  return v;
+}
+
+// batched-decode GEMM for T <= 64 (IMIE_GEMM_BT=0 disables; tuning and tests)
+static bool gemm_bt() {
+  static const bool v = [] { const char* e = getenv("IMIE_GEMM_BT"); return !(e && atoi(e) == 0); }();
+  return v;
+}
+
+// batched-decode GEMM: workgroups below which the K range is split (IMIE_BT_MINWG; tuning)
+static int64_t bt_min_wgs() {
+  static const int64_t v = [] { const char* e = getenv("IMIE_BT_MINWG"); return (int64_t)(e ? atoi(e) : 128); }();
   return v;
 }
 
@@ -1694,7 +1948,58 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     all_ps = all_ps && nps[i] > 0 && xg_bytes < (1ull << 32) && sg_bytes < (1ull << 32) && sc_bytes < (1ull << 32);
   }
   for (int i = 0; i < cnt && all_ps; ++i) all_ps = q1_ensure_signs(const_cast<Q1Weight&>(*ws[i]), st) == 0;
-  if (all_ps) {
+  // batched decode (one token tile of <= 64): q1_gemm_bt_kernel where its int32 partial folds can be exact
+  bool bt = false;
+  if (!all_ps && T <= 64 && gemm_bt()) {
+    int64_t ncol = 0, worst = 0;
+    bt = true;
+    for (int i = 0; i < cnt; ++i) {
+      bt = bt && gas[i].kfold > 0;
+      ncol += (ws[i]->N + 127) / 128;
+      const int64_t q = (((int64_t)ws[i]->maxsc << 30) >> gas[i].frac) + 1;
+      worst = q > worst ? q : worst;
+    }
+    const int64_t kf = worst > 0 ? ((((int64_t)1 << 31) - 2) / worst) : 0;
+    const uint64_t tg_bytes = (uint64_t)nbp * Tp * 8;
+    for (int i = 0; i < cnt && bt; ++i) {
+      const uint64_t bb = (uint64_t)ws[i]->ntiles * nslabs * 64 * 16, sb = (uint64_t)ws[i]->ntiles * nslabs * 64 * 4;
+      bt = bb < (1ull << 32) && sb < (1ull << 32);
+    }
+    bt = bt && kf >= 1 && xg_bytes < (1ull << 32) && tg_bytes < (1ull << 32);
+    if (bt) {
+      BtArgs P;
+      int64_t cols = 0;
+      for (int i = 0; i < cnt; ++i) {
+        P.s[i] = gas[i];
+        cols += (ws[i]->N + 127) / 128;
+        P.tend[i] = cols;
+        P.bt_bytes[i] = (uint32_t)((uint64_t)ws[i]->ntiles * nslabs * 64 * 16);
+        P.sc_bytes[i] = (uint32_t)((uint64_t)ws[i]->ntiles * nslabs * 64 * 4);
+      }
+      for (int i = cnt; i < kMaxSegs; ++i) { P.s[i] = gas[0]; P.tend[i] = cols; P.bt_bytes[i] = P.sc_bytes[i] = 0; }
+      P.cnt = cnt;
+      P.kf = (int)(kf > (1 << 20) ? (1 << 20) : kf);
+      P.xg_bytes = (uint32_t)xg_bytes;
+      P.tg_bytes = (uint32_t)tg_bytes;
+      // K ranges (64-bit atomics across them) only when the output groups alone leave most of the chip idle
+      int nkr = 1;
+      while (nkr < 4 && cols * nkr < bt_min_wgs() && w0.nb / (2 * nkr) >= 8) nkr *= 2;
+      while ((w0.nb + nkr - 1) / nkr > kBtMaxBlk) ++nkr;   // the range's weights must fit the workgroup's LDS
+      P.nkr = nkr;
+      if (nkr > 1 && !accumulate && prepped != 3)
+        for (int i = 0; i < cnt; ++i) {
+          const int64_t n = T * ws[i]->N;
+          hipLaunchKernelGGL(q1_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, outs[i], n);
+        }
+      const dim3 grid((unsigned)cols, (unsigned)nkr);
+      if (T <= 16) hipLaunchKernelGGL((q1_gemm_bt_kernel<1, 6>), grid, dim3(256), 0, st, P);
+      else if (T <= 32) hipLaunchKernelGGL((q1_gemm_bt_kernel<2, 6>), grid, dim3(512), 0, st, P);
+      else hipLaunchKernelGGL((q1_gemm_bt_kernel<4, 3>), grid, dim3(1024), 0, st, P);
+      IMIE_HIP(hipGetLastError());
+    }
+  }
+  if (bt) {
+  } else if (all_ps) {
     // one launch for every weight: their output tiles side by side
     PsArgs P;
     int np = 1;
@@ -2102,6 +2407,7 @@ int imie_q1_launch_pro(const int64_t* handles, int cnt, const Q1Pro& pro, int ki
 int imie_q1_gemm_splits(int64_t handle, int64_t T) {
   const Q1Weight* w = q1_get(handle);
   if (!w || T < kGemmMinT || T >= kPmMinT) return 0;
+  if (T <= 64 && gemm_bt()) return 1;                // the batched-decode kernel adds into cleared outputs
   const int64_t ntt = (T + 63) / 64, nto = (w->N + 127) / 128;
   const int64_t tiles = ntt >= 8 ? 8 * ((ntt + 7) / 8) * nto : ntt * nto;
   return tiles < 256 && w->nb >= 8 ? 1 : 0;

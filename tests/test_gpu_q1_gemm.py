@@ -190,3 +190,36 @@ def test_gemm_sign_copy_partial_ranges(gpu, nb, s):
     x[16:24] = -cap3
     got = gpu.q1_apply_gpu(x, bits, scale, 16)
     assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, 16))
+
+
+# ---- 8 <= T <= 64: the batched-decode kernel (one token tile, K ranges of 1 / 2 / 4 blocks) ----------------------
+@pytest.mark.parametrize("N,nb,T", [(300, 12, 8), (300, 12, 16), (257, 5, 17), (1000, 8, 32), (64, 13, 33),
+                                    (513, 4, 48), (4096, 32, 64), (40, 96, 31)])
+def test_gemm_batched_decode_shapes(gpu, N, nb, T):
+    seed = N * 13 + nb * 7 + T
+    bits = prng.uniform_bytes(seed, 1, (N, nb, 16))
+    scale = prng.uniform_int(seed, 2, (N, nb), -(1 << 13), 1 << 13)
+    x = prng.uniform_int(seed, 3, (T, nb * 128), -(1 << 22), 1 << 22)
+    x[T // 2, :] = 0                                  # a token whose slabs need no limbs
+    got = gpu.q1_apply_gpu(x, bits, scale, 16)
+    assert got is not None and np.array_equal(got, c_oracle.q1_linear(x, bits, scale, 16))
+
+
+@pytest.mark.parametrize("frac,T", [(16, 32), (31, 20), (24, 64)])
+def test_gemm_batched_decode_epilogue_extremes(gpu, frac, T):
+    """Scales at +-(2^(frac-1) - 1) and activations at the 3-limb cap: |q| ~ 2^29 per block, so the host takes
+    ranges of at most 2 blocks for the int32 partial; one slab needing 4 limbs goes through the wide path."""
+    cap3 = 127 * (1 + 256 + 65536)
+    N, nb = 96, 16
+    rng = np.random.default_rng(frac + T)
+    bits = rng.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+    bits[:8] = 0xFF
+    bits[8:16] = 0
+    smax = (1 << (frac - 1)) - 1
+    scale = rng.choice(np.array([smax, -smax, smax - 1, 1], dtype=np.int64), size=(N, nb))
+    x = rng.choice(np.array([cap3, -cap3, cap3 - 1, 0], dtype=np.int64), size=(T, nb * 128))
+    x[:4] = cap3
+    x[4:8] = -cap3
+    x[T - 1, 5 * 128 + 3] = cap3 + 1                  # slab 1 needs 4 limbs for every token of the tile
+    got = gpu.q1_apply_gpu(x, bits, scale, frac)
+    assert got is not None and np.array_equal(got, q1_linear(x, bits, scale, frac))
