@@ -300,7 +300,8 @@ __global__ void attn_init_kernel(AttnDesc d) {
 // the XCDs' L2 slices.
 //   D1 scores : wave = 4 keys x 16 lanes (8 dims per lane, 32 B vector loads), rep dots per key, 16-lane shuffle
 //               reduction; scores[(b,h)][j]; chunk max per head -> cmax[chunk][row], chunk max|K| -> ckm
-//   D2 exp    : row max = max over cmax; e_j = 2^-(...) stored in place; chunk Z -> cz[chunk][row]
+//   D2 exp    : row max = max over cmax; e_j = 2^-(...); chunk Z -> cz[chunk][row]; e_j stored in place for the
+//               int64 cache's PV (the kv8 PV recomputes e_j from the score and the row max: no write-back)
 //   D3 PV     : Z = sum over cz; per 256-key tile p_j = (e_j << f) / Z through a 2^64 / Z reciprocal with a
 //               correction loop (exact for every e_j << f < 2^64), staged in LDS; a wave covers 2 keys per step
 //               (32 lanes x 4 dims); chunk PV sums -> part[chunk][row][dim], chunk max|p| / max|V| -> cmp / cvm
@@ -448,7 +449,9 @@ __global__ __launch_bounds__(256) void dec_scores_kernel(AttnDesc d) {
   }
 }
 
-template <int REP>
+// STORE = false (kv8 path): only the chunk Z sums are written; the PV kernel recomputes each e_j from its score
+// and the row maximum, so the scores are not rewritten in place (half of this kernel's traffic)
+template <int REP, bool STORE = true>
 __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
   __shared__ int64_t s_rmax[REP];
   __shared__ uint64_t s_z[4][REP];
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
       int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)(one ? sv[r] : d.scores[row * d.Lmax + j]));
       if (dd > d.dclip) dd = d.dclip;
       const uint64_t e = (uint64_t)exp_clipped(dd, d.frac, d.log2e, fx32);
-      d.scores[row * d.Lmax + j] = (int64_t)e;
+      if (STORE) d.scores[row * d.Lmax + j] = (int64_t)e;
       z += e;
     }
 #pragma unroll
@@ -947,6 +950,7 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   constexpr int RBH = (REP + 3) / 4;
   __shared__ __align__(16) int8_t sPd[RBH][16][64];
   __shared__ uint64_t s_z[REP], s_mp[4][REP];
+  __shared__ int64_t s_m[REP];
   __shared__ double s_rzd[REP];
   const int64_t bkv = blockIdx.x, b = imie_udiv32(bkv, d.Hkv), kv = imie_umod32(bkv, d.Hkv);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
@@ -992,12 +996,17 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   int64_t scA[RW], scB[RW];
   load_step(j0, d.Lmax, bvA, scA);
   uint64_t cz0[RW];
+  int64_t cm0[RW];
 #pragma unroll
   for (int k = 0; k < RW; ++k) {
     const int r = wave + 4 * k;
-    const uint64_t z0 = (r < REP && lane < d.nch) ? d.cz[(int64_t)lane * rows + b * d.H + kv * REP + r] : 0;
-    const uint64_t z1 = (r < REP && lane + 64 < d.nch) ? d.cz[(int64_t)(lane + 64) * rows + b * d.H + kv * REP + r] : 0;
+    const int64_t ri = b * d.H + kv * REP + r;
+    const uint64_t z0 = (r < REP && lane < d.nch) ? d.cz[(int64_t)lane * rows + ri] : 0;
+    const uint64_t z1 = (r < REP && lane + 64 < d.nch) ? d.cz[(int64_t)(lane + 64) * rows + ri] : 0;
     cz0[k] = z0 + z1;
+    const int64_t m0 = (r < REP && lane < d.nch) ? d.cmax[(int64_t)lane * rows + ri] : INT64_MIN;
+    const int64_t m1 = (r < REP && lane + 64 < d.nch) ? d.cmax[(int64_t)(lane + 64) * rows + ri] : INT64_MIN;
+    cm0[k] = m0 > m1 ? m0 : m1;
   }
   const int64_t L = dec_len(d, b);
   if (j0 >= L) {
@@ -1012,11 +1021,21 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
     const int r = wave + 4 * k;
     if (r >= REP) break;
     uint64_t z = cz0[k];
-    for (int64_t c = lane + 128; c < d.nch; c += 64) z += d.cz[c * rows + b * d.H + kv * REP + r];
+    int64_t mx = cm0[k];
+    for (int64_t c = lane + 128; c < d.nch; c += 64) {
+      z += d.cz[c * rows + b * d.H + kv * REP + r];
+      const int64_t v = d.cmax[c * rows + b * d.H + kv * REP + r];
+      mx = v > mx ? v : mx;
+    }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
-    if (lane == 0) { s_z[r] = z; s_rzd[r] = z != 0 ? 1.0 / (double)z : 0.0; }
+    for (int o = 32; o >= 1; o >>= 1) {
+      z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
+      const int64_t w2 = __shfl_xor(mx, o, 64);
+      mx = w2 > mx ? w2 : mx;
+    }
+    if (lane == 0) { s_z[r] = z; s_rzd[r] = z != 0 ? 1.0 / (double)z : 0.0; s_m[r] = mx; }
   }
+  const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
   for (int i = tid; i < RBH * 16 * 64; i += 256) (&sPd[0][0][0])[i] = 0;
   __syncthreads();
   const int Lp = imie_limbs_needed((uint64_t)1 << d.frac);
@@ -1056,7 +1075,12 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
         if (r >= REP) break;
         const uint64_t Z = s_z[r];
         int64_t p = 0;
-        if (kk < tn && Z != 0) p = prob_div(scv[k], d.frac, Z, s_rzd[r]);
+        if (kk < tn && Z != 0) {
+          // e_j of dec_exp_kernel from the score and the row maximum
+          int64_t dd = (int64_t)((uint64_t)s_m[r] - (uint64_t)scv[k]);
+          if (dd > d.dclip) dd = d.dclip;
+          p = prob_div(exp_clipped(dd, d.frac, d.log2e, fx32), d.frac, Z, s_rzd[r]);
+        }
         mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
         int64_t x = p;
         for (int lp = 0; lp < 4; ++lp) {
@@ -2134,10 +2158,17 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
       IMIE_DEC_R(dec_scores_kernel, int64_t);
     }
     IMIE_HIP(hipGetLastError());
-    if (rep == 1) hipLaunchKernelGGL(dec_exp_kernel<1>, gd, dim3(256), 0, st, d);
-    else if (rep == 2) hipLaunchKernelGGL(dec_exp_kernel<2>, gd, dim3(256), 0, st, d);
-    else if (rep == 4) hipLaunchKernelGGL(dec_exp_kernel<4>, gd, dim3(256), 0, st, d);
-    else hipLaunchKernelGGL(dec_exp_kernel<8>, gd, dim3(256), 0, st, d);
+    if (d.kv32) {                                     // PV recomputes e from the scores
+      if (rep == 1) hipLaunchKernelGGL((dec_exp_kernel<1, false>), gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL((dec_exp_kernel<2, false>), gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL((dec_exp_kernel<4, false>), gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL((dec_exp_kernel<8, false>), gd, dim3(256), 0, st, d);
+    } else {
+      if (rep == 1) hipLaunchKernelGGL(dec_exp_kernel<1>, gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL(dec_exp_kernel<2>, gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL(dec_exp_kernel<4>, gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL(dec_exp_kernel<8>, gd, dim3(256), 0, st, d);
+    }
     IMIE_HIP(hipGetLastError());
     if (d.kv32) {
       if (rep == 1) hipLaunchKernelGGL(dec_pv8_kernel<1>, gd, dim3(256), 0, st, d);

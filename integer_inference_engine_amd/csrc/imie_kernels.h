@@ -106,9 +106,9 @@ struct QkHeadArgs {
   int8_t* qd;
   uint64_t* qmax;
   int* qlimbs;
-  // many rows (M > 1): per-workgroup RoPE envelope maxima gpart[(row * (H + Hkv) + head) * 2 + {0, 1}] instead of
-  // same-address atomics (reduced into guard by imie_qk_head_finish_launch), and the kv8 V planes appended by
-  // that launch's coalesced kernel instead of per-element byte scatters
+  // several rows: per-workgroup RoPE envelope maxima gpart[(row * (H + Hkv) + head) * 2 + {0, 1}] instead of
+  // same-address atomics from every workgroup (reduced into guard by imie_qk_head_finish_launch); with M > 1 the
+  // kv8 V planes are also appended by that launch's coalesced kernel instead of per-element byte scatters
   uint64_t* gpart;
 };
 // kv8 = 1: the digit-plane cache of imie_kvfmt.h; 0: int64 rows

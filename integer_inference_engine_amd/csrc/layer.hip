@@ -255,7 +255,7 @@ int net_ensure(Net& n, int64_t M, int64_t lmax) {
       n.pos.ensure((size_t)rows * 8) || n.starts.ensure((size_t)n.B * 8) || n.guard.ensure((size_t)n.nl * 32) ||
       n.status.ensure(64) || n.attn.ensure(imie_attn_scratch_bytes(n.B, n.H, n.Hkv, M, n.hd, lmax)) ||
       n.kvrow.ensure((size_t)(2 * rows * n.Hkv) * 8) ||
-      (M > 1 && n.gpart.ensure((size_t)(rows * (n.H + n.Hkv) * 2) * 8)))
+      (rows > 1 && n.gpart.ensure((size_t)(rows * (n.H + n.Hkv) * 2) * 8)))
     return IMIE_EARG;
   return IMIE_OK;
 }
@@ -388,7 +388,7 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
         a.run_k = run_k(n, l); a.run_v = run_v(n, l);
       }
       if (d.qd) { a.qd = (int8_t*)d.qd; a.qlimbs = (int*)d.qlimbs; a.qmax = d.maxq; }
-      if (M > 1) a.gpart = (uint64_t*)n.gpart.p;
+      if (rows > 1) a.gpart = (uint64_t*)n.gpart.p;   // several rows: no same-address atomics on the guard
       CK(imie_qk_head_launch(a, n.kv32, st));
       CK(imie_qk_head_finish_launch(a, n.kv32, st));
       if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));

@@ -382,8 +382,19 @@ int imie_rmsnorm_gemm_prep_launch(const int64_t* x, int64_t rows, int64_t cols, 
   if (rows <= 0) return IMIE_OK;
   if (cols != gp.nb * 128 || cols > kPrepCols || rows < imie_q1::kGemmMinT) return IMIE_EARG;
   const imie_q1::Q1PrepOut po = {};
-  hipLaunchKernelGGL((rmsnorm_kernel<2, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac, eps,
-                     gain, out, status, po, zero, gp);
+  static const int nt_env = [] { const char* e = getenv("IMIE_NORM_GEMM_NT"); return e ? atoi(e) : 0; }();  // tuning
+  const int nt = nt_env ? nt_env : (rows <= 128 ? 1024 : 256);
+  // few rows (batched decode): each row's latency chain is the launch, so more threads per row; many rows
+  // (prefill): 256 threads x 16 columns keep more rows in flight per CU
+  if (nt == 1024)
+    hipLaunchKernelGGL((rmsnorm_kernel<2, 1024, 4>), dim3((unsigned)rows), dim3(1024), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, zero, gp);
+  else if (nt == 512)
+    hipLaunchKernelGGL((rmsnorm_kernel<2, 512, 8>), dim3((unsigned)rows), dim3(512), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, zero, gp);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<2, 256, 16>), dim3((unsigned)rows), dim3(256), 0, st, x, cols, (int)frac, eps,
+                       gain, out, status, po, zero, gp);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }

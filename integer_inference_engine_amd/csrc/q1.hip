@@ -1965,7 +1965,8 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
       const uint64_t bb = (uint64_t)ws[i]->ntiles * nslabs * 64 * 16, sb = (uint64_t)ws[i]->ntiles * nslabs * 64 * 4;
       bt = bb < (1ull << 32) && sb < (1ull << 32);
     }
-    bt = bt && kf >= 1 && xg_bytes < (1ull << 32) && tg_bytes < (1ull << 32);
+    // very wide outputs (an LM head) run several rounds of these one-per-CU workgroups: the narrow kernel instead
+    bt = bt && kf >= 1 && xg_bytes < (1ull << 32) && tg_bytes < (1ull << 32) && ncol <= 512;
     if (bt) {
       BtArgs P;
       int64_t cols = 0;

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
       blk[imie_kv8::k_off(slot, db, j, a.hd)] = (int8_t)(wk0 >> (8 * db));
       blk[imie_kv8::k_off(slot, db, j + half, a.hd)] = (int8_t)(wk1 >> (8 * db));
     }
-    if (a.gpart) return;                              // V planes: kv8_v_append_kernel (coalesced over slots)
+    if (a.M > 1) return;                              // V planes: kv8_v_append_kernel (coalesced over slots)
     int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
     const uint32_t wv0 = imie_kv8::encode(imie_kv8::fits(v0) ? v0 : 0);
     const uint32_t wv1 = imie_kv8::encode(imie_kv8::fits(v1) ? v1 : 0);
@@ -226,7 +226,7 @@ int imie_qk_head_finish_launch(const QkHeadArgs& a, int kv8, hipStream_t st) {
   const unsigned g = (unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64);
   hipLaunchKernelGGL(guard_reduce_kernel, dim3(g), dim3(256), 0, st, a.gpart, n, a.H, heads, a.guard);
   IMIE_HIP(hipGetLastError());
-  if (kv8) {
+  if (kv8 && a.M > 1) {
     if (a.hd > 128) return IMIE_EARG;
     const dim3 grid((unsigned)((a.M + 63) / 64), (unsigned)(a.rows / a.M * a.Hkv));
     hipLaunchKernelGGL(kv8_v_append_kernel, grid, dim3(256), 0, st, a);
