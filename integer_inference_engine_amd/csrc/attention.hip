@@ -295,7 +295,7 @@ __global__ void attn_init_kernel(AttnDesc d) {
 // ---------------------------------------------------------------------------------------------------------
 // Decode fast path (M == 1): one query per (b, head); the rep = H / Hkv heads of a KV group share every K/V read.
 // The keys of each (b, kv) are split into nch chunks of `chunk` keys (a multiple of 64, sized so the grid has
-// ~2048 workgroups); grid = (B * Hkv, nch). Every cross-chunk quantity (row max, Z, max|K|, max|V|, max|p|, the
+// ~4096 workgroups); grid = (B * Hkv, nch). Every cross-chunk quantity (row max, Z, max|K|, max|V|, max|p|, the
 // PV sums) is written per chunk and reduced by its consumer: no same-address atomics, which serialize across
 // the XCDs' L2 slices.
 //   D1 scores : wave = 4 keys x 16 lanes (8 dims per lane, 32 B vector loads), rep dots per key, 16-lane shuffle
@@ -2051,14 +2051,14 @@ bool pv_wide() {
   return v;
 }
 
-// decode chunking: ~8192 workgroups over the (b, kv) groups, chunks of >= 64 keys (multiple of 64). Many small
-// chunks balance ragged batches (config 5, contexts 1K..32K: 674 tok/s at 8192 against 655 at 2048 and 654 at
-// 16384); a single sequence of 4K keys is at the 64-key minimum either way.
+// decode chunking: ~4096 workgroups over the (b, kv) groups, chunks of >= 64 keys (multiple of 64). Config 5
+// (32 sequences, contexts 1K..32K) measured 41.2 ms a step at 4096, 42.2-42.5 at 2048 / 3072 / 8192, 43.2 at 16384
+// and 52.3 at 32768; a single sequence of 4K keys is at the 64-key minimum either way.
 void dec_geometry(int64_t B, int64_t Hkv, int64_t Lmax, int64_t* chunk, int64_t* nch) {
   static const int64_t target = [] {               // workgroups to aim for (IMIE_DEC_WGS overrides, tuning)
     const char* e = getenv("IMIE_DEC_WGS");
     const long v = e ? atol(e) : 0;
-    return v > 0 ? (int64_t)v : (int64_t)8192;
+    return v > 0 ? (int64_t)v : (int64_t)4096;        // config 5 (32 ragged rows): 41.2 ms a step against 42.4 at 8192
   }();
   const int64_t groups = B * Hkv;
   int64_t want = target / (groups > 0 ? groups : 1);
