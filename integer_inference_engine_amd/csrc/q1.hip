@@ -318,21 +318,31 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
         // one limb (e.g. int8 activations): rows = (block, bit position mod 4) with mask-only B operands
         // (bytes 0 / 2^s, 0x80 reading as -128); 128 * pos = sum d0[q] << (7 - q) + sum d1[q] << (3 - q)
         const int as = n & 3;
-        uint4 a0, a1;
-        if (Lcap >= 4) {
-          const uint4* src = aact ? stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8 + as : zslot;
-          a0 = src[0];
-          a1 = src[aact ? 4 : 0];
-        } else {
+        uint4 a0 = uint4{0, 0, 0, 0}, a1 = uint4{0, 0, 0, 0};
+        if (Lcap < 4) {
           const uint4* src = xq + ((int64_t)t * kMaxLimbs * nbp + sl * kSlabBlocks + g) * 8 + as;
           a0 = aact ? src[0] : uint4{0, 0, 0, 0};
           a1 = aact ? src[4] : uint4{0, 0, 0, 0};
         }
         v4i areg[8];
+        if (Lcap >= 4) {
+          // from LDS: each register reads either the lane's digits or the zero slot (a per-lane address select
+          // instead of four data selects per register)
+          const uint4* src = aact ? stage + ((t * spk + (sl - s0)) * Lcap) * 32 + g * 8 + as : zslot;
 #pragma unroll
-        for (int sh = 0; sh < 4; ++sh) {
-          areg[sh] = as == sh ? v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w} : v4i{0, 0, 0, 0};
-          areg[sh + 4] = as == sh ? v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w} : v4i{0, 0, 0, 0};
+          for (int sh = 0; sh < 4; ++sh) {
+            const uint4* p0 = as == sh ? src : zslot;
+            const uint4* p1 = as == sh ? src + (aact ? 4 : 0) : zslot;
+            const uint4 u0 = *p0, u1 = *p1;
+            areg[sh] = v4i{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w};
+            areg[sh + 4] = v4i{(int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+          }
+        } else {
+#pragma unroll
+          for (int sh = 0; sh < 4; ++sh) {
+            areg[sh] = as == sh ? v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w} : v4i{0, 0, 0, 0};
+            areg[sh + 4] = as == sh ? v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w} : v4i{0, 0, 0, 0};
+          }
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -340,8 +350,7 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
           v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
 #pragma unroll
           for (int sh = 0; sh < 8; ++sh) {
-            uint32_t m = 0x01010101u << sh;
-            asm volatile("" : "+s"(m));   // keep each B expansion next to its MFMA (no hoisting across tiles)
+            const uint32_t m = 0x01010101u << sh;
             const v4i b = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
             if (sh < 4) d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[sh], b, d0, 0, 0, 0);
             else d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[sh], b, d1, 0, 0, 0);
