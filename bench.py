@@ -542,6 +542,11 @@ def main() -> int:
                              f"{c['match'] and c1['match'] and (cp is None or cp['match'])}"}
 
     dec = None
+    # the device's practical read ceiling (streaming nontemporal loads over a buffer of the same size), to set the
+    # matvec's fraction of the published peak beside what the memory system actually sustains
+    rpk = ctypes.c_double()
+    read_peak = rpk.value / 1e9 if so.imie_hbm_read_peak(step_bytes, ctypes.byref(rpk)) == 0 else None
+
     if args.decode_tokens > 0 or args.c5_tokens > 0:
         del bits, scale
         so.bonsai_q1_free_weights()
@@ -575,6 +580,8 @@ def main() -> int:
                                        "WRITE_SIZE of this launch, copy-calibrated" if traffic else None,
                      "frac_step": round(value / HBM_PEAK_GBS, 4),
                      "kernel": "q1_gemv_mfma_kernel", "kernel_avg_us": round(k_avg_s * 1e6, 3),
+                     "measured_read_peak": round(read_peak, 1) if read_peak else None,
+                     "frac_of_measured_read_peak": round(achieved / read_peak, 4) if read_peak else None,
                      "prep_avg_us": round(pms.value / max(1, pcnt.value) * 1e3, 3)},
         "cpu_baseline": cpu,
         "decode_8b_b1": {k: v for k, v in dec.items() if k != "_c5"} if dec and args.decode_tokens > 0 else None,

@@ -43,6 +43,10 @@ int imie_probe_mfma(const int8_t *a, const int8_t *b, int32_t *d);
 /* Sustained int8 MFMA throughput of the device in ops/s (8 independent 16x16x64 chains per wave, 4 waves per
  * SIMD, HIP events). No reference counterpart (measurement: the measured peak the prefill GEMM is quoted against). */
 int imie_mfma_peak(double *ops_per_s);
+/* Sustained HBM read bandwidth in bytes/s over a `bytes` (>= 16 MiB) device buffer: nontemporal 16-byte loads from
+ * 16 workgroups per CU, best of three timed launches. No reference counterpart (measurement: the practical read
+ * ceiling the Q1 matvec is quoted against beside the published 8 TB/s). */
+int imie_hbm_read_peak(int64_t bytes, double *bytes_per_s);
 
 /* ---- packed Q1_0 linear: out[t,o] = sum_b ((sum_i sign*x) * scale[o,b]) >> frac, mod 2^64 ----------- */
 /* bonsai_q1_gpu.cu:2200-2241 `bonsai_q1_linear_gpu` (bound at gpu_native.py:44-52, called :212-217). */

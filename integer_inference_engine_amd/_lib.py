@@ -27,6 +27,7 @@ SIGNATURES = {
     "imie_synchronize": (c_int, []),
     "imie_probe_mfma": (c_int, [c_void_p, c_void_p, c_void_p]),
     "imie_mfma_peak": (c_int, [c_void_p]),
+    "imie_hbm_read_peak": (c_int, [c_int64, c_void_p]),
     "imie_sample_token": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "imie_sample_dev": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p]),

@@ -180,6 +180,54 @@ extern "C" int imie_mfma_peak(double* ops_per_s) {
   return IMIE_OK;
 }
 
+// Sustained HBM read bandwidth of this device: a streaming kernel over `bytes` of device memory (16 CU-filling
+// workgroups per CU, four independent 16-byte nontemporal loads per thread per iteration, XOR-reduced), timed with
+// HIP events, best of three launches after a warm-up. The bench quotes the Q1 matvec against it as well as against
+// the published 8 TB/s.
+__global__ __launch_bounds__(256) void imie_read_peak_kernel(const v4i* __restrict__ p, size_t n, int32_t* sink) {
+  size_t i = (size_t)blockIdx.x * 1024 + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * 1024;
+  v4i acc = {0, 0, 0, 0};
+  for (; i + 768 < n; i += stride) {
+    v4i v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(p + i + 256 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u];
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x7F3A5C11) sink[threadIdx.x] = 1;   // keeps the loads live
+}
+
+extern "C" int imie_hbm_read_peak(int64_t bytes, double* bytes_per_s) {
+  std::lock_guard<std::recursive_mutex> g(imie_lock());
+  if (!bytes_per_s || bytes < (1 << 24) || imie_device_ready() != 0) return IMIE_EARG;
+  int dev = 0, cus = 0;
+  IMIE_HIP(hipGetDevice(&dev));
+  IMIE_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const size_t n = (size_t)bytes / 16;
+  void *buf = nullptr, *sink = nullptr;
+  IMIE_HIP(hipMalloc(&buf, n * 16));
+  if (hipMalloc(&sink, 1024) != hipSuccess) { imie_free(buf); return IMIE_EARG; }
+  IMIE_HIP(hipMemset(buf, 0x5A, n * 16));
+  hipEvent_t e0, e1;
+  IMIE_HIP(hipEventCreate(&e0));
+  IMIE_HIP(hipEventCreate(&e1));
+  float best = 0.f;
+  for (int rep = 0; rep < 4; ++rep) {                 // the first launch warms up clocks and code
+    float ms = 0.f;
+    IMIE_HIP(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL(imie_read_peak_kernel, dim3((unsigned)(cus * 16)), dim3(256), 0, 0, (const v4i*)buf, n,
+                       (int32_t*)sink);
+    IMIE_HIP(hipEventRecord(e1, 0));
+    IMIE_HIP(hipEventSynchronize(e1));
+    IMIE_HIP(hipEventElapsedTime(&ms, e0, e1));
+    if (rep > 0 && (best == 0.f || ms < best)) best = ms;
+  }
+  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); imie_free(buf); imie_free(sink);
+  *bytes_per_s = (double)(n * 16) / (best * 1e-3);
+  return IMIE_OK;
+}
+
 // ---- per-kernel event profiler ---------------------------------------------------------------------------
 namespace {
 struct ProfSlot {

@@ -47,6 +47,17 @@ def test_mfma_peak_calibration_is_plausible(gpu):
     assert 1.0e15 < v.value < 5.6e15
 
 
+def test_hbm_read_peak_calibration_is_plausible(gpu):
+    """The measured sustained HBM read rate the bench quotes the matvec against: between 2 TB/s and the published
+    8 TB/s."""
+    from integer_inference_engine_amd import _lib
+    so = _lib.lib()
+    v = ctypes.c_double()
+    assert so.imie_hbm_read_peak(1 << 28, ctypes.byref(v)) == 0
+    assert 2.0e12 < v.value < 8.0e12
+    assert so.imie_hbm_read_peak(1 << 20, ctypes.byref(v)) != 0          # below the 16 MiB minimum: refused
+
+
 @pytest.mark.parametrize("N,nb,T", [(16, 4, 1), (37, 3, 1), (256, 32, 1), (1024, 96, 1), (100, 5, 3), (64, 8, 7),
                                     # decode-sized launches whose waves request 4 / 2 slabs at once, with a short
                                     # last slab range (10 = 4 + 4 + 2 slabs, 25 = 12 * 2 + 1)
