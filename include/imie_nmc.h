@@ -51,6 +51,9 @@ int imie_moe_ffn_batched_dev(const long long *gate_h, const long long *up_h, con
                              const int64_t *h_dev, const int64_t *gates_dev, long long d_model, long long e_ffn,
                              int fa, int fw, int64_t *out_dev, void *stream);
 int imie_moe_status(int clear, void *stream);
+/* fp16 -> round-half-even(h * 2^fw) as the Q4_K / Q6_K kernels compute it, over n host values (synchronous). No
+ * reference counterpart: a test hook for the exhaustive check against the integer rule (nmc_qk_kernel.c:16-39). */
+int imie_fp16_fixed_probe(const uint16_t *h, int64_t n, int fw, int64_t *out);
 /* registry / workspace / profiling (nmc_qk_cuda.cu:82-90, 1783-1815; qk_cuda.py:870-965). */
 void qk_free_all(void);
 long long qk_resident_count(void);

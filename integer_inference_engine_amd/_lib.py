@@ -125,6 +125,7 @@ SIGNATURES = {
     "imie_moe_ffn_batched_dev": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int,
                                                             c_int, c_void_p, c_void_p]),
     "imie_moe_status": (c_int, [c_int, c_void_p]),
+    "imie_fp16_fixed_probe": (c_int, [c_void_p, c_int64, c_int, c_void_p]),
     "qk_register_i64": (c_int64, [c_void_p, c_int64, c_int64]),
     "qk_rmsnorm_router": (c_int, [c_int64, c_int64, c_void_p, c_int64, c_int, c_int, c_uint64, c_int, c_int64, c_int64,
                                   c_void_p, c_void_p, c_void_p]),

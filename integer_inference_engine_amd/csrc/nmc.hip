@@ -67,6 +67,25 @@ __device__ inline int64_t fp16_fixed(uint32_t h, int fw) {
   return ((h >> 15) & 1) ? -r : r;
 }
 
+// fp16_fixed with the right-shift rounding done by the float unit: m 2^sh for sh < 0 is exact in single precision
+// (m < 2^11) and rint rounds it half to even like the integer rule (values below one half, where the integer rule
+// clamps its shift, round to 0 either way); sh >= 0 is the exact left shift. Branch-free, about half the integer
+// rule's instructions; exponent 31 is treated as finite exactly as there.
+__device__ inline int64_t fp16_fixed_fast(uint32_t h, int fw) {
+  const uint32_t e = (h >> 10) & 31, mant = h & 0x3FF;
+  const uint32_t m = e == 0 ? mant : (mant | 0x400);
+  const int sh = (e == 0 ? 1 : (int)e) - 25 + fw;
+  const int64_t up = (int64_t)((uint64_t)m << (sh > 0 ? sh : 0));
+  const int64_t dn = (int64_t)(uint32_t)__builtin_rintf(__builtin_ldexpf((float)m, sh < 0 ? sh : 0));
+  const int64_t r = sh >= 0 ? up : dn;
+  return ((h >> 15) & 1) ? -r : r;
+}
+
+__global__ void fp16_fixed_probe_kernel(const uint16_t* __restrict__ h, int64_t n, int fw, int64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = fp16_fixed_fast(h[i], fw);
+}
+
 struct Item {               // one weight applied to `count` x rows
   const uint8_t* w;
   int64_t out_f, nb;
@@ -109,7 +128,7 @@ __device__ void qk_group_tile(const Item* __restrict__ items, const int* __restr
       const bool fast = s_wide == 0;
       const uint8_t* blk = row + b * bs;
       if (it.qtype == 0) {
-        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed_fast(blk[2] | (blk[3] << 8), fw);
         const uint8_t* sc = blk + 4;
         const uint8_t* qs = blk + 16;
 #pragma unroll 1
@@ -143,7 +162,7 @@ __device__ void qk_group_tile(const Item* __restrict__ items, const int* __restr
         const uint8_t* ql = blk;
         const uint8_t* qh = blk + 128;
         const int8_t* sc = (const int8_t*)(blk + 192);
-        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[208] | (blk[209] << 8), fw);
 #pragma unroll 1
         for (int j = 0; j < 16; ++j) {
           // sub-block j covers positions 16 j .. 16 j + 15: half = j / 8, quarter qq = (j % 8) / 2, is = j % 2
@@ -430,7 +449,7 @@ __global__ __launch_bounds__(256) void qk_mfma_kernel(const Item* __restrict__ i
       const uint8_t* blk = wrow + b * BS;
       int64_t S1[4] = {0, 0, 0, 0}, S2[4] = {0, 0, 0, 0};
       if (QT == 0) {
-        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed_fast(blk[2] | (blk[3] << 8), fw);
         const uint8_t* scb = blk + 4;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -468,7 +487,7 @@ __global__ __launch_bounds__(256) void qk_mfma_kernel(const Item* __restrict__ i
         const uint8_t* ql = blk;
         const uint8_t* qh = blk + 128;
         const int8_t* scs = (const int8_t*)(blk + 192);
-        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[208] | (blk[209] << 8), fw);
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
@@ -577,7 +596,7 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
       __syncthreads();
       const uint8_t* blk = wrow + b * BS;
       if (QT == 0) {
-        const int64_t dq = fp16_fixed(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed(blk[2] | (blk[3] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[0] | (blk[1] << 8), fw), dmq = fp16_fixed_fast(blk[2] | (blk[3] << 8), fw);
         const uint8_t* scb = blk + 4;
         const uint4 qa = *(const uint4*)(blk + 16 + 32 * q), qb = *(const uint4*)(blk + 32 + 32 * q);
         const uint32_t qd[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
@@ -617,7 +636,7 @@ __global__ __launch_bounds__(256) void qk_dot4_kernel(const Item* __restrict__ i
         const uint8_t* ql = blk + 64 * half;
         const uint8_t* qh = blk + 128 + 32 * half;
         const int8_t* scs = (const int8_t*)(blk + 192);
-        const int64_t dq = fp16_fixed(blk[208] | (blk[209] << 8), fw);
+        const int64_t dq = fp16_fixed_fast(blk[208] | (blk[209] << 8), fw);
         const uint4 l0 = *(const uint4*)ql, l1 = *(const uint4*)(ql + 16), l2 = *(const uint4*)(ql + 32),
                     l3 = *(const uint4*)(ql + 48);
         const uint4 h0 = *(const uint4*)qh, h1 = *(const uint4*)(qh + 16);
@@ -905,7 +924,7 @@ template <int NG>
 __device__ inline void q4_block_mfma(const Q4Lane& w, const int8_t* buf, int gstride, const MoeA& a, int lg, int fw,
                                      Acc128 (&acc)[NG], bool two) {
   const uint32_t hb = w.h.x;
-  const int64_t dq = fp16_fixed(hb & 0xFFFF, fw), dmq = fp16_fixed(hb >> 16, fw);
+  const int64_t dq = fp16_fixed_fast(hb & 0xFFFF, fw), dmq = fp16_fixed_fast(hb >> 16, fw);
   const uint32_t scw[3] = {w.h.y, w.h.z, w.h.w};
   auto scb = [&](int i) { return (int)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
   int sc[8], mn[8];
@@ -1086,7 +1105,7 @@ __device__ inline Q6Lane q6_lane_load(const uint8_t* blk, int kg) {
 // lg1 = 1) or limbs 0..3 of four more tokens (acc1, lg1 = 0); the block's unpacked weights and scales serve both.
 __device__ inline void q6_block_mfma(const Q6Lane& w, const int8_t* buf, int gstride, const MoeA& a, int kg, int fw,
                                      Acc128& acc0, Acc128& acc1, int lg1, bool two) {
-  const int64_t dq = fp16_fixed(w.d, fw);
+  const int64_t dq = fp16_fixed_fast(w.d, fw);
   const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
   auto scs = [&](int i) { return (int)(int8_t)((scw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
   const bool klo = kg < 2;
@@ -1549,6 +1568,23 @@ int imie_qk_moe_dev(const long long* gate_h, const long long* up_h, const long l
 }
 
 extern "C" {
+
+// fp16 -> fixed point as the Q4_K / Q6_K kernels compute it (fp16_fixed_fast), over n host values; synchronous.
+// Test hook (no reference counterpart): the exhaustive check against the oracle's integer rule.
+int imie_fp16_fixed_probe(const uint16_t* h, int64_t n, int fw, int64_t* out) {
+  std::lock_guard<std::recursive_mutex> lk(imie_lock());
+  if (!h || !out || n <= 0 || fw < 0 || fw > 62 || imie_device_ready() != 0) return IMIE_EARG;
+  hipStream_t st = imie_stream();
+  static DevBuf a, b;                                 // grow-only staging, like the other host-pointer entry points
+  if (a.ensure((size_t)n * 2) || b.ensure((size_t)n * 8)) return IMIE_EARG;
+  IMIE_HIP(hipMemcpyAsync(a.p, h, (size_t)n * 2, hipMemcpyHostToDevice, st));
+  hipLaunchKernelGGL(fp16_fixed_probe_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint16_t*)a.p,
+                     n, fw, (int64_t*)b.p);
+  IMIE_HIP(hipGetLastError());
+  IMIE_HIP(hipMemcpyAsync(out, b.p, (size_t)n * 8, hipMemcpyDeviceToHost, st));
+  IMIE_HIP(hipStreamSynchronize(st));
+  return IMIE_OK;
+}
 
 // nmc_qk_cuda.cu:755 `qk_cuda_abi_version`; the reference bridge requires 5 (qk_cuda.py:22, 83-92).
 int qk_cuda_abi_version(void) { return 5; }

@@ -131,3 +131,18 @@ def test_config4_moe_block_byte_exact(qkg):
     assert got is not None
     bad = np.count_nonzero(got != want)
     assert bad == 0, f"{bad} mismatches"
+
+
+@pytest.mark.parametrize("fw", [0, 1, 7, 16, 24, 29, 40, 41, 45])
+def test_fp16_fixed_device_form_is_exhaustively_exact(fw):
+    """The kernels' fp16 -> fixed conversion (double-precision form, integer rule for exponent 31 and fw > 40)
+    against the oracle's integer rule over all 65536 fp16 bit patterns (nmc_qk_kernel.c:16-39)."""
+    import ctypes
+    from integer_inference_engine_amd import _lib
+    so = _lib.lib()
+    h = np.arange(1 << 16, dtype=np.uint16)
+    got = np.empty(1 << 16, dtype=np.int64)
+    assert so.imie_fp16_fixed_probe(h.ctypes.data, h.size, fw, got.ctypes.data) == 0
+    want = qk.fp16_fixed(h, fw)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"fw={fw}: {bad.size} mismatches, first h={int(h[bad[0]]):#06x} got {got[bad[0]]} want {want[bad[0]]}"
