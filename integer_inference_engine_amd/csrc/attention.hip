@@ -944,8 +944,10 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
 }
 
 // Decode PV (M == 1). Workgroup = (b, kv, chunk); per 64-key step the p digits of the REP heads are staged in LDS
-// as the A operand (row 4 (r % 4) + lp of head block r / 4); wave w owns dim tiles w and w + 4.
-template <int REP>
+// as the A operand (row 4 (r % 4) + lp of head block r / 4); wave w owns dim tiles w and w + 4. RECOMP: e_j is
+// recomputed here from the score and the row maximum (dec_exp_kernel<REP, false> wrote no e); otherwise the
+// scores array holds e_j.
+template <int REP, bool RECOMP>
 __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
   constexpr int RBH = (REP + 3) / 4;
   __shared__ __align__(16) int8_t sPd[RBH][16][64];
@@ -1076,10 +1078,13 @@ __global__ __launch_bounds__(256) void dec_pv8_kernel(AttnDesc d) {
         const uint64_t Z = s_z[r];
         int64_t p = 0;
         if (kk < tn && Z != 0) {
-          // e_j of dec_exp_kernel from the score and the row maximum
-          int64_t dd = (int64_t)((uint64_t)s_m[r] - (uint64_t)scv[k]);
-          if (dd > d.dclip) dd = d.dclip;
-          p = prob_div(exp_clipped(dd, d.frac, d.log2e, fx32), d.frac, Z, s_rzd[r]);
+          int64_t e = scv[k];
+          if (RECOMP) {                                  // e_j of dec_exp_kernel from the score and the row maximum
+            int64_t dd = (int64_t)((uint64_t)s_m[r] - (uint64_t)scv[k]);
+            if (dd > d.dclip) dd = d.dclip;
+            e = exp_clipped(dd, d.frac, d.log2e, fx32);
+          }
+          p = prob_div(e, d.frac, Z, s_rzd[r]);
         }
         mp[r] = (uint64_t)p > mp[r] ? (uint64_t)p : mp[r];
         int64_t x = p;
@@ -2158,7 +2163,10 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
       IMIE_DEC_R(dec_scores_kernel, int64_t);
     }
     IMIE_HIP(hipGetLastError());
-    if (d.kv32) {                                     // PV recomputes e from the scores
+    // kv8 with several sequences: PV recomputes e from the scores (no write-back of e, the bytes a big batch is
+    // bound by); one sequence: e is written back, which keeps the exponentials off PV's per-step latency chain
+    const bool recomp = d.kv32 && d.B > 1;
+    if (recomp) {
       if (rep == 1) hipLaunchKernelGGL((dec_exp_kernel<1, false>), gd, dim3(256), 0, st, d);
       else if (rep == 2) hipLaunchKernelGGL((dec_exp_kernel<2, false>), gd, dim3(256), 0, st, d);
       else if (rep == 4) hipLaunchKernelGGL((dec_exp_kernel<4, false>), gd, dim3(256), 0, st, d);
@@ -2170,11 +2178,16 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
       else hipLaunchKernelGGL(dec_exp_kernel<8>, gd, dim3(256), 0, st, d);
     }
     IMIE_HIP(hipGetLastError());
-    if (d.kv32) {
-      if (rep == 1) hipLaunchKernelGGL(dec_pv8_kernel<1>, gd, dim3(256), 0, st, d);
-      else if (rep == 2) hipLaunchKernelGGL(dec_pv8_kernel<2>, gd, dim3(256), 0, st, d);
-      else if (rep == 4) hipLaunchKernelGGL(dec_pv8_kernel<4>, gd, dim3(256), 0, st, d);
-      else hipLaunchKernelGGL(dec_pv8_kernel<8>, gd, dim3(256), 0, st, d);
+    if (d.kv32 && recomp) {
+      if (rep == 1) hipLaunchKernelGGL((dec_pv8_kernel<1, true>), gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL((dec_pv8_kernel<2, true>), gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL((dec_pv8_kernel<4, true>), gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL((dec_pv8_kernel<8, true>), gd, dim3(256), 0, st, d);
+    } else if (d.kv32) {
+      if (rep == 1) hipLaunchKernelGGL((dec_pv8_kernel<1, false>), gd, dim3(256), 0, st, d);
+      else if (rep == 2) hipLaunchKernelGGL((dec_pv8_kernel<2, false>), gd, dim3(256), 0, st, d);
+      else if (rep == 4) hipLaunchKernelGGL((dec_pv8_kernel<4, false>), gd, dim3(256), 0, st, d);
+      else hipLaunchKernelGGL((dec_pv8_kernel<8, false>), gd, dim3(256), 0, st, d);
     } else {
       IMIE_DEC_R(dec_pv_kernel, int64_t);
     }
