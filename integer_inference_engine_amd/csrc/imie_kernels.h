@@ -113,11 +113,9 @@ struct QkHeadArgs {
 };
 // kv8 = 1: the digit-plane cache of imie_kvfmt.h; 0: int64 rows
 int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
-// after imie_qk_head_launch with gpart set: guard <- max over gpart; kv8: the V digit planes of the new rows
+// after imie_qk_head_launch with gpart set: guard <- max over gpart; kv8 with M > 1: the V digit planes of the new
+// rows, and their maxima (rowk / rowv) folded into run_k / run_v
 int imie_qk_head_finish_launch(const QkHeadArgs& a, int kv8, hipStream_t st);
-// kv8 cache: fold the appended rows' maxima (rowk / rowv, M rows per sequence) into run_k / run_v
-int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
-                          uint64_t* run_k, uint64_t* run_v, hipStream_t st);
 
 // Integer sampler config (committed fixed-point settings; layout shared with include/imie_bonsai.h).
 // mode: 0 greedy, 1 temp, 2 top_k, 3 top_p, 4 min_p (the reference ABI's numbering, bonsai_q1_gpu.cu:905-910)

@@ -293,8 +293,9 @@ int norm_into_matvec(Net& n, const int64_t* x, int64_t rows, const int64_t* g, i
       z.cnt = i + 1;
     }
     if (z.cnt != cnt) z.cnt = 0;                      // all or none: the GEMM is told the outputs are clear
-    if ((rc = imie_rmsnorm_gemm_prep_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, gp, z, st))) return rc;
-    return imie_q1_launch_multi(hs, cnt, xn, rows, n.frac, outs, 0, &n.q1w, st, z.cnt ? 3 : 2);
+    // the GEMM reads only the digit table: the normalised rows themselves are not written
+    if ((rc = imie_rmsnorm_gemm_prep_launch(x, rows, n.d, n.frac, n.eps, g, nullptr, status, gp, z, st))) return rc;
+    return imie_q1_launch_multi(hs, cnt, nullptr, rows, n.frac, outs, 0, &n.q1w, st, z.cnt ? 3 : 2);
   }
   int rc = imie_rmsnorm_launch(x, rows, n.d, n.frac, n.eps, g, xn, status, st);
   if (rc) return rc;
@@ -391,7 +392,6 @@ int net_run_core(Net& n, int64_t* x, int64_t M, int64_t lmax, hipStream_t st) {
       if (rows > 1) a.gpart = (uint64_t*)n.gpart.p;   // several rows: no same-address atomics on the guard
       CK(imie_qk_head_launch(a, n.kv32, st));
       CK(imie_qk_head_finish_launch(a, n.kv32, st));
-      if (n.kv32) CK(imie_kv_runmax_launch(a.rowk, a.rowv, n.B, M, n.Hkv, a.run_k, a.run_v, st));
     }
     CK(imie_attention_launch(d, st));
     if (pro) {

@@ -58,7 +58,8 @@ __device__ inline void prep_row_gemm(const int64_t* s_y, int64_t row, const imie
 // into the Q1 digit table (one wave per 512-slab), and the workgroups clear the zero list of the next matvec.
 constexpr int kPrepCols = 4096;
 
-// PREP: 0 none, 1 the matvec digit table (po, zero), 2 the GEMM digit table (gp)
+// PREP: 0 none, 1 the matvec digit table (po, zero), 2 the GEMM digit table (gp). With a table, out may be null
+// (the GEMM reads only the table: no int64 copy of the normalised rows is written).
 template <int PREP, int NT, int kNormPer>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__ x, int64_t cols, int frac,
                                                       int64_t eps, const int64_t* __restrict__ gain,
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
       const uint64_t ag = imie_absu64(g);
       mxg = ag > mxg ? ag : mxg;
     } else {
-      out[row * cols + c] = nv;
+      if (out) out[row * cols + c] = nv;
       if (PREP) s_y[c] = nv;
     }
     if (keep) *keep = nv;
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const int64_t* __restrict__
       const int64_t c = tid + (int64_t)k * nt;
       if (c < cols) {
         const int64_t y = imie_floor_shift((int64_t)((uint64_t)nvk[k] * (uint64_t)gv[k]), frac);
-        out[row * cols + c] = y;
+        if (out) out[row * cols + c] = y;
         if (PREP) s_y[c] = y;
       }
     }

@@ -131,69 +131,86 @@ __global__ __launch_bounds__(64) void qk_head_kernel(QkHeadArgs a) {
   vp[j + half] = v1;
 }
 
-__global__ __launch_bounds__(64) void kv_runmax_kernel(const uint64_t* __restrict__ rowk,
-                                                       const uint64_t* __restrict__ rowv, int64_t M, int64_t Hkv,
-                                                       uint64_t* __restrict__ run_k, uint64_t* __restrict__ run_v) {
-  const int64_t bkv = blockIdx.x, b = bkv / Hkv, kv = bkv % Hkv;
-  uint64_t mk = 0, mv = 0;
-  for (int64_t m = threadIdx.x; m < M; m += 64) {
-    const uint64_t a = rowk[(b * M + m) * Hkv + kv], c = rowv[(b * M + m) * Hkv + kv];
-    mk = a > mk ? a : mk;
-    mv = c > mv ? c : mv;
-  }
-  mk = imie_wave_max_u64(mk);
-  mv = imie_wave_max_u64(mv);
-  if (threadIdx.x == 0) {
-    run_k[bkv] = mk > run_k[bkv] ? mk : run_k[bkv];
-    run_v[bkv] = mv > run_v[bkv] ? mv : run_v[bkv];
-  }
-}
-
-
-// RoPE envelope maxima of a many-row head stage: grid-stride max over the per-workgroup partials, one atomic
-// per wave and quantity
+// RoPE envelope maxima of a many-row head stage: grid-stride max over the per-workgroup partials (256 threads),
+// one atomic per workgroup and quantity
 __global__ __launch_bounds__(256) void guard_reduce_kernel(const uint64_t* __restrict__ gpart, int64_t n, int64_t H,
                                                            int64_t heads, uint64_t* __restrict__ guard) {
   uint64_t m[4] = {0, 0, 0, 0};
+  // n < 2^32 (rows x heads); unrolled so that several iterations' loads are in flight together
+#pragma unroll 8
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-    const int k = (e % heads) < H ? 0 : 2;
+    const int k = imie_umod32(e, heads) < H ? 0 : 2;
     const uint64_t a = gpart[2 * e], c = gpart[2 * e + 1];
     if (k == 0) { m[0] = a > m[0] ? a : m[0]; m[1] = c > m[1] ? c : m[1]; }
     else { m[2] = a > m[2] ? a : m[2]; m[3] = c > m[3] ? c : m[3]; }
   }
+  // workgroup maxima through LDS, then one atomic per quantity and workgroup (same-address atomics from every
+  // wave serialise across the XCDs)
+  __shared__ uint64_t s_m[4][4];
+  const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint64_t v = imie_wave_max_u64_full(m[i]);
-    if ((threadIdx.x & 63) == 0 && v != 0) amax_u64(&guard[i], v);
+    if ((threadIdx.x & 63) == 0) s_m[wave][i] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    uint64_t v = s_m[0][threadIdx.x];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = s_m[w][threadIdx.x] > v ? s_m[w][threadIdx.x] : v;
+    if (v != 0) amax_u64(&guard[threadIdx.x], v);
   }
 }
 
 // kv8 V append of many rows: workgroup = (64 consecutive new positions of sequence b, kv head). The rows'
 // digits are transposed through LDS to the cache's [digit][dim][slot] order, so each store instruction writes
-// 64 consecutive slots.
+// 64 consecutive slots. Each thread's 32 V elements (element tid + 256 k of the 64 x hd tile) are requested in
+// one round before any is encoded. The workgroup also folds its rows' max|K| / max|V| into the running maxima.
 __global__ __launch_bounds__(256) void kv8_v_append_kernel(QkHeadArgs a) {
   __shared__ int8_t sv[4][128][64];
-  const int64_t bkv = blockIdx.y, b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  const int64_t bkv = blockIdx.y, b = imie_udiv32(bkv, a.Hkv), kvh = imie_umod32(bkv, a.Hkv);
   const int64_t m0 = (int64_t)blockIdx.x * 64;
   const int tid = threadIdx.x;
-  for (int64_t i = tid; i < 64 * a.hd; i += 256) {
-    const int64_t ml = i / a.hd, c = i % a.hd, m = m0 + ml;
-    const int64_t v = m < a.M ? a.v[((b * a.M + m) * a.Hkv + kvh) * a.hd + c] : 0;
-    const uint32_t w = imie_kv8::encode(imie_kv8::fits(v) ? v : 0);   // out-of-range rows are flagged upstream
+  const int hd = (int)a.hd;                           // <= 128: 64 * hd <= 32 * 256 elements
+  // lane's position (slot of the store phase), requested with the V loads
+  const int lane = tid & 63, wave = tid >> 6;
+  const int64_t m = m0 + lane;
+  const bool live = m < a.M;
+  int64_t pg = 0, slot = 0;
+  uint64_t rk = 0, rv = 0;                            // the rows' max|K|, max|V| (head stage), for run_k / run_v
+  if (live) {
+    if (wave == 0) { rk = a.rowk[(b * a.M + m) * a.Hkv + kvh]; rv = a.rowv[(b * a.M + m) * a.Hkv + kvh]; }
+    const int64_t p = a.pos[b * a.M + m];
+    const uint32_t pq = (uint32_t)p / (uint32_t)a.P;
+    pg = a.pt[b * a.mp + pq];
+    slot = (uint32_t)p - pq * (uint32_t)a.P;
+  }
+  int64_t vv[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int i = tid + 256 * k;
+    const int ml = (int)((uint32_t)i / (uint32_t)hd), c = i - ml * hd;
+    const int64_t m = m0 + ml;
+    vv[k] = (ml < 64 && m < a.M) ? a.v[((b * a.M + m) * a.Hkv + kvh) * hd + c] : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int i = tid + 256 * k;
+    const int ml = (int)((uint32_t)i / (uint32_t)hd), c = i - ml * hd;
+    if (ml >= 64) break;
+    const uint32_t w = imie_kv8::encode(imie_kv8::fits(vv[k]) ? vv[k] : 0);   // out-of-range rows: flagged upstream
 #pragma unroll
     for (int db = 0; db < 4; ++db) sv[db][c][ml] = (int8_t)(w >> (8 * db));
   }
+  if (wave == 0) {                                   // running maxima of the cache (one atomic per quantity)
+    rk = imie_wave_max_u64_full(rk);
+    rv = imie_wave_max_u64_full(rv);
+    if (lane == 0) { amax_u64(&a.run_k[bkv], rk); amax_u64(&a.run_v[bkv], rv); }
+  }
   __syncthreads();
-  const int lane = tid & 63, wave = tid >> 6;
-  const int64_t m = m0 + lane;
-  if (m >= a.M) return;
-  const int64_t p = a.pos[b * a.M + m];
-  const uint32_t pq = (uint32_t)p / (uint32_t)a.P;
-  const int64_t pg = a.pt[b * a.mp + pq], slot = (uint32_t)p - pq * (uint32_t)a.P;
+  if (!live) return;
   int8_t* vblk = (int8_t*)a.vpool + imie_kv8::block_base(pg, kvh, a.Hkv, a.hd, a.P);
-  for (int64_t e = wave; e < 4 * a.hd; e += 4) {
-    const int db = (int)(e / a.hd);
-    const int64_t c = e % a.hd;
+  for (int e = wave; e < 4 * hd; e += 4) {
+    const int db = (int)((uint32_t)e / (uint32_t)hd), c = e - db * hd;
     vblk[imie_kv8::v_off(slot, db, c, a.hd, a.P)] = sv[db][c][lane];
   }
 }
@@ -208,14 +225,6 @@ int imie_qk_head_launch(const QkHeadArgs& a, int kv8, hipStream_t st) {
   const dim3 grid((unsigned)rows, (unsigned)(a.H + a.Hkv));
   if (kv8) hipLaunchKernelGGL(qk_head_kernel<true>, grid, dim3(64), 0, st, a);
   else hipLaunchKernelGGL(qk_head_kernel<false>, grid, dim3(64), 0, st, a);
-  IMIE_HIP(hipGetLastError());
-  return IMIE_OK;
-}
-
-int imie_kv_runmax_launch(const uint64_t* rowk, const uint64_t* rowv, int64_t B, int64_t M, int64_t Hkv,
-                          uint64_t* run_k, uint64_t* run_v, hipStream_t st) {
-  if (B <= 0 || M <= 1) return IMIE_OK;
-  hipLaunchKernelGGL(kv_runmax_kernel, dim3((unsigned)(B * Hkv)), dim3(64), 0, st, rowk, rowv, M, Hkv, run_k, run_v);
   IMIE_HIP(hipGetLastError());
   return IMIE_OK;
 }
