@@ -770,8 +770,9 @@ __device__ inline int64_t kv8_row_base(const AttnDesc& d, int64_t b, int64_t kv,
 // limbs of head 4 * hb + g for key n and recombines them in place. With d.qd set, the head stage has already
 // written q's digit planes, limb counts and max|q|, and the A operands are read from memory directly;
 // otherwise the first wave-pass digitizes q into LDS.
-template <int REP>
-__global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
+// Three waves per SIMD (at most 168 VGPRs) up to four heads per kv head; eight heads keep two (no spills in the loop).
+template <int REP, int KS>
+__global__ __launch_bounds__(256, REP <= 4 ? 3 : 2) void dec_scores8_kernel(AttnDesc d) {
   constexpr int RBH = (REP + 3) / 4;
   __shared__ int64_t s_max[4][REP];
   __shared__ uint64_t s_mq[4];
@@ -780,11 +781,12 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   const int64_t rows = d.B * d.H;
   const int64_t L = dec_len(d, b);
   const int64_t j0 = (int64_t)blockIdx.y * d.chunk;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), m = lane & 15,
+            g = lane >> 4;
   const int64_t* qg = d.q + b * d.qsb + kv * REP * d.qsh;
   v4i av[RBH][2][2];
   int Lq = 0, LB = 0;
-  const int KS = (int)((d.hd + 63) / 64);
+  static_assert(KS == 1 || KS == 2, "KS: 64-dim K steps, (hd + 63) / 64");
   int64_t smax[RBH];
 #pragma unroll
   for (int hb = 0; hb < RBH; ++hb) smax[hb] = INT64_MIN;
@@ -797,13 +799,31 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   page_split(d, j0, pi0, pin0);
   page_split(d, max(j0, min(j0 + d.chunk, d.Lmax) - 1), pi1, pin1);
   const bool pgreg = pi1 - pi0 < 64;
-  const int64_t pgl = (pgreg && lane <= pi1 - pi0) ? d.pt[b * d.mp + pi0 + lane] : 0;
-  // 16-key tiles t = j0 + 16 wave + 64 i; the next tile's K slices are loaded before this tile's MFMAs
-  auto load_tile = [&](int64_t t, int64_t lim, v4i (&bk)[4][2]) {   // keys below lim (masked later by jend)
+  int64_t pgl = (pgreg && lane <= pi1 - pi0) ? d.pt[b * d.mp + pi0 + lane] : 0;
+  // 16-key tiles t = j0 + 16 wave + 64 i; the next tile's K slices are loaded before this tile's MFMAs. PG (a
+  // compile-time copy of pgreg): the loop of the common case holds no page-table load, whose possible pending
+  // write on the other path would make the compiler wait for every load in flight
+  // The loads are issued whether or not the tile exists (live false: every lane reads the pool's first 16 bytes,
+  // one cache line): a load that may be skipped leaves the compiler unable to count the loads in flight, and it
+  // then waits for all of them before the MFMAs.
+  // A tile's scores are stored at the start of the next load_tile, before that tile's loads, and their registers
+  // are kept live across those loads: the compiler waits for a store before its data registers are rewritten, and
+  // the vector memory counter is in order, so a store issued after the loads would make that wait include them.
+  int64_t pend_v[RBH], pend_i[RBH];
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb) { pend_v[hb] = 0; pend_i[hb] = -1; }
+  auto flush = [&]() {
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb)
+      if (pend_i[hb] >= 0) d.scores[pend_i[hb]] = pend_v[hb];
+  };
+  auto load_tile = [&](auto pgc, bool live, int64_t t, int64_t lim, v4i (&bk)[4][2]) {   // keys below lim
+    constexpr bool PG = decltype(pgc)::value;
+    flush();
     const int64_t j = t + m;
-    const bool valid = j < lim;
+    const bool valid = live && j < lim;
     int64_t base = 0, slot = 0;
-    if (pgreg) {                                      // every lane active here (t is wave-uniform)
+    if constexpr (PG) {                               // every lane active here (t is wave-uniform)
       int64_t pi;
       page_split(d, valid ? j : j0, pi, slot);
       const int64_t pg = __shfl(pgl, (int)(pi - pi0), 64);
@@ -811,13 +831,23 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
     } else if (valid) {
       base = kv8_row_base(d, b, kv, j, &slot) + imie_kv8::k_off(slot, 0, 0, d.hd);
     }
+    // every lane loads, with no select on the data: a conditional load is a branch, after which the compiler
+    // waits for every load in flight (vmcnt 0, the next tile's prefetch too) before the MFMAs, and a select
+    // waits for its load at once. Lanes of keys past `lim` read an in-bounds address (their score columns are
+    // never stored); dims at or past hd read dims 0.. of the same slot, which meet zero q digits.
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        bk[db][h] = (valid && h < KS && 64 * h + 16 * g < d.hd)
-                        ? *(const v4i*)(Kb + base + imie_kv8::k_piece(db, 64 * h + 16 * g, d.hd))
-                        : v4i{0, 0, 0, 0};
+      for (int h = 0; h < KS; ++h) {
+        const int64_t c = 64 * h + 16 * g;
+        bk[db][h] = *(const v4i*)(Kb + (live ? base + imie_kv8::k_piece(db, c < d.hd ? c : 0, d.hd) : 0));
+      }
+    // keeps the loads here: otherwise they sink into the block that consumes them, or the consumer's MFMAs (and
+    // their waits) are scheduled above them
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int hb = 0; hb < RBH; ++hb) asm volatile("" ::"v"(pend_v[hb]), "v"(pend_i[hb]));
+    __builtin_amdgcn_sched_barrier(0);
   };
   auto score_tile = [&](int64_t t, const v4i (&bk)[4][2]) {
     const int64_t j = t + m;
@@ -829,7 +859,7 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           v4i D = mfma8(av[hb][lb][0], bk[db][0], v4i{0, 0, 0, 0});
-          if (KS > 1) D = mfma8(av[hb][lb][1], bk[db][1], D);
+          if constexpr (KS > 1) D = mfma8(av[hb][lb][1], bk[db][1], D);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * lb + i + db;              // 256^e = 0 mod 2^64 for e >= 8
@@ -837,12 +867,11 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
           }
         }
       const int r = 4 * hb + g;
-      if (valid && r < REP) {
-        int64_t sc = (int64_t)S >> d.frac;
-        sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
-        d.scores[(b * d.H + kv * REP + r) * d.Lmax + j] = sc;
-        smax[hb] = sc > smax[hb] ? sc : smax[hb];
-      }
+      int64_t sc = (int64_t)S >> d.frac;
+      sc = (int64_t)((uint64_t)sc * (uint64_t)d.inv_sqrt) >> d.frac;
+      pend_v[hb] = sc;
+      pend_i[hb] = (valid && r < REP) ? (b * d.H + kv * REP + r) * d.Lmax + j : -1;
+      if (valid && r < REP) smax[hb] = sc > smax[hb] ? sc : smax[hb];
     }
   };
   v4i bkA[4][2], bkB[4][2];
@@ -850,7 +879,8 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
   // the first K tile in flight during the q setup, bounded by the score row stride rather than the sequence length
   // (no wait for the length): keys past it give scores that are never stored
   const int64_t lim0 = min(j0 + d.chunk, d.Lmax);
-  if (t < lim0) load_tile(t, lim0, bkA);
+  if (pgreg) load_tile(std::true_type{}, t < lim0, t, lim0, bkA);
+  else load_tile(std::false_type{}, t < lim0, t, lim0, bkA);
   if (d.qd) {
     // digits prepared by the head stage (all eight limb planes written): A operands straight from memory, loaded
     // together with the limb counts and masked once those arrive
@@ -916,17 +946,37 @@ __global__ __launch_bounds__(256) void dec_scores8_kernel(AttnDesc d) {
         for (int h = 0; h < 2; ++h)
           av[hb][lb][h] = (64 * h + 16 * g < d.hd) ? *(const v4i*)&sQd[hb][lb][m][64 * h + 16 * g] : v4i{0, 0, 0, 0};
   }
-  LB = (Lq + 3) / 4;
-  while (t < jend) {
-    const int64_t t2 = t + 64;
-    if (t2 < jend) load_tile(t2, jend, bkB);
-    score_tile(t, bkA);
-    if (t2 >= jend) break;
-    const int64_t t3 = t2 + 64;
-    if (t3 < jend) load_tile(t3, jend, bkA);
-    score_tile(t2, bkB);
-    t = t3;
-  }
+  // at least one limb block (zero digits score 0): the tile's MFMAs, and with them the waits for its loads, are
+  // then on every path, and no load of a consumed tile is still counted at the loop's back edge
+  LB = Lq > 4 ? 2 : 1;
+  // the loop's loop-invariant operands loaded before it (page ids, q digits) are re-defined here by empty asm
+  // statements (one wait for them, here): as load results, their age is lost over the loop's back edge and the
+  // compiler would wait for every load in flight (vmcnt 0, the K prefetch too) before each use in the loop
+  asm volatile("" : "+v"(pgl));
+#pragma unroll
+  for (int hb = 0; hb < RBH; ++hb)
+#pragma unroll
+    for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(av[hb][lb][h]));
+  auto walk = [&](auto pgc) {
+    // every load so far (the first K tile, the q digits) is complete at the loop's entry: a load still in flight
+    // there would make the compiler's wait tracking conservative in every iteration
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0)
+    while (t < jend) {
+      const int64_t t2 = t + 64;
+      load_tile(pgc, t2 < jend, t2, jend, bkB);
+      score_tile(t, bkA);
+      if (t2 >= jend) break;
+      const int64_t t3 = t2 + 64;
+      load_tile(pgc, t3 < jend, t3, jend, bkA);
+      score_tile(t2, bkB);
+      t = t3;
+    }
+  };
+  if (pgreg) walk(std::true_type{});
+  else walk(std::false_type{});
+  flush();
 #pragma unroll
   for (int hb = 0; hb < RBH; ++hb) {
     int64_t mx = smax[hb];
@@ -2155,10 +2205,14 @@ int imie_attention_launch(AttnDesc d, hipStream_t st) {
     if (rep == 1) IMIE_DEC(K_, KT_, 1); else if (rep == 2) IMIE_DEC(K_, KT_, 2);                           \
     else if (rep == 4) IMIE_DEC(K_, KT_, 4); else IMIE_DEC(K_, KT_, 8)
     if (d.kv32) {
-      if (rep == 1) hipLaunchKernelGGL(dec_scores8_kernel<1>, gd, dim3(256), 0, st, d);
-      else if (rep == 2) hipLaunchKernelGGL(dec_scores8_kernel<2>, gd, dim3(256), 0, st, d);
-      else if (rep == 4) hipLaunchKernelGGL(dec_scores8_kernel<4>, gd, dim3(256), 0, st, d);
-      else hipLaunchKernelGGL(dec_scores8_kernel<8>, gd, dim3(256), 0, st, d);
+#define IMIE_SC8(R_)                                                                                          \
+      if (d.hd > 64) hipLaunchKernelGGL((dec_scores8_kernel<R_, 2>), gd, dim3(256), 0, st, d);                \
+      else hipLaunchKernelGGL((dec_scores8_kernel<R_, 1>), gd, dim3(256), 0, st, d)
+      if (rep == 1) { IMIE_SC8(1); }
+      else if (rep == 2) { IMIE_SC8(2); }
+      else if (rep == 4) { IMIE_SC8(4); }
+      else { IMIE_SC8(8); }
+#undef IMIE_SC8
     } else {
       IMIE_DEC_R(dec_scores_kernel, int64_t);
     }
