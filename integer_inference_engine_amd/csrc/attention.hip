@@ -68,6 +68,19 @@ __device__ inline RowInfo row_info(const AttnDesc& d, int64_t r) {
   return ri;
 }
 
+// Page id of page pi of sequence b for a wave-uniform (b, pi), read through the constant address space: the page
+// table is not written during an attention launch, so the load is a scalar one (its own counter). A vector load
+// of it would be counted with the K / V loads in flight, and the wait for it (the address of the next loads
+// depends on it) would wait for all of them.
+__device__ inline int64_t page_id_uniform(const AttnDesc& d, int64_t b, int64_t pi) {
+  // the address through readfirstlane: kept in scalar registers even where the compiler had moved it to vector
+  // ones (a vector address makes the load a vector one)
+  const uint64_t a = (uint64_t)(d.pt + b * d.mp + pi);
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
+  return *(const __attribute__((address_space(4))) int64_t*)u;
+}
+
 // key j -> (page index within the sequence, slot in the page); positions are below 2^31
 __device__ inline void page_split(const AttnDesc& d, int64_t j, int64_t& pi, int64_t& in) {
   if (d.pshift >= 0) {
@@ -1796,7 +1809,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     int64_t pi, slot;
     page_split(d, tu, pi, slot);
     // wave-uniform 64-bit base (scalar registers) plus 32-bit lane offsets: no 64-bit address arithmetic per load
-    const int8_t* kblk = Kb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P) +
+    const int8_t* kblk = Kb + imie_kv8::block_base(page_id_uniform(d, b, pi), kv, d.Hkv, HDv, d.P) +
                          imie_kv8::k_off(slot, 0, 0, HDv);
     // keys past the sequence length are loaded from their (allocated) slots and masked where the scores are used
 #pragma unroll
@@ -1809,6 +1822,9 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
         const v4i v = ld16u(kblk, off, (uint32_t)(4 * 16 * HDv));
         bk[db][hh] = c < HDv ? v : v4i{0, 0, 0, 0};
       }
+    // keeps the loads here: otherwise the scheduler sinks them to their consumer or lifts its MFMAs above them
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
   };
   // scores of the lane's 4 rows for key t + m from the tile's K digits; invalid entries INT64_MIN
   auto scores = [&](int64_t t, const v4i (&bk)[4][2], ST sc[4]) {
@@ -1872,19 +1888,23 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   };
   // pass 1: row maxima (signed max as the unsigned max of values offset by INT64_MIN)
   // this wave's tiles t = 16 wave, + 64, ... below vis, the next tile's K in flight while one is scored
+  // The next tile's loads are issued whatever it is (past vis: the current tile again, whose page is allocated):
+  // a load that may be skipped leaves the compiler unable to count the loads in flight, and it then waits for
+  // all of them before the MFMAs.
   auto walk = [&](auto&& use) {
     v4i bkA[4][2], bkB[4][2];
     int64_t t = 16 * wave;
     if (t < vis) load_k(t, bkA);
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): nothing in flight at the loop's entry
     while (t < vis) {
       const int64_t t2 = t + STEP;
-      if (t2 < vis) load_k(t2, bkB);
+      load_k(t2 < vis ? t2 : t, bkB);
       ST sc[4];
       scores(t, bkA, sc);
       use(sc);
       if (t2 >= vis) break;
       const int64_t t3 = t2 + STEP;
-      if (t3 < vis) load_k(t3, bkA);
+      load_k(t3 < vis ? t3 : t2, bkA);
       scores(t2, bkB, sc);
       use(sc);
       t = t3;
@@ -1982,7 +2002,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   };
   // pass 3: p digits of each 64-key step into LDS, then PV
   const int Lp = F32 ? 3 : imie_limbs_needed((uint64_t)1 << d.frac);   // <= 4 (frac <= 29); 3 at frac 16
-  const int DT = (int)(d.hd / 16);
+  const int DT = (int)(HDv / 16);
   const int8_t* Vb = (const int8_t*)d.V;
   v4i Tp[DPW][NTP];
   uint64_t O[DPW][4];
@@ -2010,11 +2030,12 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   auto load_v = [&](int64_t t0, v4i (&bv)[DPW][KSP][4]) {
 #pragma unroll
     for (int ks = 0; ks < KSP; ++ks) {                         // each 64 keys lie in one page
-      const int64_t tu = (int64_t)__builtin_amdgcn_readfirstlane((int)(t0 + 64 * ks));
+      // a 64-key block past vis re-reads the step's first block (allocated); its p digits are 0
+      const int64_t tw = t0 + 64 * ks < vis ? t0 + 64 * ks : t0;
+      const int64_t tu = (int64_t)__builtin_amdgcn_readfirstlane((int)tw);
       int64_t pi, slot0;
       page_split(d, tu, pi, slot0);
-      const int8_t* vblk = Vb + imie_kv8::block_base(d.pt[b * d.mp + pi], kv, d.Hkv, HDv, d.P);
-      const bool live = tu < vis;
+      const int8_t* vblk = Vb + imie_kv8::block_base(page_id_uniform(d, b, pi), kv, d.Hkv, HDv, d.P);
       const int8_t* vs = vblk + slot0;                         // uniform; lane offsets below are 32-bit
 #pragma unroll
       for (int tt = 0; tt < DPW; ++tt) {
@@ -2022,10 +2043,12 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const uint32_t off = ((uint32_t)db * (uint32_t)HDv + (uint32_t)(16 * tile + m)) * (uint32_t)d.P + 16u * g;
-          bv[tt][ks][db] = (live && tile < DT) ? ld16u(vs, off, (uint32_t)(4 * HDv * d.P)) : v4i{0, 0, 0, 0};
+          bv[tt][ks][db] = tile < DT ? ld16u(vs, off, (uint32_t)(4 * HDv * d.P)) : v4i{0, 0, 0, 0};
         }
       }
     }
+    asm volatile("" ::: "memory");                            // keeps the loads here (see load_k)
+    __builtin_amdgcn_sched_barrier(0);
   };
   v4i bk[4][2], bv[DPW][KSP][4];
   if (16 * wave < vis) load_k(16 * wave, bk);
@@ -2034,7 +2057,8 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     const int64_t t = t0 + 16 * wave;
     ST sc[4] = {SMIN, SMIN, SMIN, SMIN};
     if (t < vis) scores(t, bk, sc);
-    if (t + STEP < vis) load_k(t + STEP, bk);
+    // issued whatever the next step is (past vis: this tile again; see walk)
+    load_k(t + STEP < vis ? t + STEP : (t < vis ? t : 16 * wave), bk);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t e = expv(sc[i], i);
@@ -2061,7 +2085,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
             if (lp + db < NTP) Tp[tt][lp + db] = mfma8(a, bv[tt][ks][db], Tp[tt][lp + db]);
         }
       }
-    if (t0 + STEP < vis) load_v(t0 + STEP, bv);
+    load_v(t0 + STEP < vis ? t0 + STEP : t0, bv);
     if (++steps == 64) { fold(); steps = 0; }
   }
   fold();
