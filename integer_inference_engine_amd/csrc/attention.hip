@@ -517,12 +517,26 @@ __global__ __launch_bounds__(256) void dec_exp_kernel(AttnDesc d) {
     const int64_t row = b * d.H + kv * REP + r;
     const int64_t mx = s_rmax[r];
     uint64_t z = 0;
-    for (int64_t j = j0 + threadIdx.x; j < jend; j += blockDim.x) {
-      int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)(one ? sv[r] : d.scores[row * d.Lmax + j]));
+    auto one_e = [&](int64_t j, int64_t s) {
+      int64_t dd = (int64_t)((uint64_t)mx - (uint64_t)s);
       if (dd > d.dclip) dd = d.dclip;
       const uint64_t e = (uint64_t)exp_clipped(dd, d.frac, d.log2e, fx32);
       if (STORE) d.scores[row * d.Lmax + j] = (int64_t)e;
       z += e;
+    };
+    if (one) {
+      if (jt < jend) one_e(jt, sv[r]);
+    } else {
+      // long chunks: eight of the thread's scores requested per round (a load per iteration would wait for
+      // each in turn); keys past jend read an in-bounds score and are not used
+      for (int64_t j = j0 + threadIdx.x; j < jend; j += 8 * 256) {
+        int64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = d.scores[row * d.Lmax + min(j + 256 * u, jend - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (j + 256 * u < jend) one_e(j + 256 * u, v[u]);
+      }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) z += (uint64_t)__shfl_xor((int64_t)z, o, 64);
