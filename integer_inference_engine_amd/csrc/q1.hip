@@ -139,17 +139,22 @@ __global__ __launch_bounds__(64) void q1_prep_kernel(const int64_t* __restrict__
 // rms == 0. The envelope max|n| * max|gain| <= INT64_MAX is checked per element where n is formed.
 constexpr int kProNormCols = 4096;
 template <int NT>
-__device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, uint64_t& rms) {
+__device__ inline void pro_norm_row_load(const Q1Pro& p, int64_t (&v)[kProNormCols / NT]) {
+#pragma unroll
+  for (int k = 0; k < kProNormCols / NT; ++k) {
+    const int64_t c = threadIdx.x + NT * k;
+    v[k] = p.x[c < p.cols ? c : 0];                   // unconditional loads (no per-element branch); masked at use
+  }
+}
+// v: the row as loaded by pro_norm_row_load (issued before the weights, so the wait for it is not a wait for them)
+template <int NT>
+__device__ bool pro_norm_stats(const Q1Pro& p, uint64_t* s_red, int64_t* s_x, uint64_t& rms,
+                               int64_t (&v)[kProNormCols / NT]) {
   using namespace imie_fx;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kPer = kProNormCols / NT;
-  int64_t v[kPer];
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int64_t c = tid + NT * k;
-    const int64_t x = p.x[c < p.cols ? c : 0];       // unconditional loads (no per-element branch)
-    v[k] = c < p.cols ? x : 0;
-  }
+  for (int k = 0; k < kPer; ++k) v[k] = tid + NT * k < p.cols ? v[k] : 0;
   uint64_t amax = 0;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
@@ -414,15 +419,19 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
   };
 
   // this wave's first weight slab (PF: all of its slabs) is requested before the shared digit staging, so the
-  // latencies overlap
-  if (PF > 0) {
+  // latencies overlap; with a prologue, after the prologue's own inputs: the memory counter is in order, so the
+  // prologue's wait for its inputs would otherwise wait for every weight load too
+  auto issue_weights = [&]() {
+    if (PF > 0) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (live && j < nsl) load(j, s0 + j);
-  } else if (live) {
-    if (PERS) load_unit(0, 0);
-    else load(0, s0);
-  }
+      for (int j = 0; j < PF; ++j)
+        if (live && j < nsl) load(j, s0 + j);
+    } else if (live) {
+      if (PERS) load_unit(0, 0);
+      else load(0, s0);
+    }
+  };
+  if (PRO == kProNone) issue_weights();
   if (PRO != kProNone) {
     __shared__ uint64_t s_red[4 * (NT / 64)];
     // the range's inputs, element c0 + threadIdx.x + NT k for threadIdx.x + NT k < 512 nsl, all requested before any
@@ -438,13 +447,16 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
       ya[k] = PRO == kProNorm ? 0 : pro.x[cc];
       yb[k] = PRO == kProSiluMul ? pro.x2[cc] : (PRO == kProNorm ? pro.gain[cc] : 0);
     }
+    int64_t rowv[kProNormCols / NT];
+    if (PRO == kProNorm) pro_norm_row_load<NT>(pro, rowv);
+    const uint64_t gmax = PRO == kProNorm ? *pro.gmax : 0;
+    issue_weights();
     zero_share(pro.zero, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, (int64_t)gridDim.x * gridDim.y, threadIdx.x,
                NT);
-    const uint64_t gmax = PRO == kProNorm ? *pro.gmax : 0;
     uint64_t rms = 0;
     if (PRO == kProNorm) {
       __shared__ int64_t s_x[kProNormCols];
-      if (!pro_norm_stats<NT>(pro, s_red, s_x, rms)) return;      // the same verdict in every workgroup
+      if (!pro_norm_stats<NT>(pro, s_red, s_x, rms, rowv)) return;   // the same verdict in every workgroup
 #pragma unroll
       for (int k = 0; k < KY; ++k) {                          // this range's x from the row staged in LDS
         const int64_t c = c0 + threadIdx.x + NT * k;
