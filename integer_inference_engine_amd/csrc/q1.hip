@@ -236,9 +236,11 @@ template <bool S64, int R, int TT, int PF = 0, int PRO = kProNone, int NT = 256,
 __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
     Q1Segs sg, const uint4* __restrict__ xq, const int64_t* __restrict__ totals, const int* __restrict__ lslab,
     int64_t nslabs, int64_t nbp, int T, int frac, int64_t spk, int Lcap, int atomic_out, Q1Pro pro) {
-  static_assert(PRO == kProNone || (R == 1 && TT == 1 && PF > 0), "prologue: one token, one tile, prefetched range");
+  static_assert(PRO == kProNone || (R == 1 && TT == 1 && PF > 0) || (PERS && PRO == kProCopy),
+                "prologue: one token, one tile, prefetched range (or the persistent kernel's copy prologue)");
   static_assert(PRO != kProNone || NT == 256, "NT: workgroup size of the prologue variants");
-  static_assert(!PERS || (TT == 1 && PF == 0 && PRO == kProNone), "persistent: one token, pipelined slabs");
+  static_assert(!PERS || (TT == 1 && PF == 0 && (PRO == kProNone || PRO == kProCopy) && NT == 256),
+                "persistent: one token, pipelined slabs, at most 8 slabs staged by a copy prologue");
   extern __shared__ __align__(16) unsigned char smem[];
   uint4* stage = (uint4*)smem;                                   // [TT][spk][Lcap][32]
   const int lane = threadIdx.x & 63;
@@ -436,7 +438,8 @@ __global__ __launch_bounds__(NT) void q1_gemv_mfma_kernel(
     __shared__ uint64_t s_red[4 * (NT / 64)];
     // the range's inputs, element c0 + threadIdx.x + NT k for threadIdx.x + NT k < 512 nsl, all requested before any
     // use (a loop over a run-time count would wait for each load in turn)
-    constexpr int KY = PF * 512 / NT > 1 ? PF * 512 / NT : 1;
+    constexpr int PSL = PERS ? 8 : PF;                   // slabs a prologue stages (persistent: all, K <= 4096)
+    constexpr int KY = PSL * 512 / NT > 1 ? PSL * 512 / NT : 1;
     const int64_t nel = nsl * 512;
     const int64_t c0 = s0 * 512;
     int64_t ya[KY], yb[KY];
@@ -2178,7 +2181,10 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
     for (int i = 0; i < cnt; ++i) { zero.p[i] = outs[i]; zero.n[i] = T * ws[i]->N; }
   }
   const int64_t K = w0.nb * 128;
-  if (!prepped) {
+  // the persistent launch on K <= 4096 builds its digit table itself (copy prologue): no prep launch
+  static const bool pers_pro_on = [] { const char* e = getenv("IMIE_Q1_PERS_PRO"); return !(e && atoi(e) == 0); }();
+  const bool pers_pro = pers && !prepped && pers_pro_on && nslabs <= 8 && x_dev;
+  if (!prepped && !pers_pro) {
     imie_prof_mark(IMIE_K_Q1_PREP, st, true);
     Q1PrepOut po = {(uint32_t*)wk.xq.p, (int64_t*)wk.totals.p, (int*)wk.lslab.p, w0.nb, nbp, nslabs};
     hipLaunchKernelGGL(q1_prep_kernel, dim3((unsigned)nslabs, (unsigned)T), dim3(64), 0, st, x_dev, K, po, zero);
@@ -2189,7 +2195,9 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
   // staged limbs come in whole groups of four (a limb group reads either LDS or the global table)
   int Lcap = (int)(budget / ((size_t)Tc * spk * 512));
   Lcap = Lcap >= 8 ? 8 : (Lcap >= 4 ? 4 : 0);
-  const size_t lds = (size_t)Tc * spk * Lcap * 512 + 128;   // + the zero slot (8 x 16 B)
+  if (pers_pro) Lcap = 8;                            // the prologue stages every limb (spk <= 8: 32 KB)
+  // + the zero slot (8 x 16 B); a prologue also keeps the slab limb counts and block totals
+  const size_t lds = (size_t)Tc * spk * Lcap * 512 + 128 + (pers_pro ? 32 + 256 : 0);
   const int fr = (int)(frac > 63 ? 63 : frac);
   const dim3 grid((unsigned)((groups + 3) / 4), (unsigned)ksplit);
   dim3 pgrid = grid;
@@ -2222,7 +2230,17 @@ static int q1_apply_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_d
 #define IMIE_Q1_LAUNCH_PF(S64_, PF_)                                                                         \
   hipLaunchKernelGGL((q1_gemv_mfma_kernel<S64_, 1, 1, PF_>), grid, dim3(256), lds, st, sgt, xq, tot, ls, nslabs, \
                      nbp, tn, fr, spk, Lcap, mode, Q1Pro{})
-    if (pers) {
+    if (pers_pro) {
+      Q1Pro pro = {};
+      pro.x = x_dev;
+      pro.cols = K;
+      if (w0.scale64)
+        hipLaunchKernelGGL((q1_gemv_mfma_kernel<true, 4, 1, 0, kProCopy, 256, true>), pgrid, dim3(256), lds, st, sgt,
+                           nullptr, nullptr, nullptr, nslabs, nbp, tn, fr, spk, Lcap, mode, pro);
+      else
+        hipLaunchKernelGGL((q1_gemv_mfma_kernel<false, 4, 1, 0, kProCopy, 256, true>), pgrid, dim3(256), lds, st, sgt,
+                           nullptr, nullptr, nullptr, nslabs, nbp, tn, fr, spk, Lcap, mode, pro);
+    } else if (pers) {
       if (w0.scale64)
         hipLaunchKernelGGL((q1_gemv_mfma_kernel<true, 4, 1, 0, kProNone, 256, true>), pgrid, dim3(256), lds, st, sgt,
                            xq, tot, ls, nslabs, nbp, tn, fr, spk, Lcap, mode, Q1Pro{});
