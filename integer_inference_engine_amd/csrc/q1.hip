@@ -1884,6 +1884,10 @@ static bool gemm_pm() {
   return v;
 }
 
+static int ps_shape() {
+  static const int v = [] { const char* e = getenv("IMIE_PS_SHAPE"); return e ? atoi(e) : 1; }();
+  return v;
+}
 static int ps_map() { const char* e = getenv("IMIE_PS_MAP"); return e ? atoi(e) : 1; }
 
 // the multi-weight unfolded-partial kernel where its bounds hold (IMIE_GEMM_PS=0 disables; tuning and tests)
@@ -2046,8 +2050,10 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
     const int64_t nblk = ((ntt128 + kPsBt - 1) / kPsBt) * ((tiles + kPsBo - 1) / kPsBo);
     const dim3 pgrid((unsigned)(P.map ? (nblk + 7) / 8 * 8 * (kPsBt * kPsBo)
                                       : (ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * tiles : ntt128 * tiles)));
-    // one partial: 16 waves of 32 x 32 (128 VGPRs); two: 8 waves of 32 x 64 (the second partial's registers)
-    if (np == 1) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1>), pgrid, dim3(1024), 0, st, P);
+    // 8 waves of 32 x 64 (IMIE_PS_SHAPE=0 with one partial: 16 waves of 32 x 32, four per SIMD, which read
+    // twice the LDS operand bytes per MFMA)
+    if (np == 1 && ps_shape() == 0) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1>), pgrid, dim3(1024), 0, st, P);
+    else if (np == 1) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 1>), pgrid, dim3(512), 0, st, P);
     else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2>), pgrid, dim3(512), 0, st, P);
     IMIE_HIP(hipGetLastError());
   } else {
