@@ -1722,7 +1722,7 @@ __global__ __launch_bounds__(64 * NW) void pf_fused8_kernel(AttnDesc d) {
   const int64_t pt = npt - 1 - imie_umod32(blockIdx.x, npt);   // longest rows first
   const int64_t b = imie_udiv32(bh, d.H), h = imie_umod32(bh, d.H), kv = imie_udiv32(h, d.H / d.Hkv);
   const int64_t bkv = b * d.Hkv + kv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), m = lane & 15, g = lane >> 4;
   if (blockIdx.x == 0 && tid == 0) check_rope_guard(d);
   const int64_t row0 = bh * d.M + pt * kFfRows;                // query row r = (b * H + h) * M + m
   const int64_t len = d.starts ? d.starts[b] + d.M : d.lengths[b];
@@ -1738,11 +1738,13 @@ __global__ __launch_bounds__(64 * NW) void pf_fused8_kernel(AttnDesc d) {
   {
     const int qi = (tid >> 4) & 15, qc = 8 * (tid & 15);
     const bool qrow = tid < 256 && pt * kFfRows + qi < d.M;
+    // the tile's rows are consecutive positions of one (b, h): q offsets by stride, no per-row index division
+    const int64_t qrow_off = b * d.qsb + h * d.qsh + (pt * kFfRows + qi) * d.qsm;
     int64_t qv[8];
     uint64_t mq = 0;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      qv[c] = (qrow && qc + c < d.hd) ? d.q[qoff(d, row0 + qi) + qc + c] : 0;
+      qv[c] = (qrow && qc + c < d.hd) ? d.q[qrow_off + qc + c] : 0;
       const uint64_t a = imie_absu64(qv[c]);
       mq = a > mq ? a : mq;
     }
@@ -1753,10 +1755,21 @@ __global__ __launch_bounds__(64 * NW) void pf_fused8_kernel(AttnDesc d) {
     uint64_t mqa = 0;
     for (int i = 0; i < kFfRows; ++i) mqa = s_mq[i] > mqa ? s_mq[i] : mqa;
     const int Lq0 = imie_limbs_needed(mqa);
+    // balanced base-256 digits, limb by limb: the digit is the low byte read as int8, and the rest of the value
+    // is (x - digit) >> 8; a thread's 8 dims of one limb go to LDS as one 8-byte store
     if (tid < 256)
-      for (int lq = 0; lq < 8; ++lq)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) sQ[lq][qi][qc + c] = lq < Lq0 ? (int8_t)bal_digit(qv[c], lq) : (int8_t)0;
+      for (int lq = 0; lq < 8; ++lq) {
+        uint64_t pk = 0;
+        if (lq < Lq0) {                                        // uniform: limbs above the count are zero
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            pk |= (uint64_t)(uint8_t)qv[c] << (8 * c);
+            qv[c] = (int64_t)((uint64_t)qv[c] - (uint64_t)(int64_t)(int8_t)qv[c]) >> 8;
+          }
+        }
+        *(uint64_t*)&sQ[lq][qi][qc] = pk;
+      }
     __syncthreads();
   }
   uint64_t mqa = 0;
@@ -1802,7 +1815,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   constexpr UT SBIT = (UT)1 << (8 * sizeof(UT) - 1);
   constexpr int NTP = F32 ? 6 : 7;                             // PV exponents lp + db (lp < 3 when F32)
   const int64_t bkv = b * d.Hkv + kv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), m = lane & 15, g = lane >> 4;
   auto row_lv = [&](int i) -> int64_t {                         // keys visible to tile row i (0: no row)
     const int64_t mm = pt * kFfRows + i;
     if (mm >= d.M) return 0;
@@ -1810,6 +1823,8 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   };
   int64_t vis = 0;
   for (int i = 0; i < kFfRows; ++i) vis = max(vis, row_lv(i));
+  vis = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)vis) |
+        ((int64_t)__builtin_amdgcn_readfirstlane((int)(vis >> 32)) << 32);   // uniform: scalar loop bounds
   const int64_t HDv = HD ? HD : d.hd;                          // head dim (compile-time for the 128 case)
   const int KS = (int)((HDv + 63) / 64);
   int32_t lvr[4];                                              // visible keys of this lane's rows 4 g + i
@@ -1840,6 +1855,20 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
+  // the q digit operands of this lane (row m, dims 16 g .. and 64 + 16 g ..) for every limb: with at most 3 limbs
+  // they stay in registers for all passes (24 VGPRs) instead of being read from LDS for every key tile
+  constexpr bool QREG = LQ <= 3;
+  auto q_operand = [&](int lq, int hh) -> v4i {
+    if (hh == 1 && KS < 2) return v4i{0, 0, 0, 0};
+    if (64 * hh + 16 * g >= HDv) return v4i{0, 0, 0, 0};
+    return *(const v4i*)&sQ[lq][m][64 * hh + 16 * g];
+  };
+  v4i qreg[QREG ? LQ : 1][2];
+#pragma unroll
+  for (int lq = 0; lq < (QREG ? LQ : 0); ++lq) {
+    qreg[lq][0] = q_operand(lq, 0);
+    qreg[lq][1] = q_operand(lq, 1);
+  }
   // scores of the lane's 4 rows for key t + m from the tile's K digits; invalid entries INT64_MIN
   auto scores = [&](int64_t t, const v4i (&bk)[4][2], ST sc[4]) {
     const int32_t j = (int32_t)t + m;
@@ -1848,10 +1877,8 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     for (int e = 0; e < NE; ++e) T[e] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int lq = 0; lq < LQ; ++lq) {                          // limbs above the tile's count hold zero digits
-      v4i a0 = *(const v4i*)&sQ[lq][m][16 * g];
-      v4i a1 = KS > 1 ? *(const v4i*)&sQ[lq][m][64 + 16 * g] : v4i{0, 0, 0, 0};
-      if (16 * g >= HDv) a0 = v4i{0, 0, 0, 0};
-      if (64 + 16 * g >= HDv) a1 = v4i{0, 0, 0, 0};
+      const v4i a0 = QREG ? qreg[QREG ? lq : 0][0] : q_operand(lq, 0);
+      const v4i a1 = QREG ? qreg[QREG ? lq : 0][1] : q_operand(lq, 1);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         if (lq + db >= NE) continue;
@@ -1929,9 +1956,9 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   const int64_t rows_all = d.B * d.H * d.M;
   const bool fx32 = (d.dclip >> 32) == 0 && (d.log2e >> 32) == 0;
   auto expv = [&](ST s, int i) -> int64_t {
-    if (s == SMIN) return 0;
     if constexpr (F32) {
-      // exp2_neg_fixed32 at frac 16 with dclip < 2^20 and log2e < 2^17: every product fits 32 bits
+      // exp2_neg_fixed32 at frac 16 with dclip < 2^20 and log2e < 2^17: every product fits 32 bits. Evaluated
+      // for every entry and masked at the end (a select, not a branch per row)
       uint32_t dd = (uint32_t)(Mx[i] - s);
       if (dd > (uint32_t)d.dclip) dd = (uint32_t)d.dclip;
       const uint32_t u = (uint32_t)(((uint64_t)dd * (uint32_t)d.log2e) >> 16);
@@ -1939,8 +1966,10 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
       const uint32_t f2 = (f * f) >> 16, f3 = (f2 * f) >> 16;
       const int32_t poly = 65536 - (int32_t)((45426u * f) >> 16) + (int32_t)((15743u * f2) >> 16) -
                            (int32_t)((3638u * f3) >> 16);
-      return poly <= 0 ? 0 : (int64_t)((uint32_t)poly >> k);      // k < 32 (u < 2^21)
+      const uint32_t e = poly <= 0 ? 0u : (uint32_t)poly >> k;   // k < 32 (u < 2^21)
+      return (int64_t)(s == SMIN ? 0u : e);
     } else {
+      if (s == SMIN) return 0;
       int64_t dd = (int64_t)((uint64_t)Mx[i] - (uint64_t)s);
       if (dd > d.dclip) dd = d.dclip;
       return exp_clipped(dd, d.frac, d.log2e, fx32);
@@ -2003,20 +2032,22 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   // quotient (< 2^17), so its floor is off by at most one; the remainder (e << 16) - q Z lies in (-Z, 2Z), below
   // 2^31 in magnitude, so it is exact in wrapping 32-bit arithmetic and settles q
   auto probv = [&](int64_t e, int i) -> int64_t {
-    if (Z[i] == 0) return 0;
     if constexpr (F32) {
       uint32_t q = (uint32_t)((float)(uint32_t)e * rzf[i]);
       const int32_t r = (int32_t)(((uint32_t)e << 16) - q * (uint32_t)Z[i]);
-      if (r < 0) --q;
-      else if ((uint32_t)r >= (uint32_t)Z[i]) ++q;
-      return (int64_t)q;
+      q = r < 0 ? q - 1 : ((uint32_t)r >= (uint32_t)Z[i] ? q + 1 : q);
+      return (int64_t)(Z[i] == 0 ? 0u : q);                    // Z = 0: a row with no visible keys
     } else {
+      if (Z[i] == 0) return 0;
       return prob_div(e, d.frac, Z[i], rz[i]);
     }
   };
   // pass 3: p digits of each 64-key step into LDS, then PV
   const int Lp = F32 ? 3 : imie_limbs_needed((uint64_t)1 << d.frac);   // <= 4 (frac <= 29); 3 at frac 16
   const int DT = (int)(HDv / 16);
+  const int64_t qtile = b * d.qsb + h * d.qsh + pt * kFfRows * d.qsm;   // offset of the tile's first row
+  // every wave's dim tiles exist when the waves cover the head dim exactly (head dim 128, 4 waves of 2 tiles)
+  constexpr bool ALLT = HD != 0 && 16 * DPW * NW == HD;
   const int8_t* Vb = (const int8_t*)d.V;
   v4i Tp[DPW][NTP];
   uint64_t O[DPW][4];
@@ -2057,7 +2088,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const uint32_t off = ((uint32_t)db * (uint32_t)HDv + (uint32_t)(16 * tile + m)) * (uint32_t)d.P + 16u * g;
-          bv[tt][ks][db] = tile < DT ? ld16u(vs, off, (uint32_t)(4 * HDv * d.P)) : v4i{0, 0, 0, 0};
+          bv[tt][ks][db] = (ALLT || tile < DT) ? ld16u(vs, off, (uint32_t)(4 * HDv * d.P)) : v4i{0, 0, 0, 0};
         }
       }
     }
@@ -2093,7 +2124,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
         const v4i a = *(const v4i*)&sP[buf][lp][m][64 * ks + 16 * g];
 #pragma unroll
         for (int tt = 0; tt < DPW; ++tt) {
-          if (DPW * wave + tt >= DT) continue;
+          if (!ALLT && DPW * wave + tt >= DT) continue;
 #pragma unroll
           for (int db = 0; db < 4; ++db)
             if (lp + db < NTP) Tp[tt][lp + db] = mfma8(a, bv[tt][ks][db], Tp[tt][lp + db]);
@@ -2117,7 +2148,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     for (int i = 0; i < 4; ++i) {
       const int rr = 4 * g + i;
       if (lvr[i] == 0) continue;
-      d.out[qoff(d, row0 + rr) + 16 * tile + m] = (int64_t)O[tt][i] >> d.frac;
+      d.out[qtile + rr * d.qsm + 16 * tile + m] = (int64_t)O[tt][i] >> d.frac;
     }
   }
   if (tid < kFfRows && row_lv(tid) > 0) {
