@@ -1869,9 +1869,12 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     qreg[lq][0] = q_operand(lq, 0);
     qreg[lq][1] = q_operand(lq, 1);
   }
-  // scores of the lane's 4 rows for key t + m from the tile's K digits; invalid entries INT64_MIN
-  auto scores = [&](int64_t t, const v4i (&bk)[4][2], ST sc[4]) {
-    const int32_t j = (int32_t)t + m;
+  // scores of the lane's 4 rows for key t + m from the tile's K digits; invalid entries INT64_MIN. Transposed
+  // (TR, pass 3): the same MFMAs with the operands swapped give S^T, whose lane holds keys t + 4 g + i of row m
+  const int32_t lvm = (int32_t)row_lv(m);                      // visible keys of row m
+  auto scores = [&](int64_t t, const v4i (&bk)[4][2], ST sc[4], auto tr) {
+    constexpr bool TR = decltype(tr)::value;
+    const int32_t j = (int32_t)t + (TR ? 4 * g : m);
     v4i T[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) T[e] = v4i{0, 0, 0, 0};
@@ -1882,8 +1885,8 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         if (lq + db >= NE) continue;
-        v4i x = mfma8(a0, bk[db][0], T[lq + db]);
-        if (KS > 1) x = mfma8(a1, bk[db][1], x);
+        v4i x = TR ? mfma8(bk[db][0], a0, T[lq + db]) : mfma8(a0, bk[db][0], T[lq + db]);
+        if (KS > 1) x = TR ? mfma8(bk[db][1], a1, x) : mfma8(a1, bk[db][1], x);
         T[lq + db] = x;
       }
     }
@@ -1904,7 +1907,7 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
         s = (int64_t)Sx >> d.frac;
         s = (int64_t)((uint64_t)s * (uint64_t)d.inv_sqrt) >> d.frac;
       }
-      sc[i] = j < lvr[i] ? (ST)s : SMIN;
+      sc[i] = (TR ? j + i < lvm : j < lvr[i]) ? (ST)s : SMIN;
     }
   };
   // cross-lane (16 keys) and cross-wave reduction of per-row values held as lanes (g, i)
@@ -1941,12 +1944,12 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
       const int64_t t2 = t + STEP;
       load_k(t2 < vis ? t2 : t, bkB);
       ST sc[4];
-      scores(t, bkA, sc);
+      scores(t, bkA, sc, std::false_type{});
       use(sc);
       if (t2 >= vis) break;
       const int64_t t3 = t2 + STEP;
       load_k(t3 < vis ? t3 : t2, bkA);
-      scores(t2, bkB, sc);
+      scores(t2, bkB, sc, std::false_type{});
       use(sc);
       t = t3;
     }
@@ -2014,19 +2017,31 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
       }
     return;
   }
+  // pass 3 works on S^T: each lane's entries belong to row m, whose maximum and Z it needs
+  ST Mr;
+  UT Zr;
   if constexpr (PASSES == 2) {
+    Mr = lvm ? (ST)(int64_t)d.acc[row0 + m] : (ST)0;
+    Zr = lvm ? (UT)d.acc[rows_all + row0 + m] : (UT)0;
+  } else {
+    // row m's values sit in element m & 3 of the lanes with g = m >> 2
+    Mr = 0;
+    Zr = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      Mx[i] = lvr[i] ? (ST)(int64_t)d.acc[row0 + 4 * g + i] : (ST)0;
-      Z[i] = lvr[i] ? (UT)d.acc[rows_all + row0 + 4 * g + i] : (UT)0;
+      const ST mv = (ST)__shfl((int64_t)Mx[i], 16 * (m >> 2), 64);
+      const UT zv = (UT)(uint64_t)__shfl((int64_t)(uint64_t)Z[i], 16 * (m >> 2), 64);
+      if ((m & 3) == i) { Mr = mv; Zr = zv; }
     }
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { Mx[i] = Mr; Z[i] = Zr; }     // expv / probv read row m's values
   double rz[4];
   float rzf[4];                                                 // F32: 2^16 / Z for the single-precision quotient
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    rz[i] = Z[i] != 0 ? 1.0 / (double)Z[i] : 0.0;
-    rzf[i] = Z[i] != 0 ? (float)(65536.0 / (double)Z[i]) : 0.0f;
+    rz[i] = Zr != 0 ? 1.0 / (double)Zr : 0.0;
+    rzf[i] = Zr != 0 ? (float)(65536.0 / (double)Zr) : 0.0f;
   }
   // p = floor((e << frac) / Z). F32 (e <= 2^16, Z < 2^30): the float estimate e * (2^16 / Z) is within 2^-5 of the
   // quotient (< 2^17), so its floor is off by at most one; the remainder (e << 16) - q Z lies in (-Z, 2Z), below
@@ -2101,20 +2116,23 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
   for (int64_t t0 = 0; t0 < vis; t0 += STEP, buf ^= 1) {
     const int64_t t = t0 + 16 * wave;
     ST sc[4] = {SMIN, SMIN, SMIN, SMIN};
-    if (t < vis) scores(t, bk, sc);
+    if (t < vis) scores(t, bk, sc, std::true_type{});
     // issued whatever the next step is (past vis: this tile again; see walk)
     load_k(t + STEP < vis ? t + STEP : (t < vis ? t : 16 * wave), bk);
+    uint32_t pk[4] = {0, 0, 0, 0};                              // per limb: the digits of keys 4 g .. 4 g + 3
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t e = expv(sc[i], i);
       const int64_t p = probv(e, i);
-      mp[i] = (UT)p > mp[i] ? (UT)p : mp[i];
+      mp[0] = (UT)p > mp[0] ? (UT)p : mp[0];
       // balanced base-256 digits of 0 <= p <= 2^frac < 2^30: the bytes of p + 0x80808080, each less 0x80
       const uint32_t dg = ((uint32_t)p + 0x80808080u) ^ 0x80808080u;
 #pragma unroll
-      for (int lp = 0; lp < 4; ++lp)
-        if (lp < Lp) sP[buf][lp][4 * g + i][16 * wave + m] = (int8_t)(dg >> (8 * lp));
+      for (int lp = 0; lp < 4; ++lp) pk[lp] |= ((dg >> (8 * lp)) & 0xFFu) << (8 * i);
     }
+#pragma unroll
+    for (int lp = 0; lp < 4; ++lp)                            // one 4-byte store per limb: row m, 4 keys
+      if (lp < Lp) *(uint32_t*)&sP[buf][lp][m][16 * wave + 4 * g] = pk[lp];
     __syncthreads();                                          // the step's p digits are in LDS
 #pragma unroll
     for (int ks = 0; ks < KSP; ++ks)
@@ -2134,11 +2152,16 @@ __device__ __forceinline__ void pf_fused8_body(const AttnDesc& d, FfShared& S, i
     if (++steps == 64) { fold(); steps = 0; }
   }
   fold();
-  // p maxima of the rows for the PV bound (lanes of one g share rows)
-  uint64_t MP[4];
+  // p maxima of the rows for the PV bound: row m's over the lanes m + 16 g, then per wave into s_red
   {
-    uint64_t mp64[4] = {mp[0], mp[1], mp[2], mp[3]};
-    reduce_rows(mp64, true, MP);
+    uint64_t v = mp[0];
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+      const uint64_t w2 = (uint64_t)__shfl_xor((int64_t)v, o, 64);
+      v = w2 > v ? w2 : v;
+    }
+    if (g == 0) s_red[wave][m] = v;
+    __syncthreads();
   }
 #pragma unroll
   for (int tt = 0; tt < DPW; ++tt) {
