@@ -95,3 +95,44 @@ def test_kv8_prefill_layouts_ragged_continued(gpu, layout):
                 assert np.array_equal(k[:, s0:], nk[li]) and np.array_equal(v[:, s0:], nv[li]), (b, li)
     finally:
         net.close()
+
+
+def test_kv8_prefill_head128_mixed_launch_paths(gpu):
+    """Head dim 128 with one kv head's cached K near 2^26: the query tiles of its 4 heads fail the 32-bit score bound
+    (128 max|q| max|K| < 2^47) and are left by the 32-bit launch to the general one, which walks the flagged tiles;
+    the other kv head's tiles stay on the 32-bit path. Two ragged sequences continuing seeded caches."""
+    import torch
+    H, Hkv, hd = 8, 2, 128
+    seed = 97
+    model = workloads.bonsai_model(seed, d=256, H=H, Hkv=Hkv, hd=hd, dff=512, n_layers=2, vocab=64, ctx=CAP)
+    cfg = model["cfg"]
+    c = {"H": H, "Hkv": Hkv, "hd": hd}
+    starts, M = [50, 130], 40
+    print(f"[kv8-prefill-shapes] mixed 32-bit / general tiles {starts} + {M}", flush=True)
+    ks, vs = [], []
+    for b in range(2):
+        kb, vb = [], []
+        for li in range(cfg["n_layers"]):
+            k = prng.uniform_int(seed, 10 + 4 * b + li, (Hkv, starts[b], hd), -(1 << 20), 1 << 20)
+            k[0] = prng.uniform_int(seed, 30 + 4 * b + li, (starts[b], hd), -(1 << 26), 1 << 26)
+            kb.append(k)
+            vb.append(prng.uniform_int(seed, 12 + 4 * b + li, (Hkv, starts[b], hd), -(1 << 20), 1 << 20))
+        ks.append(kb)
+        vs.append(vb)
+    net = _net(gpu, model, 2)
+    try:
+        for b in range(2):
+            net.seed(b, np.stack(ks[b]), np.stack(vs[b]))
+        xs = [q1_rows(*model["embed"], prng.uniform_int(seed, 20 + b, (M,), 0, cfg["vocab"])) for b in range(2)]
+        x = torch.from_numpy(np.concatenate(xs)).cuda()
+        assert net.forward(x, starts, M) == 0
+        got = x.cpu().numpy()
+        for b, s0 in enumerate(starts):
+            want, nk, nv = _oracle(model, c, xs[b], ks[b], vs[b], s0)
+            bad = np.flatnonzero(got[b * M:(b + 1) * M] != want)
+            assert bad.size == 0, f"sequence {b}: {bad.size} values differ"
+            for li in range(cfg["n_layers"]):
+                k, v = net.export_kv(li, b, s0 + M)
+                assert np.array_equal(k[:, s0:], nk[li]) and np.array_equal(v[:, s0:], nv[li]), (b, li)
+    finally:
+        net.close()
