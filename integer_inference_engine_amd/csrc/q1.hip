@@ -1368,8 +1368,9 @@ __global__ __launch_bounds__(256) void q1_gemm_wide_kernel(GemmArgs a) {
 //   host proves, from the weight's row sums of |scale| and |S| < 2^30 (3 limbs), that the sum over the partial's
 //   block range stays below 2^31 in magnitude, so the partial is exact after sign extension whatever it wrapped
 //   through on the way (NP = 2: the second half of the blocks in a second partial). No int64 accumulators: a
-//   16 x 32 .. 32 x 32 sub-tile per wave fits 128 VGPRs, so 16 waves (four per SIMD) hide one another's MFMA ->
-//   VALU dependencies and barrier waits.
+//   32 x 64 sub-tile per wave (8 waves, two per SIMD) holds 8 independent MFMA chains, and each A operand row read
+//   from LDS serves 4 output groups and each B row 2 token groups (a 32 x 32 sub-tile, 16 waves at 128 VGPRs,
+//   reads twice the LDS bytes per MFMA).
 // * The copies of block b + 1 are issued in three parts, one before each limb's MFMAs of block b, so the copy
 //   traffic is spread over the block instead of queueing in front of it.
 // * Slabs needing more than 3 limbs over a 64-token half (rare: activations beyond 2^23) are computed by the same
