@@ -1008,6 +1008,10 @@ __device__ inline void pm_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff
 // 16 the swizzle term depends on the lane only, so each operand read is one ds_read_b128 at a constant offset.
 constexpr int kPmTok = 128;
 
+// ACC: the launch adds into its outputs (a residual); the epilogue then reads each 16 x 16 tile's 4 outputs before
+// writing them (a read after a store the compiler cannot tell apart waits for that store, one round trip per
+// element). Without ACC the epilogue only stores, and the rest of the kernel compiles as before.
+template <bool ACC>
 __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg_bytes, uint32_t sg_bytes,
                                                          uint32_t sc_bytes) {
   constexpr int MT = 2, NT = 4;
@@ -1226,13 +1230,20 @@ __global__ __launch_bounds__(512) void q1_gemm_pm_kernel(GemmArgs a, uint32_t xg
     for (int jj = 0; jj < NT; ++jj) {
       const int64_t o = o0 + 16 * jj + m;
       if (o >= a.N) continue;
+      int64_t prev[4] = {0, 0, 0, 0};
+      if constexpr (ACC) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t t = t0 + 16 * i + 4 * g + r;
+          prev[r] = t < a.T ? a.out[t * a.N + o] : 0;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t t = t0 + 16 * i + 4 * g + r;
         if (t >= a.T) continue;
         const int64_t v = (int64_t)((uint64_t)acc[i][jj][r] + (uint64_t)(int64_t)part[i][jj][r]);
-        int64_t* dst = a.out + t * a.N + o;
-        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)v) : v;
+        a.out[t * a.N + o] = (int64_t)((uint64_t)prev[r] + (uint64_t)v);
       }
     }
 }
@@ -1388,7 +1399,8 @@ struct PsArgs {
   int map;                         // 1: blocked tile order (see the kernel)
 };
 
-template <int MT, int NT, int NP>
+// ACC: some segment adds into its outputs (the segment's accumulate flag); see q1_gemm_pm_kernel
+template <int MT, int NT, int NP, bool ACC = false>
 __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) {
   constexpr int NW = 64 / (MT * NT);             // waves of 16 MT x 16 NT covering the 128 x 128 tile
   constexpr int WO = 128 / (16 * NT);            // waves along the outputs
@@ -1576,14 +1588,23 @@ __global__ __launch_bounds__(4096 / (MT * NT)) void q1_gemm_ps_kernel(PsArgs P) 
     for (int jj = 0; jj < NT; ++jj) {
       const int64_t o = o0 + 16 * jj + m;
       if (o >= a.N) continue;
+      int64_t prev[4] = {0, 0, 0, 0};
+      if constexpr (ACC) {
+        if (a.accumulate) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t t = t0 + 16 * i + 4 * g + q;
+            prev[q] = t < T ? a.out[t * a.N + o] : 0;
+          }
+        }
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t t = t0 + 16 * i + 4 * g + q;
         if (t >= T) continue;
         int64_t v = (int64_t)part[i][jj][q];
         if constexpr (NP == 2) v += (int64_t)sav[i][jj][q];
-        int64_t* dst = a.out + t * a.N + o;
-        *dst = a.accumulate ? (int64_t)((uint64_t)*dst + (uint64_t)v) : v;
+        a.out[t * a.N + o] = (int64_t)((uint64_t)prev[q] + (uint64_t)v);
       }
     }
   if (wide0 || wide1) {                               // uniform over the workgroup
@@ -2053,9 +2074,18 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
                                       : (ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * tiles : ntt128 * tiles)));
     // 8 waves of 32 x 64 (IMIE_PS_SHAPE=0 with one partial: 16 waves of 32 x 32, four per SIMD, which read
     // twice the LDS operand bytes per MFMA)
-    if (np == 1 && ps_shape() == 0) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1>), pgrid, dim3(1024), 0, st, P);
-    else if (np == 1) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 1>), pgrid, dim3(512), 0, st, P);
-    else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2>), pgrid, dim3(512), 0, st, P);
+    bool acc = false;
+    for (int i = 0; i < cnt; ++i) acc = acc || gas[i].accumulate != 0;
+    if (np == 1 && ps_shape() == 0) {
+      if (acc) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1, true>), pgrid, dim3(1024), 0, st, P);
+      else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 2, 1, false>), pgrid, dim3(1024), 0, st, P);
+    } else if (np == 1) {
+      if (acc) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 1, true>), pgrid, dim3(512), 0, st, P);
+      else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 1, false>), pgrid, dim3(512), 0, st, P);
+    } else {
+      if (acc) hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2, true>), pgrid, dim3(512), 0, st, P);
+      else hipLaunchKernelGGL((q1_gemm_ps_kernel<2, 4, 2, false>), pgrid, dim3(512), 0, st, P);
+    }
     IMIE_HIP(hipGetLastError());
   } else {
     for (int i = 0; i < cnt; ++i) {
@@ -2070,8 +2100,12 @@ static int q1_gemm_multi(const Q1Weight* const* ws, int cnt, const int64_t* x_de
         ga.wide_any = (int*)wk.wide.p;
         const int64_t ntt128 = (T + kPmTok - 1) / kPmTok;
         const dim3 pgrid((unsigned)(ntt128 >= 8 ? 8 * ((ntt128 + 7) / 8) * ga.nto : ntt128 * ga.nto));
-        hipLaunchKernelGGL(q1_gemm_pm_kernel, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes, (uint32_t)sg_bytes,
-                           (uint32_t)sc_bytes);
+        if (ga.accumulate)
+          hipLaunchKernelGGL(q1_gemm_pm_kernel<true>, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes,
+                             (uint32_t)sg_bytes, (uint32_t)sc_bytes);
+        else
+          hipLaunchKernelGGL(q1_gemm_pm_kernel<false>, pgrid, dim3(512), 0, st, ga, (uint32_t)xg_bytes,
+                             (uint32_t)sg_bytes, (uint32_t)sc_bytes);
         hipLaunchKernelGGL(q1_gemm_wide_kernel<false>, grid, dim3(256), 0, st, ga);
       } else {
         // few token tiles (batched decode): split K over grid.y so the launch fills the chip; each split adds its
