@@ -166,7 +166,9 @@ __global__ __launch_bounds__(256) void guard_reduce_kernel(const uint64_t* __res
 // 64 consecutive slots. Each thread's 32 V elements (element tid + 256 k of the 64 x hd tile) are requested in
 // one round before any is encoded. The workgroup also folds its rows' max|K| / max|V| into the running maxima.
 __global__ __launch_bounds__(256) void kv8_v_append_kernel(QkHeadArgs a) {
-  __shared__ int8_t sv[4][128][64];
+  // rows padded from 64 to 68 bytes: the byte writes of 64 consecutive dims (stride one row) then fall in 64
+  // distinct banks (at 64 bytes they shared 4)
+  __shared__ int8_t sv[4][128][68];
   const int64_t bkv = blockIdx.y, b = imie_udiv32(bkv, a.Hkv), kvh = imie_umod32(bkv, a.Hkv);
   const int64_t m0 = (int64_t)blockIdx.x * 64;
   const int tid = threadIdx.x;
